@@ -1,0 +1,242 @@
+#!/usr/bin/env python3
+"""Decode-step benchmark of the fused decode-on-codes KV attention on one MI355X.
+
+A step is one decode-attention pass for every sequence of the batch over its
+whole two-tier cache (K4 asym-NF4 + 2 % fp16 outliers, V3 PolarQuant, fp16 hot
+window of 512).  The cache is pre-filled through the GPU encode path with
+seeded synthetic fp16 keys/values of the measurement spec (lognormal
+per-channel key scale, 2 % x10 channels, RoPE; N(0,1) values); queries are
+fp16 N(0,1).  Inputs are resident in HBM before timing starts.  Several cache
+replicas (>= 1 GB together) are used round-robin so the 256 MB Infinity Cache
+cannot serve repeat steps.
+
+Prints one JSON line.  `value` is microseconds per decode step (lower is
+better); `roofline.achieved` is the canonical compressed-KV bytes of one step
+divided by the average duration of the split-K kernel, timed with HIP events
+on the stream it runs on.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "turboquant-pro_amd"))
+
+METRIC = "decode-attention µs/step + achieved HBM GB/s on codes, bs16×32K GQA-8"
+HBM_PEAK_GBS = 8000.0
+
+CONFIGS = {
+    # the BASELINE metric's workload: Llama-3-8B GQA shape at batch 16 x 32K
+    "headline": dict(B=16, Hkv=8, Hq=32, L=32768, vbits=3),
+    "c1_8k": dict(B=16, Hkv=8, Hq=32, L=8192, vbits=3),
+    "c2_128k": dict(B=1, Hkv=8, Hq=32, L=131072, vbits=3),
+    "c0_mha4k": dict(B=1, Hkv=32, Hq=32, L=4096, vbits=4),
+    "c4_70b": dict(B=32, Hkv=8, Hq=64, L=32768, vbits=3),
+}
+
+
+def n_groups(L, W=512):
+    G = (W + 1) // 2
+    return 0 if L <= W else (L - (W + 1)) // G + 1
+
+
+def step_bytes(lens, Hkv, Hq, D=128, kbits=4, vbits=3, W=512, n_out=640, out_bytes=2):
+    """Canonical compressed bytes of one decode step (storage-of-record sizes):
+    per (sequence, kv head) n_cold*(D*kb/8 + D*vb/8 + 4) + n_grp*(2*D*4 + n_out*6)
+    + n_hot*2*D*2, plus q in and output per query head."""
+    G = (W + 1) // 2
+    tot = 0
+    for L in lens:
+        ng = n_groups(L, W)
+        n_cold, n_hot = ng * G, L - ng * G
+        tot += Hkv * (n_cold * (D * kbits // 8 + D * vbits // 8 + 4) + ng * (2 * D * 4 + n_out * 6)
+                      + n_hot * 2 * D * 2 + (Hq // Hkv) * D * (2 + out_bytes))
+    return tot
+
+
+def synth_chunk(torch, gen, scale, t0, n, B, Hkv, D=128, theta=10000.0):
+    """fp16 keys/values for positions [t0, t0+n): N(0,1) * per-channel scale,
+    RoPE (rotate_half); values N(0,1)."""
+    dev = scale.device
+    k = torch.randn((B, Hkv, n, D), generator=gen, device=dev, dtype=torch.float32) * scale
+    half = D // 2
+    inv = theta ** (-2.0 * torch.arange(half, device=dev, dtype=torch.float64) / D)
+    ang = torch.arange(t0, t0 + n, device=dev, dtype=torch.float64)[:, None] * inv[None, :]
+    cos = torch.cat([ang.cos(), ang.cos()], 1).float()
+    sin = torch.cat([ang.sin(), ang.sin()], 1).float()
+    rh = torch.cat([-k[..., half:], k[..., :half]], -1)
+    k = (k * cos + rh * sin).half()
+    v = torch.randn((B, Hkv, n, D), generator=gen, device=dev, dtype=torch.float32).half()
+    return k, v
+
+
+def build_pool(torch, cfg, seed, chunk=4096):
+    from turboquant_pro_amd import TQKVPool
+    B, Hkv, Hq, L = cfg["B"], cfg["Hkv"], cfg["Hq"], cfg["L"]
+    pool = TQKVPool(n_kv_heads=Hkv, n_q_heads=Hq, max_batch=B, max_seq_len=L,
+                    value_bits=cfg["vbits"], seed=seed)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    scale = torch.exp(torch.randn((B, Hkv, 1, 128), generator=gen, device="cuda"))
+    n_hot_ch = round(0.02 * 128)
+    for b in range(B):
+        for h in range(Hkv):
+            ch = torch.randperm(128, generator=gen, device="cuda")[:n_hot_ch]
+            scale[b, h, 0, ch] *= 10.0
+    t = 0
+    while t < L:
+        n = min(chunk, L - t)
+        k, v = synth_chunk(torch, gen, scale, t, n, B, Hkv)
+        pool.append(k, v)
+        t += n
+    torch.cuda.synchronize()
+    return pool
+
+
+def cpu_baseline(cfg, budget_s=12.0):
+    """The oracle's NumPy dequantize-then-attend (the reference CPU decode path)
+    timed on this host on a bounded sample: whole-cache decode of single
+    (sequence, kv head) pairs at the workload's context, scaled to the step."""
+    import numpy as np
+    sys.path.insert(0, ROOT)
+    from oracle import tq_oracle as O
+    L, g = cfg["L"], cfg["Hq"] // cfg["Hkv"]
+    k, v, q = O.synthetic_kv(1, 1, 1, g, L)
+    pi, pi_t = O.rotation(0, 128)
+    sc = O.SequenceCache(hot_window=512, value_bits=cfg["vbits"], outlier_frac=0.02).build(
+        k[0], v[0], pi, pi_t)
+    times = []
+    t_start = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        out = sc.attend(q[0])
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > budget_s or len(times) >= 5:
+            break
+    assert np.isfinite(out).all()
+    per_pair = float(np.median(times))
+    pairs = cfg["B"] * cfg["Hkv"]
+    return {"value": per_pair * pairs * 1e6, "unit": "us/step", "cores": 1, "kind": "port",
+            "sample": f"{len(times)} runs of one (sequence, kv head) pair at L={L} with {g} q-heads, "
+                      f"median {per_pair * 1e3:.1f} ms x {pairs} pairs; NumPy single thread, "
+                      f"cpu={_cpu_model()}, os.cpu_count()={os.cpu_count()}"}
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="headline", choices=sorted(CONFIGS))
+    ap.add_argument("--replicas", type=int, default=2)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; the decode shards by "
+                          "(sequence, kv head) with no communication, but multi-GPU runs are "
+                          "out of scope here", "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    import torch
+    from turboquant_pro_amd import _native as N
+
+    cfg = CONFIGS[args.config]
+    B, Hkv, Hq, L = cfg["B"], cfg["Hkv"], cfg["Hq"], cfg["L"]
+    print(f"[bench] config={args.config} {cfg} replicas={args.replicas}", file=sys.stderr, flush=True)
+    t0 = time.time()
+    pools = [build_pool(torch, cfg, seed=1000 + r) for r in range(args.replicas)]
+    print(f"[bench] prefill done in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(7)
+    q = torch.randn((B, Hq, 128), generator=gen, device="cuda").half()
+    outs = [torch.empty((B, Hq, 128), dtype=torch.float32, device="cuda") for _ in pools]
+
+    for i in range(args.warmup):
+        pools[i % len(pools)].decode(q, out=outs[i % len(pools)])
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for i in range(args.steps):
+        pools[i % len(pools)].decode(q, out=outs[i % len(pools)])
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms_per_step = e0.elapsed_time(e1) / args.steps
+
+    # the dominant kernel alone: events around the split-K launch on its stream
+    lib = N.lib()
+    st = ctypes.c_void_p(stream.cuda_stream)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    for i in range(args.steps):
+        p = pools[i % len(pools)]
+        ws, need = p.workspace(B, max(p.lengths))
+        evs[i][0].record(stream)
+        N.check(lib.tqk_decode_splits(ctypes.byref(p.desc), ctypes.byref(p.ptrs), B, q.data_ptr(),
+                                      p.seq_lens.data_ptr(), max(p.lengths), ws.data_ptr(), need, st),
+                "tqk_decode_splits")
+        evs[i][1].record(stream)
+        N.check(lib.tqk_decode_merge(ctypes.byref(p.desc), ctypes.byref(p.ptrs), B, max(p.lengths),
+                                     outs[i % len(pools)].data_ptr(), ws.data_ptr(), need, st),
+                "tqk_decode_merge")
+    torch.cuda.synchronize()
+    split_ms = sum(a.elapsed_time(b) for a, b in evs) / args.steps
+    nbytes = step_bytes([L] * B, Hkv, Hq, vbits=cfg["vbits"])
+    achieved = nbytes / (split_ms * 1e-3) / 1e9
+    step_gbs = nbytes / (ms_per_step * 1e-3) / 1e9
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(cfg)
+
+    line = {
+        "metric": METRIC,
+        "value": round(ms_per_step * 1e3, 2),
+        "unit": "us/step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (seeded lognormal-scaled RoPE fp16 keys with 2% x10 channels, N(0,1) "
+                "values and queries), cache filled through the GPU encode path",
+        "config": {"workload": f"decode step, batch {B} x context {L}, {Hq} q-heads / {Hkv} kv-heads, "
+                               f"head_dim 128, K4 asym-NF4 + 2% fp16 outliers, V{cfg['vbits']} "
+                               f"PolarQuant, fp16 hot window 512",
+                   "name": args.config, "batch": B, "context": L, "n_q_heads": Hq,
+                   "n_kv_heads": Hkv, "replicas": args.replicas},
+        "step_bytes": nbytes,
+        "step_gbs": round(step_gbs, 1),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "tqk_decode_split_valu", "kernel_us": round(split_ms * 1e3, 2)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

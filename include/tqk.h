@@ -1,0 +1,177 @@
+/*
+ * tqk.h -- C ABI of the MI355X (gfx950) TurboQuant Pro KV-cache kernels.
+ *
+ * One hot path: the two-tier TurboQuant KV cache (fp16 hot window + flushed
+ * groups of per-channel asym-NF4 4-bit keys with an fp16 outlier side-list and
+ * PolarQuant 3/4-bit values) and the fused decode-step attention over it.
+ *
+ * Conventions
+ *   - Every pointer is a DEVICE pointer unless its comment says host.
+ *   - The caller owns every buffer (including the decode workspace); the
+ *     library allocates nothing per call.
+ *   - Every entry point returns an int status (TQK_OK or an error code) and
+ *     never throws or aborts across the ABI.
+ *   - Work is enqueued on the given HIP stream (hipStream_t passed as void*;
+ *     NULL = the default stream) and is stream-ordered.
+ *   - fp16 data is passed as uint16_t bit patterns (IEEE binary16).
+ *
+ * Storage layout in HBM (one cache pool = one attention layer):
+ *   kcodes [num_pages][n_kv_heads][page_tokens][head_dim/2]   u8   (storage of record)
+ *   vcodes [num_pages][n_kv_heads][page_tokens][head_dim*vb/8] u8  (storage of record)
+ *   vnorm  [num_pages][n_kv_heads][page_tokens]               f32
+ *   gscale [num_gslots][n_kv_heads][head_dim]                 f32  (nf4_scale)
+ *   gmean  [num_gslots][n_kv_heads][head_dim]                 f32  (nf4_mean)
+ *   ocount [num_gslots][n_kv_heads]                           i32
+ *   oent   [num_gslots][n_kv_heads][outlier_cap]              u32  ((s*D + j) | fp16 << 16)
+ *   hot_k, hot_v [batch][n_kv_heads][hot_ring][head_dim]      fp16 ring, token t at t % hot_ring
+ *   block_table [batch][max_pages_per_seq]   i32 physical page of logical page t / page_tokens
+ *   group_table [batch][max_groups_per_seq]  i32 group slot of group t / group_tokens
+ * The K and V rows are byte-for-byte the reference's packed layouts
+ * (turboquant_pro/per_channel_kv.py:87-93 and turboquant_pro/core.py:350-398):
+ * the bytes of one (group, head) in page order are the reference container's
+ * `indices` slice for that head.
+ */
+#ifndef TQK_H_
+#define TQK_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TQK_OK 0
+#define TQK_EINVAL 1        /* bad argument / shape (Python: ValueError) */
+#define TQK_EUNSUPPORTED 2  /* configuration has no GPU form (Python: NotImplementedError) */
+#define TQK_EHIP 3          /* a HIP runtime call failed (Python: RuntimeError) */
+#define TQK_EWORKSPACE 4    /* workspace too small */
+
+typedef struct tqk_cache_desc {
+  int32_t n_kv_heads;           /* Hkv */
+  int32_t n_q_heads;            /* Hq, a multiple of Hkv (q-head i reads kv-head i / (Hq/Hkv)) */
+  int32_t head_dim;             /* D; 128 */
+  int32_t hot_window;           /* W; groups flush when the hot window exceeds W */
+  int32_t group_tokens;         /* G = (W + 1) / 2, 1..256 */
+  int32_t page_tokens;          /* P, divides G */
+  int32_t key_bits;             /* 4 (per-channel asym-NF4) */
+  int32_t value_bits;           /* 3 or 4 (PolarQuant) */
+  int32_t outliers_per_channel; /* k = max(1, round(G * outlier_frac)), 0 = no side-list */
+  int32_t outlier_cap;          /* oent capacity per (group slot, head) */
+  int32_t max_pages_per_seq;    /* block_table row stride */
+  int32_t max_groups_per_seq;   /* group_table row stride */
+  int32_t hot_ring;             /* ring capacity in tokens, >= W */
+  float sm_scale;               /* softmax scale, 1/sqrt(D) */
+} tqk_cache_desc;
+
+typedef struct tqk_cache_ptrs {
+  uint8_t* kcodes;
+  uint8_t* vcodes;
+  float* vnorm;
+  float* gscale;
+  float* gmean;
+  int32_t* ocount;
+  uint32_t* oent;
+  uint16_t* hot_k;
+  uint16_t* hot_v;
+  const int32_t* block_table;
+  const int32_t* group_table;
+  const float* pi;      /* (D, D) row-major: unrotate y -> y @ pi */
+  const float* pi_t;    /* (D, D) row-major: rotate x -> x @ pi_t */
+  const float* vcent;   /* 2^vb fp32 value centroids (already / sqrt(D)) */
+  const float* vbnd;    /* 2^vb - 1 fp32 value boundaries */
+} tqk_cache_ptrs;
+
+/* Library ABI version (bumped on any signature or layout change). */
+int tqk_version(void);
+
+/* Validate a descriptor; TQK_OK when the GPU path supports it. */
+int tqk_check_desc(const tqk_cache_desc* d);
+
+/* Bytes of decode workspace needed for `batch` sequences of at most
+ * `max_len` tokens.  Host function, no GPU work. */
+size_t tqk_decode_workspace_bytes(const tqk_cache_desc* d, int32_t batch, int32_t max_len);
+
+/*
+ * Fused decode-step attention over the two-tier cache, one query token per
+ * sequence: out[b][i] = softmax(q[b][i] . K_b^T * sm_scale) V_b over all
+ * seq_lens[b] cached tokens of kv-head i / (Hq/Hkv), with the coded groups
+ * attended in code space (no reconstruction) and the hot window in fp16.
+ *   q        [batch][n_q_heads][head_dim] fp16
+ *   seq_lens [batch] i32 (device), every entry in [1, max_len]
+ *   out      [batch][n_q_heads][head_dim] fp32
+ * Replaces TurboQuantKVCache.fused_decode (turboquant_pro/core.py:1168-1265)
+ * and the per-page kernel launches behind it (turboquant_pro/kv_kernel.py:319-381).
+ */
+int tqk_decode(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t batch,
+               const uint16_t* q, const int32_t* seq_lens, int32_t max_len, float* out,
+               void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Same step, returning the unnormalised online-softmax state instead of the
+ * output: m [batch][n_q_heads], l [batch][n_q_heads], acc [batch][n_q_heads][D]
+ * (real space), so that out = acc / l and states merge with
+ * merge_partials (turboquant_pro/kv_fused.py:139-153; the kernel-level
+ * partial contract of turboquant_pro/kv_kernel.py:212-213).
+ */
+int tqk_decode_partials(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t batch,
+                        const uint16_t* q, const int32_t* seq_lens, int32_t max_len,
+                        float* m, float* l, float* acc, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
+/*
+ * The two phases of tqk_decode, for callers that time or overlap them:
+ * tqk_decode_splits writes every split's online-softmax state into the
+ * workspace; tqk_decode_merge combines them (the flash-combine of
+ * turboquant_pro/kv_kernel.py:377-381), rotates the coded part back and
+ * normalises.  Same arguments and workspace as tqk_decode.
+ */
+int tqk_decode_splits(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t batch,
+                      const uint16_t* q, const int32_t* seq_lens, int32_t max_len,
+                      void* workspace, size_t workspace_bytes, void* stream);
+int tqk_decode_merge(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t batch,
+                     int32_t max_len, float* out, void* workspace, size_t workspace_bytes,
+                     void* stream);
+
+/*
+ * Quantize-on-flush: encode `n_items` groups, item i = (items[2i], items[2i+1])
+ * = (sequence b, group index g), all kv heads.  Token t of sequence b is read
+ * from the hot ring when t < prev_len[b], else from the appended chunk at
+ * chunk_k[b][h][t - prev_len[b]][:] (chunk row stride chunk_tokens).
+ * Writes K/V codes, norms, group scale/mean and the outlier side-list
+ * bit-exactly as PerChannelKV.compress (turboquant_pro/per_channel_kv.py:285-401)
+ * and TurboQuantKV.compress (turboquant_pro/core.py:542-617) would.
+ * `overflow` (device i32, caller zeroes it) is set non-zero when a (group, head)
+ * has more outliers than outlier_cap; the side-list is then truncated.
+ * Replaces TurboQuantKVCache._flush_to_cold (turboquant_pro/core.py:1011-1038).
+ */
+int tqk_encode_groups(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t batch,
+                      int32_t n_items, const int32_t* items, const int32_t* prev_len,
+                      const uint16_t* chunk_k, const uint16_t* chunk_v, int32_t chunk_tokens,
+                      int32_t* overflow, void* stream);
+
+/*
+ * Copy appended tokens into the hot ring: for each sequence b, tokens
+ * [max(prev_len[b], hot_start[b]), prev_len[b] + n_new[b]) of the chunk go to
+ * ring slot t % hot_ring.  Part of TurboQuantKVCache.append
+ * (turboquant_pro/core.py:986-1009).
+ */
+int tqk_append_hot(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t batch,
+                   const int32_t* prev_len, const int32_t* n_new, const int32_t* hot_start,
+                   const uint16_t* chunk_k, const uint16_t* chunk_v, int32_t chunk_tokens,
+                   void* stream);
+
+/*
+ * Reconstruct fp32 keys and values of `n_items` groups (items as in
+ * tqk_encode_groups): kout/vout [n_items][n_kv_heads][G][D].  The GPU form of
+ * PerChannelKV.decompress (turboquant_pro/per_channel_kv.py:497-539) and
+ * TurboQuantKV.decompress (turboquant_pro/core.py:619-654), used by
+ * TurboQuantKVCache.get_keys / get_values.
+ */
+int tqk_dequant_groups(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t n_items,
+                       const int32_t* items, float* kout, float* vout, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TQK_H_ */

@@ -67,7 +67,8 @@ int tqo_encode_keys(const float* x, int H, int S, int D, int k_out, uint8_t* cod
       const float* xj = x + (size_t)h * S * D + j;
       float acc = 0.0f;
       for (int s = 0; s < S; ++s) acc = acc + xj[(size_t)s * D];
-      float mu = acc / (float)S;
+      /* np.mean divides the fp32 sum by an intp count: float64 division, then fp32 */
+      float mu = (float)((double)acc / (double)S);
       float amax = 0.0f;
       for (int s = 0; s < S; ++s) {
         float d = fabsf(xj[(size_t)s * D] - mu);

@@ -1,0 +1,76 @@
+"""CPU-side checks of the boundary: the library loads, exports every symbol
+include/tqk.h declares, and its host-only functions validate descriptors.
+No GPU work is launched."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _lib():
+    from turboquant_pro_amd import _native as N
+    if not os.path.exists(N.LIB_PATH):
+        pytest.skip("libtqk.so not built (run __graft_entry__.build())")
+    return N, N.lib()
+
+
+def test_header_declares_exactly_the_bound_symbols():
+    with open(os.path.join(ROOT, "include", "tqk.h")) as f:
+        hdr = f.read()
+    declared = set(re.findall(r"^(?:int|size_t)\s+(tqk_\w+)\(", hdr, re.M))
+    from turboquant_pro_amd import _native as N
+    assert declared == set(N.EXPORTS)
+
+
+def test_library_exports_every_symbol():
+    N, lib = _lib()
+    for name in N.EXPORTS:
+        assert hasattr(lib, name), name
+    assert lib.tqk_version() == N.ABI_VERSION
+
+
+def _desc(N, **kw):
+    base = dict(n_kv_heads=8, n_q_heads=32, head_dim=128, hot_window=512, group_tokens=256,
+                page_tokens=256, key_bits=4, value_bits=3, outliers_per_channel=5,
+                outlier_cap=2560, max_pages_per_seq=126, max_groups_per_seq=126, hot_ring=512,
+                sm_scale=1 / 128 ** 0.5)
+    base.update(kw)
+    return N.CacheDesc(**base)
+
+
+def test_check_desc_status_codes():
+    N, lib = _lib()
+    ok = _desc(N)
+    assert lib.tqk_check_desc(ctypes.byref(ok)) == N.TQK_OK
+    assert lib.tqk_check_desc(ctypes.byref(_desc(N, head_dim=64))) == N.TQK_EUNSUPPORTED
+    assert lib.tqk_check_desc(ctypes.byref(_desc(N, value_bits=2))) == N.TQK_EUNSUPPORTED
+    assert lib.tqk_check_desc(ctypes.byref(_desc(N, n_q_heads=12))) == N.TQK_EINVAL
+    assert lib.tqk_check_desc(ctypes.byref(_desc(N, group_tokens=128))) == N.TQK_EINVAL
+    assert lib.tqk_check_desc(ctypes.byref(_desc(N, page_tokens=24))) == N.TQK_EINVAL
+    assert lib.tqk_check_desc(ctypes.byref(_desc(N, hot_window=1023, group_tokens=512))) == \
+        N.TQK_EUNSUPPORTED
+    assert lib.tqk_check_desc(None) == N.TQK_EINVAL
+
+
+def test_workspace_bytes_grow_with_context():
+    N, lib = _lib()
+    d = _desc(N)
+    a = lib.tqk_decode_workspace_bytes(ctypes.byref(d), 16, 8192)
+    b = lib.tqk_decode_workspace_bytes(ctypes.byref(d), 16, 32768)
+    assert 0 < a < b
+    assert lib.tqk_decode_workspace_bytes(ctypes.byref(d), 0, 10) == 0
+
+
+def test_error_mapping():
+    from turboquant_pro_amd import _native as N
+    N.check(N.TQK_OK, "x")
+    with pytest.raises(NotImplementedError):
+        N.check(N.TQK_EUNSUPPORTED, "x")
+    with pytest.raises(ValueError):
+        N.check(N.TQK_EINVAL, "x")
+    with pytest.raises(RuntimeError):
+        N.check(N.TQK_EHIP, "x")

@@ -1,0 +1,59 @@
+// Shared device helpers and tables for the gfx950 TurboQuant KV kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/tqk.h"
+
+#define TQK_D 128          // head_dim supported by the GPU path
+#define TQK_MAX_G 256      // largest group (flush) size
+
+// NormalFloat-4 levels, turboquant_pro/per_channel_kv.py:64-84.
+__constant__ static const float kNF4[16] = {
+    -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,
+    -0.28444138169288635f, -0.18477343022823334f, -0.09105003625154495f, 0.0f,
+    0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f,
+    0.33791524171829224f, 0.44070982933044434f, 0.5626170039176941f,
+    0.7229568362236023f, 1.0f};
+
+__device__ __forceinline__ float h2f(uint16_t x) {
+  return (float)__builtin_bit_cast(_Float16, x);
+}
+__device__ __forceinline__ uint16_t f2h(float x) {  // round to nearest even
+  return __builtin_bit_cast(uint16_t, (_Float16)x);
+}
+
+// 4-bit nibble bit reversal: the key stream stores each code LSB-first inside
+// MSB-first bytes (turboquant_pro/per_channel_kv.py:87-93), so byte n holds
+// rev4(code[2n]) << 4 | rev4(code[2n+1]).
+__host__ __device__ __forceinline__ uint32_t rev4(uint32_t x) {
+  return ((x & 1u) << 3) | ((x & 2u) << 1) | ((x & 4u) >> 1) | ((x & 8u) >> 3);
+}
+
+// Number of flushed groups after `len` appends: the first flush fires at
+// hot_window + 1 tokens, then every G tokens (turboquant_pro/core.py:1006-1016).
+__host__ __device__ __forceinline__ int n_groups_of(int len, int hot_window, int G) {
+  return (len <= hot_window) ? 0 : (len - (hot_window + 1)) / G + 1;
+}
+
+// Row index of token t (absolute position in its sequence) for kv head h in
+// the page pool.
+__device__ __forceinline__ size_t page_row(const int32_t* __restrict__ block_table, int max_pages,
+                                           int b, int t, int P, int Hkv, int h) {
+  const int phys = block_table[(size_t)b * max_pages + t / P];
+  return ((size_t)phys * Hkv + h) * P + (t % P);
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_max(T v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}

@@ -1,0 +1,406 @@
+// Quantize-on-flush, hot-ring append and group reconstruction (gfx950).
+//
+// Bit-exactness contract (this file is compiled with -ffp-contract=off and
+// uses explicitly rounded __f*_rn operations): every code, scale, mean, norm
+// and outlier entry equals what the reference's NumPy encoder produces for the
+// same fp16 inputs.  NumPy's operation order is restated exactly:
+//   keys   (turboquant_pro/per_channel_kv.py:269-401, nf4_asym "calibrated")
+//     mean  = token-order sequential fp32 sum / G
+//     amax  = max(max_s |x_s - mean|, 1e-8)            (NaN propagates)
+//     cent  = mean + amax * NF4[l]
+//     code  = first argmin_l |x - cent_l|               (NaN counts as minimal)
+//     outlier threshold = k-th largest |x| (ties kept), flat (s, j) order
+//   values (turboquant_pro/core.py:569-606, CPU full-QR branch)
+//     norm  = sqrt(pairwise-8 sum of squares)            (numpy pairwise_sum, n = 128)
+//     u     = v / max(norm, 1e-30)
+//     y_e   = sequential over d of (u_d * PiT[d][e]), separately rounded
+//     code  = #{ boundaries < y_e }                      (searchsorted, side="left")
+#include "tqk_common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+
+struct EncodeArgs {
+  tqk_cache_desc d;
+  tqk_cache_ptrs p;
+  const int32_t* items;
+  const int32_t* prev_len;
+  const uint16_t* chunk_k;
+  const uint16_t* chunk_v;
+  int chunk_tokens;
+  int32_t* overflow;
+};
+
+// Source row (fp16, D values) of token t of sequence b, kv head h: the hot
+// ring for tokens already in the cache, the appended chunk for new ones.
+__device__ __forceinline__ const uint16_t* token_src(const EncodeArgs& a, const uint16_t* ring,
+                                                     const uint16_t* chunk, int b, int h, int t) {
+  const tqk_cache_desc& d = a.d;
+  const int prev = a.prev_len[b];
+  if (t < prev)
+    return ring + (((size_t)b * d.n_kv_heads + h) * d.hot_ring + (t % d.hot_ring)) * TQK_D;
+  return chunk + (((size_t)b * d.n_kv_heads + h) * a.chunk_tokens + (t - prev)) * TQK_D;
+}
+
+__device__ __forceinline__ uint32_t abs_h(uint16_t x) { return x & 0x7FFFu; }
+
+template <int VB>
+__global__ __launch_bounds__(kThreads) void tqk_encode_group(EncodeArgs a) {
+  constexpr int D = TQK_D;
+  const int item = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+  const tqk_cache_desc& d = a.d;
+  const int b = a.items[2 * item], g = a.items[2 * item + 1];
+  const int G = d.group_tokens, P = d.page_tokens, Hkv = d.n_kv_heads;
+  const int slot = a.p.group_table[(size_t)b * d.max_groups_per_seq + g];
+  const int kout = d.outliers_per_channel;
+
+  __shared__ uint16_t kt_s[TQK_MAX_G][D + 8];  // key tile, fp16 bits (row padded vs bank conflicts)
+  __shared__ float cent_s[D][17];            // per-channel grids (padded)
+  __shared__ uint32_t thr_s[D];              // fp16 magnitude threshold per channel
+  __shared__ int32_t wsum_s[4];
+
+  // ---- stage the key tile ----------------------------------------------
+  for (int idx = tid; idx < G * 16; idx += kThreads) {
+    const int t = idx >> 4, c = idx & 15;
+    const uint4* src =
+        reinterpret_cast<const uint4*>(token_src(a, a.p.hot_k, a.chunk_k, b, h, g * G + t));
+    reinterpret_cast<uint4*>(&kt_s[t][0])[c] = src[c];
+  }
+  __syncthreads();
+
+  // ---- per-channel statistics (threads 0..127) and outlier thresholds (128..255)
+  const size_t mbase = ((size_t)slot * Hkv + h) * D;
+  if (tid < D) {
+    const int j = tid;
+    float acc = 0.0f;
+    for (int s = 0; s < G; ++s) acc = __fadd_rn(acc, h2f(kt_s[s][j]));
+    // np.mean divides the fp32 sum by an intp count: a float64 division, then fp32
+    const float mu = (float)((double)acc / (double)G);
+    float amax = 0.0f;
+    bool nan = (mu != mu);
+    for (int s = 0; s < G; ++s) {
+      const float dv = fabsf(__fsub_rn(h2f(kt_s[s][j]), mu));
+      nan |= (dv != dv);
+      amax = fmaxf(amax, dv);
+    }
+    amax = nan ? __builtin_nanf("") : fmaxf(amax, 1e-8f);
+#pragma unroll
+    for (int l = 0; l < 16; ++l) cent_s[j][l] = __fadd_rn(mu, __fmul_rn(amax, kNF4[l]));
+    a.p.gscale[mbase + j] = amax;
+    a.p.gmean[mbase + j] = mu;
+  } else if (kout > 0 && kout < G) {
+    // k-th largest |x| as the largest fp16 magnitude pattern T with
+    // #{ |x_s| >= T } >= k (NaN patterns order above inf, as np.partition does).
+    const int j = tid - D;
+    uint32_t T = 0;
+    for (int bit = 14; bit >= 0; --bit) {
+      const uint32_t cand = T | (1u << bit);
+      int cnt = 0;
+      for (int s = 0; s < G; ++s) cnt += (abs_h(kt_s[s][j]) >= cand);
+      if (cnt >= kout) T = cand;
+    }
+    thr_s[j] = T;
+  }
+  __syncthreads();
+
+  // ---- codes: thread = (channel pair, token quarter); one byte per (token, pair)
+  {
+    const int jp = tid & 63, sq = tid >> 6;
+    float c0[16], c1[16];
+#pragma unroll
+    for (int l = 0; l < 16; ++l) {
+      c0[l] = cent_s[2 * jp][l];
+      c1[l] = cent_s[2 * jp + 1][l];
+    }
+    const int per_q = (G + 3) / 4;
+    const int s0 = sq * per_q, s1 = min(G, s0 + per_q);
+    for (int s = s0; s < s1; ++s) {
+      const float x0 = h2f(kt_s[s][2 * jp]), x1 = h2f(kt_s[s][2 * jp + 1]);
+      int b0 = 0, b1 = 0;
+      float d0 = fabsf(__fsub_rn(x0, c0[0])), d1 = fabsf(__fsub_rn(x1, c1[0]));
+#pragma unroll
+      for (int l = 1; l < 16; ++l) {
+        const float e0 = fabsf(__fsub_rn(x0, c0[l])), e1 = fabsf(__fsub_rn(x1, c1[l]));
+        // np.argmin: strictly smaller wins; the first NaN wins over any number
+        if (e0 < d0 || (e0 != e0 && d0 == d0)) { d0 = e0; b0 = l; }
+        if (e1 < d1 || (e1 != e1 && d1 == d1)) { d1 = e1; b1 = l; }
+      }
+      const size_t row = page_row(a.p.block_table, d.max_pages_per_seq, b, g * G + s, P, Hkv, h);
+      a.p.kcodes[row * (D / 2) + jp] = (uint8_t)((rev4(b0) << 4) | rev4(b1));
+    }
+  }
+
+  // ---- outlier side-list in flat (token, channel) order ---------------------
+  if (kout > 0) {
+    const bool all = kout >= G;
+    int cnt = 0;
+    if (tid < G) {
+      for (int j = 0; j < D; ++j) {
+        const float mag = fabsf(h2f(kt_s[tid][j]));
+        cnt += all ? 1 : (mag >= fabsf(h2f((uint16_t)thr_s[j])));
+      }
+    }
+    // block exclusive scan of cnt
+    int incl = cnt;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int v = __shfl_up(incl, o, 64);
+      if ((tid & 63) >= o) incl += v;
+    }
+    if ((tid & 63) == 63) wsum_s[tid >> 6] = incl;
+    __syncthreads();
+    int wofs = 0;
+    for (int w = 0; w < (tid >> 6); ++w) wofs += wsum_s[w];
+    const int total = wsum_s[0] + wsum_s[1] + wsum_s[2] + wsum_s[3];
+    int off = wofs + incl - cnt;
+    const size_t obase = (size_t)slot * Hkv + h;
+    if (tid < G && cnt > 0) {
+      for (int j = 0; j < D; ++j) {
+        const uint16_t xv = kt_s[tid][j];
+        const bool sel = all || (fabsf(h2f(xv)) >= fabsf(h2f((uint16_t)thr_s[j])));
+        if (sel) {
+          if (off < d.outlier_cap)
+            a.p.oent[obase * d.outlier_cap + off] = (uint32_t)(tid * D + j) | ((uint32_t)xv << 16);
+          ++off;
+        }
+      }
+    }
+    if (tid == 0) {
+      a.p.ocount[obase] = total;
+      if (total > d.outlier_cap && a.overflow) atomicOr(a.overflow, 1);
+    }
+  } else if (tid == 0) {
+    a.p.ocount[(size_t)slot * Hkv + h] = 0;
+  }
+
+  // ---- values: one token per thread ---------------------------------------
+  if (tid < G) {
+    const int t = g * G + tid;
+    const uint4* src = reinterpret_cast<const uint4*>(token_src(a, a.p.hot_v, a.chunk_v, b, h, t));
+    float u[D];
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      const uint4 w4 = src[c];
+      const uint32_t wv[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        u[c * 8 + 2 * k] = h2f((uint16_t)(wv[k] & 0xFFFFu));
+        u[c * 8 + 2 * k + 1] = h2f((uint16_t)(wv[k] >> 16));
+      }
+    }
+    float r[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) r[k] = __fmul_rn(u[k], u[k]);
+#pragma unroll
+    for (int m = 1; m < 16; ++m)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) r[k] = __fadd_rn(r[k], __fmul_rn(u[8 * m + k], u[8 * m + k]));
+    const float ss = __fadd_rn(__fadd_rn(__fadd_rn(r[0], r[1]), __fadd_rn(r[2], r[3])),
+                               __fadd_rn(__fadd_rn(r[4], r[5]), __fadd_rn(r[6], r[7])));
+    const float nrm = __builtin_sqrtf(ss);  // correctly rounded (-fhip-fp32-correctly-rounded-divide-sqrt)
+    const float safe = fmaxf(nrm, 1e-30f);
+#pragma unroll
+    for (int k = 0; k < D; ++k) u[k] = __fdiv_rn(u[k], safe);
+
+    float bnd[15];
+#pragma unroll
+    for (int k = 0; k < (1 << VB) - 1; ++k) bnd[k] = a.p.vbnd[k];
+
+    const size_t row = page_row(a.p.block_table, d.max_pages_per_seq, b, t, P, Hkv, h);
+    constexpr int VROW = D * VB / 8;
+    uint32_t outw[VROW / 4];
+#pragma unroll
+    for (int k = 0; k < VROW / 4; ++k) outw[k] = 0u;
+    const float* __restrict__ pi = a.p.pi;  // pi[e][d] == pi_t[d][e]
+    for (int e0 = 0; e0 < D; e0 += 4) {
+      float y[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int dd = 0; dd < D; ++dd) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) y[k] = __fadd_rn(y[k], __fmul_rn(u[dd], pi[(e0 + k) * D + dd]));
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        uint32_t code = 0;
+#pragma unroll
+        for (int q = 0; q < (1 << VB) - 1; ++q) code += (bnd[q] < y[k]) ? 1u : 0u;
+        const int e = e0 + k;
+        const int bitpos = e * VB;  // little-endian bit stream (3-bit: 8 codes per 24 bits)
+        outw[bitpos >> 5] |= code << (bitpos & 31);
+        if ((bitpos & 31) + VB > 32) outw[(bitpos >> 5) + 1] |= code >> (32 - (bitpos & 31));
+      }
+    }
+    uint4* dst = reinterpret_cast<uint4*>(a.p.vcodes + row * VROW);
+#pragma unroll
+    for (int k = 0; k < VROW / 16; ++k)
+      dst[k] = make_uint4(outw[4 * k], outw[4 * k + 1], outw[4 * k + 2], outw[4 * k + 3]);
+    a.p.vnorm[row] = nrm;
+  }
+}
+
+struct HotArgs {
+  tqk_cache_desc d;
+  uint16_t* hot_k;
+  uint16_t* hot_v;
+  const int32_t* prev_len;
+  const int32_t* n_new;
+  const int32_t* hot_start;
+  const uint16_t* chunk_k;
+  const uint16_t* chunk_v;
+  int chunk_tokens;
+};
+
+// grid (batch, Hkv); copies the surviving new tokens into the ring.
+__global__ __launch_bounds__(kThreads) void tqk_append_hot_kernel(HotArgs a) {
+  const int b = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+  const tqk_cache_desc& d = a.d;
+  const int prev = a.prev_len[b], nn = a.n_new[b];
+  const int t0 = max(prev, a.hot_start[b]), t1 = prev + nn;
+  const int R = d.hot_ring;
+  const size_t rb = ((size_t)b * d.n_kv_heads + h) * R;
+  const size_t cb = ((size_t)b * d.n_kv_heads + h) * a.chunk_tokens;
+  for (int idx = tid; idx < (t1 - t0) * 16; idx += kThreads) {
+    const int t = t0 + (idx >> 4), c = idx & 15;
+    const size_t src = (cb + (t - prev)) * TQK_D;
+    const size_t dst = (rb + (t % R)) * TQK_D;
+    reinterpret_cast<uint4*>(a.hot_k + dst)[c] = reinterpret_cast<const uint4*>(a.chunk_k + src)[c];
+    reinterpret_cast<uint4*>(a.hot_v + dst)[c] = reinterpret_cast<const uint4*>(a.chunk_v + src)[c];
+  }
+}
+
+struct DequantArgs {
+  tqk_cache_desc d;
+  tqk_cache_ptrs p;
+  const int32_t* items;
+  float* kout;
+  float* vout;
+};
+
+// grid (n_items, Hkv), one token per thread: reconstruct keys (grid value then
+// the fp16 outlier overwrite) and values ((cent[code] @ Pi) * norm, NumPy order).
+template <int VB>
+__global__ __launch_bounds__(kThreads) void tqk_dequant_group(DequantArgs a) {
+  constexpr int D = TQK_D;
+  constexpr int VROW = D * VB / 8;
+  const int item = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+  const tqk_cache_desc& d = a.d;
+  const int b = a.items[2 * item], g = a.items[2 * item + 1];
+  const int G = d.group_tokens, P = d.page_tokens, Hkv = d.n_kv_heads;
+  const int slot = a.p.group_table[(size_t)b * d.max_groups_per_seq + g];
+  const size_t mbase = ((size_t)slot * Hkv + h) * D;
+  float* ko = a.kout + ((size_t)item * Hkv + h) * G * D;
+  float* vo = a.vout + ((size_t)item * Hkv + h) * G * D;
+  if (tid < G) {
+    const size_t row = page_row(a.p.block_table, d.max_pages_per_seq, b, g * G + tid, P, Hkv, h);
+    const uint8_t* kr = a.p.kcodes + row * (D / 2);
+    for (int jj = 0; jj < D / 2; ++jj) {
+      const uint32_t byte = kr[jj];
+      const int j0 = 2 * jj, j1 = 2 * jj + 1;
+      ko[(size_t)tid * D + j0] =
+          __fadd_rn(__fmul_rn(a.p.gscale[mbase + j0], kNF4[rev4(byte >> 4)]), a.p.gmean[mbase + j0]);
+      ko[(size_t)tid * D + j1] =
+          __fadd_rn(__fmul_rn(a.p.gscale[mbase + j1], kNF4[rev4(byte & 15u)]), a.p.gmean[mbase + j1]);
+    }
+    const uint8_t* vr = a.p.vcodes + row * VROW;
+    float y[D];
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      const int bitpos = j * VB;
+      uint32_t w = vr[bitpos >> 3] | ((uint32_t)vr[min((bitpos >> 3) + 1, VROW - 1)] << 8);
+      y[j] = a.p.vcent[(w >> (bitpos & 7)) & ((1u << VB) - 1)];
+    }
+    const float nrm = a.p.vnorm[row];
+    for (int e = 0; e < D; ++e) {
+      float x = 0.f;
+#pragma unroll
+      for (int j = 0; j < D; ++j) x = __fadd_rn(x, __fmul_rn(y[j], a.p.pi[j * D + e]));
+      vo[(size_t)tid * D + e] = __fmul_rn(x, nrm);
+    }
+  }
+  __syncthreads();
+  const size_t obase = (size_t)slot * Hkv + h;
+  const int no = min(a.p.ocount[obase], d.outlier_cap);
+  for (int e = tid; e < no; e += kThreads) {
+    const uint32_t ent = a.p.oent[obase * d.outlier_cap + e];
+    ko[ent & 0xFFFFu] = h2f((uint16_t)(ent >> 16));
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int tqk_encode_groups(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t batch,
+                      int32_t n_items, const int32_t* items, const int32_t* prev_len,
+                      const uint16_t* chunk_k, const uint16_t* chunk_v, int32_t chunk_tokens,
+                      int32_t* overflow, void* stream) {
+  int rc = tqk_check_desc(d);
+  if (rc != TQK_OK) return rc;
+  if (!p || batch <= 0 || n_items < 0 || chunk_tokens < 0) return TQK_EINVAL;
+  if (n_items == 0) return TQK_OK;
+  if (!items || !prev_len) return TQK_EINVAL;
+  EncodeArgs a;
+  a.d = *d;
+  a.p = *p;
+  a.items = items;
+  a.prev_len = prev_len;
+  a.chunk_k = chunk_k;
+  a.chunk_v = chunk_v;
+  a.chunk_tokens = chunk_tokens;
+  a.overflow = overflow;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid(n_items, d->n_kv_heads);
+  if (d->value_bits == 3)
+    hipLaunchKernelGGL(tqk_encode_group<3>, grid, dim3(kThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL(tqk_encode_group<4>, grid, dim3(kThreads), 0, st, a);
+  return hipGetLastError() == hipSuccess ? TQK_OK : TQK_EHIP;
+}
+
+int tqk_append_hot(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t batch,
+                   const int32_t* prev_len, const int32_t* n_new, const int32_t* hot_start,
+                   const uint16_t* chunk_k, const uint16_t* chunk_v, int32_t chunk_tokens,
+                   void* stream) {
+  int rc = tqk_check_desc(d);
+  if (rc != TQK_OK) return rc;
+  if (!p || batch <= 0 || !prev_len || !n_new || !hot_start || !chunk_k || !chunk_v ||
+      chunk_tokens <= 0)
+    return TQK_EINVAL;
+  HotArgs a;
+  a.d = *d;
+  a.hot_k = p->hot_k;
+  a.hot_v = p->hot_v;
+  a.prev_len = prev_len;
+  a.n_new = n_new;
+  a.hot_start = hot_start;
+  a.chunk_k = chunk_k;
+  a.chunk_v = chunk_v;
+  a.chunk_tokens = chunk_tokens;
+  hipLaunchKernelGGL(tqk_append_hot_kernel, dim3(batch, d->n_kv_heads), dim3(kThreads), 0,
+                     reinterpret_cast<hipStream_t>(stream), a);
+  return hipGetLastError() == hipSuccess ? TQK_OK : TQK_EHIP;
+}
+
+int tqk_dequant_groups(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t n_items,
+                       const int32_t* items, float* kout, float* vout, void* stream) {
+  int rc = tqk_check_desc(d);
+  if (rc != TQK_OK) return rc;
+  if (!p || n_items < 0 || (n_items > 0 && (!items || !kout || !vout))) return TQK_EINVAL;
+  if (n_items == 0) return TQK_OK;
+  DequantArgs a;
+  a.d = *d;
+  a.p = *p;
+  a.items = items;
+  a.kout = kout;
+  a.vout = vout;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid(n_items, d->n_kv_heads);
+  if (d->value_bits == 3)
+    hipLaunchKernelGGL(tqk_dequant_group<3>, grid, dim3(kThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL(tqk_dequant_group<4>, grid, dim3(kThreads), 0, st, a);
+  return hipGetLastError() == hipSuccess ? TQK_OK : TQK_EHIP;
+}
+
+}  // extern "C"

@@ -1,0 +1,12 @@
+"""MI355X-native (gfx950) TurboQuant Pro KV cache: quantize-on-append and fused
+decode-on-codes attention behind the reference's cache API.
+
+The compute path is the HIP library ``lib/libtqk.so`` (C ABI in
+``include/tqk.h``); this package is the host side that plans launches and
+mirrors the reference interface.
+"""
+
+__version__ = "0.1.0"
+
+from .codebooks import group_tokens_for, n_groups_for, random_rotation, value_codebook  # noqa: F401
+from .pool import TQKVPool  # noqa: F401

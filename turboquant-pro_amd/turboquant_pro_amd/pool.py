@@ -1,0 +1,276 @@
+"""GPU-resident two-tier TurboQuant KV cache for a batch of sequences.
+
+``TQKVPool`` holds one attention layer's cache for up to ``max_batch``
+sequences in HBM, in the layout documented in ``include/tqk.h``:
+
+* coded groups live in pages (``page_tokens`` tokens x all kv heads) found
+  through a per-sequence block table, with per-(group, head) metadata (NF4
+  scale/mean, outlier side-list) in group slots found through a group table;
+* the fp16 hot window is a per-(sequence, head) ring of ``hot_window`` tokens.
+
+Appending runs the quantize-on-flush kernel for every group that the append
+completes (the reference flush cadence: first flush at ``hot_window + 1``
+tokens, then every ``(hot_window + 1) // 2``), then copies the surviving new
+tokens into the ring.  Decoding runs the fused split-K kernel.  Host code only
+plans launches; all per-token work is on the GPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import numpy as np
+
+from . import _native as N
+from .codebooks import (group_tokens_for, n_groups_for, outliers_per_channel, random_rotation,
+                        value_codebook)
+
+
+def _torch():
+    import torch
+    return torch
+
+
+class TQKVPool:
+    def __init__(self, n_kv_heads: int, n_q_heads: int | None = None, head_dim: int = 128, *,
+                 max_batch: int = 1, max_seq_len: int = 8192, hot_window: int = 512,
+                 key_bits: int = 4, value_bits: int = 3, outlier_frac: float = 0.02,
+                 page_tokens: int | None = None, outlier_cap: int | None = None,
+                 seed=None, rotation: tuple | None = None, block_table=None, device=None):
+        torch = _torch()
+        if not torch.cuda.is_available():
+            raise RuntimeError("TQKVPool runs on a ROCm GPU (gfx950); none is visible")
+        self.device = torch.device(device if device is not None else "cuda")
+        Hq = n_kv_heads if n_q_heads is None else n_q_heads
+        G = group_tokens_for(hot_window)
+        P = G if page_tokens is None else page_tokens
+        k_out = outliers_per_channel(G, outlier_frac)
+        if outlier_cap is None:
+            outlier_cap = min(G * head_dim, 4 * k_out * head_dim) if k_out else 0
+        max_groups = max(1, n_groups_for(max_seq_len, hot_window))
+        max_pages = max(1, (max_groups * G + P - 1) // P) if P > 0 else 1
+        self.n_kv_heads, self.n_q_heads, self.head_dim = n_kv_heads, Hq, head_dim
+        self.max_batch, self.max_seq_len, self.hot_window = max_batch, max_seq_len, hot_window
+        self.key_bits, self.value_bits, self.outlier_frac = key_bits, value_bits, outlier_frac
+        self.group_tokens, self.page_tokens = G, P
+        self.max_groups, self.max_pages = max_groups, max_pages
+        self.desc = N.CacheDesc(
+            n_kv_heads=n_kv_heads, n_q_heads=Hq, head_dim=head_dim, hot_window=hot_window,
+            group_tokens=G, page_tokens=P, key_bits=key_bits, value_bits=value_bits,
+            outliers_per_channel=k_out, outlier_cap=outlier_cap,
+            max_pages_per_seq=max_pages, max_groups_per_seq=max_groups,
+            hot_ring=hot_window, sm_scale=1.0 / math.sqrt(head_dim))
+        N.check(N.lib().tqk_check_desc(ctypes.byref(self.desc)), "TQKVPool")
+
+        dev = self.device
+        n_pages = max_batch * max_pages
+        n_slots = max_batch * max_groups
+        u8, f32, i32, f16 = torch.uint8, torch.float32, torch.int32, torch.float16
+        self.kcodes = torch.zeros((n_pages, n_kv_heads, P, head_dim * key_bits // 8), dtype=u8, device=dev)
+        self.vcodes = torch.zeros((n_pages, n_kv_heads, P, head_dim * value_bits // 8), dtype=u8, device=dev)
+        self.vnorm = torch.zeros((n_pages, n_kv_heads, P), dtype=f32, device=dev)
+        self.gscale = torch.zeros((n_slots, n_kv_heads, head_dim), dtype=f32, device=dev)
+        self.gmean = torch.zeros((n_slots, n_kv_heads, head_dim), dtype=f32, device=dev)
+        self.ocount = torch.zeros((n_slots, n_kv_heads), dtype=i32, device=dev)
+        self.oent = torch.zeros((n_slots, n_kv_heads, max(outlier_cap, 1)), dtype=i32, device=dev)
+        self.hot_k = torch.zeros((max_batch, n_kv_heads, hot_window, head_dim), dtype=f16, device=dev)
+        self.hot_v = torch.zeros((max_batch, n_kv_heads, hot_window, head_dim), dtype=f16, device=dev)
+        if block_table is None:
+            bt = np.arange(n_pages, dtype=np.int32).reshape(max_batch, max_pages)
+        else:
+            bt = np.asarray(block_table, dtype=np.int32).reshape(max_batch, max_pages)
+            if bt.min() < 0 or bt.max() >= n_pages:
+                raise ValueError("block_table entries must index the page pool")
+        self.block_table = torch.from_numpy(bt.copy()).to(dev)
+        gt = np.arange(n_slots, dtype=np.int32).reshape(max_batch, max_groups)
+        self.group_table = torch.from_numpy(gt).to(dev)
+        if rotation is None:
+            rotation = random_rotation(seed, head_dim)
+        pi, pi_t = rotation
+        cent, bnd = value_codebook(value_bits, head_dim)
+        self.pi = torch.from_numpy(np.ascontiguousarray(pi, np.float32)).to(dev)
+        self.pi_t = torch.from_numpy(np.ascontiguousarray(pi_t, np.float32)).to(dev)
+        self.vcent = torch.from_numpy(cent).to(dev)
+        self.vbnd = torch.from_numpy(bnd).to(dev)
+        self.ptrs = N.CachePtrs(
+            kcodes=self.kcodes.data_ptr(), vcodes=self.vcodes.data_ptr(),
+            vnorm=self.vnorm.data_ptr(), gscale=self.gscale.data_ptr(),
+            gmean=self.gmean.data_ptr(), ocount=self.ocount.data_ptr(),
+            oent=self.oent.data_ptr(), hot_k=self.hot_k.data_ptr(), hot_v=self.hot_v.data_ptr(),
+            block_table=self.block_table.data_ptr(), group_table=self.group_table.data_ptr(),
+            pi=self.pi.data_ptr(), pi_t=self.pi_t.data_ptr(), vcent=self.vcent.data_ptr(),
+            vbnd=self.vbnd.data_ptr())
+        self.lengths = [0] * max_batch
+        self.seq_lens = torch.zeros(max_batch, dtype=i32, device=dev)
+        self._overflow = torch.zeros(1, dtype=i32, device=dev)
+        self._ws = None
+
+    # ------------------------------------------------------------------ #
+    def _stream(self):
+        return ctypes.c_void_p(_torch().cuda.current_stream(self.device).cuda_stream)
+
+    def n_groups(self, b: int) -> int:
+        return n_groups_for(self.lengths[b], self.hot_window)
+
+    def hot_length(self, b: int) -> int:
+        return self.lengths[b] - self.n_groups(b) * self.group_tokens
+
+    def reset(self) -> None:
+        self.lengths = [0] * self.max_batch
+        self.seq_lens.zero_()
+
+    # ------------------------------------------------------------------ #
+    def append(self, k, v, n_new=None, check_overflow: bool = True) -> None:
+        """Append tokens: ``k``, ``v`` fp16 ``(max_batch, Hkv, T, D)`` on the
+        device; sequence ``b`` takes its first ``n_new[b]`` tokens (all T by
+        default).  Equivalent to T one-token ``TurboQuantKVCache.append`` calls
+        per sequence (turboquant_pro/core.py:986-1038)."""
+        torch = _torch()
+        B, T = self.max_batch, int(k.shape[2])
+        if tuple(k.shape) != (B, self.n_kv_heads, T, self.head_dim) or k.shape != v.shape:
+            raise ValueError(f"append expects ({B}, {self.n_kv_heads}, T, {self.head_dim}) K and V")
+        if k.dtype != torch.float16 or v.dtype != torch.float16:
+            raise ValueError("append expects fp16 keys and values")
+        k = k.contiguous()
+        v = v.contiguous()
+        n_new = [T] * B if n_new is None else [int(x) for x in n_new]
+        if len(n_new) != B or min(n_new) < 0 or max(n_new) > T:
+            raise ValueError("n_new must give 0 <= n <= T for every sequence")
+        prev = list(self.lengths)
+        new = [p + n for p, n in zip(prev, n_new)]
+        if max(new) > self.max_seq_len:
+            raise ValueError(f"sequence length {max(new)} exceeds max_seq_len={self.max_seq_len}")
+        items = []
+        for b in range(B):
+            for g in range(n_groups_for(prev[b], self.hot_window), n_groups_for(new[b], self.hot_window)):
+                items += [b, g]
+        hot_start = [n_groups_for(L, self.hot_window) * self.group_tokens for L in new]
+        host = torch.tensor(prev + n_new + hot_start + items, dtype=torch.int32)
+        dev = host.to(self.device, non_blocking=False)
+        prev_d, nnew_d, hs_d = dev[:B], dev[B:2 * B], dev[2 * B:3 * B]
+        items_d = dev[3 * B:]
+        L = N.lib()
+        st = self._stream()
+        if items:
+            if check_overflow:
+                self._overflow.zero_()
+            N.check(L.tqk_encode_groups(ctypes.byref(self.desc), ctypes.byref(self.ptrs), B,
+                                        len(items) // 2, items_d.data_ptr(), prev_d.data_ptr(),
+                                        k.data_ptr(), v.data_ptr(), T,
+                                        self._overflow.data_ptr(), st), "tqk_encode_groups")
+        if T > 0:
+            N.check(L.tqk_append_hot(ctypes.byref(self.desc), ctypes.byref(self.ptrs), B,
+                                     prev_d.data_ptr(), nnew_d.data_ptr(), hs_d.data_ptr(),
+                                     k.data_ptr(), v.data_ptr(), T, st), "tqk_append_hot")
+        self.lengths = new
+        self.seq_lens.copy_(torch.tensor(new, dtype=torch.int32), non_blocking=False)
+        if items and check_overflow and int(self._overflow.item()) != 0:
+            raise RuntimeError("outlier side-list exceeded outlier_cap for a group; "
+                               "rebuild the pool with a larger outlier_cap")
+
+    # ------------------------------------------------------------------ #
+    def workspace(self, batch: int, max_len: int):
+        torch = _torch()
+        need = N.lib().tqk_decode_workspace_bytes(ctypes.byref(self.desc), batch, max_len)
+        if self._ws is None or self._ws.numel() < need:
+            self._ws = torch.empty(int(need), dtype=torch.uint8, device=self.device)
+        return self._ws, int(need)
+
+    def _check_q(self, q):
+        torch = _torch()
+        B = self.max_batch
+        if tuple(q.shape) != (B, self.n_q_heads, self.head_dim) or q.dtype != torch.float16:
+            raise ValueError(f"decode expects fp16 q of shape ({B}, {self.n_q_heads}, {self.head_dim})")
+        if min(self.lengths) <= 0:
+            raise RuntimeError("cache is empty")
+        return q.contiguous()
+
+    def decode(self, q, out=None):
+        """One decode step for every sequence: ``q`` fp16 ``(B, Hq, D)`` ->
+        fp32 ``(B, Hq, D)`` attention output over each sequence's whole cache."""
+        torch = _torch()
+        q = self._check_q(q)
+        B, max_len = self.max_batch, max(self.lengths)
+        if out is None:
+            out = torch.empty((B, self.n_q_heads, self.head_dim), dtype=torch.float32, device=self.device)
+        ws, need = self.workspace(B, max_len)
+        N.check(N.lib().tqk_decode(ctypes.byref(self.desc), ctypes.byref(self.ptrs), B,
+                                   q.data_ptr(), self.seq_lens.data_ptr(), max_len, out.data_ptr(),
+                                   ws.data_ptr(), need, self._stream()), "tqk_decode")
+        return out
+
+    def decode_partials(self, q):
+        """Unnormalised online-softmax state ``(m, l, acc)`` of one decode step:
+        ``(B, Hq)``, ``(B, Hq)``, ``(B, Hq, D)`` fp32 with ``out = acc / l``."""
+        torch = _torch()
+        q = self._check_q(q)
+        B, max_len = self.max_batch, max(self.lengths)
+        m = torch.empty((B, self.n_q_heads), dtype=torch.float32, device=self.device)
+        l_ = torch.empty_like(m)
+        acc = torch.empty((B, self.n_q_heads, self.head_dim), dtype=torch.float32, device=self.device)
+        ws, need = self.workspace(B, max_len)
+        N.check(N.lib().tqk_decode_partials(ctypes.byref(self.desc), ctypes.byref(self.ptrs), B,
+                                            q.data_ptr(), self.seq_lens.data_ptr(), max_len,
+                                            m.data_ptr(), l_.data_ptr(), acc.data_ptr(),
+                                            ws.data_ptr(), need, self._stream()),
+                "tqk_decode_partials")
+        return m, l_, acc
+
+    # ------------------------------------------------------------------ #
+    def dequant_groups(self, items):
+        """fp32 reconstructions of groups ``[(b, g), ...]``: keys and values,
+        each ``(n, Hkv, G, D)`` (PerChannelKV.decompress / TurboQuantKV.decompress)."""
+        torch = _torch()
+        n = len(items)
+        G, H, D = self.group_tokens, self.n_kv_heads, self.head_dim
+        kout = torch.empty((n, H, G, D), dtype=torch.float32, device=self.device)
+        vout = torch.empty_like(kout)
+        if n:
+            it = torch.tensor([x for bg in items for x in bg], dtype=torch.int32).to(self.device)
+            N.check(N.lib().tqk_dequant_groups(ctypes.byref(self.desc), ctypes.byref(self.ptrs), n,
+                                               it.data_ptr(), kout.data_ptr(), vout.data_ptr(),
+                                               self._stream()), "tqk_dequant_groups")
+        return kout, vout
+
+    def hot_window_tokens(self, b: int):
+        """fp16 ``(Hkv, n_hot, D)`` keys and values of sequence b's hot window."""
+        torch = _torch()
+        L, n_cold = self.lengths[b], self.n_groups(b) * self.group_tokens
+        idx = torch.arange(n_cold, L, device=self.device) % self.hot_window
+        return self.hot_k[b][:, idx], self.hot_v[b][:, idx]
+
+    def _rows(self, b: int, g: int):
+        torch = _torch()
+        t = torch.arange(g * self.group_tokens, (g + 1) * self.group_tokens, device=self.device)
+        phys = self.block_table[b][t // self.page_tokens].long()
+        return phys, (t % self.page_tokens)
+
+    def export_group(self, b: int, g: int) -> dict:
+        """Group ``g`` of sequence ``b`` in the reference container layout:
+        ``kpacked`` (CompressedPerChannelKV.indices), ``nf4_scale``/``nf4_mean``
+        ``(H, D)``, ``outlier_idx`` int32 / ``outlier_val`` fp16 (flat over
+        ``(1, H, G, D)``), ``vpacked`` (CompressedKV.indices), ``vnorms`` ``(H, G)``."""
+        phys, off = self._rows(b, g)
+        H, G, D = self.n_kv_heads, self.group_tokens, self.head_dim
+        kp = self.kcodes[phys, :, off].permute(1, 0, 2).contiguous()   # (H, G, 64)
+        vp = self.vcodes[phys, :, off].permute(1, 0, 2).contiguous()
+        vn = self.vnorm[phys, :, off].permute(1, 0).contiguous()
+        slot = int(self.group_table[b, g])
+        cnt = self.ocount[slot].cpu().numpy()
+        ent = self.oent[slot].cpu().numpy().view(np.uint32)
+        idx, val = [], []
+        for h in range(H):
+            e = ent[h, :min(int(cnt[h]), ent.shape[1])]
+            idx.append((e & 0xFFFF).astype(np.int64) + h * G * D)
+            val.append((e >> 16).astype(np.uint16))
+        return {
+            "kpacked": kp.cpu().numpy().reshape(-1),
+            "nf4_scale": self.gscale[slot].cpu().numpy(),
+            "nf4_mean": self.gmean[slot].cpu().numpy(),
+            "outlier_idx": np.concatenate(idx).astype(np.int32) if idx else np.zeros(0, np.int32),
+            "outlier_val": np.concatenate(val).view(np.float16) if val else np.zeros(0, np.float16),
+            "outlier_count": cnt.astype(np.int64),
+            "vpacked": vp.cpu().numpy().reshape(-1),
+            "vnorms": vn.cpu().numpy(),
+        }
