@@ -17,19 +17,24 @@
  *
  * Storage layout in HBM (one cache pool = one attention layer):
  *   kcodes [num_pages][n_kv_heads][page_tokens][head_dim/2]   u8   (storage of record)
- *   vcodes [num_pages][n_kv_heads][page_tokens][head_dim*vb/8] u8  (storage of record)
+ *   vcodes [num_pages][n_kv_heads][page_tokens][head_dim*vb/8] u8  (storage of record, see below)
  *   vnorm  [num_pages][n_kv_heads][page_tokens]               f32
  *   gscale [num_gslots][n_kv_heads][head_dim]                 f32  (nf4_scale)
  *   gmean  [num_gslots][n_kv_heads][head_dim]                 f32  (nf4_mean)
- *   ocount [num_gslots][n_kv_heads]                           i32
+ *   ocount [num_gslots][n_kv_heads][8]  i32 cumulative outlier counts at tokens 32,64,..,256 (last = total)
  *   oent   [num_gslots][n_kv_heads][outlier_cap]              u32  ((s*D + j) | fp16 << 16)
  *   hot_k, hot_v [batch][n_kv_heads][hot_ring][head_dim]      fp16 ring, token t at t % hot_ring
  *   block_table [batch][max_pages_per_seq]   i32 physical page of logical page t / page_tokens
  *   group_table [batch][max_groups_per_seq]  i32 group slot of group t / group_tokens
  * The K and V rows are byte-for-byte the reference's packed layouts
  * (turboquant_pro/per_channel_kv.py:87-93 and turboquant_pro/core.py:350-398):
- * the bytes of one (group, head) in page order are the reference container's
- * `indices` slice for that head.
+ * the key bytes of one (group, head) in page order are the reference
+ * container's `indices` slice for that head.  Value bytes are the reference's
+ * per-token pack when page_tokens % 16 != 0 or group_tokens % 32 != 0; otherwise
+ * each 16-token tile of a page holds 64 units of head_dim*vb/32 bytes, unit
+ * (lg, c) = tokens [4lg, 4lg+4) x channels [8c, 8c+8) with the code of token u,
+ * channel nt at bit (2*nt + u/2)*2*vb + (u%2)*vb -- a lossless permutation of
+ * the same bits that lets one MFMA lane load its operand with one access.
  */
 #ifndef TQK_H_
 #define TQK_H_

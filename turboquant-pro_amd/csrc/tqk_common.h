@@ -8,6 +8,27 @@
 
 #define TQK_D 128          // head_dim supported by the GPU path
 #define TQK_MAX_G 256      // largest group (flush) size
+#define TQK_OBLK 32        // outlier side-list bound granularity (tokens)
+#define TQK_NOB 8          // cumulative outlier counts kept per (group slot, head)
+
+// Value codes use the MFMA-tiled byte order when every 16-token tile lies in
+// one page and groups are whole 32-token blocks; otherwise per-token rows.
+__host__ __device__ __forceinline__ bool v_tiled(int G, int P) {
+  return (P % 16 == 0) && (G % 32 == 0);
+}
+
+// Byte offset of the value-code unit holding tokens [4*lg, 4*lg+4) of a
+// 16-token tile and channels [8*c, 8*c+8), relative to the tile start.
+// A unit is vrow/4 bytes (12 for 3-bit, 16 for 4-bit codes).
+__host__ __device__ __forceinline__ int v_unit_offset(int lg, int c, int vrow) {
+  return (16 * lg + c) * (vrow / 4);
+}
+// Bit position, inside a unit, of the code of token u (0..3 within the unit)
+// and channel nt (0..7 within the unit): codes of the token pairs (0,1) and
+// (2,3) of one channel sit next to each other as one 2*vb-bit field.
+__host__ __device__ __forceinline__ int v_unit_bit(int u, int nt, int vb) {
+  return (2 * nt + (u >> 1)) * (2 * vb) + (u & 1) * vb;
+}
 
 // NormalFloat-4 levels, turboquant_pro/per_channel_kv.py:64-84.
 __constant__ static const float kNF4[16] = {

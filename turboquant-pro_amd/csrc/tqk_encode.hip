@@ -132,6 +132,10 @@ __global__ __launch_bounds__(kThreads) void tqk_encode_group(EncodeArgs a) {
   }
 
   // ---- outlier side-list in flat (token, channel) order ---------------------
+  // ocount holds cumulative counts at every TQK_OBLK-token boundary of the
+  // group (entry TQK_NOB-1 = total), so a decode block finds its entries
+  // without searching.
+  const size_t obase = (size_t)slot * Hkv + h;
   if (kout > 0) {
     const bool all = kout >= G;
     int cnt = 0;
@@ -154,7 +158,10 @@ __global__ __launch_bounds__(kThreads) void tqk_encode_group(EncodeArgs a) {
     for (int w = 0; w < (tid >> 6); ++w) wofs += wsum_s[w];
     const int total = wsum_s[0] + wsum_s[1] + wsum_s[2] + wsum_s[3];
     int off = wofs + incl - cnt;
-    const size_t obase = (size_t)slot * Hkv + h;
+    // token s = TQK_OBLK*k - 1 closes block k-1: its inclusive offset is the bound
+    if (tid < G && ((tid + 1) % TQK_OBLK) == 0 && (tid + 1) / TQK_OBLK <= TQK_NOB)
+      a.p.ocount[obase * TQK_NOB + (tid + 1) / TQK_OBLK - 1] = off + cnt;
+    if (tid < TQK_NOB && TQK_OBLK * (tid + 1) > G) a.p.ocount[obase * TQK_NOB + tid] = total;
     if (tid < G && cnt > 0) {
       for (int j = 0; j < D; ++j) {
         const uint16_t xv = kt_s[tid][j];
@@ -166,15 +173,18 @@ __global__ __launch_bounds__(kThreads) void tqk_encode_group(EncodeArgs a) {
         }
       }
     }
-    if (tid == 0) {
-      a.p.ocount[obase] = total;
-      if (total > d.outlier_cap && a.overflow) atomicOr(a.overflow, 1);
-    }
-  } else if (tid == 0) {
-    a.p.ocount[(size_t)slot * Hkv + h] = 0;
+    if (tid == 0 && total > d.outlier_cap && a.overflow) atomicOr(a.overflow, 1);
+  } else if (tid < TQK_NOB) {
+    a.p.ocount[obase * TQK_NOB + tid] = 0;
   }
 
   // ---- values: one token per thread ---------------------------------------
+  constexpr int VROW = D * VB / 8;
+  const bool tiled = v_tiled(G, P);
+  // tiled layout: codes are staged in the (no longer needed) key tile and
+  // re-assembled into 4-token x 8-channel units below
+  uint8_t (*vc_s)[D] = reinterpret_cast<uint8_t (*)[D]>(&kt_s[0][0]);
+  __syncthreads();
   if (tid < G) {
     const int t = g * G + tid;
     const uint4* src = reinterpret_cast<const uint4*>(token_src(a, a.p.hot_v, a.chunk_v, b, h, t));
@@ -208,7 +218,6 @@ __global__ __launch_bounds__(kThreads) void tqk_encode_group(EncodeArgs a) {
     for (int k = 0; k < (1 << VB) - 1; ++k) bnd[k] = a.p.vbnd[k];
 
     const size_t row = page_row(a.p.block_table, d.max_pages_per_seq, b, t, P, Hkv, h);
-    constexpr int VROW = D * VB / 8;
     uint32_t outw[VROW / 4];
 #pragma unroll
     for (int k = 0; k < VROW / 4; ++k) outw[k] = 0u;
@@ -226,16 +235,45 @@ __global__ __launch_bounds__(kThreads) void tqk_encode_group(EncodeArgs a) {
 #pragma unroll
         for (int q = 0; q < (1 << VB) - 1; ++q) code += (bnd[q] < y[k]) ? 1u : 0u;
         const int e = e0 + k;
-        const int bitpos = e * VB;  // little-endian bit stream (3-bit: 8 codes per 24 bits)
-        outw[bitpos >> 5] |= code << (bitpos & 31);
-        if ((bitpos & 31) + VB > 32) outw[(bitpos >> 5) + 1] |= code >> (32 - (bitpos & 31));
+        if (tiled) {
+          vc_s[tid][e] = (uint8_t)code;
+        } else {
+          const int bitpos = e * VB;  // little-endian bit stream (3-bit: 8 codes per 24 bits)
+          outw[bitpos >> 5] |= code << (bitpos & 31);
+          if ((bitpos & 31) + VB > 32) outw[(bitpos >> 5) + 1] |= code >> (32 - (bitpos & 31));
+        }
       }
     }
-    uint4* dst = reinterpret_cast<uint4*>(a.p.vcodes + row * VROW);
+    if (!tiled) {
+      uint4* dst = reinterpret_cast<uint4*>(a.p.vcodes + row * VROW);
 #pragma unroll
-    for (int k = 0; k < VROW / 16; ++k)
-      dst[k] = make_uint4(outw[4 * k], outw[4 * k + 1], outw[4 * k + 2], outw[4 * k + 3]);
+      for (int k = 0; k < VROW / 16; ++k)
+        dst[k] = make_uint4(outw[4 * k], outw[4 * k + 1], outw[4 * k + 2], outw[4 * k + 3]);
+    }
     a.p.vnorm[row] = nrm;
+  }
+  if (tiled) {
+    __syncthreads();
+    // one unit = tokens [16T + 4lg, +4) x channels [8c, +8) of 16-token tile T
+    for (int un = tid; un < (G / 16) * 64; un += kThreads) {
+      const int T = un >> 6, lg = (un >> 4) & 3, c = un & 15;
+      uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int uu = 0; uu < 4; ++uu) {
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) {
+          const uint32_t code = vc_s[16 * T + 4 * lg + uu][8 * c + nt];
+          const int bit = v_unit_bit(uu, nt, VB);
+          w[bit >> 5] |= code << (bit & 31);
+          if ((bit & 31) + VB > 32) w[(bit >> 5) + 1] |= code >> (32 - (bit & 31));
+        }
+      }
+      const int t0 = g * G + 16 * T;  // tile start (absolute token), never straddles a page
+      const size_t row0 = page_row(a.p.block_table, d.max_pages_per_seq, b, t0, P, Hkv, h);
+      uint32_t* dst = reinterpret_cast<uint32_t*>(a.p.vcodes + row0 * VROW + v_unit_offset(lg, c, VROW));
+#pragma unroll
+      for (int k = 0; k < VROW / 16; ++k) dst[k] = w[k];
+    }
   }
 }
 
@@ -302,13 +340,27 @@ __global__ __launch_bounds__(kThreads) void tqk_dequant_group(DequantArgs a) {
       ko[(size_t)tid * D + j1] =
           __fadd_rn(__fmul_rn(a.p.gscale[mbase + j1], kNF4[rev4(byte & 15u)]), a.p.gmean[mbase + j1]);
     }
-    const uint8_t* vr = a.p.vcodes + row * VROW;
     float y[D];
+    if (v_tiled(G, P)) {
+      // unit (lg, c) of the token's 16-token tile; tile rows start at row - (t % 16)
+      const int tt = (g * G + tid) % 16;
+      const uint8_t* tile = a.p.vcodes + (row - tt) * VROW;
+      const int lg = tt >> 2, uu = tt & 3;
 #pragma unroll
-    for (int j = 0; j < D; ++j) {
-      const int bitpos = j * VB;
-      uint32_t w = vr[bitpos >> 3] | ((uint32_t)vr[min((bitpos >> 3) + 1, VROW - 1)] << 8);
-      y[j] = a.p.vcent[(w >> (bitpos & 7)) & ((1u << VB) - 1)];
+      for (int j = 0; j < D; ++j) {
+        const uint8_t* un = tile + v_unit_offset(lg, j >> 3, VROW);
+        const int bit = v_unit_bit(uu, j & 7, VB);
+        const uint32_t w = un[bit >> 3] | ((uint32_t)un[min((bit >> 3) + 1, VROW / 4 - 1)] << 8);
+        y[j] = a.p.vcent[(w >> (bit & 7)) & ((1u << VB) - 1)];
+      }
+    } else {
+      const uint8_t* vr = a.p.vcodes + row * VROW;
+#pragma unroll
+      for (int j = 0; j < D; ++j) {
+        const int bitpos = j * VB;
+        uint32_t w = vr[bitpos >> 3] | ((uint32_t)vr[min((bitpos >> 3) + 1, VROW - 1)] << 8);
+        y[j] = a.p.vcent[(w >> (bitpos & 7)) & ((1u << VB) - 1)];
+      }
     }
     const float nrm = a.p.vnorm[row];
     for (int e = 0; e < D; ++e) {
@@ -320,7 +372,7 @@ __global__ __launch_bounds__(kThreads) void tqk_dequant_group(DequantArgs a) {
   }
   __syncthreads();
   const size_t obase = (size_t)slot * Hkv + h;
-  const int no = min(a.p.ocount[obase], d.outlier_cap);
+  const int no = min(a.p.ocount[obase * TQK_NOB + TQK_NOB - 1], d.outlier_cap);
   for (int e = tid; e < no; e += kThreads) {
     const uint32_t ent = a.p.oent[obase * d.outlier_cap + e];
     ko[ent & 0xFFFFu] = h2f((uint16_t)(ent >> 16));

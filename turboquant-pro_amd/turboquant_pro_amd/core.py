@@ -227,7 +227,7 @@ class TurboQuantKVCache:
         (turboquant_pro/core.py:1267-1295); hot tokens are held in fp16."""
         H, D, G = self.n_heads, self.head_dim, self._pool.group_tokens
         ng = self._pool.n_groups(0)
-        n_out = int(self._pool.ocount[:ng].sum().item()) if ng else 0
+        n_out = int(self._pool.ocount[:ng, :, -1].sum().item()) if ng else 0
         key_bytes = ng * (H * G * D * self.key_bits // 8 + 2 * H * D * 4) + n_out * 6
         val_bytes = ng * (H * G * D * self.value_bits // 8 + H * G * 4)
         cold = float(key_bytes + val_bytes)

@@ -23,6 +23,7 @@ import math
 import numpy as np
 
 from . import _native as N
+from .formats import pack_values, untile_value_rows
 from .codebooks import (group_tokens_for, n_groups_for, outliers_per_channel, random_rotation,
                         value_codebook)
 
@@ -55,6 +56,8 @@ class TQKVPool:
         self.key_bits, self.value_bits, self.outlier_frac = key_bits, value_bits, outlier_frac
         self.group_tokens, self.page_tokens = G, P
         self.max_groups, self.max_pages = max_groups, max_pages
+        # value codes in the MFMA-tiled byte order (see formats.py)
+        self.tiled = (P % 16 == 0) and (G % 32 == 0)
         self.desc = N.CacheDesc(
             n_kv_heads=n_kv_heads, n_q_heads=Hq, head_dim=head_dim, hot_window=hot_window,
             group_tokens=G, page_tokens=P, key_bits=key_bits, value_bits=value_bits,
@@ -72,7 +75,8 @@ class TQKVPool:
         self.vnorm = torch.zeros((n_pages, n_kv_heads, P), dtype=f32, device=dev)
         self.gscale = torch.zeros((n_slots, n_kv_heads, head_dim), dtype=f32, device=dev)
         self.gmean = torch.zeros((n_slots, n_kv_heads, head_dim), dtype=f32, device=dev)
-        self.ocount = torch.zeros((n_slots, n_kv_heads), dtype=i32, device=dev)
+        # cumulative outlier counts at every 32-token boundary of a group (last = total)
+        self.ocount = torch.zeros((n_slots, n_kv_heads, 8), dtype=i32, device=dev)
         self.oent = torch.zeros((n_slots, n_kv_heads, max(outlier_cap, 1)), dtype=i32, device=dev)
         self.hot_k = torch.zeros((max_batch, n_kv_heads, hot_window, head_dim), dtype=f16, device=dev)
         self.hot_v = torch.zeros((max_batch, n_kv_heads, hot_window, head_dim), dtype=f16, device=dev)
@@ -254,10 +258,13 @@ class TQKVPool:
         phys, off = self._rows(b, g)
         H, G, D = self.n_kv_heads, self.group_tokens, self.head_dim
         kp = self.kcodes[phys, :, off].permute(1, 0, 2).contiguous()   # (H, G, 64)
-        vp = self.vcodes[phys, :, off].permute(1, 0, 2).contiguous()
+        vp = self.vcodes[phys, :, off].permute(1, 0, 2).contiguous().cpu().numpy()  # (H, G, vrow)
+        if self.tiled:
+            vp = np.stack([pack_values(untile_value_rows(vp[h], self.value_bits, D), self.value_bits)
+                           for h in range(H)])
         vn = self.vnorm[phys, :, off].permute(1, 0).contiguous()
         slot = int(self.group_table[b, g])
-        cnt = self.ocount[slot].cpu().numpy()
+        cnt = self.ocount[slot, :, -1].cpu().numpy()
         ent = self.oent[slot].cpu().numpy().view(np.uint32)
         idx, val = [], []
         for h in range(H):
@@ -271,6 +278,6 @@ class TQKVPool:
             "outlier_idx": np.concatenate(idx).astype(np.int32) if idx else np.zeros(0, np.int32),
             "outlier_val": np.concatenate(val).view(np.float16) if val else np.zeros(0, np.float16),
             "outlier_count": cnt.astype(np.int64),
-            "vpacked": vp.cpu().numpy().reshape(-1),
+            "vpacked": np.ascontiguousarray(vp).reshape(-1),
             "vnorms": vn.cpu().numpy(),
         }
