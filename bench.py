@@ -232,7 +232,7 @@ def main():
         "step_gbs": round(step_gbs, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "tqk_decode_split_valu", "kernel_us": round(split_ms * 1e3, 2)},
+                     "kernel": "tqk_decode_split_mfma", "kernel_us": round(split_ms * 1e3, 2)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -26,10 +26,14 @@
  *   hot_k, hot_v [batch][n_kv_heads][hot_ring][head_dim]      fp16 ring, token t at t % hot_ring
  *   block_table [batch][max_pages_per_seq]   i32 physical page of logical page t / page_tokens
  *   group_table [batch][max_groups_per_seq]  i32 group slot of group t / group_tokens
- * The K and V rows are byte-for-byte the reference's packed layouts
+ * The K and V rows are the reference's packed layouts
  * (turboquant_pro/per_channel_kv.py:87-93 and turboquant_pro/core.py:350-398):
  * the key bytes of one (group, head) in page order are the reference
- * container's `indices` slice for that head.  Value bytes are the reference's
+ * container's `indices` slice for that head, except that every position held
+ * in oent stores the NF4 zero level (code 7, nibble 0xE): the dense part of a
+ * decode then contributes exactly the channel mean there and the side-list
+ * adds val - mean.  The reference's code at such a position is the nearest
+ * NF4 level to the stored fp16 value (recomputed on export).  Value bytes are the reference's
  * per-token pack when page_tokens % 16 != 0 or group_tokens % 32 != 0; otherwise
  * each 16-token tile of a page holds 64 units of head_dim*vb/32 bytes, unit
  * (lg, c) = tokens [4lg, 4lg+4) x channels [8c, 8c+8) with the code of token u,

@@ -40,3 +40,39 @@ def test_pack_values_matches_oracle_pack():
         for n in (1, 8, 13, 256):
             c = rng.integers(0, 2 ** vb, size=n, dtype=np.uint8)
             assert np.array_equal(F.pack_values(c, vb), O.pack_value_codes(c, vb))
+
+
+def _zero_level(packed, idx, H, S, D):
+    """Stored form of reference key codes: NF4 zero level at outlier positions."""
+    codes = O.unpack_key_codes(packed, H * S * D, 4).reshape(-1).copy()
+    codes[idx] = F.NF4_ZERO_CODE
+    return O.pack_key_codes(codes.reshape(1, H, S, D), 4).reshape(H, S, D // 2)
+
+
+def test_restore_outlier_codes_matches_reference_codes(golden_dir):
+    """Export restores the reference's kpacked from the zero-level storage form:
+    on the reference's own group fixture and on oracle groups with ties."""
+    import os
+    g = np.load(os.path.join(golden_dir, "cache_k4v3_w512.npz"))
+    H, D = g["k"].shape[0], g["k"].shape[2]
+    S = g["g0_kpacked"].size * 2 // (H * D)
+    for i in range(int(g["n_groups"])):
+        idx = g[f"g{i}_oidx"].astype(np.int64)
+        stored = _zero_level(g[f"g{i}_kpacked"], idx, H, S, D)
+        back = F.restore_outlier_codes(stored, idx, g[f"g{i}_oval"], g[f"g{i}_nf4_scale"],
+                                       g[f"g{i}_nf4_mean"])
+        assert np.array_equal(back.reshape(-1), g[f"g{i}_kpacked"])
+    rng = np.random.default_rng(3)
+    x = (np.round(rng.standard_normal((2, 64, 128)) * 2) / 2).astype(np.float16).astype(np.float32)
+    x[1, :, 7] = 0.0
+    kg = O.encode_keys(x, 0.05)
+    idx = kg.outlier_idx.astype(np.int64)
+    stored = _zero_level(kg.packed, idx, 2, 64, 128)
+    assert not np.array_equal(stored.reshape(-1), kg.packed)
+    back = F.restore_outlier_codes(stored, idx, kg.outlier_val, kg.nf4_scale, kg.nf4_mean)
+    assert np.array_equal(back.reshape(-1), kg.packed)
+
+
+def test_nf4_zero_code_is_exact_zero():
+    assert F.NF4[F.NF4_ZERO_CODE] == 0.0
+    assert np.array_equal(F.NF4, O.NF4.astype(np.float32))

@@ -128,7 +128,10 @@ DECODE_CASES = [
     (2, 2, 4, 300, 3, 512, None),      # hot window only
     (1, 2, 8, 513, 3, 512, None),      # exactly one flush
     (3, 2, 8, 1537, 3, 512, 16),       # paged 16-token pages
-    (1, 2, 2, 90, 3, 16, None),        # small window: groups of 8
+    (1, 2, 2, 90, 3, 16, None),        # small window: groups of 8 (per-token value rows)
+    (1, 2, 8, 200, 3, 64, None),       # groups of 32 (one block), hot ring of 64
+    (2, 2, 4, 777, 3, 512, 32),        # 32-token pages, partial hot block
+    (1, 8, 8, 1500, 3, 512, None),     # MHA with V3
 ]
 
 

@@ -318,31 +318,62 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
 
 
 // ---------------------------------------------------------------------------
-// MFMA split kernel for coded groups (value codes in the tiled order).
+// MFMA split kernel (value codes in the tiled order, hot window ring % 32 == 0).
 //
-// One wave owns one group at a time and walks it in 32-token blocks:
+// 512 threads = 8 waves share one LDS code table.  A workgroup is either a
+// coded split (its waves walk groups g0 + w, g0 + w + 8, ...) or the hot
+// split of its (sequence, kv head) (waves walk 32-token blocks of the fp16
+// window).  Every wave keeps an online-softmax state per query head and the
+// workgroup folds the eight states into one partial at the end.
+//
+// Coded 32-token block (two 16-token tiles A, B):
 //   QK^T  C[token][col] += A[token][ch] * B[ch][col]   (v_mfma_f32_16x16x32_f16)
-//         A = NF4 level of the key code, split fp16 hi + lo (two MFMAs),
-//         B = q * nf4_scale split fp16 hi (cols 0..GQ-1) + lo (cols GQ..2GQ-1);
+//         A = NF4 level of the key code as fp16 hi + lo (two MFMAs),
+//         B = q * nf4_scale as fp16 hi (cols 0..GQ-1) and lo (cols GQ..2GQ-1);
 //         col h + col h+GQ is the full-precision score of query head h.
 //   PV    O[row][ch] += P[row][token] * V[token][ch]
 //         P = softmax weight * value norm, hi rows 0..GQ-1, lo rows GQ..2GQ-1,
-//         V = value centroid split fp16 hi + lo (two MFMAs).
-// The QK^T output layout (lane = 16*lg + col holds tokens 4lg..4lg+3) is the
-// PV A-operand layout, so scores never leave registers except for the sparse
-// outlier corrections, which go through a per-wave LDS block.
-// Key bytes and value fields are turned into fp16 hi/lo operand pairs through
-// a bank-replicated LDS table (16 copies, one per lane of a 16-lane LDS pass).
+//         V = value centroid as fp16 hi + lo (two MFMAs).
+// The QK^T accumulator layout (lane 16*lg + col holds tokens 4lg..4lg+3 of a
+// tile) is the PV A-operand layout, so scores stay in registers; only blocks
+// that hold outliers round-trip through a per-wave LDS block for the sparse
+// q_j * (val - dense) corrections.  Key bytes and value fields become fp16
+// hi/lo operand pairs through a bank-replicated LDS table (one copy per lane
+// of a 16-lane LDS pass).  The next block's loads are issued before the
+// current block is computed.
 // ---------------------------------------------------------------------------
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 union H8 {
   half8_t h;
   uint32_t u[4];
+  uint4 v;
 };
 
-constexpr int kLutEntry = 256;   // bytes per table entry: 16 key copies | 16 value copies
-constexpr int kLutV = 128;       // value copies start here inside an entry
+constexpr int kMThreads = 512;   // 8 waves
+constexpr int kMWaves = 8;
+constexpr int kMaxGPS = 64;      // groups per cold split of the MFMA kernel (metadata in LDS)
+constexpr int kMetaInts = 32;    // per group: 16 tile rows, 8 outlier bounds, slot*Hkv+h
+constexpr int kLutEntry = 256;   // bytes per table entry
+
+// Code tables in LDS.  Every entry holds one 8-byte {hi pair, lo pair} copy
+// per lane of an LDS pass so that random lookups never share a bank:
+//   3-bit values: value table [64 entries x 32 copies] at 0, key table
+//                 [256 entries x 32 copies] at kKeyBase3 (80 KiB);
+//   4-bit values: 256 entries x (16 key copies | 16 value copies) (64 KiB).
+template <int VB> struct LutGeom;
+template <> struct LutGeom<3> {
+  static constexpr int kBytes = 64 * 256 + 256 * 256;
+  static constexpr uint32_t kKeyBase = 64 * 256;
+  static constexpr int kCopies = 32;
+  static constexpr uint32_t kValOff = 0;  // value entry e at e*256 + copy*8
+};
+template <> struct LutGeom<4> {
+  static constexpr int kBytes = 256 * 256;
+  static constexpr uint32_t kKeyBase = 0;
+  static constexpr int kCopies = 16;
+  static constexpr uint32_t kValOff = 128;  // value copies after the 16 key copies
+};
 
 __device__ __forceinline__ uint2 split_pair(float x0, float x1) {
   const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
@@ -353,33 +384,154 @@ __device__ __forceinline__ uint2 split_pair(float x0, float x1) {
                         ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16));
 }
 
+// Orders LDS accesses of one wave across lanes.  A wave's LDS instructions
+// execute in issue order, so program order is enough; this only stops the
+// compiler from moving memory operations across the point (and, unlike a
+// fence, does not wait for the wave's outstanding global loads).
 __device__ __forceinline__ void wave_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  asm volatile("" ::: "memory");
 }
 
-// LDS address of key-table entry (byte k of word x), copy offset in `off` (< 256):
-// one v_perm_b32: byte 1 <- x.byte[k], byte 0 <- off.byte[0], bytes 2..3 <- 0.
+// Cross-lane helpers without LDS traffic.
+__device__ __forceinline__ uint32_t fbits(float x) { return __builtin_bit_cast(uint32_t, x); }
+__device__ __forceinline__ float bitsf(uint32_t x) { return __builtin_bit_cast(float, x); }
+// max / sum over lanes {l, l^16, l^32, l^48}: the four token groups of a column
+__device__ __forceinline__ float colgroup_max(float x) {
+  auto a = __builtin_amdgcn_permlane32_swap(fbits(x), fbits(x), false, false);
+  x = fmaxf(bitsf(a[0]), bitsf(a[1]));
+  auto b = __builtin_amdgcn_permlane16_swap(fbits(x), fbits(x), false, false);
+  return fmaxf(bitsf(b[0]), bitsf(b[1]));
+}
+__device__ __forceinline__ float colgroup_sum(float x) {
+  auto a = __builtin_amdgcn_permlane32_swap(fbits(x), fbits(x), false, false);
+  x = bitsf(a[0]) + bitsf(a[1]);
+  auto b = __builtin_amdgcn_permlane16_swap(fbits(x), fbits(x), false, false);
+  return bitsf(b[0]) + bitsf(b[1]);
+}
+// value of lane (row-local) column c +/- N within the 16-lane row (DPP row rotate)
+template <int N>
+__device__ __forceinline__ float row_ror(float x) {
+  return bitsf((uint32_t)__builtin_amdgcn_update_dpp(0, (int)fbits(x), 0x120 + N, 0xF, 0xF, false));
+}
+
+// LDS address of key-table entry (byte K of word x) for copy offset `off`
+// (< 256): one v_perm_b32 -- byte 1 <- x.byte[K], byte 0 <- off, bytes 2,3 <- 0.
 template <int K>
 __device__ __forceinline__ uint32_t lut_addr_byte(uint32_t x, uint32_t off) {
   return __builtin_amdgcn_perm(x, off, 0x0C0C0000u | ((4u + K) << 8));
 }
 
-// 6-bit field m of a 96-bit value-code unit (3-bit codes).
+// 6-bit field M of a 96-bit value-code unit (3-bit codes), with 32-bit funnel
+// shifts only: a 64-bit join of two words would be merged into one 8-byte read
+// of the prefetch buffer, which then can no longer live in registers.
+template <int W>
+__device__ __forceinline__ uint32_t u4_word(const uint4& u) {
+  return W == 0 ? u.x : W == 1 ? u.y : W == 2 ? u.z : u.w;
+}
 template <int M>
-__device__ __forceinline__ uint32_t v3_field(uint32_t u0, uint32_t u1, uint32_t u2) {
-  if constexpr (M <= 9) {
-    const uint64_t lo = (uint64_t)u0 | ((uint64_t)u1 << 32);
-    return (uint32_t)(lo >> (6 * M)) & 63u;
+__device__ __forceinline__ uint32_t v3_field(const uint4& u) {
+  constexpr int o = 6 * M, w = o / 32, sh = o % 32;
+  if constexpr (sh + 6 <= 32) {
+    return (u4_word<w>(u) >> sh) & 63u;
   } else {
-    const uint64_t hi = (uint64_t)u1 | ((uint64_t)u2 << 32);
-    return (uint32_t)(hi >> (6 * M - 32)) & 63u;
+    return __builtin_amdgcn_alignbit(u4_word<w + 1>(u), u4_word<w>(u), sh) & 63u;
   }
 }
 
+template <int VB>
+struct ColdBlock {
+  uint4 kA, kB;  // 16 key bytes of token c of tile A / B
+  // value unit (lg, c) of tile A / B (12 bytes for 3-bit codes: .w unused).
+  // Plain vector members, no arrays: an indexed private array here is moved
+  // to LDS by the compiler, which then waits on every prefetch right away.
+  uint4 uA, uB;
+  float nv;        // value norm of token 16 * ((c >> 2) & 1) + 4lg + (c & 3)
+  uint2 ent;       // outlier entries 2*lane, 2*lane + 1 of the block
+  int e0, ne;      // the block's outliers are entries [e0, e0 + ne) of its group
+  uint32_t obase;  // slot * Hkv + h of the block's group
+  float2 av, mv;   // (nf4_scale, nf4_mean) of channels 2*lane, 2*lane + 1 of the group
+};
+
+// Per-wave online-softmax state for query head (c % GQ) and the PV accumulators.
+struct WaveState {
+  float m, l;
+  floatx4_t O[8];
+};
+
+// Online softmax over the 8 scores of this lane (head c % GQ, tokens
+// 4lg..4lg+3 of tiles A and B).  Every lane of a column holds the same state
+// for its head; accumulator row r = 4lg + i belongs to head r % GQ, whose
+// correction factor is read from column (r % GQ) with v_readlane.
+template <int GQ>
+__device__ __forceinline__ void softmax_block(WaveState& st, const float (&s)[8], float (&p)[8],
+                                              int lg) {
+  float bm = s[0];
+#pragma unroll
+  for (int i = 1; i < 8; ++i) bm = fmaxf(bm, s[i]);
+  bm = colgroup_max(bm);
+  const float mn = fmaxf(st.m, bm);
+  const float corr = __expf(st.m - mn);
+  st.m = mn;
+  float ps = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    p[i] = __expf(s[i] - mn);
+    ps += p[i];
+  }
+  st.l = st.l * corr + colgroup_sum(ps);
+  // the accumulators only need rescaling when some head's running max moved
+  if (__builtin_amdgcn_ballot_w64(corr < 1.0f) == 0) return;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    // no indexed array here: a lane-dependent pick from one would live in scratch
+    const float c0 = bitsf((uint32_t)__builtin_amdgcn_readlane((int)fbits(corr), i % GQ));
+    float ci = c0;
+    if constexpr (GQ > 4) {
+      const float c1 = bitsf((uint32_t)__builtin_amdgcn_readlane((int)fbits(corr), (4 + i) % GQ));
+      ci = (lg & 1) ? c1 : c0;
+    }
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) st.O[nt][i] *= ci;
+  }
+}
+
+// Lane I of each 16-lane row, broadcast to the row (DPP row_newbcast).
+template <int I>
+__device__ __forceinline__ float row_bcast(float x) {
+  return bitsf((uint32_t)__builtin_amdgcn_update_dpp(0, (int)fbits(x), 0x150 + I, 0xF, 0xF, false));
+}
+
+// fp16 pair (RNE) of two floats in one dword, and the fp32 value of a half
+__device__ __forceinline__ uint32_t pk_f16(float x, float y) {
+  typedef float float2_t __attribute__((ext_vector_type(2)));
+  typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+  const half2_t hv = __builtin_convertvector((float2_t){x, y}, half2_t);
+  return __builtin_bit_cast(uint32_t, hv);
+}
+__device__ __forceinline__ float lo_f16(uint32_t pk) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(pk & 0xFFFFu)); }
+__device__ __forceinline__ float hi_f16(uint32_t pk) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(pk >> 16)); }
+
+// PV A operand of one 16-token tile for this lane (row = column c): the
+// weights x0..x3 of tokens 4lg..4lg+3, each twice to meet the value's fp16
+// hi and lo k-slots -- [x0 x1 x0 x1 x2 x3 x2 x3] -- as fp16 hi (rows < GQ),
+// fp16 lo (rows GQ..2GQ-1) or zero (other rows).
+__device__ __forceinline__ H8 p_operand(float x0, float x1, float x2, float x3, bool active, bool is_hi) {
+  const uint32_t h01 = pk_f16(x0, x1), h23 = pk_f16(x2, x3);
+  const uint32_t l01 = pk_f16(x0 - lo_f16(h01), x1 - hi_f16(h01));
+  const uint32_t l23 = pk_f16(x2 - lo_f16(h23), x3 - hi_f16(h23));
+  const uint32_t v01 = active ? (is_hi ? h01 : l01) : 0u;
+  const uint32_t v23 = active ? (is_hi ? h23 : l23) : 0u;
+  H8 r;
+  r.u[0] = v01;
+  r.u[1] = v01;
+  r.u[2] = v23;
+  r.u[3] = v23;
+  return r;
+}
+
 template <int GQ, int VB>
-__global__ __launch_bounds__(kThreads, 2) void tqk_decode_split_mfma(DecodeArgs a) {
+__global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs a) {
   constexpr int D = TQK_D;
   constexpr int VROW = D * VB / 8;
   constexpr int UNIT = VROW / 4;
@@ -391,266 +543,416 @@ __global__ __launch_bounds__(kThreads, 2) void tqk_decode_split_mfma(DecodeArgs 
   const int L = a.seq_lens[b];
   const int ng = n_groups_of(L, d.hot_window, G);
   const float sm = d.sm_scale;
+  const bool hot = split >= a.n_cold_splits;
 
-  __shared__ __align__(16) uint8_t lut[256 * kLutEntry];
-  __shared__ float q_s[GQ][D];
-  __shared__ float am_s[4][2][D];
-  __shared__ float sc_s[4][32][GQ];
-
-  {
-    const int e = tid;
-    const uint2 kv = split_pair(kNF4[rev4((uint32_t)e >> 4)], kNF4[rev4((uint32_t)e & 15u)]);
-    uint2 vv = make_uint2(0u, 0u);
-    if (e < (1 << (2 * VB))) {
-      const int m = (1 << VB) - 1;
-      vv = split_pair(a.p.vcent[e & m], a.p.vcent[e >> VB]);
-    }
-    uint8_t* ent = lut + e * kLutEntry;
-#pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      *reinterpret_cast<uint2*>(ent + q * 8) = kv;
-      *reinterpret_cast<uint2*>(ent + kLutV + q * 8) = vv;
+  __shared__ __align__(16) uint8_t lut[LutGeom<VB>::kBytes];
+  __shared__ __align__(16) float qt_s[D][GQ];           // q transposed: [channel][head]
+  __shared__ __align__(16) float2 am_s[kMWaves][D];     // (nf4_scale, nf4_mean) of the wave's group
+  // outlier correction operands: entry token (255 = none) and q_h * (val - dense)
+  // as fp16 hi (column h) / lo (column GQ + h), column-major, padded columns
+  __shared__ __align__(16) uint8_t otb_s[kMWaves][128];
+  __shared__ __align__(16) _Float16 ocb_s[kMWaves][2 * GQ][136];
+  // Metadata of the split's groups, read once here so the block stream issues
+  // nothing but block loads: [0, 16) first row of each 16-token tile,
+  // [16, 24) cumulative outlier bounds, [24] slot * Hkv + h.
+  __shared__ int meta_s[kMaxGPS][kMetaInts];
+  if (!hot) {
+    const int gbeg = split * a.groups_per_split;
+    const int gcnt = max(0, min(ng, gbeg + a.groups_per_split) - gbeg);
+    for (int x = tid; x < gcnt * kMetaInts; x += kMThreads) {
+      const int jg = x / kMetaInts, f = x % kMetaInts, g = gbeg + jg;
+      const int slot = a.p.group_table[(size_t)b * d.max_groups_per_seq + g];
+      const uint32_t obase = (uint32_t)slot * (uint32_t)Hkv + (uint32_t)h;
+      int v = 0;
+      if (f < 16) {
+        if (f < G / 16) v = (int)page_row(a.p.block_table, d.max_pages_per_seq, b, g * G + 16 * f, P, Hkv, h);
+      } else if (f < 16 + TQK_NOB) {
+        v = min(a.p.ocount[(size_t)obase * TQK_NOB + (f - 16)], d.outlier_cap);
+      } else if (f == 16 + TQK_NOB) {
+        v = (int)obase;
+      }
+      meta_s[jg][f] = v;
     }
   }
-  for (int i = tid; i < GQ * D; i += kThreads)
-    q_s[i / D][i % D] = h2f(a.q[((size_t)b * Hq + h * GQ + i / D) * D + i % D]);
+
+  if (!hot) {
+    // unit u (8 bytes): key part first (entry u / copies, copy u % copies), then values;
+    // consecutive lanes write consecutive units
+    using LG = LutGeom<VB>;
+    constexpr int NC = LG::kCopies;
+    constexpr int NV = 1 << (2 * VB);
+    for (int u = tid; u < 256 * NC + NV * NC; u += kMThreads) {
+      uint2 val;
+      uint32_t off;
+      if (u < 256 * NC) {
+        const int e = u / NC;
+        val = split_pair(kNF4[rev4((uint32_t)e >> 4)], kNF4[rev4((uint32_t)e & 15u)]);
+        off = LG::kKeyBase + (uint32_t)e * kLutEntry + (uint32_t)(u % NC) * 8u;
+      } else {
+        const int v = u - 256 * NC, e = v / NC, m = (1 << VB) - 1;
+        val = split_pair(a.p.vcent[e & m], a.p.vcent[e >> VB]);
+        off = (uint32_t)e * kLutEntry + LG::kValOff + (uint32_t)(v % NC) * 8u;
+      }
+      *reinterpret_cast<uint2*>(lut + off) = val;
+    }
+  }
+  for (int i = tid; i < GQ * D; i += kMThreads)
+    qt_s[i % D][i / D] = h2f(a.q[((size_t)b * Hq + h * GQ + i / D) * D + i % D]);
   __syncthreads();
 
   const int hcol = c % GQ;
   const bool active = c < NCOL, is_hi = c < GQ;
-  const uint32_t koff = (uint32_t)c * 8u, voff = (uint32_t)kLutV + (uint32_t)c * 8u;
-  const int32_t* __restrict__ bt = a.p.block_table;
-  const uint8_t* __restrict__ kcodes = a.p.kcodes;
-  const uint8_t* __restrict__ vcodes = a.p.vcodes;
-  const float* __restrict__ vnorm = a.p.vnorm;
-
-  float m_run = -INFINITY, l_run = 0.f;
-  floatx4_t O[8];
+  // partner column of c in the hi/lo pair (c ^ GQ), via one of two row rotates
+  const bool rot_a = (int)row_ror<GQ>((float)c) == (c ^ GQ);
+  auto pair_sum = [&](float x) {
+    const float pa_ = row_ror<GQ>(x), pb_ = row_ror<(16 - GQ) % 16>(x);
+    return x + (rot_a ? pa_ : pb_);
+  };
+  WaveState st;
+  st.m = -INFINITY;
+  st.l = 0.f;
 #pragma unroll
-  for (int nt = 0; nt < 8; ++nt) O[nt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+  for (int nt = 0; nt < 8; ++nt) st.O[nt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 
-  const int g0 = split * a.groups_per_split;
-  const int g1 = min(ng, g0 + a.groups_per_split);
-  for (int g = g0 + w; g < g1; g += 4) {
-    const int slot = a.p.group_table[(size_t)b * d.max_groups_per_seq + g];
-    const size_t mbase = ((size_t)slot * Hkv + h) * D;
-    {
-      const float2 av = reinterpret_cast<const float2*>(a.p.gscale + mbase)[lane];
-      const float2 mv = reinterpret_cast<const float2*>(a.p.gmean + mbase)[lane];
-      am_s[w][0][2 * lane] = av.x;
-      am_s[w][0][2 * lane + 1] = av.y;
-      am_s[w][1][2 * lane] = mv.x;
-      am_s[w][1][2 * lane + 1] = mv.y;
-    }
-    wave_sync();
-    // B operand of QK^T: channel 32*lg + 8*ks + e, column c
-    H8 Bw[4];
-    float biasp = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int ch = 32 * lg + 8 * ks + e;
-        const float qv = q_s[hcol][ch];
-        const float wv = qv * am_s[w][0][ch];
-        const _Float16 hi = (_Float16)wv;
-        const _Float16 lo = (_Float16)(wv - (float)hi);
-        Bw[ks].h[e] = active ? (is_hi ? hi : lo) : (_Float16)0.f;
-        biasp += qv * am_s[w][1][ch];
-      }
-    }
-    biasp += __shfl_xor(biasp, 16, 64);
-    biasp += __shfl_xor(biasp, 32, 64);
-    const float bias = biasp;
-    const size_t obase = (size_t)slot * Hkv + h;
-    const int32_t* __restrict__ ob = a.p.ocount + obase * TQK_NOB;
-    const uint32_t* __restrict__ oent = a.p.oent + obase * d.outlier_cap;
-
+  if (!hot) {
+    constexpr int NC = LutGeom<VB>::kCopies;
+    const uint32_t koff = (uint32_t)(lane % NC) * 8u;
+    const uint32_t voff = LutGeom<VB>::kValOff + (uint32_t)(lane % NC) * 8u;
+    const uint8_t* __restrict__ klut = lut + LutGeom<VB>::kKeyBase;
+    const int cap = d.outlier_cap;
+    // outlier entries are read at clamped indices (never past the group's list)
+    const uint32_t* __restrict__ oent_all = cap > 0 ? a.p.oent : reinterpret_cast<const uint32_t*>(a.p.ocount);
+    const int capm1 = cap > 0 ? cap - 1 : 0;
+    // this wave streams the split's groups wu, wu + 8, ... (meta_s rows), block after block
+    const int wu = __builtin_amdgcn_readfirstlane(w);
+    const int gbeg = split * a.groups_per_split;
+    const int gcnt = max(0, min(ng, gbeg + a.groups_per_split) - gbeg);
+    const int nw = wu < gcnt ? (gcnt - wu + kMWaves - 1) / kMWaves : 0;
     const int nblk = G / 32;
-    for (int blk = 0; blk < nblk; ++blk) {
-      const int t0 = g * G + 32 * blk;
-      const size_t rowA = page_row(bt, d.max_pages_per_seq, b, t0, P, Hkv, h);
-      const size_t rowB = page_row(bt, d.max_pages_per_seq, b, t0 + 16, P, Hkv, h);
-      const uint4 kA = *reinterpret_cast<const uint4*>(kcodes + (rowA + c) * (D / 2) + 16 * lg);
-      const uint4 kB = *reinterpret_cast<const uint4*>(kcodes + (rowB + c) * (D / 2) + 16 * lg);
-      uint32_t uA[UNIT / 4], uB[UNIT / 4];
-      {
-        const uint32_t* pA = reinterpret_cast<const uint32_t*>(vcodes + rowA * VROW + (16 * lg + c) * UNIT);
-        const uint32_t* pB = reinterpret_cast<const uint32_t*>(vcodes + rowB * VROW + (16 * lg + c) * UNIT);
-#pragma unroll
-        for (int k = 0; k < UNIT / 4; ++k) {
-          uA[k] = pA[k];
-          uB[k] = pB[k];
+    const int T = nw * nblk;
+    // per-lane parts of the block addresses (the row parts are wave-uniform)
+    const uint32_t koffL = (uint32_t)c * (D / 2) + 16u * (uint32_t)lg;
+    const uint32_t uoffL = (uint32_t)(16 * lg + c) * UNIT;
+    const int ntl = 4 * lg + (c & 3);  // token (of tile A if c & 4 == 0, else B) whose norm this lane reads
+    auto meta = [&](int j, int f) { return __builtin_amdgcn_readfirstlane(meta_s[wu + kMWaves * j][f]); };
+
+    // Every step issues the same loads (past the end: the last block again,
+    // already in L2), so the waits on the oldest buffer stay exact.
+    int jl = 0, kbl = 0, nl = 0;  // next block to load: wave group jl, block kbl, stream index nl
+    auto load_next = [&](ColdBlock<VB>& cb) {
+      const size_t rowA = (size_t)(uint32_t)meta(jl, 2 * kbl);
+      const size_t rowB = (size_t)(uint32_t)meta(jl, 2 * kbl + 1);
+      const uint32_t obase = (uint32_t)meta(jl, 16 + TQK_NOB);
+      const int e0 = kbl == 0 ? 0 : meta(jl, 16 + kbl - 1);
+      const int e1 = meta(jl, 16 + kbl);
+      cb.kA = *reinterpret_cast<const uint4*>(a.p.kcodes + rowA * (D / 2) + koffL);
+      cb.kB = *reinterpret_cast<const uint4*>(a.p.kcodes + rowB * (D / 2) + koffL);
+      const uint8_t* vA = a.p.vcodes + rowA * VROW + uoffL;
+      const uint8_t* vB = a.p.vcodes + rowB * VROW + uoffL;
+      if constexpr (VB == 3) {
+        const uint32_t* pA = reinterpret_cast<const uint32_t*>(vA);
+        const uint32_t* pB = reinterpret_cast<const uint32_t*>(vB);
+        cb.uA = make_uint4(pA[0], pA[1], pA[2], 0u);
+        cb.uB = make_uint4(pB[0], pB[1], pB[2], 0u);
+      } else {
+        cb.uA = *reinterpret_cast<const uint4*>(vA);
+        cb.uB = *reinterpret_cast<const uint4*>(vB);
+      }
+      cb.nv = a.p.vnorm[((c & 4) ? rowB : rowA) + ntl];
+      const uint32_t* oe = oent_all + (size_t)obase * cap;
+      // entries past e1 are masked where they are used (the outlier pass)
+      const int i0 = e0 + 2 * lane;
+      cb.ent = make_uint2(oe[min(i0, capm1)], oe[min(i0 + 1, capm1)]);
+      cb.e0 = e0;
+      cb.ne = e1 - e0;
+      cb.obase = obase;
+      // the group's (scale, mean) travel with every block, so the start of a
+      // group waits on nothing newer than the block itself
+      cb.av = reinterpret_cast<const float2*>(a.p.gscale + (size_t)obase * D)[lane];
+      cb.mv = reinterpret_cast<const float2*>(a.p.gmean + (size_t)obase * D)[lane];
+      if (nl + 1 < T) {
+        ++nl;
+        if (++kbl == nblk) {
+          kbl = 0;
+          ++jl;
         }
       }
-      const float4 nA = *reinterpret_cast<const float4*>(vnorm + rowA + 4 * lg);
-      const float4 nB = *reinterpret_cast<const float4*>(vnorm + rowB + 4 * lg);
+    };
 
-      // ---- QK^T
+    H8 Bw[8];
+    float bias = 0.f;
+    // start of a group: (scale, mean) to LDS for the outlier pass, then the
+    // QK^T weight operand and the mean bias
+    auto begin_group = [&](const ColdBlock<VB>& cur) {
+      am_s[w][2 * lane] = make_float2(cur.av.x, cur.mv.x);
+      am_s[w][2 * lane + 1] = make_float2(cur.av.y, cur.mv.y);
+      wave_sync();
+      // B operand of QK^T for MFMA ks2 (channels ch_i = 32lg + 4ks2 + i): the
+      // key operand holds [hi(ch0) hi(ch1) lo(ch0) lo(ch1) hi(ch2) hi(ch3) lo(ch2) lo(ch3)],
+      // so the weights go [W0 W1 W0 W1 W2 W3 W2 W3]; column c is q*scale of head c % GQ
+      // as fp16 hi (c < GQ) or lo (GQ <= c < 2GQ)
+      float biasp = 0.f;
+#pragma unroll
+      for (int ks2 = 0; ks2 < 8; ++ks2) {
+        uint32_t wpk[2];
+#pragma unroll
+        for (int hp = 0; hp < 2; ++hp) {
+          const int ch = 32 * lg + 4 * ks2 + 2 * hp;
+          const float q0 = qt_s[ch][hcol], q1 = qt_s[ch + 1][hcol];
+          const float2 am0 = am_s[w][ch], am1 = am_s[w][ch + 1];
+          const float w0 = q0 * am0.x, w1 = q1 * am1.x;
+          biasp += q0 * am0.y + q1 * am1.y;
+          const uint32_t hv = pk_f16(w0, w1);
+          const uint32_t lv = pk_f16(w0 - lo_f16(hv), w1 - hi_f16(hv));
+          wpk[hp] = active ? (is_hi ? hv : lv) : 0u;
+        }
+        Bw[ks2].u[0] = wpk[0];
+        Bw[ks2].u[1] = wpk[0];
+        Bw[ks2].u[2] = wpk[1];
+        Bw[ks2].u[3] = wpk[1];
+      }
+      bias = colgroup_sum(biasp);
+    };
+
+      auto qk_tile = [&](const uint4 kq) {
+        floatx4_t C = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks2 = 0; ks2 < 8; ++ks2) {
+          const uint32_t word = (ks2 >> 1) == 0 ? kq.x : (ks2 >> 1) == 1 ? kq.y : (ks2 >> 1) == 2 ? kq.z : kq.w;
+          const uint32_t sb = 4u + 2u * (uint32_t)(ks2 & 1);
+          const uint2 t0 = *reinterpret_cast<const uint2*>(klut + __builtin_amdgcn_perm(word, koff, 0x0C0C0000u | (sb << 8)));
+          const uint2 t1 = *reinterpret_cast<const uint2*>(klut + __builtin_amdgcn_perm(word, koff, 0x0C0C0000u | ((sb + 1u) << 8)));
+          H8 av;
+          av.u[0] = t0.x;
+          av.u[1] = t0.y;
+          av.u[2] = t1.x;
+          av.u[3] = t1.y;
+          C = __builtin_amdgcn_mfma_f32_16x16x32_f16(av.h, Bw[ks2].h, C, 0, 0, 0);
+        }
+        return C;
+      };
+      auto pv_tile = [&](const uint4& un, const H8& pa) {
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) {
+          uint32_t f0, f1;
+          if constexpr (VB == 3) {
+            switch (nt) {
+#define TQK_V3(NT) case NT: f0 = v3_field<2 * NT>(un); f1 = v3_field<2 * NT + 1>(un); break;
+              TQK_V3(0) TQK_V3(1) TQK_V3(2) TQK_V3(3) TQK_V3(4) TQK_V3(5) TQK_V3(6) TQK_V3(7)
+#undef TQK_V3
+            }
+          } else {
+            const uint32_t word = (nt >> 1) == 0 ? un.x : (nt >> 1) == 1 ? un.y : (nt >> 1) == 2 ? un.z : un.w;
+            f0 = (word >> (16 * (nt & 1))) & 0xFFu;
+            f1 = (word >> (16 * (nt & 1) + 8)) & 0xFFu;
+          }
+          const uint2 t0 = *reinterpret_cast<const uint2*>(lut + ((f0 << 8) | voff));
+          const uint2 t1 = *reinterpret_cast<const uint2*>(lut + ((f1 << 8) | voff));
+          H8 vb;
+          vb.u[0] = t0.x;
+          vb.u[1] = t0.y;
+          vb.u[2] = t1.x;
+          vb.u[3] = t1.y;
+          st.O[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa.h, vb.h, st.O[nt], 0, 0, 0);
+        }
+      };
+
+      auto process = [&](const ColdBlock<VB>& cur, int blk) {
+        const uint32_t* __restrict__ oent = oent_all + (size_t)cur.obase * cap;
+        floatx4_t CA = qk_tile(cur.kA);
+        floatx4_t CB = qk_tile(cur.kB);
+        // ---- sparse outliers of this block, folded into the QK^T accumulators:
+        //   C[t][col] += sum_e onehot[t][e] * contrib[e][col],
+        //   contrib[e][h] = q_h[j_e] * (val_e - dense_e) as hi (col h) / lo (col GQ+h)
+        const int e0 = cur.e0, ne = cur.ne;
+        if (ne > 0) {
+          for (int base = 0; base < ne; base += 128) {
+            const int cnt = min(128, ne - base);
+            // entries 2*lane and 2*lane + 1 of this chunk
+            uint2 ent = cur.ent;
+            if (base > 0) {
+              // rare (> 128 entries in one block): read the chunk and drain
+              // here, so the common path keeps exact wait counts
+              const int i0 = e0 + base + 2 * lane;
+              const uint32_t x0 = oent[min(i0, capm1)], x1 = oent[min(i0 + 1, capm1)];
+              __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+              ent = make_uint2((2 * lane < cnt) ? x0 : 0u, (2 * lane + 1 < cnt) ? x1 : 0u);
+            }
+            float delta[2];
+            uint32_t tbv[2];
+            int jv[2];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+              const uint32_t en = u ? ent.y : ent.x;
+              const bool ok = 2 * lane + u < cnt;
+              const int pos = en & 0xFFFFu;
+              const int tb = ok ? (pos >> 7) - 32 * blk : 0;
+              const int j = pos & (D - 1);
+              // the stored code of an outlier is the zero level: dense part = mean
+              delta[u] = ok ? h2f((uint16_t)(en >> 16)) - am_s[w][j].y : 0.f;
+              tbv[u] = ok ? (uint32_t)tb : 255u;
+              jv[u] = j;
+            }
+            *reinterpret_cast<uint16_t*>(&otb_s[w][2 * lane]) = (uint16_t)(tbv[0] | (tbv[1] << 8));
+            float qv[2][GQ];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+              if constexpr (GQ >= 4) {
+#pragma unroll
+                for (int hh = 0; hh < GQ; hh += 4) {
+                  const float4 q4 = *reinterpret_cast<const float4*>(&qt_s[jv[u]][hh]);
+                  qv[u][hh] = q4.x; qv[u][hh + 1] = q4.y; qv[u][hh + 2] = q4.z; qv[u][hh + 3] = q4.w;
+                }
+              } else {
+#pragma unroll
+                for (int k2 = 0; k2 < GQ; ++k2) qv[u][k2] = qt_s[jv[u]][k2];
+              }
+            }
+#pragma unroll
+            for (int hh = 0; hh < GQ; ++hh) {
+              const float x0 = qv[0][hh] * delta[0], x1 = qv[1][hh] * delta[1];
+              const uint32_t hv = pk_f16(x0, x1);
+              *reinterpret_cast<uint32_t*>(&ocb_s[w][hh][2 * lane]) = hv;
+              *reinterpret_cast<uint32_t*>(&ocb_s[w][GQ + hh][2 * lane]) =
+                  pk_f16(x0 - lo_f16(hv), x1 - hi_f16(hv));
+            }
+            wave_sync();
+            for (int ch = 0; ch < (cnt + 31) / 32; ++ch) {
+              const uint2 tb8 = *reinterpret_cast<const uint2*>(&otb_s[w][32 * ch + 8 * lg]);
+              H8 oa, obh, cbv;
+#pragma unroll
+              for (int e = 0; e < 8; ++e) {
+                const uint32_t t = ((e < 4 ? tb8.x : tb8.y) >> (8 * (e & 3))) & 0xFFu;
+                oa.h[e] = (t == (uint32_t)c) ? (_Float16)1.f : (_Float16)0.f;
+                obh.h[e] = (t == (uint32_t)(16 + c)) ? (_Float16)1.f : (_Float16)0.f;
+              }
+              cbv.v = active ? *reinterpret_cast<const uint4*>(&ocb_s[w][c][32 * ch + 8 * lg])
+                             : make_uint4(0u, 0u, 0u, 0u);
+              CA = __builtin_amdgcn_mfma_f32_16x16x32_f16(oa.h, cbv.h, CA, 0, 0, 0);
+              CB = __builtin_amdgcn_mfma_f32_16x16x32_f16(obh.h, cbv.h, CB, 0, 0, 0);
+            }
+            wave_sync();
+          }
+        }
+        float sc[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          sc[i] = (pair_sum(CA[i]) + bias) * sm;
+          sc[4 + i] = (pair_sum(CB[i]) + bias) * sm;
+        }
+        float p[8];
+        softmax_block<GQ>(st, sc, p, lg);
+        const H8 paA = p_operand(p[0] * row_bcast<0>(cur.nv), p[1] * row_bcast<1>(cur.nv),
+                                 p[2] * row_bcast<2>(cur.nv), p[3] * row_bcast<3>(cur.nv), active, is_hi);
+        const H8 paB = p_operand(p[4] * row_bcast<4>(cur.nv), p[5] * row_bcast<5>(cur.nv),
+                                 p[6] * row_bcast<6>(cur.nv), p[7] * row_bcast<7>(cur.nv), active, is_hi);
+        pv_tile(cur.uA, paA);
+        pv_tile(cur.uB, paB);
+      };
+
+
+
+    // Two blocks in flight: step i issues the loads of block i + 2 and
+    // computes block i (buffers rotate A -> B -> C).
+    int kbp = 0;  // block index of the computed block within its group
+    auto step = [&](const ColdBlock<VB>& cur, ColdBlock<VB>& nxt) {
+      if (kbp == 0) begin_group(cur);
+      load_next(nxt);
+      process(cur, kbp);
+      if (++kbp == nblk) kbp = 0;
+    };
+    if (T > 0) {
+      ColdBlock<VB> bA, bB, bC;
+      load_next(bA);
+      load_next(bB);
+      for (int i = 0; i < T; i += 3) {
+        step(bA, bC);
+        if (i + 1 >= T) break;
+        step(bB, bA);
+        if (i + 2 >= T) break;
+        step(bC, bB);
+      }
+    }
+  } else {
+    // ---- fp16 hot window: tokens [n_cold, L) from the ring, 32-token blocks
+    const int n_cold = ng * G, R = d.hot_ring;
+    const size_t hbase = ((size_t)b * Hkv + h) * R;
+    const int nhb = (L - n_cold + 31) / 32;
+    // B operand of QK^T: q (fp16, exact) of head c for channels 32ks + 8lg + e
+    H8 Bq[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      if (c < GQ)
+        Bq[ks].v = *reinterpret_cast<const uint4*>(a.q + ((size_t)b * Hq + h * GQ + c) * D + 32 * ks + 8 * lg);
+      else
+        Bq[ks].v = make_uint4(0u, 0u, 0u, 0u);
+    }
+    for (int hb = w; hb < nhb; hb += kMWaves) {
+      const int t0 = n_cold + 32 * hb;
+      const uint16_t* kr = a.p.hot_k + (hbase + (t0 % R)) * D;   // 32 consecutive ring rows
+      const uint16_t* vr = a.p.hot_v + (hbase + (t0 % R)) * D;
       floatx4_t CA = {0.f, 0.f, 0.f, 0.f}, CB = {0.f, 0.f, 0.f, 0.f};
-      const uint32_t kwA[4] = {kA.x, kA.y, kA.z, kA.w};
-      const uint32_t kwB[4] = {kB.x, kB.y, kB.z, kB.w};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        H8 ah, al, bh, bl;
-        uint2 t;
-#define TQK_KLOAD(K)                                                                 \
-  t = *reinterpret_cast<const uint2*>(lut + lut_addr_byte<K>(kwA[ks], koff));        \
-  ah.u[K] = t.x;                                                                     \
-  al.u[K] = t.y;                                                                     \
-  t = *reinterpret_cast<const uint2*>(lut + lut_addr_byte<K>(kwB[ks], koff));        \
-  bh.u[K] = t.x;                                                                     \
-  bl.u[K] = t.y;
-        TQK_KLOAD(0)
-        TQK_KLOAD(1)
-        TQK_KLOAD(2)
-        TQK_KLOAD(3)
-#undef TQK_KLOAD
-        CA = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah.h, Bw[ks].h, CA, 0, 0, 0);
-        CA = __builtin_amdgcn_mfma_f32_16x16x32_f16(al.h, Bw[ks].h, CA, 0, 0, 0);
-        CB = __builtin_amdgcn_mfma_f32_16x16x32_f16(bh.h, Bw[ks].h, CB, 0, 0, 0);
-        CB = __builtin_amdgcn_mfma_f32_16x16x32_f16(bl.h, Bw[ks].h, CB, 0, 0, 0);
+        H8 ka, kb;
+        ka.v = *reinterpret_cast<const uint4*>(kr + (size_t)c * D + 32 * ks + 8 * lg);
+        kb.v = *reinterpret_cast<const uint4*>(kr + (size_t)(16 + c) * D + 32 * ks + 8 * lg);
+        CA = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka.h, Bq[ks].h, CA, 0, 0, 0);
+        CB = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb.h, Bq[ks].h, CB, 0, 0, 0);
       }
       float s[8];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        s[i] = (CA[i] + __shfl_xor(CA[i], GQ, 64) + bias) * sm;
-        s[4 + i] = (CB[i] + __shfl_xor(CB[i], GQ, 64) + bias) * sm;
+        s[i] = (t0 + 4 * lg + i < L) ? CA[i] * sm : -INFINITY;
+        s[4 + i] = (t0 + 16 + 4 * lg + i < L) ? CB[i] * sm : -INFINITY;
       }
-
-      // ---- sparse outliers of this block: q_j * (val - dense) through LDS
-      const int e0 = min(blk == 0 ? 0 : ob[blk - 1], d.outlier_cap);
-      const int e1 = min(ob[blk], d.outlier_cap);
-      if (e1 > e0) {
-        if (c < GQ) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            sc_s[w][4 * lg + i][c] = s[i];
-            sc_s[w][16 + 4 * lg + i][c] = s[4 + i];
-          }
-        }
-        wave_sync();
-        for (int e = e0 + lane; e < e1; e += 64) {
-          const uint32_t ent = oent[e];
-          const int pos = ent & 0xFFFFu;
-          const float val = h2f((uint16_t)(ent >> 16));
-          const int bt_ = (pos >> 7) - 32 * blk, j = pos & (D - 1);
-          const size_t row = (bt_ < 16) ? rowA + bt_ : rowB + (bt_ - 16);
-          const uint32_t byte = kcodes[row * (D / 2) + (j >> 1)];
-          const uint32_t code = (j & 1) ? rev4(byte & 15u) : rev4(byte >> 4);
-          const float delta = (val - (am_s[w][0][j] * kNF4[code] + am_s[w][1][j])) * sm;
-#pragma unroll
-          for (int hh = 0; hh < GQ; ++hh) atomicAdd(&sc_s[w][bt_][hh], q_s[hh][j] * delta);
-        }
-        wave_sync();
-        if (active) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            s[i] = sc_s[w][4 * lg + i][hcol];
-            s[4 + i] = sc_s[w][16 + 4 * lg + i][hcol];
-          }
-        }
-        wave_sync();
-      }
-
-      // ---- online softmax for head hcol
-      float bm = s[0];
-#pragma unroll
-      for (int i = 1; i < 8; ++i) bm = fmaxf(bm, s[i]);
-      bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
-      bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
-      const float mn = fmaxf(m_run, bm);
-      const float corr = __expf(m_run - mn);
-      m_run = mn;
-      float p[8], ps = 0.f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        p[i] = __expf(s[i] - mn);
-        ps += p[i];
-      }
-      ps += __shfl_xor(ps, 16, 64);
-      ps += __shfl_xor(ps, 32, 64);
-      l_run = l_run * corr + ps;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float ci = __shfl(corr, 16 * lg + 4 * lg + i, 64);
-#pragma unroll
-        for (int nt = 0; nt < 8; ++nt) O[nt][i] *= ci;
-      }
-      // P operand rows: hi (c < GQ) / lo (GQ <= c < 2GQ) of p * norm
+      float p[8];
+      softmax_block<GQ>(st, s, p, lg);
       H8 pa;
-      {
-        const float nv[8] = {nA.x, nA.y, nA.z, nA.w, nB.x, nB.y, nB.z, nB.w};
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float x = p[e] * nv[e];
-          const _Float16 hi = (_Float16)x;
-          const _Float16 lo = (_Float16)(x - (float)hi);
-          pa.h[e] = active ? (is_hi ? hi : lo) : (_Float16)0.f;
-        }
+      for (int e = 0; e < 8; ++e) {
+        const _Float16 hi = (_Float16)p[e];
+        const _Float16 lo = (_Float16)(p[e] - (float)hi);
+        pa.h[e] = active ? (is_hi ? hi : lo) : (_Float16)0.f;
       }
-      // ---- PV over the 8 channel tiles (channel 8*c + nt)
+      // values: token e of this lane (tile A 4lg+e, tile B 16+4lg+e), channels 8c..8c+7
+      uint4 vv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int tt = (e < 4) ? 4 * lg + e : 16 + 4 * lg + (e - 4);
+        vv[e] = (t0 + tt < L) ? *reinterpret_cast<const uint4*>(vr + (size_t)tt * D + 8 * c)
+                              : make_uint4(0u, 0u, 0u, 0u);
+      }
 #pragma unroll
       for (int nt = 0; nt < 8; ++nt) {
-        H8 vh, vl;
-        uint32_t f[4];
-        if constexpr (VB == 3) {
-#define TQK_F3(M) (nt == (M) / 2 ? 0 : 0)
-          switch (nt) {
-#define TQK_V3CASE(NT)                                        \
-  case NT:                                                    \
-    f[0] = v3_field<2 * NT>(uA[0], uA[1], uA[2]);             \
-    f[1] = v3_field<2 * NT + 1>(uA[0], uA[1], uA[2]);         \
-    f[2] = v3_field<2 * NT>(uB[0], uB[1], uB[2]);             \
-    f[3] = v3_field<2 * NT + 1>(uB[0], uB[1], uB[2]);         \
-    break;
-            TQK_V3CASE(0) TQK_V3CASE(1) TQK_V3CASE(2) TQK_V3CASE(3)
-            TQK_V3CASE(4) TQK_V3CASE(5) TQK_V3CASE(6) TQK_V3CASE(7)
-#undef TQK_V3CASE
-#undef TQK_F3
-          }
+        H8 vb;
+        const uint32_t sel = (nt & 1) ? 0x07060302u : 0x05040100u;
 #pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            const uint2 t = *reinterpret_cast<const uint2*>(lut + ((f[k] << 8) | voff));
-            vh.u[k] = t.x;
-            vl.u[k] = t.y;
-          }
-        } else {
-          // 4-bit: field m = byte m of the 16-byte unit
-          const uint32_t wa = uA[nt >> 1], wb = uB[nt >> 1];
-          const int k0 = 2 * (nt & 1);
-          f[0] = (wa >> (8 * k0)) & 0xFFu;
-          f[1] = (wa >> (8 * k0 + 8)) & 0xFFu;
-          f[2] = (wb >> (8 * k0)) & 0xFFu;
-          f[3] = (wb >> (8 * k0 + 8)) & 0xFFu;
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            const uint2 t = *reinterpret_cast<const uint2*>(lut + ((f[k] << 8) | voff));
-            vh.u[k] = t.x;
-            vl.u[k] = t.y;
-          }
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t* v0 = reinterpret_cast<const uint32_t*>(&vv[2 * k]);
+          const uint32_t* v1 = reinterpret_cast<const uint32_t*>(&vv[2 * k + 1]);
+          vb.u[k] = __builtin_amdgcn_perm(v1[nt >> 1], v0[nt >> 1], sel);
         }
-        O[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa.h, vh.h, O[nt], 0, 0, 0);
-        O[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa.h, vl.h, O[nt], 0, 0, 0);
+        st.O[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa.h, vb.h, st.O[nt], 0, 0, 0);
       }
     }
   }
 
-  // ---- combine the four waves' states (the table is no longer needed)
+  // ---- fold the eight waves' states (the code table is no longer needed)
   __syncthreads();
-  float* cm = reinterpret_cast<float*>(lut);  // [4][GQ]
-  float* cl = cm + 4 * GQ;                    // [4][GQ]
-  float* co = cl + 4 * GQ;                    // [4][GQ][D]
+  float* cm = reinterpret_cast<float*>(lut);  // [8][GQ]
+  float* cl = cm + kMWaves * GQ;              // [8][GQ]
+  float* co = cl + kMWaves * GQ;              // [8][GQ][D]
   if (lg == 0 && c < GQ) {
-    cm[w * GQ + c] = m_run;
-    cl[w * GQ + c] = l_run;
+    cm[w * GQ + c] = st.m;
+    cl[w * GQ + c] = st.l;
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = 4 * lg + i;
     if (r < GQ) {
 #pragma unroll
-      for (int nt = 0; nt < 8; ++nt) co[(w * GQ + r) * D + 8 * c + nt] = O[nt][i];
+      for (int nt = 0; nt < 8; ++nt) co[(w * GQ + r) * D + 8 * c + nt] = st.O[nt][i];
     }
   }
   wave_sync();
@@ -659,21 +961,21 @@ __global__ __launch_bounds__(kThreads, 2) void tqk_decode_split_mfma(DecodeArgs 
     const int r = 4 * lg + i;
     if (r >= GQ && r < NCOL) {
 #pragma unroll
-      for (int nt = 0; nt < 8; ++nt) co[(w * GQ + r - GQ) * D + 8 * c + nt] += O[nt][i];
+      for (int nt = 0; nt < 8; ++nt) co[(w * GQ + r - GQ) * D + 8 * c + nt] += st.O[nt][i];
     }
   }
   __syncthreads();
   const int ns = a.n_cold_splits + a.n_hot_splits;
-  for (int x = tid; x < GQ * D; x += kThreads) {
+  for (int x = tid; x < GQ * D; x += kMThreads) {
     const int i = x / D, j = x % D;
     float M = -INFINITY;
 #pragma unroll
-    for (int ww = 0; ww < 4; ++ww)
+    for (int ww = 0; ww < kMWaves; ++ww)
       if (cl[ww * GQ + i] > 0.f) M = fmaxf(M, cm[ww * GQ + i]);
     float den = 0.f, acc = 0.f;
     if (M > -INFINITY) {
 #pragma unroll
-      for (int ww = 0; ww < 4; ++ww) {
+      for (int ww = 0; ww < kMWaves; ++ww) {
         const float l = cl[ww * GQ + i];
         if (l > 0.f) {
           const float wt = __expf(cm[ww * GQ + i] - M);
@@ -727,6 +1029,11 @@ __global__ __launch_bounds__(TQK_D) void tqk_merge(MergeArgs a) {
   }
 }
 
+// The MFMA kernel needs tiled value codes and a hot ring of whole 32-token blocks.
+__host__ __device__ inline bool mfma_path(const tqk_cache_desc& d) {
+  return v_tiled(d.group_tokens, d.page_tokens) && (d.hot_ring % 32 == 0);
+}
+
 struct Plan {
   int n_cold_splits, n_hot_splits, groups_per_split, hot_per_split;
   size_t ws_bytes;
@@ -740,13 +1047,16 @@ Plan make_plan(const tqk_cache_desc* d, int batch, int max_len) {
   pl.hot_per_split = kThreads;
   pl.n_hot_splits = (hot_max + kThreads - 1) / kThreads;
   if (pl.n_hot_splits < 1) pl.n_hot_splits = 1;
+  if (mfma_path(*d)) pl.n_hot_splits = 1;  // one 8-wave workgroup walks the whole window
   const long units = (long)batch * d->n_kv_heads * (ngmax > 0 ? ngmax : 0);
   int gps;
-  if (v_tiled(G, d->page_tokens)) {
-    // MFMA kernel: four waves per workgroup, each a run of groups
-    int gpw = (int)((units + 4L * 1536 - 1) / (4L * 1536));
+  if (mfma_path(*d)) {
+    // MFMA kernel: eight waves per workgroup, one group per wave at a time;
+    // aim for about two workgroups per CU over the whole launch
+    int gpw = (int)((units + 8L * 512 - 1) / (8L * 512));
     if (gpw < 1) gpw = 1;
-    gps = 4 * gpw;
+    if (gpw > kMaxGPS / 8) gpw = kMaxGPS / 8;  // group metadata of a split lives in LDS
+    gps = 8 * gpw;
   } else {
     gps = (int)((units + 4095) / 4096);
     if (gps < 1) gps = 1;
@@ -761,30 +1071,17 @@ Plan make_plan(const tqk_cache_desc* d, int batch, int max_len) {
 
 template <int GQ>
 hipError_t launch_split(const DecodeArgs& a, dim3 grid, hipStream_t st) {
-  const bool tiled = v_tiled(a.d.group_tokens, a.d.page_tokens);
-  if (!tiled) {
+  if (!mfma_path(a.d)) {
     if (a.d.value_bits == 3)
       hipLaunchKernelGGL((tqk_decode_split_valu<GQ, 3>), grid, dim3(kThreads), 0, st, a);
     else
       hipLaunchKernelGGL((tqk_decode_split_valu<GQ, 4>), grid, dim3(kThreads), 0, st, a);
     return hipGetLastError();
   }
-  if (a.n_cold_splits > 0) {
-    const dim3 gc(a.n_cold_splits, grid.y, grid.z);
-    if (a.d.value_bits == 3)
-      hipLaunchKernelGGL((tqk_decode_split_mfma<GQ, 3>), gc, dim3(kThreads), 0, st, a);
-    else
-      hipLaunchKernelGGL((tqk_decode_split_mfma<GQ, 4>), gc, dim3(kThreads), 0, st, a);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-  }
-  DecodeArgs ah = a;
-  ah.split_base = a.n_cold_splits;
-  const dim3 gh(a.n_hot_splits, grid.y, grid.z);
   if (a.d.value_bits == 3)
-    hipLaunchKernelGGL((tqk_decode_split_valu<GQ, 3>), gh, dim3(kThreads), 0, st, ah);
+    hipLaunchKernelGGL((tqk_decode_split_mfma<GQ, 3>), grid, dim3(kMThreads), 0, st, a);
   else
-    hipLaunchKernelGGL((tqk_decode_split_valu<GQ, 4>), gh, dim3(kThreads), 0, st, ah);
+    hipLaunchKernelGGL((tqk_decode_split_mfma<GQ, 4>), grid, dim3(kMThreads), 0, st, a);
   return hipGetLastError();
 }
 

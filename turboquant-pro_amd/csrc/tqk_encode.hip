@@ -59,6 +59,9 @@ __global__ __launch_bounds__(kThreads) void tqk_encode_group(EncodeArgs a) {
   __shared__ float cent_s[D][17];            // per-channel grids (padded)
   __shared__ uint32_t thr_s[D];              // fp16 magnitude threshold per channel
   __shared__ int32_t wsum_s[4];
+  // packed key codes of the group, written out after the outlier pass has put
+  // the NF4 zero level (code 7) at every stored outlier position
+  __shared__ __align__(16) uint8_t kc_s[TQK_MAX_G][D / 2];
 
   // ---- stage the key tile ----------------------------------------------
   for (int idx = tid; idx < G * 16; idx += kThreads) {
@@ -126,8 +129,7 @@ __global__ __launch_bounds__(kThreads) void tqk_encode_group(EncodeArgs a) {
         if (e0 < d0 || (e0 != e0 && d0 == d0)) { d0 = e0; b0 = l; }
         if (e1 < d1 || (e1 != e1 && d1 == d1)) { d1 = e1; b1 = l; }
       }
-      const size_t row = page_row(a.p.block_table, d.max_pages_per_seq, b, g * G + s, P, Hkv, h);
-      a.p.kcodes[row * (D / 2) + jp] = (uint8_t)((rev4(b0) << 4) | rev4(b1));
+      kc_s[s][jp] = (uint8_t)((rev4(b0) << 4) | rev4(b1));
     }
   }
 
@@ -167,8 +169,14 @@ __global__ __launch_bounds__(kThreads) void tqk_encode_group(EncodeArgs a) {
         const uint16_t xv = kt_s[tid][j];
         const bool sel = all || (fabsf(h2f(xv)) >= fabsf(h2f((uint16_t)thr_s[j])));
         if (sel) {
-          if (off < d.outlier_cap)
+          if (off < d.outlier_cap) {
             a.p.oent[obase * d.outlier_cap + off] = (uint32_t)(tid * D + j) | ((uint32_t)xv << 16);
+            // the stored code becomes the zero level (rev4(7) = 14), so the dense
+            // part of a decode contributes only the mean here and the side-list
+            // adds val - mean; export restores the nearest-level code from val
+            uint8_t& kb = kc_s[tid][j >> 1];
+            kb = (j & 1) ? (uint8_t)((kb & 0xF0u) | 14u) : (uint8_t)((kb & 0x0Fu) | (14u << 4));
+          }
           ++off;
         }
       }
@@ -185,6 +193,13 @@ __global__ __launch_bounds__(kThreads) void tqk_encode_group(EncodeArgs a) {
   // re-assembled into 4-token x 8-channel units below
   uint8_t (*vc_s)[D] = reinterpret_cast<uint8_t (*)[D]>(&kt_s[0][0]);
   __syncthreads();
+  // key code rows, 16 bytes per thread
+  for (int idx = tid; idx < G * (D / 32); idx += kThreads) {
+    const int t = idx / (D / 32), ch = idx % (D / 32);
+    const size_t row = page_row(a.p.block_table, d.max_pages_per_seq, b, g * G + t, P, Hkv, h);
+    *reinterpret_cast<uint4*>(a.p.kcodes + row * (D / 2) + 16 * ch) =
+        *reinterpret_cast<const uint4*>(&kc_s[t][16 * ch]);
+  }
   if (tid < G) {
     const int t = g * G + tid;
     const uint4* src = reinterpret_cast<const uint4*>(token_src(a, a.p.hot_v, a.chunk_v, b, h, t));

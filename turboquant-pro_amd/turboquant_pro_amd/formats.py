@@ -1,8 +1,13 @@
 """Conversions between the HBM layout of the gfx950 cache and the reference's
 container byte layouts (host side, NumPy; used for export and inspection).
 
-* Key codes are stored exactly as the reference packs them
-  (turboquant_pro/per_channel_kv.py:87-93): 64 bytes per (token, head).
+* Key codes are stored as the reference packs them
+  (turboquant_pro/per_channel_kv.py:87-93), 64 bytes per (token, head), with
+  one difference: at every position held in the fp16 outlier side-list the
+  stored code is the NF4 zero level (7), so a decode's dense pass contributes
+  exactly the channel mean there and the side-list adds ``val - mean``.  The
+  reference's code at such a position is the nearest level to the stored fp16
+  value; :func:`restore_outlier_codes` puts it back on export.
 * Value codes are the reference's little-endian pack
   (turboquant_pro/core.py:350-398) when stored per token; with the MFMA-tiled
   order (page_tokens % 16 == 0 and group_tokens % 32 == 0) each 16-token tile
@@ -14,6 +19,57 @@ container byte layouts (host side, NumPy; used for export and inspection).
 from __future__ import annotations
 
 import numpy as np
+
+# NormalFloat-4 levels (turboquant_pro/per_channel_kv.py:64-84), as the fp32
+# constants the kernels use.
+NF4 = np.array([
+    -1.0, -0.6961928009986877, -0.5250730514526367, -0.39491748809814453,
+    -0.28444138169288635, -0.18477343022823334, -0.09105003625154495, 0.0,
+    0.07958029955625534, 0.16093020141124725, 0.24611230194568634,
+    0.33791524171829224, 0.44070982933044434, 0.5626170039176941,
+    0.7229568362236023, 1.0], dtype=np.float32)
+NF4_ZERO_CODE = 7
+
+
+def _rev4(c: np.ndarray) -> np.ndarray:
+    c = c.astype(np.uint8)
+    return (((c & 1) << 3) | ((c & 2) << 1) | ((c & 4) >> 1) | ((c & 8) >> 3)).astype(np.uint8)
+
+
+def nf4_codes(x: np.ndarray, scale: np.ndarray, mean: np.ndarray) -> np.ndarray:
+    """Nearest-level NF4 code of fp32 ``x`` given per-element ``scale``/``mean``,
+    in the reference's arithmetic (turboquant_pro/per_channel_kv.py:347-383):
+    centroid ``mean + scale * NF4[l]`` rounded to fp32 per operation, first
+    index of the smallest ``|x - centroid|`` (a NaN distance wins, as
+    ``np.argmin`` has it)."""
+    x = np.asarray(x, np.float32)[..., None]
+    cent = (np.asarray(mean, np.float32)[..., None] + np.asarray(scale, np.float32)[..., None] * NF4)
+    return np.argmin(np.abs(x - cent), axis=-1).astype(np.uint8)
+
+
+def restore_outlier_codes(kp: np.ndarray, idx: np.ndarray, val: np.ndarray,
+                          scale: np.ndarray, mean: np.ndarray) -> np.ndarray:
+    """Put the reference's key codes back at outlier positions.
+
+    ``kp`` (H, G, D/2) packed codes as stored; ``idx`` flat positions into
+    (H, G, D) and ``val`` their fp16 values; ``scale``/``mean`` (H, D)."""
+    kp = np.array(kp, dtype=np.uint8, copy=True)
+    H, G, half = kp.shape
+    D = 2 * half
+    if idx.size == 0:
+        return kp
+    idx = idx.astype(np.int64)
+    h, t, j = idx // (G * D), (idx // D) % G, idx % D
+    code = nf4_codes(val.astype(np.float32), scale[h, j], mean[h, j])
+    nib = _rev4(code)
+    # even channels in the high nibble, odd in the low one; one parity at a
+    # time so two outliers sharing a byte both land
+    for par in (0, 1):
+        m = (j % 2) == par
+        hh, tt, bb, nn = h[m], t[m], j[m] // 2, nib[m]
+        byte = kp[hh, tt, bb]
+        kp[hh, tt, bb] = ((byte & 0x0F) | (nn << 4)) if par == 0 else ((byte & 0xF0) | nn)
+    return kp
 
 
 def pack_values(codes: np.ndarray, bits: int) -> np.ndarray:

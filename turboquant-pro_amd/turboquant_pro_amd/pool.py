@@ -23,7 +23,7 @@ import math
 import numpy as np
 
 from . import _native as N
-from .formats import pack_values, untile_value_rows
+from .formats import pack_values, restore_outlier_codes, untile_value_rows
 from .codebooks import (group_tokens_for, n_groups_for, outliers_per_channel, random_rotation,
                         value_codebook)
 
@@ -257,7 +257,7 @@ class TQKVPool:
         ``(1, H, G, D)``), ``vpacked`` (CompressedKV.indices), ``vnorms`` ``(H, G)``."""
         phys, off = self._rows(b, g)
         H, G, D = self.n_kv_heads, self.group_tokens, self.head_dim
-        kp = self.kcodes[phys, :, off].permute(1, 0, 2).contiguous()   # (H, G, 64)
+        kp = self.kcodes[phys, :, off].permute(1, 0, 2).contiguous().cpu().numpy()  # (H, G, 64)
         vp = self.vcodes[phys, :, off].permute(1, 0, 2).contiguous().cpu().numpy()  # (H, G, vrow)
         if self.tiled:
             vp = np.stack([pack_values(untile_value_rows(vp[h], self.value_bits, D), self.value_bits)
@@ -271,12 +271,16 @@ class TQKVPool:
             e = ent[h, :min(int(cnt[h]), ent.shape[1])]
             idx.append((e & 0xFFFF).astype(np.int64) + h * G * D)
             val.append((e >> 16).astype(np.uint16))
+        oidx = np.concatenate(idx) if idx else np.zeros(0, np.int64)
+        oval = np.concatenate(val).view(np.float16) if val else np.zeros(0, np.float16)
+        scale, mean = self.gscale[slot].cpu().numpy(), self.gmean[slot].cpu().numpy()
+        kp = restore_outlier_codes(kp, oidx, oval, scale, mean)
         return {
-            "kpacked": kp.cpu().numpy().reshape(-1),
-            "nf4_scale": self.gscale[slot].cpu().numpy(),
-            "nf4_mean": self.gmean[slot].cpu().numpy(),
-            "outlier_idx": np.concatenate(idx).astype(np.int32) if idx else np.zeros(0, np.int32),
-            "outlier_val": np.concatenate(val).view(np.float16) if val else np.zeros(0, np.float16),
+            "kpacked": kp.reshape(-1),
+            "nf4_scale": scale,
+            "nf4_mean": mean,
+            "outlier_idx": oidx.astype(np.int32),
+            "outlier_val": oval,
             "outlier_count": cnt.astype(np.int64),
             "vpacked": np.ascontiguousarray(vp).reshape(-1),
             "vnorms": vn.cpu().numpy(),
