@@ -100,6 +100,24 @@ def build_pool(torch, cfg, seed, chunk=4096):
     return pool
 
 
+COPY_PROBE_BYTES = 256 << 20
+
+
+def measured_traffic(config):
+    """HBM bytes per launch of the split kernel on this workload, as measured by
+    the FETCH_SIZE / WRITE_SIZE counter passes summarised in
+    profiles/tqk_decode_split_mfma_<config>_traffic.md (each counter scaled by
+    its reading on a plain copy of known size); None when not measured."""
+    import re
+    path = os.path.join(ROOT, "profiles", f"tqk_decode_split_mfma_{config}_traffic.md")
+    try:
+        with open(path) as f:
+            m = re.search(r"traffic_bytes_per_launch\s*=\s*(\d+)", f.read())
+    except OSError:
+        return None
+    return int(m.group(1)) if m else None
+
+
 def cpu_baseline(cfg, budget_s=12.0):
     """The oracle's NumPy dequantize-then-attend (the reference CPU decode path)
     timed on this host on a bounded sample: whole-cache decode of single
@@ -148,6 +166,9 @@ def main():
     ap.add_argument("--config", default="headline", choices=sorted(CONFIGS))
     ap.add_argument("--replicas", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="after timing, copy a 256 MiB buffer 3 times (calibration kernel for "
+                         "the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; the decode shards by "
@@ -205,6 +226,15 @@ def main():
     achieved = nbytes / (split_ms * 1e-3) / 1e9
     step_gbs = nbytes / (ms_per_step * 1e-3) / 1e9
 
+    if args.copy_probe:
+        src = torch.empty(COPY_PROBE_BYTES // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": COPY_PROBE_BYTES, "copies": 3}), file=sys.stderr, flush=True)
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(cfg)
@@ -231,7 +261,8 @@ def main():
         "step_bytes": nbytes,
         "step_gbs": round(step_gbs, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(args.config),
                      "kernel": "tqk_decode_split_mfma", "kernel_us": round(split_ms * 1e3, 2)},
         "cpu_baseline": cpu,
     }
