@@ -352,6 +352,10 @@ union H8 {
 
 constexpr int kMThreads = 512;   // 8 waves
 constexpr int kMWaves = 8;
+#ifndef TQK_COLD_BUFFERS
+#define TQK_COLD_BUFFERS 3
+#endif
+constexpr int kColdBuf = TQK_COLD_BUFFERS;  // cold-stream register buffers (one more than blocks in flight)
 constexpr int kMaxGPS = 64;      // groups per cold split of the MFMA kernel (metadata in LDS)
 constexpr int kMetaInts = 32;    // per group: 16 tile rows, 8 outlier bounds, slot*Hkv+h
 constexpr int kLutEntry = 256;   // bytes per table entry
@@ -552,6 +556,10 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   // as fp16 hi (column h) / lo (column GQ + h), column-major, padded columns
   __shared__ __align__(16) uint8_t otb_s[kMWaves][128];
   __shared__ __align__(16) _Float16 ocb_s[kMWaves][2 * GQ][136];
+  // NF4 levels [0, 16) and value centroids [16, 16 + 2^vb), for the table fill
+  __shared__ float lvl_s[32];
+  if (tid < 16) lvl_s[tid] = kNF4[tid];
+  else if (tid < 16 + (1 << VB)) lvl_s[tid] = a.p.vcent[tid - 16];
   // Metadata of the split's groups, read once here so the block stream issues
   // nothing but block loads: [0, 16) first row of each 16-token tile,
   // [16, 24) cumulative outlier bounds, [24] slot * Hkv + h.
@@ -575,9 +583,13 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     }
   }
 
+  for (int i = tid; i < GQ * D; i += kMThreads)
+    qt_s[i % D][i / D] = h2f(a.q[((size_t)b * Hq + h * GQ + i / D) * D + i % D]);
+  __syncthreads();
   if (!hot) {
     // unit u (8 bytes): key part first (entry u / copies, copy u % copies), then values;
-    // consecutive lanes write consecutive units
+    // consecutive lanes write consecutive units; levels come from LDS, so the
+    // fill issues no memory loads
     using LG = LutGeom<VB>;
     constexpr int NC = LG::kCopies;
     constexpr int NV = 1 << (2 * VB);
@@ -586,18 +598,16 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       uint32_t off;
       if (u < 256 * NC) {
         const int e = u / NC;
-        val = split_pair(kNF4[rev4((uint32_t)e >> 4)], kNF4[rev4((uint32_t)e & 15u)]);
+        val = split_pair(lvl_s[rev4((uint32_t)e >> 4)], lvl_s[rev4((uint32_t)e & 15u)]);
         off = LG::kKeyBase + (uint32_t)e * kLutEntry + (uint32_t)(u % NC) * 8u;
       } else {
         const int v = u - 256 * NC, e = v / NC, m = (1 << VB) - 1;
-        val = split_pair(a.p.vcent[e & m], a.p.vcent[e >> VB]);
+        val = split_pair(lvl_s[16 + (e & m)], lvl_s[16 + (e >> VB)]);
         off = (uint32_t)e * kLutEntry + LG::kValOff + (uint32_t)(v % NC) * 8u;
       }
       *reinterpret_cast<uint2*>(lut + off) = val;
     }
   }
-  for (int i = tid; i < GQ * D; i += kMThreads)
-    qt_s[i % D][i / D] = h2f(a.q[((size_t)b * Hq + h * GQ + i / D) * D + i % D]);
   __syncthreads();
 
   const int hcol = c % GQ;
@@ -816,20 +826,27 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
               *reinterpret_cast<uint32_t*>(&ocb_s[w][GQ + hh][2 * lane]) =
                   pk_f16(x0 - lo_f16(hv), x1 - hi_f16(hv));
             }
+            // entries are token-sorted: those of tile A (tokens 0..15) come first
+            const int nA = (int)__popcll(__ballot(tbv[0] < 16u)) + (int)__popcll(__ballot(tbv[1] < 16u));
             wave_sync();
             for (int ch = 0; ch < (cnt + 31) / 32; ++ch) {
               const uint2 tb8 = *reinterpret_cast<const uint2*>(&otb_s[w][32 * ch + 8 * lg]);
-              H8 oa, obh, cbv;
-#pragma unroll
-              for (int e = 0; e < 8; ++e) {
-                const uint32_t t = ((e < 4 ? tb8.x : tb8.y) >> (8 * (e & 3))) & 0xFFu;
-                oa.h[e] = (t == (uint32_t)c) ? (_Float16)1.f : (_Float16)0.f;
-                obh.h[e] = (t == (uint32_t)(16 + c)) ? (_Float16)1.f : (_Float16)0.f;
-              }
+              H8 cbv;
               cbv.v = active ? *reinterpret_cast<const uint4*>(&ocb_s[w][c][32 * ch + 8 * lg])
                              : make_uint4(0u, 0u, 0u, 0u);
-              CA = __builtin_amdgcn_mfma_f32_16x16x32_f16(oa.h, cbv.h, CA, 0, 0, 0);
-              CB = __builtin_amdgcn_mfma_f32_16x16x32_f16(obh.h, cbv.h, CB, 0, 0, 0);
+              // one-hot of token row r over this lane's 8 entries, only for the
+              // tiles the chunk's entries touch
+              auto onehot = [&](uint32_t r) {
+                H8 o;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                  const uint32_t t = ((e < 4 ? tb8.x : tb8.y) >> (8 * (e & 3))) & 0xFFu;
+                  o.h[e] = (t == r) ? (_Float16)1.f : (_Float16)0.f;
+                }
+                return o;
+              };
+              if (32 * ch < nA) CA = __builtin_amdgcn_mfma_f32_16x16x32_f16(onehot((uint32_t)c).h, cbv.h, CA, 0, 0, 0);
+              if (32 * ch + 32 > nA) CB = __builtin_amdgcn_mfma_f32_16x16x32_f16(onehot((uint32_t)(16 + c)).h, cbv.h, CB, 0, 0, 0);
             }
             wave_sync();
           }
@@ -852,8 +869,8 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
 
 
 
-    // Two blocks in flight: step i issues the loads of block i + 2 and
-    // computes block i (buffers rotate A -> B -> C).
+    // A ring of kColdBuf buffers, kColdBuf - 1 blocks in flight: step i
+    // issues the loads of block i + kColdBuf - 1 and computes block i.
     int kbp = 0;  // block index of the computed block within its group
     auto step = [&](const ColdBlock<VB>& cur, ColdBlock<VB>& nxt) {
       if (kbp == 0) begin_group(cur);
@@ -862,15 +879,15 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       if (++kbp == nblk) kbp = 0;
     };
     if (T > 0) {
-      ColdBlock<VB> bA, bB, bC;
-      load_next(bA);
-      load_next(bB);
-      for (int i = 0; i < T; i += 3) {
-        step(bA, bC);
-        if (i + 1 >= T) break;
-        step(bB, bA);
-        if (i + 2 >= T) break;
-        step(bC, bB);
+      ColdBlock<VB> ring[kColdBuf];
+#pragma unroll
+      for (int s = 0; s < kColdBuf - 1; ++s) load_next(ring[s]);
+      for (int i = 0; i < T; i += kColdBuf) {
+#pragma unroll
+        for (int s = 0; s < kColdBuf; ++s) {
+          if (i + s >= T) break;
+          step(ring[s], ring[(s + kColdBuf - 1) % kColdBuf]);
+        }
       }
     }
   } else {
