@@ -724,133 +724,170 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       bias = colgroup_sum(biasp);
     };
 
-      auto qk_tile = [&](const uint4 kq) {
-        floatx4_t C = {0.f, 0.f, 0.f, 0.f};
+      // A operand of QK^T MFMA ks2 for key word kq: the LUT rows of two code
+      // bytes give [hi(ch0) hi(ch1) lo(ch0) lo(ch1)] x 2 (k-slots of the hi/lo split)
+      auto key_operand = [&](const uint4& kq, int ks2) {
+        const uint32_t word = (ks2 >> 1) == 0 ? kq.x : (ks2 >> 1) == 1 ? kq.y : (ks2 >> 1) == 2 ? kq.z : kq.w;
+        const uint32_t sb = 4u + 2u * (uint32_t)(ks2 & 1);
+        const uint2 t0 = *reinterpret_cast<const uint2*>(klut + __builtin_amdgcn_perm(word, koff, 0x0C0C0000u | (sb << 8)));
+        const uint2 t1 = *reinterpret_cast<const uint2*>(klut + __builtin_amdgcn_perm(word, koff, 0x0C0C0000u | ((sb + 1u) << 8)));
+        H8 av;
+        av.u[0] = t0.x;
+        av.u[1] = t0.y;
+        av.u[2] = t1.x;
+        av.u[3] = t1.y;
+        return av;
+      };
+      // both tiles' QK^T: every table read is issued before the first MFMA,
+      // so the LDS latency is paid once per block, not once per MFMA
+      auto qk_pair = [&](const uint4& ka, const uint4& kb, floatx4_t& CA, floatx4_t& CB) {
+        H8 oA[8], oB[8];
 #pragma unroll
         for (int ks2 = 0; ks2 < 8; ++ks2) {
-          const uint32_t word = (ks2 >> 1) == 0 ? kq.x : (ks2 >> 1) == 1 ? kq.y : (ks2 >> 1) == 2 ? kq.z : kq.w;
-          const uint32_t sb = 4u + 2u * (uint32_t)(ks2 & 1);
-          const uint2 t0 = *reinterpret_cast<const uint2*>(klut + __builtin_amdgcn_perm(word, koff, 0x0C0C0000u | (sb << 8)));
-          const uint2 t1 = *reinterpret_cast<const uint2*>(klut + __builtin_amdgcn_perm(word, koff, 0x0C0C0000u | ((sb + 1u) << 8)));
-          H8 av;
-          av.u[0] = t0.x;
-          av.u[1] = t0.y;
-          av.u[2] = t1.x;
-          av.u[3] = t1.y;
-          C = __builtin_amdgcn_mfma_f32_16x16x32_f16(av.h, Bw[ks2].h, C, 0, 0, 0);
+          oA[ks2] = key_operand(ka, ks2);
+          oB[ks2] = key_operand(kb, ks2);
         }
-        return C;
+        // keep the reads ahead of the MFMAs (GQ = 8 has no registers to spare)
+        if constexpr (GQ <= 4) __builtin_amdgcn_sched_barrier(0);
+        CA = floatx4_t{0.f, 0.f, 0.f, 0.f};
+        CB = floatx4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks2 = 0; ks2 < 8; ++ks2) {
+          CA = __builtin_amdgcn_mfma_f32_16x16x32_f16(oA[ks2].h, Bw[ks2].h, CA, 0, 0, 0);
+          CB = __builtin_amdgcn_mfma_f32_16x16x32_f16(oB[ks2].h, Bw[ks2].h, CB, 0, 0, 0);
+        }
       };
-      auto pv_tile = [&](const uint4& un, const H8& pa) {
+      // B operand of PV MFMA nt for value unit un: centroid pairs of fields 2nt, 2nt + 1
+      auto val_operand = [&](const uint4& un, int nt) {
+        uint32_t f0, f1;
+        if constexpr (VB == 3) {
+          switch (nt) {
+#define TQK_V3(NT) case NT: f0 = v3_field<2 * NT>(un); f1 = v3_field<2 * NT + 1>(un); break;
+            TQK_V3(0) TQK_V3(1) TQK_V3(2) TQK_V3(3) TQK_V3(4) TQK_V3(5) TQK_V3(6) TQK_V3(7)
+#undef TQK_V3
+          }
+        } else {
+          const uint32_t word = (nt >> 1) == 0 ? un.x : (nt >> 1) == 1 ? un.y : (nt >> 1) == 2 ? un.z : un.w;
+          f0 = (word >> (16 * (nt & 1))) & 0xFFu;
+          f1 = (word >> (16 * (nt & 1) + 8)) & 0xFFu;
+        }
+        const uint2 t0 = *reinterpret_cast<const uint2*>(lut + ((f0 << 8) | voff));
+        const uint2 t1 = *reinterpret_cast<const uint2*>(lut + ((f1 << 8) | voff));
+        H8 vb;
+        vb.u[0] = t0.x;
+        vb.u[1] = t0.y;
+        vb.u[2] = t1.x;
+        vb.u[3] = t1.y;
+        return vb;
+      };
+      auto pv_pair = [&](const uint4& uA, const uint4& uB, const H8& pA, const H8& pB) {
+        H8 vA[8], vB[8];
 #pragma unroll
         for (int nt = 0; nt < 8; ++nt) {
-          uint32_t f0, f1;
-          if constexpr (VB == 3) {
-            switch (nt) {
-#define TQK_V3(NT) case NT: f0 = v3_field<2 * NT>(un); f1 = v3_field<2 * NT + 1>(un); break;
-              TQK_V3(0) TQK_V3(1) TQK_V3(2) TQK_V3(3) TQK_V3(4) TQK_V3(5) TQK_V3(6) TQK_V3(7)
-#undef TQK_V3
+          vA[nt] = val_operand(uA, nt);
+          vB[nt] = val_operand(uB, nt);
+        }
+        if constexpr (GQ <= 4) __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) st.O[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pA.h, vA[nt].h, st.O[nt], 0, 0, 0);
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) st.O[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pB.h, vB[nt].h, st.O[nt], 0, 0, 0);
+      };
+
+      // ---- sparse outliers, folded into the QK^T accumulators:
+      //   C[t][col] += sum_e onehot[t][e] * x[e][col],
+      //   x[e][h] = q_h[j_e] * (val_e - mean_j) as fp16 hi (col h) / lo (col GQ + h)
+      // (the stored code of an outlier is the NF4 zero level, so the dense
+      // pass contributed exactly mean_j there, inside the bias).
+      // Stage: entries 2*lane, 2*lane + 1 of a chunk of <= 128 (token-sorted)
+      // -> token bytes in otb_s, x in ocb_s; returns how many belong to tile A.
+      auto stage_entries = [&](const uint2 ent, int cnt, int blk) {
+        float delta[2];
+        uint32_t tbv[2];
+        int jv[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const uint32_t en = u ? ent.y : ent.x;
+          const bool ok = 2 * lane + u < cnt;
+          const int pos = en & 0xFFFFu;
+          const int j = pos & (D - 1);
+          delta[u] = ok ? h2f((uint16_t)(en >> 16)) - am_s[w][j].y : 0.f;
+          tbv[u] = ok ? (uint32_t)((pos >> 7) - 32 * blk) : 255u;
+          jv[u] = j;
+        }
+        *reinterpret_cast<uint16_t*>(&otb_s[w][2 * lane]) = (uint16_t)(tbv[0] | (tbv[1] << 8));
+        float qv[2][GQ];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          if constexpr (GQ >= 4) {
+#pragma unroll
+            for (int hh = 0; hh < GQ; hh += 4) {
+              const float4 q4 = *reinterpret_cast<const float4*>(&qt_s[jv[u]][hh]);
+              qv[u][hh] = q4.x; qv[u][hh + 1] = q4.y; qv[u][hh + 2] = q4.z; qv[u][hh + 3] = q4.w;
             }
           } else {
-            const uint32_t word = (nt >> 1) == 0 ? un.x : (nt >> 1) == 1 ? un.y : (nt >> 1) == 2 ? un.z : un.w;
-            f0 = (word >> (16 * (nt & 1))) & 0xFFu;
-            f1 = (word >> (16 * (nt & 1) + 8)) & 0xFFu;
+#pragma unroll
+            for (int k2 = 0; k2 < GQ; ++k2) qv[u][k2] = qt_s[jv[u]][k2];
           }
-          const uint2 t0 = *reinterpret_cast<const uint2*>(lut + ((f0 << 8) | voff));
-          const uint2 t1 = *reinterpret_cast<const uint2*>(lut + ((f1 << 8) | voff));
-          H8 vb;
-          vb.u[0] = t0.x;
-          vb.u[1] = t0.y;
-          vb.u[2] = t1.x;
-          vb.u[3] = t1.y;
-          st.O[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa.h, vb.h, st.O[nt], 0, 0, 0);
+        }
+#pragma unroll
+        for (int hh = 0; hh < GQ; ++hh) {
+          const float x0 = qv[0][hh] * delta[0], x1 = qv[1][hh] * delta[1];
+          const uint32_t hv = pk_f16(x0, x1);
+          *reinterpret_cast<uint32_t*>(&ocb_s[w][hh][2 * lane]) = hv;
+          *reinterpret_cast<uint32_t*>(&ocb_s[w][GQ + hh][2 * lane]) = pk_f16(x0 - lo_f16(hv), x1 - hi_f16(hv));
+        }
+        // token-sorted: the entries of tile A (tokens 0..15) come first
+        return (int)__popcll(__ballot(tbv[0] < 16u)) + (int)__popcll(__ballot(tbv[1] < 16u));
+      };
+      // Apply a staged chunk: one-hot MFMAs, 32 entries each, only for the
+      // tiles a 32-entry slice touches.
+      auto apply_entries = [&](int cnt, int nA, floatx4_t& CA, floatx4_t& CB) {
+        for (int ch = 0; ch < (cnt + 31) / 32; ++ch) {
+          const uint2 tb8 = *reinterpret_cast<const uint2*>(&otb_s[w][32 * ch + 8 * lg]);
+          H8 cbv;
+          cbv.v = active ? *reinterpret_cast<const uint4*>(&ocb_s[w][c][32 * ch + 8 * lg])
+                         : make_uint4(0u, 0u, 0u, 0u);
+          auto onehot = [&](uint32_t r) {
+            H8 o;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const uint32_t t = ((e < 4 ? tb8.x : tb8.y) >> (8 * (e & 3))) & 0xFFu;
+              o.h[e] = (t == r) ? (_Float16)1.f : (_Float16)0.f;
+            }
+            return o;
+          };
+          if (32 * ch < nA) CA = __builtin_amdgcn_mfma_f32_16x16x32_f16(onehot((uint32_t)c).h, cbv.h, CA, 0, 0, 0);
+          if (32 * ch + 32 > nA) CB = __builtin_amdgcn_mfma_f32_16x16x32_f16(onehot((uint32_t)(16 + c)).h, cbv.h, CB, 0, 0, 0);
         }
       };
 
       auto process = [&](const ColdBlock<VB>& cur, int blk) {
-        const uint32_t* __restrict__ oent = oent_all + (size_t)cur.obase * cap;
-        floatx4_t CA = qk_tile(cur.kA);
-        floatx4_t CB = qk_tile(cur.kB);
-        // ---- sparse outliers of this block, folded into the QK^T accumulators:
-        //   C[t][col] += sum_e onehot[t][e] * contrib[e][col],
-        //   contrib[e][h] = q_h[j_e] * (val_e - dense_e) as hi (col h) / lo (col GQ+h)
         const int e0 = cur.e0, ne = cur.ne;
-        if (ne > 0) {
-          for (int base = 0; base < ne; base += 128) {
+        // first (usually only) outlier chunk: staged before the QK^T table
+        // reads, straight-line, so its LDS traffic overlaps the MFMAs
+        const int cnt0 = min(128, ne);
+        const int nA0 = stage_entries(cur.ent, cnt0, blk);
+        floatx4_t CA, CB;
+        qk_pair(cur.kA, cur.kB, CA, CB);
+        wave_sync();
+        apply_entries(cnt0, nA0, CA, CB);
+        if (ne > 128) {
+          // rare (> 128 entries in one block): read each further chunk and
+          // drain here, so the common path keeps exact wait counts
+          const uint32_t* __restrict__ oent = oent_all + (size_t)cur.obase * cap;
+          for (int base = 128; base < ne; base += 128) {
             const int cnt = min(128, ne - base);
-            // entries 2*lane and 2*lane + 1 of this chunk
-            uint2 ent = cur.ent;
-            if (base > 0) {
-              // rare (> 128 entries in one block): read the chunk and drain
-              // here, so the common path keeps exact wait counts
-              const int i0 = e0 + base + 2 * lane;
-              const uint32_t x0 = oent[min(i0, capm1)], x1 = oent[min(i0 + 1, capm1)];
-              __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-              ent = make_uint2((2 * lane < cnt) ? x0 : 0u, (2 * lane + 1 < cnt) ? x1 : 0u);
-            }
-            float delta[2];
-            uint32_t tbv[2];
-            int jv[2];
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-              const uint32_t en = u ? ent.y : ent.x;
-              const bool ok = 2 * lane + u < cnt;
-              const int pos = en & 0xFFFFu;
-              const int tb = ok ? (pos >> 7) - 32 * blk : 0;
-              const int j = pos & (D - 1);
-              // the stored code of an outlier is the zero level: dense part = mean
-              delta[u] = ok ? h2f((uint16_t)(en >> 16)) - am_s[w][j].y : 0.f;
-              tbv[u] = ok ? (uint32_t)tb : 255u;
-              jv[u] = j;
-            }
-            *reinterpret_cast<uint16_t*>(&otb_s[w][2 * lane]) = (uint16_t)(tbv[0] | (tbv[1] << 8));
-            float qv[2][GQ];
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-              if constexpr (GQ >= 4) {
-#pragma unroll
-                for (int hh = 0; hh < GQ; hh += 4) {
-                  const float4 q4 = *reinterpret_cast<const float4*>(&qt_s[jv[u]][hh]);
-                  qv[u][hh] = q4.x; qv[u][hh + 1] = q4.y; qv[u][hh + 2] = q4.z; qv[u][hh + 3] = q4.w;
-                }
-              } else {
-#pragma unroll
-                for (int k2 = 0; k2 < GQ; ++k2) qv[u][k2] = qt_s[jv[u]][k2];
-              }
-            }
-#pragma unroll
-            for (int hh = 0; hh < GQ; ++hh) {
-              const float x0 = qv[0][hh] * delta[0], x1 = qv[1][hh] * delta[1];
-              const uint32_t hv = pk_f16(x0, x1);
-              *reinterpret_cast<uint32_t*>(&ocb_s[w][hh][2 * lane]) = hv;
-              *reinterpret_cast<uint32_t*>(&ocb_s[w][GQ + hh][2 * lane]) =
-                  pk_f16(x0 - lo_f16(hv), x1 - hi_f16(hv));
-            }
-            // entries are token-sorted: those of tile A (tokens 0..15) come first
-            const int nA = (int)__popcll(__ballot(tbv[0] < 16u)) + (int)__popcll(__ballot(tbv[1] < 16u));
+            const int i0 = e0 + base + 2 * lane;
+            const uint32_t x0 = oent[min(i0, capm1)], x1 = oent[min(i0 + 1, capm1)];
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
             wave_sync();
-            for (int ch = 0; ch < (cnt + 31) / 32; ++ch) {
-              const uint2 tb8 = *reinterpret_cast<const uint2*>(&otb_s[w][32 * ch + 8 * lg]);
-              H8 cbv;
-              cbv.v = active ? *reinterpret_cast<const uint4*>(&ocb_s[w][c][32 * ch + 8 * lg])
-                             : make_uint4(0u, 0u, 0u, 0u);
-              // one-hot of token row r over this lane's 8 entries, only for the
-              // tiles the chunk's entries touch
-              auto onehot = [&](uint32_t r) {
-                H8 o;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                  const uint32_t t = ((e < 4 ? tb8.x : tb8.y) >> (8 * (e & 3))) & 0xFFu;
-                  o.h[e] = (t == r) ? (_Float16)1.f : (_Float16)0.f;
-                }
-                return o;
-              };
-              if (32 * ch < nA) CA = __builtin_amdgcn_mfma_f32_16x16x32_f16(onehot((uint32_t)c).h, cbv.h, CA, 0, 0, 0);
-              if (32 * ch + 32 > nA) CB = __builtin_amdgcn_mfma_f32_16x16x32_f16(onehot((uint32_t)(16 + c)).h, cbv.h, CB, 0, 0, 0);
-            }
+            const int nA = stage_entries(make_uint2(x0, x1), cnt, blk);
             wave_sync();
+            apply_entries(cnt, nA, CA, CB);
           }
         }
+        wave_sync();
         float sc[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -863,8 +900,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
                                  p[2] * row_bcast<2>(cur.nv), p[3] * row_bcast<3>(cur.nv), active, is_hi);
         const H8 paB = p_operand(p[4] * row_bcast<4>(cur.nv), p[5] * row_bcast<5>(cur.nv),
                                  p[6] * row_bcast<6>(cur.nv), p[7] * row_bcast<7>(cur.nv), active, is_hi);
-        pv_tile(cur.uA, paA);
-        pv_tile(cur.uB, paB);
+        pv_pair(cur.uA, cur.uB, paA, paB);
       };
 
 
