@@ -16,9 +16,11 @@
  *   - fp16 data is passed as uint16_t bit patterns (IEEE binary16).
  *
  * Storage layout in HBM (one cache pool = one attention layer):
- *   kcodes [num_pages][n_kv_heads][page_tokens][head_dim/2]   u8   (storage of record)
- *   vcodes [num_pages][n_kv_heads][page_tokens][head_dim*vb/8] u8  (storage of record, see below)
- *   vnorm  [num_pages][n_kv_heads][page_tokens]               f32
+ *   kcodes [n_kv_heads][n_pages][page_tokens][head_dim/2]     u8   (storage of record)
+ *   vcodes [n_kv_heads][n_pages][page_tokens][head_dim*vb/8]  u8   (storage of record, see below)
+ *   vnorm  [n_kv_heads][n_pages][page_tokens]                 f32
+ *   (head-major: a head's pages are one contiguous region, so consecutive
+ *   physical pages of a head are adjacent in memory)
  *   gscale [num_gslots][n_kv_heads][head_dim]                 f32  (nf4_scale)
  *   gmean  [num_gslots][n_kv_heads][head_dim]                 f32  (nf4_mean)
  *   ocount [num_gslots][n_kv_heads][8]  i32 cumulative outlier counts at tokens 32,64,..,256 (last = total)
@@ -70,6 +72,7 @@ typedef struct tqk_cache_desc {
   int32_t max_pages_per_seq;    /* block_table row stride */
   int32_t max_groups_per_seq;   /* group_table row stride */
   int32_t hot_ring;             /* ring capacity in tokens, >= W */
+  int32_t n_pages;              /* physical pages in the pool (block_table entries index them) */
   float sm_scale;               /* softmax scale, 1/sqrt(D) */
 } tqk_cache_desc;
 
@@ -91,7 +94,7 @@ typedef struct tqk_cache_ptrs {
   const float* vbnd;    /* 2^vb - 1 fp32 value boundaries */
 } tqk_cache_ptrs;
 
-/* Library ABI version (bumped on any signature or layout change). */
+/* Library ABI version (bumped on any signature or layout change); this header is version 2. */
 int tqk_version(void);
 
 /* Validate a descriptor; TQK_OK when the GPU path supports it. */

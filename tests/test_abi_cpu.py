@@ -36,7 +36,7 @@ def test_library_exports_every_symbol():
 def _desc(N, **kw):
     base = dict(n_kv_heads=8, n_q_heads=32, head_dim=128, hot_window=512, group_tokens=256,
                 page_tokens=256, key_bits=4, value_bits=3, outliers_per_channel=5,
-                outlier_cap=2560, max_pages_per_seq=126, max_groups_per_seq=126, hot_ring=512,
+                outlier_cap=2560, max_pages_per_seq=126, max_groups_per_seq=126, hot_ring=512, n_pages=2016,
                 sm_scale=1 / 128 ** 0.5)
     base.update(kw)
     return N.CacheDesc(**base)
@@ -53,6 +53,7 @@ def test_check_desc_status_codes():
     assert lib.tqk_check_desc(ctypes.byref(_desc(N, page_tokens=24))) == N.TQK_EINVAL
     assert lib.tqk_check_desc(ctypes.byref(_desc(N, hot_window=1023, group_tokens=512))) == \
         N.TQK_EUNSUPPORTED
+    assert lib.tqk_check_desc(ctypes.byref(_desc(N, n_pages=0))) == N.TQK_EINVAL
     assert lib.tqk_check_desc(None) == N.TQK_EINVAL
 
 

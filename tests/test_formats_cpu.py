@@ -76,3 +76,23 @@ def test_restore_outlier_codes_matches_reference_codes(golden_dir):
 def test_nf4_zero_code_is_exact_zero():
     assert F.NF4[F.NF4_ZERO_CODE] == 0.0
     assert np.array_equal(F.NF4, O.NF4.astype(np.float32))
+
+
+def test_clustered_block_table_is_a_permutation_with_adjacent_blocks():
+    """Default table for 32-token pages: a bijection onto each sequence's page
+    range in which block k of the 8 groups of a cluster occupy 8 adjacent pages."""
+    from turboquant_pro_amd.pool import TQKVPool
+    B, G = 3, 256
+    nb = G // 32
+    max_pages = 127 * nb
+    max_pages = -(-max_pages // (8 * nb)) * (8 * nb)
+    bt = TQKVPool._clustered_table(B, max_pages, 32, G)
+    for b in range(B):
+        row = bt[b]
+        assert sorted(row.tolist()) == list(range(b * max_pages, (b + 1) * max_pages))
+        for c in range(max_pages // (8 * nb)):
+            for k in range(nb):
+                pages = [row[(8 * c + w) * nb + k] for w in range(8)]
+                assert pages == list(range(pages[0], pages[0] + 8))
+    ident = TQKVPool._clustered_table(2, 10, 16, 256)
+    assert np.array_equal(ident.reshape(-1), np.arange(20))

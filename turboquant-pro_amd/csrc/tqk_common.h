@@ -61,9 +61,10 @@ __host__ __device__ __forceinline__ int n_groups_of(int len, int hot_window, int
 // Row index of token t (absolute position in its sequence) for kv head h in
 // the page pool.
 __device__ __forceinline__ size_t page_row(const int32_t* __restrict__ block_table, int max_pages,
-                                           int b, int t, int P, int Hkv, int h) {
+                                           int b, int t, int P, int n_pages, int h) {
+  // head-major pages: row of token t of sequence b in head h's region
   const int phys = block_table[(size_t)b * max_pages + t / P];
-  return ((size_t)phys * Hkv + h) * P + (t % P);
+  return ((size_t)h * n_pages + phys) * P + (t % P);
 }
 
 template <typename T>

@@ -176,7 +176,7 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
       // dense key scores: one token per thread
       float norm_t = 0.f;
       if (tid < G) {
-        const size_t row = page_row(bt, d.max_pages_per_seq, b, g * G + tid, P, Hkv, h);
+        const size_t row = page_row(bt, d.max_pages_per_seq, b, g * G + tid, P, d.n_pages, h);
         const uint4* kr = reinterpret_cast<const uint4*>(a.p.kcodes + row * (D / 2));
         float s[GQ];
 #pragma unroll
@@ -211,7 +211,7 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
         const int pos = ent & 0xFFFFu;
         const float val = h2f((uint16_t)(ent >> 16));
         const int tt = pos >> 7, j = pos & (D - 1);
-        const size_t row = page_row(bt, d.max_pages_per_seq, b, g * G + tt, P, Hkv, h);
+        const size_t row = page_row(bt, d.max_pages_per_seq, b, g * G + tt, P, d.n_pages, h);
         const uint32_t byte = a.p.kcodes[row * (D / 2) + (j >> 1)];
         const uint32_t c = (j & 1) ? rev4(byte & 15u) : rev4(byte >> 4);
         const float delta = val - (a_s[j] * kNF4[c] + mu_s[j]);
@@ -225,7 +225,7 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
       // value accumulation in rotated code space: thread = (channel pair, token quarter)
       const int tend = min(G, tq * 64 + 64);
       for (int tt = tq * 64; tt < tend; ++tt) {
-        const size_t row = page_row(bt, d.max_pages_per_seq, b, g * G + tt, P, Hkv, h);
+        const size_t row = page_row(bt, d.max_pages_per_seq, b, g * G + tt, P, d.n_pages, h);
         uint32_t f;
         if (VB == 3) {
           const uint32_t* vr = reinterpret_cast<const uint32_t*>(a.p.vcodes + row * VROW);
@@ -454,7 +454,6 @@ struct ColdBlock {
   uint2 ent;       // outlier entries 2*lane, 2*lane + 1 of the block
   int e0, ne;      // the block's outliers are entries [e0, e0 + ne) of its group
   uint32_t obase;  // slot * Hkv + h of the block's group
-  float2 av, mv;   // (nf4_scale, nf4_mean) of channels 2*lane, 2*lane + 1 of the group
 };
 
 // Per-wave online-softmax state for query head (c % GQ) and the PV accumulators.
@@ -534,6 +533,27 @@ __device__ __forceinline__ H8 p_operand(float x0, float x1, float x2, float x3, 
   return r;
 }
 
+// P operand of the PV MFMAs for this lane's eight weights (tile A tokens
+// 4lg..4lg+3, then tile B tokens 16+4lg..): fp16 hi (rows < GQ), fp16 lo
+// (rows GQ..2GQ-1) or zero (other rows).
+__device__ __forceinline__ H8 p_weights(float x0, float x1, float x2, float x3, float x4, float x5,
+                                        float x6, float x7, bool active, bool is_hi) {
+  const uint32_t h01 = pk_f16(x0, x1), h23 = pk_f16(x2, x3), h45 = pk_f16(x4, x5), h67 = pk_f16(x6, x7);
+  H8 r;
+  if (is_hi) {
+    r.u[0] = h01; r.u[1] = h23; r.u[2] = h45; r.u[3] = h67;
+  } else {
+    r.u[0] = pk_f16(x0 - lo_f16(h01), x1 - hi_f16(h01));
+    r.u[1] = pk_f16(x2 - lo_f16(h23), x3 - hi_f16(h23));
+    r.u[2] = pk_f16(x4 - lo_f16(h45), x5 - hi_f16(h45));
+    r.u[3] = pk_f16(x6 - lo_f16(h67), x7 - hi_f16(h67));
+  }
+  const uint32_t keep = active ? 0xFFFFFFFFu : 0u;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) r.u[k] &= keep;
+  return r;
+}
+
 template <int GQ, int VB>
 __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs a) {
   constexpr int D = TQK_D;
@@ -551,11 +571,16 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
 
   __shared__ __align__(16) uint8_t lut[LutGeom<VB>::kBytes];
   __shared__ __align__(16) float qt_s[D][GQ];           // q transposed: [channel][head]
-  __shared__ __align__(16) float2 am_s[kMWaves][D];     // (nf4_scale, nf4_mean) of the wave's group
+  __shared__ __align__(16) float q_h_s[GQ][D];           // q, head-major
+  // (nf4_scale[128], nf4_mean[128]) of a wave's current and next group
+  __shared__ __align__(16) float gsm_s[kMWaves][2][2 * D];
   // outlier correction operands: entry token (255 = none) and q_h * (val - dense)
   // as fp16 hi (column h) / lo (column GQ + h), column-major, padded columns
-  __shared__ __align__(16) uint8_t otb_s[kMWaves][128];
-  __shared__ __align__(16) _Float16 ocb_s[kMWaves][2 * GQ][136];
+  // (two of each when the staging of the next block is skewed one step ahead)
+  constexpr bool kSkew = GQ <= 4;
+  constexpr int kOB = kSkew ? 2 : 1;
+  __shared__ __align__(16) uint8_t otb_s[kOB][kMWaves][128];
+  __shared__ __align__(16) _Float16 ocb_s[kOB][kMWaves][2 * GQ][136];
   // NF4 levels [0, 16) and value centroids [16, 16 + 2^vb), for the table fill
   __shared__ float lvl_s[32];
   if (tid < 16) lvl_s[tid] = kNF4[tid];
@@ -573,7 +598,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       const uint32_t obase = (uint32_t)slot * (uint32_t)Hkv + (uint32_t)h;
       int v = 0;
       if (f < 16) {
-        if (f < G / 16) v = (int)page_row(a.p.block_table, d.max_pages_per_seq, b, g * G + 16 * f, P, Hkv, h);
+        if (f < G / 16) v = (int)page_row(a.p.block_table, d.max_pages_per_seq, b, g * G + 16 * f, P, d.n_pages, h);
       } else if (f < 16 + TQK_NOB) {
         v = min(a.p.ocount[(size_t)obase * TQK_NOB + (f - 16)], d.outlier_cap);
       } else if (f == 16 + TQK_NOB) {
@@ -583,8 +608,11 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     }
   }
 
-  for (int i = tid; i < GQ * D; i += kMThreads)
-    qt_s[i % D][i / D] = h2f(a.q[((size_t)b * Hq + h * GQ + i / D) * D + i % D]);
+  for (int i = tid; i < GQ * D; i += kMThreads) {
+    const float qv = h2f(a.q[((size_t)b * Hq + h * GQ + i / D) * D + i % D]);
+    qt_s[i % D][i / D] = qv;
+    q_h_s[i / D][i % D] = qv;
+  }
   __syncthreads();
   if (!hot) {
     // unit u (8 bytes): key part first (entry u / copies, copy u % copies), then values;
@@ -676,10 +704,6 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       cb.e0 = e0;
       cb.ne = e1 - e0;
       cb.obase = obase;
-      // the group's (scale, mean) travel with every block, so the start of a
-      // group waits on nothing newer than the block itself
-      cb.av = reinterpret_cast<const float2*>(a.p.gscale + (size_t)obase * D)[lane];
-      cb.mv = reinterpret_cast<const float2*>(a.p.gmean + (size_t)obase * D)[lane];
       if (nl + 1 < T) {
         ++nl;
         if (++kbl == nblk) {
@@ -689,76 +713,92 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       }
     };
 
-    H8 Bw[8];
+    // (nf4_scale, nf4_mean) of channels 2*lane, 2*lane + 1 of a wave group,
+    // staged through registers into LDS slot (group & 1): every step loads
+    // the stats of the group of the block it prefetches (before the block
+    // loads, unconditionally, so the loads are never sunk to their use) and
+    // the next step writes them, a step before that group can start.
+    float2 pend_s, pend_m;  // stats loaded by the previous step
+    int pend_slot = 0;
+    auto load_group_stats = [&](int j) {
+      const size_t mbase = (size_t)(uint32_t)meta(max(0, min(j, nw - 1)), 16 + TQK_NOB) * D;
+      pend_s = reinterpret_cast<const float2*>(a.p.gscale + mbase)[lane];
+      pend_m = reinterpret_cast<const float2*>(a.p.gmean + mbase)[lane];
+      pend_slot = j & 1;
+    };
+    auto store_group_stats = [&]() {
+      *reinterpret_cast<float2*>(&gsm_s[w][pend_slot][2 * lane]) = pend_s;
+      *reinterpret_cast<float2*>(&gsm_s[w][pend_slot][D + 2 * lane]) = pend_m;
+    };
+    // QK^T weight operand: MFMA m covers channels 32lg + 8m + i (i < 8) of lane
+    // group lg; column c holds q * nf4_scale of head c % GQ as fp16 hi
+    // (c < GQ) or lo (GQ <= c < 2GQ), zero in other columns.  The key operand
+    // is the hi (first MFMA) or lo (second) fp16 part of the NF4 levels, so
+    // the pair of columns summed gives the fp32 product.
+    H8 Bw[4];
     float bias = 0.f;
-    // start of a group: (scale, mean) to LDS for the outlier pass, then the
-    // QK^T weight operand and the mean bias
-    auto begin_group = [&](const ColdBlock<VB>& cur) {
-      am_s[w][2 * lane] = make_float2(cur.av.x, cur.mv.x);
-      am_s[w][2 * lane + 1] = make_float2(cur.av.y, cur.mv.y);
-      wave_sync();
-      // B operand of QK^T for MFMA ks2 (channels ch_i = 32lg + 4ks2 + i): the
-      // key operand holds [hi(ch0) hi(ch1) lo(ch0) lo(ch1) hi(ch2) hi(ch3) lo(ch2) lo(ch3)],
-      // so the weights go [W0 W1 W0 W1 W2 W3 W2 W3]; column c is q*scale of head c % GQ
-      // as fp16 hi (c < GQ) or lo (GQ <= c < 2GQ)
+    // Start of wave group j: weights and mean bias from slot j & 1.
+    auto begin_group = [&](int j) {
+      const float* gs = &gsm_s[w][j & 1][0];
+      const uint32_t keep = active ? 0xFFFFFFFFu : 0u;
       float biasp = 0.f;
 #pragma unroll
-      for (int ks2 = 0; ks2 < 8; ++ks2) {
-        uint32_t wpk[2];
+      for (int m = 0; m < 4; ++m) {
 #pragma unroll
-        for (int hp = 0; hp < 2; ++hp) {
-          const int ch = 32 * lg + 4 * ks2 + 2 * hp;
-          const float q0 = qt_s[ch][hcol], q1 = qt_s[ch + 1][hcol];
-          const float2 am0 = am_s[w][ch], am1 = am_s[w][ch + 1];
-          const float w0 = q0 * am0.x, w1 = q1 * am1.x;
-          biasp += q0 * am0.y + q1 * am1.y;
-          const uint32_t hv = pk_f16(w0, w1);
-          const uint32_t lv = pk_f16(w0 - lo_f16(hv), w1 - hi_f16(hv));
-          wpk[hp] = active ? (is_hi ? hv : lv) : 0u;
+        for (int hq = 0; hq < 2; ++hq) {
+          const int ch = 32 * lg + 8 * m + 4 * hq;
+          const float4 q4 = *reinterpret_cast<const float4*>(&q_h_s[hcol][ch]);
+          const float4 s4 = *reinterpret_cast<const float4*>(&gs[ch]);
+          const float4 m4 = *reinterpret_cast<const float4*>(&gs[D + ch]);
+          biasp += q4.x * m4.x + q4.y * m4.y + q4.z * m4.z + q4.w * m4.w;
+          const float w0 = q4.x * s4.x, w1 = q4.y * s4.y, w2 = q4.z * s4.z, w3 = q4.w * s4.w;
+          const uint32_t h01 = pk_f16(w0, w1), h23 = pk_f16(w2, w3);
+          const uint32_t l01 = pk_f16(w0 - lo_f16(h01), w1 - hi_f16(h01));
+          const uint32_t l23 = pk_f16(w2 - lo_f16(h23), w3 - hi_f16(h23));
+          Bw[m].u[2 * hq] = (is_hi ? h01 : l01) & keep;
+          Bw[m].u[2 * hq + 1] = (is_hi ? h23 : l23) & keep;
         }
-        Bw[ks2].u[0] = wpk[0];
-        Bw[ks2].u[1] = wpk[0];
-        Bw[ks2].u[2] = wpk[1];
-        Bw[ks2].u[3] = wpk[1];
       }
       bias = colgroup_sum(biasp);
     };
 
-      // A operand of QK^T MFMA ks2 for key word kq: the LUT rows of two code
-      // bytes give [hi(ch0) hi(ch1) lo(ch0) lo(ch1)] x 2 (k-slots of the hi/lo split)
-      auto key_operand = [&](const uint4& kq, int ks2) {
-        const uint32_t word = (ks2 >> 1) == 0 ? kq.x : (ks2 >> 1) == 1 ? kq.y : (ks2 >> 1) == 2 ? kq.z : kq.w;
-        const uint32_t sb = 4u + 2u * (uint32_t)(ks2 & 1);
-        const uint2 t0 = *reinterpret_cast<const uint2*>(klut + __builtin_amdgcn_perm(word, koff, 0x0C0C0000u | (sb << 8)));
-        const uint2 t1 = *reinterpret_cast<const uint2*>(klut + __builtin_amdgcn_perm(word, koff, 0x0C0C0000u | ((sb + 1u) << 8)));
-        H8 av;
-        av.u[0] = t0.x;
-        av.u[1] = t0.y;
-        av.u[2] = t1.x;
-        av.u[3] = t1.y;
-        return av;
+      // Key operands of QK^T MFMA m for key word kq (bytes 4m..4m+3 of the lane's
+      // 16: channels 32lg + 8m + 2q, +1 for byte q): the table row of a code byte
+      // is (fp16 hi pair, fp16 lo pair), so four reads give the hi operand and
+      // the lo operand of the two MFMAs.
+      auto key_operands = [&](uint32_t word, H8& hi, H8& lo) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint2 t = *reinterpret_cast<const uint2*>(
+              klut + __builtin_amdgcn_perm(word, koff, 0x0C0C0000u | ((4u + (uint32_t)q) << 8)));
+          hi.u[q] = t.x;
+          lo.u[q] = t.y;
+        }
       };
       // both tiles' QK^T: every table read is issued before the first MFMA,
       // so the LDS latency is paid once per block, not once per MFMA
       auto qk_pair = [&](const uint4& ka, const uint4& kb, floatx4_t& CA, floatx4_t& CB) {
-        H8 oA[8], oB[8];
+        H8 hA[4], lA[4], hB[4], lB[4];
 #pragma unroll
-        for (int ks2 = 0; ks2 < 8; ++ks2) {
-          oA[ks2] = key_operand(ka, ks2);
-          oB[ks2] = key_operand(kb, ks2);
+        for (int m = 0; m < 4; ++m) {
+          key_operands(m == 0 ? ka.x : m == 1 ? ka.y : m == 2 ? ka.z : ka.w, hA[m], lA[m]);
+          key_operands(m == 0 ? kb.x : m == 1 ? kb.y : m == 2 ? kb.z : kb.w, hB[m], lB[m]);
         }
         // keep the reads ahead of the MFMAs (GQ = 8 has no registers to spare)
         if constexpr (GQ <= 4) __builtin_amdgcn_sched_barrier(0);
         CA = floatx4_t{0.f, 0.f, 0.f, 0.f};
         CB = floatx4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks2 = 0; ks2 < 8; ++ks2) {
-          CA = __builtin_amdgcn_mfma_f32_16x16x32_f16(oA[ks2].h, Bw[ks2].h, CA, 0, 0, 0);
-          CB = __builtin_amdgcn_mfma_f32_16x16x32_f16(oB[ks2].h, Bw[ks2].h, CB, 0, 0, 0);
+        for (int m = 0; m < 4; ++m) {
+          CA = __builtin_amdgcn_mfma_f32_16x16x32_f16(hA[m].h, Bw[m].h, CA, 0, 0, 0);
+          CB = __builtin_amdgcn_mfma_f32_16x16x32_f16(hB[m].h, Bw[m].h, CB, 0, 0, 0);
+          CA = __builtin_amdgcn_mfma_f32_16x16x32_f16(lA[m].h, Bw[m].h, CA, 0, 0, 0);
+          CB = __builtin_amdgcn_mfma_f32_16x16x32_f16(lB[m].h, Bw[m].h, CB, 0, 0, 0);
         }
       };
-      // B operand of PV MFMA nt for value unit un: centroid pairs of fields 2nt, 2nt + 1
-      auto val_operand = [&](const uint4& un, int nt) {
+      // Table rows of value unit un for channel nt: fields 2nt (tokens 0, 1 of the
+      // unit) and 2nt + 1 (tokens 2, 3), each (fp16 hi pair, fp16 lo pair)
+      auto val_rows = [&](const uint4& un, int nt, uint2& r0, uint2& r1) {
         uint32_t f0, f1;
         if constexpr (VB == 3) {
           switch (nt) {
@@ -771,27 +811,27 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
           f0 = (word >> (16 * (nt & 1))) & 0xFFu;
           f1 = (word >> (16 * (nt & 1) + 8)) & 0xFFu;
         }
-        const uint2 t0 = *reinterpret_cast<const uint2*>(lut + ((f0 << 8) | voff));
-        const uint2 t1 = *reinterpret_cast<const uint2*>(lut + ((f1 << 8) | voff));
-        H8 vb;
-        vb.u[0] = t0.x;
-        vb.u[1] = t0.y;
-        vb.u[2] = t1.x;
-        vb.u[3] = t1.y;
-        return vb;
+        r0 = *reinterpret_cast<const uint2*>(lut + ((f0 << 8) | voff));
+        r1 = *reinterpret_cast<const uint2*>(lut + ((f1 << 8) | voff));
       };
-      auto pv_pair = [&](const uint4& uA, const uint4& uB, const H8& pA, const H8& pB) {
-        H8 vA[8], vB[8];
+      // PV for both tiles: MFMA (nt, hi/lo) has k-slots 8lg + i = tile A tokens
+      // 4lg..4lg+3 then tile B tokens 16+4lg.., column c = channel 8c + nt; the
+      // P operand holds the lane's eight weights (rows: heads, fp16 hi or lo)
+      auto pv_pair = [&](const uint4& uA, const uint4& uB, const H8& pw) {
+        H8 vh[8], vl[8];
 #pragma unroll
         for (int nt = 0; nt < 8; ++nt) {
-          vA[nt] = val_operand(uA, nt);
-          vB[nt] = val_operand(uB, nt);
+          uint2 a0, a1, b0, b1;
+          val_rows(uA, nt, a0, a1);
+          val_rows(uB, nt, b0, b1);
+          vh[nt].u[0] = a0.x; vh[nt].u[1] = a1.x; vh[nt].u[2] = b0.x; vh[nt].u[3] = b1.x;
+          vl[nt].u[0] = a0.y; vl[nt].u[1] = a1.y; vl[nt].u[2] = b0.y; vl[nt].u[3] = b1.y;
         }
         if constexpr (GQ <= 4) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int nt = 0; nt < 8; ++nt) st.O[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pA.h, vA[nt].h, st.O[nt], 0, 0, 0);
+        for (int nt = 0; nt < 8; ++nt) st.O[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pw.h, vh[nt].h, st.O[nt], 0, 0, 0);
 #pragma unroll
-        for (int nt = 0; nt < 8; ++nt) st.O[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pB.h, vB[nt].h, st.O[nt], 0, 0, 0);
+        for (int nt = 0; nt < 8; ++nt) st.O[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pw.h, vl[nt].h, st.O[nt], 0, 0, 0);
       };
 
       // ---- sparse outliers, folded into the QK^T accumulators:
@@ -801,7 +841,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       // pass contributed exactly mean_j there, inside the bias).
       // Stage: entries 2*lane, 2*lane + 1 of a chunk of <= 128 (token-sorted)
       // -> token bytes in otb_s, x in ocb_s; returns how many belong to tile A.
-      auto stage_entries = [&](const uint2 ent, int cnt, int blk) {
+      auto stage_entries = [&](const uint2 ent, int cnt, int blk, int buf, int gslot) {
         float delta[2];
         uint32_t tbv[2];
         int jv[2];
@@ -811,11 +851,11 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
           const bool ok = 2 * lane + u < cnt;
           const int pos = en & 0xFFFFu;
           const int j = pos & (D - 1);
-          delta[u] = ok ? h2f((uint16_t)(en >> 16)) - am_s[w][j].y : 0.f;
+          delta[u] = ok ? h2f((uint16_t)(en >> 16)) - gsm_s[w][gslot][D + j] : 0.f;
           tbv[u] = ok ? (uint32_t)((pos >> 7) - 32 * blk) : 255u;
           jv[u] = j;
         }
-        *reinterpret_cast<uint16_t*>(&otb_s[w][2 * lane]) = (uint16_t)(tbv[0] | (tbv[1] << 8));
+        *reinterpret_cast<uint16_t*>(&otb_s[buf][w][2 * lane]) = (uint16_t)(tbv[0] | (tbv[1] << 8));
         float qv[2][GQ];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
@@ -834,19 +874,19 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         for (int hh = 0; hh < GQ; ++hh) {
           const float x0 = qv[0][hh] * delta[0], x1 = qv[1][hh] * delta[1];
           const uint32_t hv = pk_f16(x0, x1);
-          *reinterpret_cast<uint32_t*>(&ocb_s[w][hh][2 * lane]) = hv;
-          *reinterpret_cast<uint32_t*>(&ocb_s[w][GQ + hh][2 * lane]) = pk_f16(x0 - lo_f16(hv), x1 - hi_f16(hv));
+          *reinterpret_cast<uint32_t*>(&ocb_s[buf][w][hh][2 * lane]) = hv;
+          *reinterpret_cast<uint32_t*>(&ocb_s[buf][w][GQ + hh][2 * lane]) = pk_f16(x0 - lo_f16(hv), x1 - hi_f16(hv));
         }
         // token-sorted: the entries of tile A (tokens 0..15) come first
         return (int)__popcll(__ballot(tbv[0] < 16u)) + (int)__popcll(__ballot(tbv[1] < 16u));
       };
       // Apply a staged chunk: one-hot MFMAs, 32 entries each, only for the
       // tiles a 32-entry slice touches.
-      auto apply_entries = [&](int cnt, int nA, floatx4_t& CA, floatx4_t& CB) {
+      auto apply_entries = [&](int cnt, int nA, floatx4_t& CA, floatx4_t& CB, int buf) {
         for (int ch = 0; ch < (cnt + 31) / 32; ++ch) {
-          const uint2 tb8 = *reinterpret_cast<const uint2*>(&otb_s[w][32 * ch + 8 * lg]);
+          const uint2 tb8 = *reinterpret_cast<const uint2*>(&otb_s[buf][w][32 * ch + 8 * lg]);
           H8 cbv;
-          cbv.v = active ? *reinterpret_cast<const uint4*>(&ocb_s[w][c][32 * ch + 8 * lg])
+          cbv.v = active ? *reinterpret_cast<const uint4*>(&ocb_s[buf][w][c][32 * ch + 8 * lg])
                          : make_uint4(0u, 0u, 0u, 0u);
           auto onehot = [&](uint32_t r) {
             H8 o;
@@ -862,16 +902,31 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         }
       };
 
-      auto process = [&](const ColdBlock<VB>& cur, int blk) {
+      // Block i computes with its outlier entries staged in buffer i & 1; with
+      // the skew, the entries of block i + 1 (nx1) are staged here, a whole
+      // step before they are applied, so their LDS round trips overlap work.
+      int pend_cnt = 0, pend_nA = 0;  // staged entries of the block computed next
+      auto process = [&](const ColdBlock<VB>& cur, int blk, const ColdBlock<VB>& nx1, int blk1,
+                         int gslot, int gslot1, int buf) {
         const int e0 = cur.e0, ne = cur.ne;
-        // first (usually only) outlier chunk: staged before the QK^T table
-        // reads, straight-line, so its LDS traffic overlaps the MFMAs
-        const int cnt0 = min(128, ne);
-        const int nA0 = stage_entries(cur.ent, cnt0, blk);
+        int cnt0, nA0;
+        if constexpr (kSkew) {
+          cnt0 = pend_cnt;
+          nA0 = pend_nA;
+        } else {
+          cnt0 = min(128, ne);
+          nA0 = stage_entries(cur.ent, cnt0, blk, 0, gslot);
+        }
         floatx4_t CA, CB;
         qk_pair(cur.kA, cur.kB, CA, CB);
-        wave_sync();
-        apply_entries(cnt0, nA0, CA, CB);
+        if constexpr (!kSkew) wave_sync();
+        apply_entries(cnt0, nA0, CA, CB, kSkew ? buf : 0);
+        if constexpr (kSkew) {
+          // next block's entries into the other buffer: independent of the
+          // rest of this step, so the scheduler interleaves it with softmax/PV
+          pend_cnt = min(128, nx1.ne);
+          pend_nA = stage_entries(nx1.ent, pend_cnt, blk1, buf ^ 1, gslot1);
+        }
         if (ne > 128) {
           // rare (> 128 entries in one block): read each further chunk and
           // drain here, so the common path keeps exact wait counts
@@ -882,9 +937,9 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
             const uint32_t x0 = oent[min(i0, capm1)], x1 = oent[min(i0 + 1, capm1)];
             __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
             wave_sync();
-            const int nA = stage_entries(make_uint2(x0, x1), cnt, blk);
+            const int nA = stage_entries(make_uint2(x0, x1), cnt, blk, kSkew ? buf : 0, gslot);
             wave_sync();
-            apply_entries(cnt, nA, CA, CB);
+            apply_entries(cnt, nA, CA, CB, kSkew ? buf : 0);
           }
         }
         wave_sync();
@@ -896,33 +951,51 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         }
         float p[8];
         softmax_block<GQ>(st, sc, p, lg);
-        const H8 paA = p_operand(p[0] * row_bcast<0>(cur.nv), p[1] * row_bcast<1>(cur.nv),
-                                 p[2] * row_bcast<2>(cur.nv), p[3] * row_bcast<3>(cur.nv), active, is_hi);
-        const H8 paB = p_operand(p[4] * row_bcast<4>(cur.nv), p[5] * row_bcast<5>(cur.nv),
-                                 p[6] * row_bcast<6>(cur.nv), p[7] * row_bcast<7>(cur.nv), active, is_hi);
-        pv_pair(cur.uA, cur.uB, paA, paB);
+        const H8 pw = p_weights(p[0] * row_bcast<0>(cur.nv), p[1] * row_bcast<1>(cur.nv),
+                                p[2] * row_bcast<2>(cur.nv), p[3] * row_bcast<3>(cur.nv),
+                                p[4] * row_bcast<4>(cur.nv), p[5] * row_bcast<5>(cur.nv),
+                                p[6] * row_bcast<6>(cur.nv), p[7] * row_bcast<7>(cur.nv), active, is_hi);
+        pv_pair(cur.uA, cur.uB, pw);
       };
 
 
 
     // A ring of kColdBuf buffers, kColdBuf - 1 blocks in flight: step i
     // issues the loads of block i + kColdBuf - 1 and computes block i.
-    int kbp = 0;  // block index of the computed block within its group
-    auto step = [&](const ColdBlock<VB>& cur, ColdBlock<VB>& nxt) {
-      if (kbp == 0) begin_group(cur);
+    int jp = 0, kbp = 0, ip = 0;  // computed block: wave group jp, block kbp, stream index ip
+    auto step = [&](const ColdBlock<VB>& cur, ColdBlock<VB>& nxt, const ColdBlock<VB>& nx1) {
+      store_group_stats();
+      load_group_stats(jl);  // group of the block load_next fetches now
+      wave_sync();
+      if (kbp == 0) begin_group(jp);
       load_next(nxt);
-      process(cur, kbp);
-      if (++kbp == nblk) kbp = 0;
+      const bool last = kbp + 1 == nblk;
+      process(cur, kbp, nx1, last ? 0 : kbp + 1, jp & 1, last ? (jp + 1) & 1 : jp & 1, ip & 1);
+      ++ip;
+      if (++kbp == nblk) {
+        kbp = 0;
+        ++jp;
+      }
     };
     if (T > 0) {
+      // groups of the first two blocks, synchronously
+      load_group_stats(0);
+      store_group_stats();
+      load_group_stats(min(1, T - 1) / nblk);
+      store_group_stats();
       ColdBlock<VB> ring[kColdBuf];
 #pragma unroll
       for (int s = 0; s < kColdBuf - 1; ++s) load_next(ring[s]);
+      if constexpr (kSkew) {
+        wave_sync();
+        pend_cnt = min(128, ring[0].ne);
+        pend_nA = stage_entries(ring[0].ent, pend_cnt, 0, 0, 0);
+      }
       for (int i = 0; i < T; i += kColdBuf) {
 #pragma unroll
         for (int s = 0; s < kColdBuf; ++s) {
           if (i + s >= T) break;
-          step(ring[s], ring[(s + kColdBuf - 1) % kColdBuf]);
+          step(ring[s], ring[(s + kColdBuf - 1) % kColdBuf], ring[(s + 1) % kColdBuf]);
         }
       }
     }
@@ -1209,7 +1282,7 @@ int run_merge(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int batch, int m
 
 extern "C" {
 
-int tqk_version(void) { return 1; }
+int tqk_version(void) { return 2; }
 
 int tqk_check_desc(const tqk_cache_desc* d) {
   if (!d) return TQK_EINVAL;
@@ -1225,7 +1298,7 @@ int tqk_check_desc(const tqk_cache_desc* d) {
   if (d->page_tokens < 1 || d->group_tokens % d->page_tokens) return TQK_EINVAL;
   if (d->hot_ring < d->hot_window) return TQK_EINVAL;
   if (d->outliers_per_channel < 0 || d->outlier_cap < 0) return TQK_EINVAL;
-  if (d->max_groups_per_seq < 0 || d->max_pages_per_seq < 0) return TQK_EINVAL;
+  if (d->max_groups_per_seq < 0 || d->max_pages_per_seq < 0 || d->n_pages < 1) return TQK_EINVAL;
   return TQK_OK;
 }
 

@@ -196,7 +196,7 @@ __global__ __launch_bounds__(kThreads) void tqk_encode_group(EncodeArgs a) {
   // key code rows, 16 bytes per thread
   for (int idx = tid; idx < G * (D / 32); idx += kThreads) {
     const int t = idx / (D / 32), ch = idx % (D / 32);
-    const size_t row = page_row(a.p.block_table, d.max_pages_per_seq, b, g * G + t, P, Hkv, h);
+    const size_t row = page_row(a.p.block_table, d.max_pages_per_seq, b, g * G + t, P, d.n_pages, h);
     *reinterpret_cast<uint4*>(a.p.kcodes + row * (D / 2) + 16 * ch) =
         *reinterpret_cast<const uint4*>(&kc_s[t][16 * ch]);
   }
@@ -232,7 +232,7 @@ __global__ __launch_bounds__(kThreads) void tqk_encode_group(EncodeArgs a) {
 #pragma unroll
     for (int k = 0; k < (1 << VB) - 1; ++k) bnd[k] = a.p.vbnd[k];
 
-    const size_t row = page_row(a.p.block_table, d.max_pages_per_seq, b, t, P, Hkv, h);
+    const size_t row = page_row(a.p.block_table, d.max_pages_per_seq, b, t, P, d.n_pages, h);
     uint32_t outw[VROW / 4];
 #pragma unroll
     for (int k = 0; k < VROW / 4; ++k) outw[k] = 0u;
@@ -284,7 +284,7 @@ __global__ __launch_bounds__(kThreads) void tqk_encode_group(EncodeArgs a) {
         }
       }
       const int t0 = g * G + 16 * T;  // tile start (absolute token), never straddles a page
-      const size_t row0 = page_row(a.p.block_table, d.max_pages_per_seq, b, t0, P, Hkv, h);
+      const size_t row0 = page_row(a.p.block_table, d.max_pages_per_seq, b, t0, P, d.n_pages, h);
       uint32_t* dst = reinterpret_cast<uint32_t*>(a.p.vcodes + row0 * VROW + v_unit_offset(lg, c, VROW));
 #pragma unroll
       for (int k = 0; k < VROW / 16; ++k) dst[k] = w[k];
@@ -345,7 +345,7 @@ __global__ __launch_bounds__(kThreads) void tqk_dequant_group(DequantArgs a) {
   float* ko = a.kout + ((size_t)item * Hkv + h) * G * D;
   float* vo = a.vout + ((size_t)item * Hkv + h) * G * D;
   if (tid < G) {
-    const size_t row = page_row(a.p.block_table, d.max_pages_per_seq, b, g * G + tid, P, Hkv, h);
+    const size_t row = page_row(a.p.block_table, d.max_pages_per_seq, b, g * G + tid, P, d.n_pages, h);
     const uint8_t* kr = a.p.kcodes + row * (D / 2);
     for (int jj = 0; jj < D / 2; ++jj) {
       const uint32_t byte = kr[jj];

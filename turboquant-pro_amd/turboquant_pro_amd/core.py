@@ -111,10 +111,12 @@ class TurboQuantKVCache:
         cap = max(need, 2 * self._capacity)
         new = self._new_pool(cap, rotation=self._rotation)
         old = self._pool
-        npg, nsl = old.kcodes.shape[0], old.gscale.shape[0]
-        new.kcodes[:npg] = old.kcodes
-        new.vcodes[:npg] = old.vcodes
-        new.vnorm[:npg] = old.vnorm
+        npg, nsl = old.kcodes.shape[1], old.gscale.shape[0]
+        # pages are head-major and the default table of a single sequence does
+        # not depend on the capacity, so page p keeps its index
+        new.kcodes[:, :npg] = old.kcodes
+        new.vcodes[:, :npg] = old.vcodes
+        new.vnorm[:, :npg] = old.vnorm
         new.gscale[:nsl] = old.gscale
         new.gmean[:nsl] = old.gmean
         new.ocount[:nsl] = old.ocount

@@ -45,12 +45,16 @@ class TQKVPool:
         self.device = torch.device(device if device is not None else "cuda")
         Hq = n_kv_heads if n_q_heads is None else n_q_heads
         G = group_tokens_for(hot_window)
-        P = G if page_tokens is None else page_tokens
+        # default: 32-token pages (one decode block each) when groups are whole blocks
+        P = (32 if G % 32 == 0 else G) if page_tokens is None else page_tokens
         k_out = outliers_per_channel(G, outlier_frac)
         if outlier_cap is None:
             outlier_cap = min(G * head_dim, 4 * k_out * head_dim) if k_out else 0
         max_groups = max(1, n_groups_for(max_seq_len, hot_window))
         max_pages = max(1, (max_groups * G + P - 1) // P) if P > 0 else 1
+        if block_table is None and P == 32 and G % 32 == 0:
+            # whole clusters of 8 groups per sequence (see _clustered_table)
+            max_pages = -(-max_pages // (8 * (G // 32))) * (8 * (G // 32))
         self.n_kv_heads, self.n_q_heads, self.head_dim = n_kv_heads, Hq, head_dim
         self.max_batch, self.max_seq_len, self.hot_window = max_batch, max_seq_len, hot_window
         self.key_bits, self.value_bits, self.outlier_frac = key_bits, value_bits, outlier_frac
@@ -63,16 +67,17 @@ class TQKVPool:
             group_tokens=G, page_tokens=P, key_bits=key_bits, value_bits=value_bits,
             outliers_per_channel=k_out, outlier_cap=outlier_cap,
             max_pages_per_seq=max_pages, max_groups_per_seq=max_groups,
-            hot_ring=hot_window, sm_scale=1.0 / math.sqrt(head_dim))
+            hot_ring=hot_window, n_pages=max_batch * max_pages, sm_scale=1.0 / math.sqrt(head_dim))
         N.check(N.lib().tqk_check_desc(ctypes.byref(self.desc)), "TQKVPool")
 
         dev = self.device
         n_pages = max_batch * max_pages
         n_slots = max_batch * max_groups
         u8, f32, i32, f16 = torch.uint8, torch.float32, torch.int32, torch.float16
-        self.kcodes = torch.zeros((n_pages, n_kv_heads, P, head_dim * key_bits // 8), dtype=u8, device=dev)
-        self.vcodes = torch.zeros((n_pages, n_kv_heads, P, head_dim * value_bits // 8), dtype=u8, device=dev)
-        self.vnorm = torch.zeros((n_pages, n_kv_heads, P), dtype=f32, device=dev)
+        # head-major pages (include/tqk.h)
+        self.kcodes = torch.zeros((n_kv_heads, n_pages, P, head_dim * key_bits // 8), dtype=u8, device=dev)
+        self.vcodes = torch.zeros((n_kv_heads, n_pages, P, head_dim * value_bits // 8), dtype=u8, device=dev)
+        self.vnorm = torch.zeros((n_kv_heads, n_pages, P), dtype=f32, device=dev)
         self.gscale = torch.zeros((n_slots, n_kv_heads, head_dim), dtype=f32, device=dev)
         self.gmean = torch.zeros((n_slots, n_kv_heads, head_dim), dtype=f32, device=dev)
         # cumulative outlier counts at every 32-token boundary of a group (last = total)
@@ -81,7 +86,7 @@ class TQKVPool:
         self.hot_k = torch.zeros((max_batch, n_kv_heads, hot_window, head_dim), dtype=f16, device=dev)
         self.hot_v = torch.zeros((max_batch, n_kv_heads, hot_window, head_dim), dtype=f16, device=dev)
         if block_table is None:
-            bt = np.arange(n_pages, dtype=np.int32).reshape(max_batch, max_pages)
+            bt = self._clustered_table(max_batch, max_pages, P, G)
         else:
             bt = np.asarray(block_table, dtype=np.int32).reshape(max_batch, max_pages)
             if bt.min() < 0 or bt.max() >= n_pages:
@@ -111,6 +116,22 @@ class TQKVPool:
         self._ws = None
 
     # ------------------------------------------------------------------ #
+    @staticmethod
+    def _clustered_table(max_batch: int, max_pages: int, P: int, G: int) -> np.ndarray:
+        """Default block table.  With 32-token pages, the pages of 8 consecutive
+        groups of a sequence form a cluster in which block k of group 8c + w
+        sits at page 8k + w: the decode's 8 waves stream groups w = 0..7 of a
+        cluster side by side, so their concurrent block reads are adjacent in
+        HBM.  Otherwise the identity mapping."""
+        bt = np.arange(max_batch * max_pages, dtype=np.int32).reshape(max_batch, max_pages)
+        if P != 32 or G % 32 != 0:
+            return bt
+        nb = G // 32                                # blocks per group
+        lp = np.arange(max_pages)                   # logical page = token block
+        g, k = lp // nb, lp % nb
+        phys = (g // 8) * (8 * nb) + k * 8 + (g % 8)
+        return (np.arange(max_batch)[:, None] * max_pages + phys[None, :]).astype(np.int32)
+
     def _stream(self):
         return ctypes.c_void_p(_torch().cuda.current_stream(self.device).cuda_stream)
 
@@ -257,12 +278,12 @@ class TQKVPool:
         ``(1, H, G, D)``), ``vpacked`` (CompressedKV.indices), ``vnorms`` ``(H, G)``."""
         phys, off = self._rows(b, g)
         H, G, D = self.n_kv_heads, self.group_tokens, self.head_dim
-        kp = self.kcodes[phys, :, off].permute(1, 0, 2).contiguous().cpu().numpy()  # (H, G, 64)
-        vp = self.vcodes[phys, :, off].permute(1, 0, 2).contiguous().cpu().numpy()  # (H, G, vrow)
+        kp = self.kcodes[:, phys, off].contiguous().cpu().numpy()  # (H, G, 64)
+        vp = self.vcodes[:, phys, off].contiguous().cpu().numpy()  # (H, G, vrow)
         if self.tiled:
             vp = np.stack([pack_values(untile_value_rows(vp[h], self.value_bits, D), self.value_bits)
                            for h in range(H)])
-        vn = self.vnorm[phys, :, off].permute(1, 0).contiguous()
+        vn = self.vnorm[:, phys, off].contiguous()
         slot = int(self.group_table[b, g])
         cnt = self.ocount[slot, :, -1].cpu().numpy()
         ent = self.oent[slot].cpu().numpy().view(np.uint32)
