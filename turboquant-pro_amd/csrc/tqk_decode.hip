@@ -456,30 +456,30 @@ struct ColdBlock {
   uint32_t obase;  // slot * Hkv + h of the block's group
 };
 
-// Per-wave online-softmax state for query head (c % GQ) and the PV accumulators.
+// Per-wave online-softmax state for query head (c & (GQ - 1)) and the PV accumulators.
+// Scores are kept in the log2 domain (q is pre-scaled by sm_scale * log2(e)).
 struct WaveState {
   float m, l;
   floatx4_t O[8];
 };
 
-// Online softmax over the 8 scores of this lane (head c % GQ, tokens
-// 4lg..4lg+3 of tiles A and B).  Every lane of a column holds the same state
-// for its head; accumulator row r = 4lg + i belongs to head r % GQ, whose
-// correction factor is read from column (r % GQ) with v_readlane.
+// Online softmax over the 8 scores of this lane (tokens 4lg..4lg+3 of tiles A
+// and B of column c).  Every lane of a column holds the same state for its
+// head; accumulator row r = 4lg + i belongs to head r & (GQ - 1), whose
+// correction factor is read from that column with v_readlane.
 template <int GQ>
 __device__ __forceinline__ void softmax_block(WaveState& st, const float (&s)[8], float (&p)[8],
                                               int lg) {
-  float bm = s[0];
-#pragma unroll
-  for (int i = 1; i < 8; ++i) bm = fmaxf(bm, s[i]);
+  float bm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+  bm = fmaxf(bm, fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
   bm = colgroup_max(bm);
   const float mn = fmaxf(st.m, bm);
-  const float corr = __expf(st.m - mn);
+  const float corr = __builtin_amdgcn_exp2f(st.m - mn);
   st.m = mn;
   float ps = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    p[i] = __expf(s[i] - mn);
+    p[i] = __builtin_amdgcn_exp2f(s[i] - mn);
     ps += p[i];
   }
   st.l = st.l * corr + colgroup_sum(ps);
@@ -488,10 +488,10 @@ __device__ __forceinline__ void softmax_block(WaveState& st, const float (&s)[8]
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     // no indexed array here: a lane-dependent pick from one would live in scratch
-    const float c0 = bitsf((uint32_t)__builtin_amdgcn_readlane((int)fbits(corr), i % GQ));
+    const float c0 = bitsf((uint32_t)__builtin_amdgcn_readlane((int)fbits(corr), i & (GQ - 1)));
     float ci = c0;
     if constexpr (GQ > 4) {
-      const float c1 = bitsf((uint32_t)__builtin_amdgcn_readlane((int)fbits(corr), (4 + i) % GQ));
+      const float c1 = bitsf((uint32_t)__builtin_amdgcn_readlane((int)fbits(corr), 4 + i));
       ci = (lg & 1) ? c1 : c0;
     }
 #pragma unroll
@@ -515,16 +515,15 @@ __device__ __forceinline__ uint32_t pk_f16(float x, float y) {
 __device__ __forceinline__ float lo_f16(uint32_t pk) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(pk & 0xFFFFu)); }
 __device__ __forceinline__ float hi_f16(uint32_t pk) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(pk >> 16)); }
 
-// PV A operand of one 16-token tile for this lane (row = column c): the
-// weights x0..x3 of tokens 4lg..4lg+3, each twice to meet the value's fp16
-// hi and lo k-slots -- [x0 x1 x0 x1 x2 x3 x2 x3] -- as fp16 hi (rows < GQ),
-// fp16 lo (rows GQ..2GQ-1) or zero (other rows).
-__device__ __forceinline__ H8 p_operand(float x0, float x1, float x2, float x3, bool active, bool is_hi) {
+// MFMA operand quad [x0 x1 x0 x1 x2 x3 x2 x3]: each value twice, so that it
+// meets both the fp16 hi and the fp16 lo k-slot of the other operand.  The
+// halves are fp16(x) (lo_sel = 0) or the fp16 residual x - fp16(x) (lo_sel = 1).
+// Used for the PV weights (x = weights of tokens 4lg..4lg+3 of a tile) and for
+// the QK^T weights (x = q * nf4_scale of four channels).
+__device__ __forceinline__ H8 dup_quad(float x0, float x1, float x2, float x3, float lo_sel) {
   const uint32_t h01 = pk_f16(x0, x1), h23 = pk_f16(x2, x3);
-  const uint32_t l01 = pk_f16(x0 - lo_f16(h01), x1 - hi_f16(h01));
-  const uint32_t l23 = pk_f16(x2 - lo_f16(h23), x3 - hi_f16(h23));
-  const uint32_t v01 = active ? (is_hi ? h01 : l01) : 0u;
-  const uint32_t v23 = active ? (is_hi ? h23 : l23) : 0u;
+  const uint32_t v01 = pk_f16(fmaf(-lo_sel, lo_f16(h01), x0), fmaf(-lo_sel, hi_f16(h01), x1));
+  const uint32_t v23 = pk_f16(fmaf(-lo_sel, lo_f16(h23), x2), fmaf(-lo_sel, hi_f16(h23), x3));
   H8 r;
   r.u[0] = v01;
   r.u[1] = v01;
@@ -533,45 +532,24 @@ __device__ __forceinline__ H8 p_operand(float x0, float x1, float x2, float x3, 
   return r;
 }
 
-// P operand of the PV MFMAs for this lane's eight weights (tile A tokens
-// 4lg..4lg+3, then tile B tokens 16+4lg..): fp16 hi (rows < GQ), fp16 lo
-// (rows GQ..2GQ-1) or zero (other rows).
-__device__ __forceinline__ H8 p_weights(float x0, float x1, float x2, float x3, float x4, float x5,
-                                        float x6, float x7, bool active, bool is_hi) {
-  const uint32_t h01 = pk_f16(x0, x1), h23 = pk_f16(x2, x3), h45 = pk_f16(x4, x5), h67 = pk_f16(x6, x7);
-  H8 r;
-  if (is_hi) {
-    r.u[0] = h01; r.u[1] = h23; r.u[2] = h45; r.u[3] = h67;
-  } else {
-    r.u[0] = pk_f16(x0 - lo_f16(h01), x1 - hi_f16(h01));
-    r.u[1] = pk_f16(x2 - lo_f16(h23), x3 - hi_f16(h23));
-    r.u[2] = pk_f16(x4 - lo_f16(h45), x5 - hi_f16(h45));
-    r.u[3] = pk_f16(x6 - lo_f16(h67), x7 - hi_f16(h67));
-  }
-  const uint32_t keep = active ? 0xFFFFFFFFu : 0u;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) r.u[k] &= keep;
-  return r;
-}
-
 template <int GQ, int VB>
 __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs a) {
   constexpr int D = TQK_D;
   constexpr int VROW = D * VB / 8;
   constexpr int UNIT = VROW / 4;
-  constexpr int NCOL = 2 * GQ;
   const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, lg = lane >> 4, c = lane & 15;
   const tqk_cache_desc& d = a.d;
   const int Hkv = d.n_kv_heads, Hq = d.n_q_heads, G = d.group_tokens, P = d.page_tokens;
   const int L = a.seq_lens[b];
   const int ng = n_groups_of(L, d.hot_window, G);
-  const float sm = d.sm_scale;
+  // scores in the log2 domain: q * sm_scale * log2(e), softmax with exp2
+  const float qscale = d.sm_scale * 1.4426950408889634f;
   const bool hot = split >= a.n_cold_splits;
 
   __shared__ __align__(16) uint8_t lut[LutGeom<VB>::kBytes];
-  __shared__ __align__(16) float qt_s[D][GQ];           // q transposed: [channel][head]
-  __shared__ __align__(16) float q_h_s[GQ][D];           // q, head-major
+  __shared__ __align__(16) float qt_s[D][GQ];           // scaled q transposed: [channel][head]
+  __shared__ __align__(16) float q_h_s[GQ][D];           // scaled q, head-major
   // (nf4_scale[128], nf4_mean[128]) of a wave's current and next group
   __shared__ __align__(16) float gsm_s[kMWaves][2][2 * D];
   // outlier correction operands: entry token (255 = none) and q_h * (val - dense)
@@ -609,7 +587,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   }
 
   for (int i = tid; i < GQ * D; i += kMThreads) {
-    const float qv = h2f(a.q[((size_t)b * Hq + h * GQ + i / D) * D + i % D]);
+    const float qv = h2f(a.q[((size_t)b * Hq + h * GQ + i / D) * D + i % D]) * qscale;
     qt_s[i % D][i / D] = qv;
     q_h_s[i / D][i % D] = qv;
   }
@@ -638,14 +616,14 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   }
   __syncthreads();
 
-  const int hcol = c % GQ;
-  const bool active = c < NCOL, is_hi = c < GQ;
-  // partner column of c in the hi/lo pair (c ^ GQ), via one of two row rotates
-  const bool rot_a = (int)row_ror<GQ>((float)c) == (c ^ GQ);
-  auto pair_sum = [&](float x) {
-    const float pa_ = row_ror<GQ>(x), pb_ = row_ror<(16 - GQ) % 16>(x);
-    return x + (rot_a ? pa_ : pb_);
-  };
+  // Columns of the score tiles and rows of the PV tiles: c < 8 carry fp16 hi
+  // parts, c >= 8 the fp16 lo parts, of head c & (GQ - 1) (heads repeat when
+  // GQ < 8; only rows with (c & 7) < GQ are read out at the end).
+  const int hq = c & (GQ - 1);
+  const bool is_hi = c < 8;
+  const float lo_sel = is_hi ? 0.f : 1.f;
+  // hi column + lo column of the same head (lane c and c ^ 8 of a row)
+  auto pair_sum = [&](float x) { return x + row_ror<8>(x); };
   WaveState st;
   st.m = -INFINITY;
   st.l = 0.f;
@@ -730,75 +708,74 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       *reinterpret_cast<float2*>(&gsm_s[w][pend_slot][2 * lane]) = pend_s;
       *reinterpret_cast<float2*>(&gsm_s[w][pend_slot][D + 2 * lane]) = pend_m;
     };
-    // QK^T weight operand: MFMA m covers channels 32lg + 8m + i (i < 8) of lane
-    // group lg; column c holds q * nf4_scale of head c % GQ as fp16 hi
-    // (c < GQ) or lo (GQ <= c < 2GQ), zero in other columns.  The key operand
-    // is the hi (first MFMA) or lo (second) fp16 part of the NF4 levels, so
-    // the pair of columns summed gives the fp32 product.
-    H8 Bw[4];
-    float bias = 0.f;
+    // QK^T: C[token][col] = sum_k A[token][k] * B[k][col] over k-slots that
+    // pair each channel's fp16 hi and lo NF4 level with the same weight.
+    // MFMA m takes key bytes 2m, 2m+1 of the lane's 16 (channels ch0..ch3 =
+    // 32lg + 4m + 0..3): A k-slots [hi ch0, hi ch1, lo ch0, lo ch1, hi ch2,
+    // hi ch3, lo ch2, lo ch3] are two table rows read straight into the
+    // operand, B = [w0 w1 w0 w1 w2 w3 w2 w3] with w = q * nf4_scale of the
+    // column's head as fp16 hi (c < 8) or lo (c >= 8).  Column c plus column
+    // c ^ 8 is the fp32 score; the mean bias enters as the initial
+    // accumulator of the hi columns.
+    H8 Bw[8];
+    floatx4_t binit;
     // Start of wave group j: weights and mean bias from slot j & 1.
     auto begin_group = [&](int j) {
       const float* gs = &gsm_s[w][j & 1][0];
-      const uint32_t keep = active ? 0xFFFFFFFFu : 0u;
       float biasp = 0.f;
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {
-#pragma unroll
-        for (int hq = 0; hq < 2; ++hq) {
-          const int ch = 32 * lg + 8 * m + 4 * hq;
-          const float4 q4 = *reinterpret_cast<const float4*>(&q_h_s[hcol][ch]);
-          const float4 s4 = *reinterpret_cast<const float4*>(&gs[ch]);
-          const float4 m4 = *reinterpret_cast<const float4*>(&gs[D + ch]);
-          biasp += q4.x * m4.x + q4.y * m4.y + q4.z * m4.z + q4.w * m4.w;
-          const float w0 = q4.x * s4.x, w1 = q4.y * s4.y, w2 = q4.z * s4.z, w3 = q4.w * s4.w;
-          const uint32_t h01 = pk_f16(w0, w1), h23 = pk_f16(w2, w3);
-          const uint32_t l01 = pk_f16(w0 - lo_f16(h01), w1 - hi_f16(h01));
-          const uint32_t l23 = pk_f16(w2 - lo_f16(h23), w3 - hi_f16(h23));
-          Bw[m].u[2 * hq] = (is_hi ? h01 : l01) & keep;
-          Bw[m].u[2 * hq + 1] = (is_hi ? h23 : l23) & keep;
-        }
+      for (int m = 0; m < 8; ++m) {
+        const int ch = 32 * lg + 4 * m;
+        const float4 q4 = *reinterpret_cast<const float4*>(&q_h_s[hq][ch]);
+        const float4 s4 = *reinterpret_cast<const float4*>(&gs[ch]);
+        const float4 m4 = *reinterpret_cast<const float4*>(&gs[D + ch]);
+        biasp += q4.x * m4.x + q4.y * m4.y + q4.z * m4.z + q4.w * m4.w;
+        Bw[m] = dup_quad(q4.x * s4.x, q4.y * s4.y, q4.z * s4.z, q4.w * s4.w, lo_sel);
       }
-      bias = colgroup_sum(biasp);
+      const float bv = is_hi ? colgroup_sum(biasp) : 0.f;
+      binit = floatx4_t{bv, bv, bv, bv};
     };
 
-      // Key operands of QK^T MFMA m for key word kq (bytes 4m..4m+3 of the lane's
-      // 16: channels 32lg + 8m + 2q, +1 for byte q): the table row of a code byte
-      // is (fp16 hi pair, fp16 lo pair), so four reads give the hi operand and
-      // the lo operand of the two MFMAs.
-      auto key_operands = [&](uint32_t word, H8& hi, H8& lo) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint2 t = *reinterpret_cast<const uint2*>(
-              klut + __builtin_amdgcn_perm(word, koff, 0x0C0C0000u | ((4u + (uint32_t)q) << 8)));
-          hi.u[q] = t.x;
-          lo.u[q] = t.y;
-        }
+      // A operand of QK^T MFMA m from the lane's key bytes (a table row of a code
+      // byte is {fp16 hi pair, fp16 lo pair} of its two channels)
+      auto key_quad = [&](const uint4& k, int m) {
+        const uint32_t word = (m >> 1) == 0 ? k.x : (m >> 1) == 1 ? k.y : (m >> 1) == 2 ? k.z : k.w;
+        const uint32_t q0 = 2u * (uint32_t)(m & 1);
+        const uint2 t0 = *reinterpret_cast<const uint2*>(
+            klut + __builtin_amdgcn_perm(word, koff, 0x0C0C0000u | ((4u + q0) << 8)));
+        const uint2 t1 = *reinterpret_cast<const uint2*>(
+            klut + __builtin_amdgcn_perm(word, koff, 0x0C0C0000u | ((5u + q0) << 8)));
+        H8 r;
+        r.u[0] = t0.x;
+        r.u[1] = t0.y;
+        r.u[2] = t1.x;
+        r.u[3] = t1.y;
+        return r;
       };
       // both tiles' QK^T: every table read is issued before the first MFMA,
       // so the LDS latency is paid once per block, not once per MFMA
       auto qk_pair = [&](const uint4& ka, const uint4& kb, floatx4_t& CA, floatx4_t& CB) {
-        H8 hA[4], lA[4], hB[4], lB[4];
+        H8 xa[8], xb[8];
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          key_operands(m == 0 ? ka.x : m == 1 ? ka.y : m == 2 ? ka.z : ka.w, hA[m], lA[m]);
-          key_operands(m == 0 ? kb.x : m == 1 ? kb.y : m == 2 ? kb.z : kb.w, hB[m], lB[m]);
+        for (int m = 0; m < 8; ++m) {
+          xa[m] = key_quad(ka, m);
+          xb[m] = key_quad(kb, m);
         }
         // keep the reads ahead of the MFMAs (GQ = 8 has no registers to spare)
         if constexpr (GQ <= 4) __builtin_amdgcn_sched_barrier(0);
-        CA = floatx4_t{0.f, 0.f, 0.f, 0.f};
-        CB = floatx4_t{0.f, 0.f, 0.f, 0.f};
+        CA = binit;
+        CB = binit;
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          CA = __builtin_amdgcn_mfma_f32_16x16x32_f16(hA[m].h, Bw[m].h, CA, 0, 0, 0);
-          CB = __builtin_amdgcn_mfma_f32_16x16x32_f16(hB[m].h, Bw[m].h, CB, 0, 0, 0);
-          CA = __builtin_amdgcn_mfma_f32_16x16x32_f16(lA[m].h, Bw[m].h, CA, 0, 0, 0);
-          CB = __builtin_amdgcn_mfma_f32_16x16x32_f16(lB[m].h, Bw[m].h, CB, 0, 0, 0);
+        for (int m = 0; m < 8; ++m) {
+          CA = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[m].h, Bw[m].h, CA, 0, 0, 0);
+          CB = __builtin_amdgcn_mfma_f32_16x16x32_f16(xb[m].h, Bw[m].h, CB, 0, 0, 0);
         }
       };
-      // Table rows of value unit un for channel nt: fields 2nt (tokens 0, 1 of the
-      // unit) and 2nt + 1 (tokens 2, 3), each (fp16 hi pair, fp16 lo pair)
-      auto val_rows = [&](const uint4& un, int nt, uint2& r0, uint2& r1) {
+      // B operand of PV MFMA (nt, tile) from value unit un: fields 2nt (tokens
+      // 0, 1 of the unit, channel 8c + nt) and 2nt + 1 (tokens 2, 3), each a
+      // table row {fp16 hi pair, fp16 lo pair}: k-slots [hi t0, hi t1, lo t0,
+      // lo t1, hi t2, hi t3, lo t2, lo t3], matching the weight quad.
+      auto val_quad = [&](const uint4& un, int nt) {
         uint32_t f0, f1;
         if constexpr (VB == 3) {
           switch (nt) {
@@ -811,36 +788,40 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
           f0 = (word >> (16 * (nt & 1))) & 0xFFu;
           f1 = (word >> (16 * (nt & 1) + 8)) & 0xFFu;
         }
-        r0 = *reinterpret_cast<const uint2*>(lut + ((f0 << 8) | voff));
-        r1 = *reinterpret_cast<const uint2*>(lut + ((f1 << 8) | voff));
+        const uint2 r0 = *reinterpret_cast<const uint2*>(lut + ((f0 << 8) | voff));
+        const uint2 r1 = *reinterpret_cast<const uint2*>(lut + ((f1 << 8) | voff));
+        H8 r;
+        r.u[0] = r0.x;
+        r.u[1] = r0.y;
+        r.u[2] = r1.x;
+        r.u[3] = r1.y;
+        return r;
       };
-      // PV for both tiles: MFMA (nt, hi/lo) has k-slots 8lg + i = tile A tokens
-      // 4lg..4lg+3 then tile B tokens 16+4lg.., column c = channel 8c + nt; the
-      // P operand holds the lane's eight weights (rows: heads, fp16 hi or lo)
-      auto pv_pair = [&](const uint4& uA, const uint4& uB, const H8& pw) {
-        H8 vh[8], vl[8];
+      // PV for both tiles: O[row][8c + nt] += P[row][token] * V[token][8c + nt],
+      // row = head hi (< 8) or lo (>= 8) weight, 16 tokens of one tile per MFMA
+      auto pv_pair = [&](const uint4& uA, const uint4& uB, const H8& pa, const H8& pb) {
+        H8 va[8], vb[8];
 #pragma unroll
         for (int nt = 0; nt < 8; ++nt) {
-          uint2 a0, a1, b0, b1;
-          val_rows(uA, nt, a0, a1);
-          val_rows(uB, nt, b0, b1);
-          vh[nt].u[0] = a0.x; vh[nt].u[1] = a1.x; vh[nt].u[2] = b0.x; vh[nt].u[3] = b1.x;
-          vl[nt].u[0] = a0.y; vl[nt].u[1] = a1.y; vl[nt].u[2] = b0.y; vl[nt].u[3] = b1.y;
+          va[nt] = val_quad(uA, nt);
+          vb[nt] = val_quad(uB, nt);
         }
         if constexpr (GQ <= 4) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int nt = 0; nt < 8; ++nt) st.O[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pw.h, vh[nt].h, st.O[nt], 0, 0, 0);
+        for (int nt = 0; nt < 8; ++nt) st.O[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa.h, va[nt].h, st.O[nt], 0, 0, 0);
 #pragma unroll
-        for (int nt = 0; nt < 8; ++nt) st.O[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pw.h, vl[nt].h, st.O[nt], 0, 0, 0);
+        for (int nt = 0; nt < 8; ++nt) st.O[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pb.h, vb[nt].h, st.O[nt], 0, 0, 0);
       };
 
       // ---- sparse outliers, folded into the QK^T accumulators:
       //   C[t][col] += sum_e onehot[t][e] * x[e][col],
-      //   x[e][h] = q_h[j_e] * (val_e - mean_j) as fp16 hi (col h) / lo (col GQ + h)
+      //   x[e][h] = q_h[j_e] * (val_e - mean_j) as fp16 hi (col h) / lo (col h + 8),
+      //   staged as rows h (hi) and GQ + h (lo) of ocb_s
       // (the stored code of an outlier is the NF4 zero level, so the dense
       // pass contributed exactly mean_j there, inside the bias).
       // Stage: entries 2*lane, 2*lane + 1 of a chunk of <= 128 (token-sorted)
       // -> token bytes in otb_s, x in ocb_s; returns how many belong to tile A.
+      const int ocol = (is_hi ? 0 : GQ) + hq;  // ocb_s row of this lane's column
       auto stage_entries = [&](const uint2 ent, int cnt, int blk, int buf, int gslot) {
         float delta[2];
         uint32_t tbv[2];
@@ -886,8 +867,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         for (int ch = 0; ch < (cnt + 31) / 32; ++ch) {
           const uint2 tb8 = *reinterpret_cast<const uint2*>(&otb_s[buf][w][32 * ch + 8 * lg]);
           H8 cbv;
-          cbv.v = active ? *reinterpret_cast<const uint4*>(&ocb_s[buf][w][c][32 * ch + 8 * lg])
-                         : make_uint4(0u, 0u, 0u, 0u);
+          cbv.v = *reinterpret_cast<const uint4*>(&ocb_s[buf][w][ocol][32 * ch + 8 * lg]);
           auto onehot = [&](uint32_t r) {
             H8 o;
 #pragma unroll
@@ -946,16 +926,16 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         float sc[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          sc[i] = (pair_sum(CA[i]) + bias) * sm;
-          sc[4 + i] = (pair_sum(CB[i]) + bias) * sm;
+          sc[i] = pair_sum(CA[i]);
+          sc[4 + i] = pair_sum(CB[i]);
         }
         float p[8];
         softmax_block<GQ>(st, sc, p, lg);
-        const H8 pw = p_weights(p[0] * row_bcast<0>(cur.nv), p[1] * row_bcast<1>(cur.nv),
-                                p[2] * row_bcast<2>(cur.nv), p[3] * row_bcast<3>(cur.nv),
-                                p[4] * row_bcast<4>(cur.nv), p[5] * row_bcast<5>(cur.nv),
-                                p[6] * row_bcast<6>(cur.nv), p[7] * row_bcast<7>(cur.nv), active, is_hi);
-        pv_pair(cur.uA, cur.uB, pw);
+        const H8 pa = dup_quad(p[0] * row_bcast<0>(cur.nv), p[1] * row_bcast<1>(cur.nv),
+                               p[2] * row_bcast<2>(cur.nv), p[3] * row_bcast<3>(cur.nv), lo_sel);
+        const H8 pb = dup_quad(p[4] * row_bcast<4>(cur.nv), p[5] * row_bcast<5>(cur.nv),
+                               p[6] * row_bcast<6>(cur.nv), p[7] * row_bcast<7>(cur.nv), lo_sel);
+        pv_pair(cur.uA, cur.uB, pa, pb);
       };
 
 
@@ -1007,12 +987,8 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     // B operand of QK^T: q (fp16, exact) of head c for channels 32ks + 8lg + e
     H8 Bq[4];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      if (c < GQ)
-        Bq[ks].v = *reinterpret_cast<const uint4*>(a.q + ((size_t)b * Hq + h * GQ + c) * D + 32 * ks + 8 * lg);
-      else
-        Bq[ks].v = make_uint4(0u, 0u, 0u, 0u);
-    }
+    for (int ks = 0; ks < 4; ++ks)
+      Bq[ks].v = *reinterpret_cast<const uint4*>(a.q + ((size_t)b * Hq + h * GQ + hq) * D + 32 * ks + 8 * lg);
     for (int hb = w; hb < nhb; hb += kMWaves) {
       const int t0 = n_cold + 32 * hb;
       const uint16_t* kr = a.p.hot_k + (hbase + (t0 % R)) * D;   // 32 consecutive ring rows
@@ -1029,8 +1005,8 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       float s[8];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        s[i] = (t0 + 4 * lg + i < L) ? CA[i] * sm : -INFINITY;
-        s[4 + i] = (t0 + 16 + 4 * lg + i < L) ? CB[i] * sm : -INFINITY;
+        s[i] = (t0 + 4 * lg + i < L) ? CA[i] * qscale : -INFINITY;
+        s[4 + i] = (t0 + 16 + 4 * lg + i < L) ? CB[i] * qscale : -INFINITY;
       }
       float p[8];
       softmax_block<GQ>(st, s, p, lg);
@@ -1038,8 +1014,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const _Float16 hi = (_Float16)p[e];
-        const _Float16 lo = (_Float16)(p[e] - (float)hi);
-        pa.h[e] = active ? (is_hi ? hi : lo) : (_Float16)0.f;
+        pa.h[e] = is_hi ? hi : (_Float16)(p[e] - (float)hi);
       }
       // values: token e of this lane (tile A 4lg+e, tile B 16+4lg+e), channels 8c..8c+7
       uint4 vv[8];
@@ -1073,6 +1048,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     cm[w * GQ + c] = st.m;
     cl[w * GQ + c] = st.l;
   }
+  // accumulator rows: r < 8 fp16-hi weights of head r, r >= 8 lo weights of head r - 8
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = 4 * lg + i;
@@ -1085,9 +1061,9 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = 4 * lg + i;
-    if (r >= GQ && r < NCOL) {
+    if (r >= 8 && r < 8 + GQ) {
 #pragma unroll
-      for (int nt = 0; nt < 8; ++nt) co[(w * GQ + r - GQ) * D + 8 * c + nt] += st.O[nt][i];
+      for (int nt = 0; nt < 8; ++nt) co[(w * GQ + r - 8) * D + 8 * c + nt] += st.O[nt][i];
     }
   }
   __syncthreads();
@@ -1104,7 +1080,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       for (int ww = 0; ww < kMWaves; ++ww) {
         const float l = cl[ww * GQ + i];
         if (l > 0.f) {
-          const float wt = __expf(cm[ww * GQ + i] - M);
+          const float wt = __builtin_amdgcn_exp2f(cm[ww * GQ + i] - M);
           den += l * wt;
           acc += co[(ww * GQ + i) * D + j] * wt;
         }
@@ -1113,7 +1089,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     const size_t o = ((size_t)b * Hq + h * GQ + i) * ns + split;
     a.pacc[o * D + j] = acc;
     if (j == 0) {
-      a.pm[o] = M;
+      a.pm[o] = M * 0.6931471805599453f;  // back to the natural-log domain of the partials
       a.pl[o] = den;
     }
   }
