@@ -505,6 +505,24 @@ __device__ __forceinline__ float row_bcast(float x) {
   return bitsf((uint32_t)__builtin_amdgcn_update_dpp(0, (int)fbits(x), 0x150 + I, 0xF, 0xF, false));
 }
 
+// (row_newbcast reads a valid lane for every lane, so no "old" value is needed)
+template <int I>
+__device__ __forceinline__ uint32_t row_bcast_u(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x150 + I, 0xF, 0xF, false);
+}
+template <int K>
+struct IntC {
+  static constexpr int value = K;
+};
+
+// Outlier entries of one block as this lane holds them (two entries): token in
+// the block (255 = none) and fp16 {hi, lo} of (val - mean) * s / 2, plus the
+// block's entry count (<= 128 per pass) and how many fall in tile A.
+struct OutEntries {
+  uint32_t t0, t1, d0, d1;
+  int cnt, nA;
+};
+
 // fp16 pair (RNE) of two floats in one dword, and the fp32 value of a half
 __device__ __forceinline__ uint32_t pk_f16(float x, float y) {
   typedef float float2_t __attribute__((ext_vector_type(2)));
@@ -548,17 +566,18 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   const bool hot = split >= a.n_cold_splits;
 
   __shared__ __align__(16) uint8_t lut[LutGeom<VB>::kBytes];
-  __shared__ __align__(16) float qt_s[D][GQ];           // scaled q transposed: [channel][head]
-  __shared__ __align__(16) float q_h_s[GQ][D];           // scaled q, head-major
+  __shared__ __align__(16) uint32_t qq_s[D][GQ];        // raw fp16 q twice {q, q}: [channel][head]
+  // scaled q, head-major; rows padded by 4 banks so that the head rows read by
+  // one lane group fall in different banks
+  __shared__ __align__(16) float q_h_s[GQ][D + 4];
   // (nf4_scale[128], nf4_mean[128]) of a wave's current and next group
   __shared__ __align__(16) float gsm_s[kMWaves][2][2 * D];
-  // outlier correction operands: entry token (255 = none) and q_h * (val - dense)
-  // as fp16 hi (column h) / lo (column GQ + h), column-major, padded columns
-  // (two of each when the staging of the next block is skewed one step ahead)
+  // outlier correction B operands of a block (two sets when the staging of
+  // the next block is skewed one step ahead): per head, each entry's raw fp16
+  // q twice
   constexpr bool kSkew = GQ <= 4;
   constexpr int kOB = kSkew ? 2 : 1;
-  __shared__ __align__(16) uint8_t otb_s[kOB][kMWaves][128];
-  __shared__ __align__(16) _Float16 ocb_s[kOB][kMWaves][2 * GQ][136];
+  __shared__ __align__(16) uint32_t oq_s[kOB][kMWaves][GQ][132];  // rows 4 banks apart
   // NF4 levels [0, 16) and value centroids [16, 16 + 2^vb), for the table fill
   __shared__ float lvl_s[32];
   if (tid < 16) lvl_s[tid] = kNF4[tid];
@@ -587,9 +606,9 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   }
 
   for (int i = tid; i < GQ * D; i += kMThreads) {
-    const float qv = h2f(a.q[((size_t)b * Hq + h * GQ + i / D) * D + i % D]) * qscale;
-    qt_s[i % D][i / D] = qv;
-    q_h_s[i / D][i % D] = qv;
+    const uint32_t qr = a.q[((size_t)b * Hq + h * GQ + i / D) * D + i % D];
+    qq_s[i % D][i / D] = qr | (qr << 16);
+    q_h_s[i / D][i % D] = h2f((uint16_t)qr) * qscale;
   }
   __syncthreads();
   if (!hot) {
@@ -650,6 +669,10 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     const uint32_t koffL = (uint32_t)c * (D / 2) + 16u * (uint32_t)lg;
     const uint32_t uoffL = (uint32_t)(16 * lg + c) * UNIT;
     const int ntl = 4 * lg + (c & 3);  // token (of tile A if c & 4 == 0, else B) whose norm this lane reads
+    // outlier entries eidx, eidx + 1 of a block are this lane's: the four
+    // entries of lane group lg in 16-entry chunk k then sit in lanes 2k and
+    // 2k + 1 of the lane group's own row (DPP row broadcast reaches them)
+    const int eidx = 16 * (c >> 1) + 4 * lg + 2 * (c & 1);
     auto meta = [&](int j, int f) { return __builtin_amdgcn_readfirstlane(meta_s[wu + kMWaves * j][f]); };
 
     // Every step issues the same loads (past the end: the last block again,
@@ -677,7 +700,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       cb.nv = a.p.vnorm[((c & 4) ? rowB : rowA) + ntl];
       const uint32_t* oe = oent_all + (size_t)obase * cap;
       // entries past e1 are masked where they are used (the outlier pass)
-      const int i0 = e0 + 2 * lane;
+      const int i0 = e0 + eidx;
       cb.ent = make_uint2(oe[min(i0, capm1)], oe[min(i0 + 1, capm1)]);
       cb.e0 = e0;
       cb.ne = e1 - e0;
@@ -798,7 +821,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         return r;
       };
       // PV for both tiles: O[row][8c + nt] += P[row][token] * V[token][8c + nt],
-      // row = head hi (< 8) or lo (>= 8) weight, 16 tokens of one tile per MFMA
+      // row = head hi (< 8) or lo (>= 8) weight, 16 tokens of one tile per MFMA.
       auto pv_pair = [&](const uint4& uA, const uint4& uB, const H8& pa, const H8& pb) {
         H8 va[8], vb[8];
 #pragma unroll
@@ -814,98 +837,114 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       };
 
       // ---- sparse outliers, folded into the QK^T accumulators:
-      //   C[t][col] += sum_e onehot[t][e] * x[e][col],
-      //   x[e][h] = q_h[j_e] * (val_e - mean_j) as fp16 hi (col h) / lo (col h + 8),
-      //   staged as rows h (hi) and GQ + h (lo) of ocb_s
-      // (the stored code of an outlier is the NF4 zero level, so the dense
-      // pass contributed exactly mean_j there, inside the bias).
-      // Stage: entries 2*lane, 2*lane + 1 of a chunk of <= 128 (token-sorted)
-      // -> token bytes in otb_s, x in ocb_s; returns how many belong to tile A.
-      const int ocol = (is_hi ? 0 : GQ) + hq;  // ocb_s row of this lane's column
+      //   C[t][col] += sum_e [t_e == t] * d_e * q_h[j_e],   d = (val - mean_j) * s / 2
+      // with s = sm_scale * log2(e); the stored code of an outlier is the NF4
+      // zero level, so the dense pass contributed exactly mean_j there (inside
+      // the bias).  16 entries per MFMA: A k-slots {hi, lo} fp16 of d_e in row
+      // t_e (zero in other rows), B k-slots {q, q} (q is exact in fp16); the hi
+      // and the lo column of a head each take half, which pair_sum adds up.
+      // Stage a pass of <= 128 (token-sorted) entries: this lane's two in
+      // registers, their q pairs per head into oq_s set buf.
+      const float dscale = 0.5f * qscale;
       auto stage_entries = [&](const uint2 ent, int cnt, int blk, int buf, int gslot) {
-        float delta[2];
-        uint32_t tbv[2];
+        uint32_t tv[2], dv[2];
         int jv[2];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
           const uint32_t en = u ? ent.y : ent.x;
-          const bool ok = 2 * lane + u < cnt;
           const int pos = en & 0xFFFFu;
           const int j = pos & (D - 1);
-          delta[u] = ok ? h2f((uint16_t)(en >> 16)) - gsm_s[w][gslot][D + j] : 0.f;
-          tbv[u] = ok ? (uint32_t)((pos >> 7) - 32 * blk) : 255u;
+          const float dl = (h2f((uint16_t)(en >> 16)) - gsm_s[w][gslot][D + j]) * dscale;
+          const _Float16 dh = (_Float16)dl;
+          dv[u] = pk_f16(dl, dl - (float)dh);
+          tv[u] = eidx + u < cnt ? (uint32_t)((pos >> 7) - 32 * blk) : 255u;
           jv[u] = j;
         }
-        *reinterpret_cast<uint16_t*>(&otb_s[buf][w][2 * lane]) = (uint16_t)(tbv[0] | (tbv[1] << 8));
-        float qv[2][GQ];
+        uint32_t qv[2][GQ];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
           if constexpr (GQ >= 4) {
 #pragma unroll
             for (int hh = 0; hh < GQ; hh += 4) {
-              const float4 q4 = *reinterpret_cast<const float4*>(&qt_s[jv[u]][hh]);
+              const uint4 q4 = *reinterpret_cast<const uint4*>(&qq_s[jv[u]][hh]);
               qv[u][hh] = q4.x; qv[u][hh + 1] = q4.y; qv[u][hh + 2] = q4.z; qv[u][hh + 3] = q4.w;
             }
           } else {
 #pragma unroll
-            for (int k2 = 0; k2 < GQ; ++k2) qv[u][k2] = qt_s[jv[u]][k2];
+            for (int k2 = 0; k2 < GQ; ++k2) qv[u][k2] = qq_s[jv[u]][k2];
           }
         }
 #pragma unroll
-        for (int hh = 0; hh < GQ; ++hh) {
-          const float x0 = qv[0][hh] * delta[0], x1 = qv[1][hh] * delta[1];
-          const uint32_t hv = pk_f16(x0, x1);
-          *reinterpret_cast<uint32_t*>(&ocb_s[buf][w][hh][2 * lane]) = hv;
-          *reinterpret_cast<uint32_t*>(&ocb_s[buf][w][GQ + hh][2 * lane]) = pk_f16(x0 - lo_f16(hv), x1 - hi_f16(hv));
-        }
+        for (int hh = 0; hh < GQ; ++hh)
+          *reinterpret_cast<uint2*>(&oq_s[buf][w][hh][eidx]) = make_uint2(qv[0][hh], qv[1][hh]);
+        OutEntries oe;
+        oe.t0 = tv[0];
+        oe.t1 = tv[1];
+        oe.d0 = dv[0];
+        oe.d1 = dv[1];
+        oe.cnt = cnt;
         // token-sorted: the entries of tile A (tokens 0..15) come first
-        return (int)__popcll(__ballot(tbv[0] < 16u)) + (int)__popcll(__ballot(tbv[1] < 16u));
+        oe.nA = (int)__popcll(__ballot(tv[0] < 16u)) + (int)__popcll(__ballot(tv[1] < 16u));
+        return oe;
       };
-      // Apply a staged chunk: one-hot MFMAs, 32 entries each, only for the
-      // tiles a 32-entry slice touches.
-      auto apply_entries = [&](int cnt, int nA, floatx4_t& CA, floatx4_t& CB, int buf) {
-        for (int ch = 0; ch < (cnt + 31) / 32; ++ch) {
-          const uint2 tb8 = *reinterpret_cast<const uint2*>(&otb_s[buf][w][32 * ch + 8 * lg]);
-          H8 cbv;
-          cbv.v = *reinterpret_cast<const uint4*>(&ocb_s[buf][w][ocol][32 * ch + 8 * lg]);
-          auto onehot = [&](uint32_t r) {
-            H8 o;
+      // Apply a staged pass: one MFMA per touched tile and 16-entry chunk k
+      // (lane group lg: entries 16k + 4lg + i, i < 4, held by lanes 2k, 2k + 1
+      // of its row).  Every chunk's q operand is read up front.
+      auto apply_entries = [&](const OutEntries& oe, floatx4_t& CA, floatx4_t& CB, int buf) {
+        uint4 qb[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              const uint32_t t = ((e < 4 ? tb8.x : tb8.y) >> (8 * (e & 3))) & 0xFFu;
-              o.h[e] = (t == r) ? (_Float16)1.f : (_Float16)0.f;
-            }
+        for (int k = 0; k < 8; ++k) qb[k] = *reinterpret_cast<const uint4*>(&oq_s[buf][w][hq][16 * k + 4 * lg]);
+        auto chunk = [&](auto kc) {
+          constexpr int k = decltype(kc)::value;
+          if (16 * k >= oe.cnt) return;
+          const uint32_t ta0 = row_bcast_u<2 * k>(oe.t0), ta1 = row_bcast_u<2 * k>(oe.t1);
+          const uint32_t da0 = row_bcast_u<2 * k>(oe.d0), da1 = row_bcast_u<2 * k>(oe.d1);
+          const uint32_t tb0 = row_bcast_u<2 * k + 1>(oe.t0), tb1 = row_bcast_u<2 * k + 1>(oe.t1);
+          const uint32_t db0 = row_bcast_u<2 * k + 1>(oe.d0), db1 = row_bcast_u<2 * k + 1>(oe.d1);
+          auto masked = [&](uint32_t row) {
+            H8 o;
+            o.u[0] = ta0 == row ? da0 : 0u;
+            o.u[1] = ta1 == row ? da1 : 0u;
+            o.u[2] = tb0 == row ? db0 : 0u;
+            o.u[3] = tb1 == row ? db1 : 0u;
             return o;
           };
-          if (32 * ch < nA) CA = __builtin_amdgcn_mfma_f32_16x16x32_f16(onehot((uint32_t)c).h, cbv.h, CA, 0, 0, 0);
-          if (32 * ch + 32 > nA) CB = __builtin_amdgcn_mfma_f32_16x16x32_f16(onehot((uint32_t)(16 + c)).h, cbv.h, CB, 0, 0, 0);
-        }
+          H8 qv;
+          qv.v = qb[k];
+          if (16 * k < oe.nA) CA = __builtin_amdgcn_mfma_f32_16x16x32_f16(masked((uint32_t)c).h, qv.h, CA, 0, 0, 0);
+          if (16 * k + 16 > oe.nA) CB = __builtin_amdgcn_mfma_f32_16x16x32_f16(masked((uint32_t)(16 + c)).h, qv.h, CB, 0, 0, 0);
+        };
+        chunk(IntC<0>{});
+        chunk(IntC<1>{});
+        chunk(IntC<2>{});
+        chunk(IntC<3>{});
+        chunk(IntC<4>{});
+        chunk(IntC<5>{});
+        chunk(IntC<6>{});
+        chunk(IntC<7>{});
       };
 
       // Block i computes with its outlier entries staged in buffer i & 1; with
       // the skew, the entries of block i + 1 (nx1) are staged here, a whole
       // step before they are applied, so their LDS round trips overlap work.
-      int pend_cnt = 0, pend_nA = 0;  // staged entries of the block computed next
+      OutEntries pend;  // staged entries of the block computed next (skewed staging)
       auto process = [&](const ColdBlock<VB>& cur, int blk, const ColdBlock<VB>& nx1, int blk1,
                          int gslot, int gslot1, int buf) {
         const int e0 = cur.e0, ne = cur.ne;
-        int cnt0, nA0;
+        OutEntries oe0;
         if constexpr (kSkew) {
-          cnt0 = pend_cnt;
-          nA0 = pend_nA;
+          oe0 = pend;
         } else {
-          cnt0 = min(128, ne);
-          nA0 = stage_entries(cur.ent, cnt0, blk, 0, gslot);
+          oe0 = stage_entries(cur.ent, min(128, ne), blk, 0, gslot);
         }
         floatx4_t CA, CB;
         qk_pair(cur.kA, cur.kB, CA, CB);
         if constexpr (!kSkew) wave_sync();
-        apply_entries(cnt0, nA0, CA, CB, kSkew ? buf : 0);
+        apply_entries(oe0, CA, CB, kSkew ? buf : 0);
         if constexpr (kSkew) {
-          // next block's entries into the other buffer: independent of the
+          // next block's entries into the other set: independent of the
           // rest of this step, so the scheduler interleaves it with softmax/PV
-          pend_cnt = min(128, nx1.ne);
-          pend_nA = stage_entries(nx1.ent, pend_cnt, blk1, buf ^ 1, gslot1);
+          pend = stage_entries(nx1.ent, min(128, nx1.ne), blk1, buf ^ 1, gslot1);
         }
         if (ne > 128) {
           // rare (> 128 entries in one block): read each further chunk and
@@ -913,13 +952,13 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
           const uint32_t* __restrict__ oent = oent_all + (size_t)cur.obase * cap;
           for (int base = 128; base < ne; base += 128) {
             const int cnt = min(128, ne - base);
-            const int i0 = e0 + base + 2 * lane;
+            const int i0 = e0 + base + eidx;
             const uint32_t x0 = oent[min(i0, capm1)], x1 = oent[min(i0 + 1, capm1)];
             __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
             wave_sync();
-            const int nA = stage_entries(make_uint2(x0, x1), cnt, blk, kSkew ? buf : 0, gslot);
+            const OutEntries ex = stage_entries(make_uint2(x0, x1), cnt, blk, kSkew ? buf : 0, gslot);
             wave_sync();
-            apply_entries(cnt, nA, CA, CB, kSkew ? buf : 0);
+            apply_entries(ex, CA, CB, kSkew ? buf : 0);
           }
         }
         wave_sync();
@@ -968,8 +1007,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       for (int s = 0; s < kColdBuf - 1; ++s) load_next(ring[s]);
       if constexpr (kSkew) {
         wave_sync();
-        pend_cnt = min(128, ring[0].ne);
-        pend_nA = stage_entries(ring[0].ent, pend_cnt, 0, 0, 0);
+        pend = stage_entries(ring[0].ent, min(128, ring[0].ne), 0, 0, 0);
       }
       for (int i = 0; i < T; i += kColdBuf) {
 #pragma unroll
