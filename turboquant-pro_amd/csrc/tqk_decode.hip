@@ -350,8 +350,8 @@ union H8 {
   uint4 v;
 };
 
-constexpr int kMThreads = 512;   // 8 waves
-constexpr int kMWaves = 8;
+constexpr int kMWaves = 8;                 // waves per workgroup (two per SIMD)
+constexpr int kMThreads = 64 * kMWaves;
 #ifndef TQK_COLD_BUFFERS
 #define TQK_COLD_BUFFERS 3
 #endif
@@ -891,12 +891,15 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       // (lane group lg: entries 16k + 4lg + i, i < 4, held by lanes 2k, 2k + 1
       // of its row).  Every chunk's q operand is read up front.
       auto apply_entries = [&](const OutEntries& oe, floatx4_t& CA, floatx4_t& CB, int buf) {
+        // wave-uniform counts, so the chunk tests below are plain scalar branches
+        const int cnt = __builtin_amdgcn_readfirstlane(oe.cnt);
+        const int nA = __builtin_amdgcn_readfirstlane(oe.nA);
         uint4 qb[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k) qb[k] = *reinterpret_cast<const uint4*>(&oq_s[buf][w][hq][16 * k + 4 * lg]);
         auto chunk = [&](auto kc) {
           constexpr int k = decltype(kc)::value;
-          if (16 * k >= oe.cnt) return;
+          if (16 * k >= cnt) return;
           const uint32_t ta0 = row_bcast_u<2 * k>(oe.t0), ta1 = row_bcast_u<2 * k>(oe.t1);
           const uint32_t da0 = row_bcast_u<2 * k>(oe.d0), da1 = row_bcast_u<2 * k>(oe.d1);
           const uint32_t tb0 = row_bcast_u<2 * k + 1>(oe.t0), tb1 = row_bcast_u<2 * k + 1>(oe.t1);
@@ -911,8 +914,8 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
           };
           H8 qv;
           qv.v = qb[k];
-          if (16 * k < oe.nA) CA = __builtin_amdgcn_mfma_f32_16x16x32_f16(masked((uint32_t)c).h, qv.h, CA, 0, 0, 0);
-          if (16 * k + 16 > oe.nA) CB = __builtin_amdgcn_mfma_f32_16x16x32_f16(masked((uint32_t)(16 + c)).h, qv.h, CB, 0, 0, 0);
+          if (16 * k < nA) CA = __builtin_amdgcn_mfma_f32_16x16x32_f16(masked((uint32_t)c).h, qv.h, CA, 0, 0, 0);
+          if (16 * k + 16 > nA) CB = __builtin_amdgcn_mfma_f32_16x16x32_f16(masked((uint32_t)(16 + c)).h, qv.h, CB, 0, 0, 0);
         };
         chunk(IntC<0>{});
         chunk(IntC<1>{});
@@ -1193,10 +1196,10 @@ Plan make_plan(const tqk_cache_desc* d, int batch, int max_len) {
   if (mfma_path(*d)) {
     // MFMA kernel: eight waves per workgroup, one group per wave at a time;
     // aim for about two workgroups per CU over the whole launch
-    int gpw = (int)((units + 8L * 512 - 1) / (8L * 512));
+    int gpw = (int)((units + (long)kMWaves * 512 - 1) / ((long)kMWaves * 512));
     if (gpw < 1) gpw = 1;
-    if (gpw > kMaxGPS / 8) gpw = kMaxGPS / 8;  // group metadata of a split lives in LDS
-    gps = 8 * gpw;
+    if (gpw > kMaxGPS / kMWaves) gpw = kMaxGPS / kMWaves;  // group metadata of a split lives in LDS
+    gps = kMWaves * gpw;
   } else {
     gps = (int)((units + 4095) / 4096);
     if (gps < 1) gps = 1;
