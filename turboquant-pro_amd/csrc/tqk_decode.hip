@@ -510,16 +510,31 @@ template <int I>
 __device__ __forceinline__ uint32_t row_bcast_u(uint32_t x) {
   return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x150 + I, 0xF, 0xF, false);
 }
+// d of lane L of this lane's 16-lane row if byte I of tw equals row, else 0:
+// a byte-select (SDWA) compare, then a select whose data operand is read
+// from lane L by DPP; the s_nop covers the VALU write of VCC before its use
+// as a lane mask.
+template <int L, int I>
+__device__ __forceinline__ uint32_t row_select(uint32_t tw, uint32_t row, uint32_t d, uint32_t zero) {
+  uint32_t out;
+  asm("v_cmp_ne_u32_sdwa vcc, %1, %2 src0_sel:BYTE_%5 src1_sel:DWORD\n\t"
+      "s_nop 1\n\t"
+      "v_cndmask_b32_dpp %0, %3, %4, vcc row_newbcast:%6 row_mask:0xf bank_mask:0xf"
+      : "=v"(out)
+      : "v"(tw), "v"(row), "v"(d), "v"(zero), "i"(I), "i"(L)
+      : "vcc");
+  return out;
+}
 template <int K>
 struct IntC {
   static constexpr int value = K;
 };
 
-// Outlier entries of one block as this lane holds them (two entries): token in
-// the block (255 = none) and fp16 {hi, lo} of (val - mean) * s / 2, plus the
+// Outlier entries of one block as this lane holds them (two entries): fp16
+// {hi, lo} of (val - mean) * s / 2 (their tokens are staged in LDS), plus the
 // block's entry count (<= 128 per pass) and how many fall in tile A.
 struct OutEntries {
-  uint32_t t0, t1, d0, d1;
+  uint32_t d0, d1;
   int cnt, nA;
 };
 
@@ -572,12 +587,12 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   __shared__ __align__(16) float q_h_s[GQ][D + 4];
   // (nf4_scale[128], nf4_mean[128]) of a wave's current and next group
   __shared__ __align__(16) float gsm_s[kMWaves][2][2 * D];
-  // outlier correction B operands of a block (two sets when the staging of
-  // the next block is skewed one step ahead): per head, each entry's raw fp16
-  // q twice
-  constexpr bool kSkew = GQ <= 4;
-  constexpr int kOB = kSkew ? 2 : 1;
-  __shared__ __align__(16) uint32_t oq_s[kOB][kMWaves][GQ][132];  // rows 4 banks apart
+  // outlier correction B operand of the block computed next: per head, each
+  // entry's raw fp16 q twice (rows 4 banks apart)
+  __shared__ __align__(16) uint32_t oq_s[kMWaves][GQ][132];
+  // ... and each entry's token in the block (255 = none): byte 4k + i of row
+  // lg is slot i of lane group lg in 16-entry chunk k
+  __shared__ __align__(16) uint8_t otb_s[kMWaves][4][32];
   // NF4 levels [0, 16) and value centroids [16, 16 + 2^vb), for the table fill
   __shared__ float lvl_s[32];
   if (tid < 16) lvl_s[tid] = kNF4[tid];
@@ -775,25 +790,6 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         r.u[3] = t1.y;
         return r;
       };
-      // both tiles' QK^T: every table read is issued before the first MFMA,
-      // so the LDS latency is paid once per block, not once per MFMA
-      auto qk_pair = [&](const uint4& ka, const uint4& kb, floatx4_t& CA, floatx4_t& CB) {
-        H8 xa[8], xb[8];
-#pragma unroll
-        for (int m = 0; m < 8; ++m) {
-          xa[m] = key_quad(ka, m);
-          xb[m] = key_quad(kb, m);
-        }
-        // keep the reads ahead of the MFMAs (GQ = 8 has no registers to spare)
-        if constexpr (GQ <= 4) __builtin_amdgcn_sched_barrier(0);
-        CA = binit;
-        CB = binit;
-#pragma unroll
-        for (int m = 0; m < 8; ++m) {
-          CA = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[m].h, Bw[m].h, CA, 0, 0, 0);
-          CB = __builtin_amdgcn_mfma_f32_16x16x32_f16(xb[m].h, Bw[m].h, CB, 0, 0, 0);
-        }
-      };
       // B operand of PV MFMA (nt, tile) from value unit un: fields 2nt (tokens
       // 0, 1 of the unit, channel 8c + nt) and 2nt + 1 (tokens 2, 3), each a
       // table row {fp16 hi pair, fp16 lo pair}: k-slots [hi t0, hi t1, lo t0,
@@ -820,22 +816,6 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         r.u[3] = r1.y;
         return r;
       };
-      // PV for both tiles: O[row][8c + nt] += P[row][token] * V[token][8c + nt],
-      // row = head hi (< 8) or lo (>= 8) weight, 16 tokens of one tile per MFMA.
-      auto pv_pair = [&](const uint4& uA, const uint4& uB, const H8& pa, const H8& pb) {
-        H8 va[8], vb[8];
-#pragma unroll
-        for (int nt = 0; nt < 8; ++nt) {
-          va[nt] = val_quad(uA, nt);
-          vb[nt] = val_quad(uB, nt);
-        }
-        if constexpr (GQ <= 4) __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int nt = 0; nt < 8; ++nt) st.O[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa.h, va[nt].h, st.O[nt], 0, 0, 0);
-#pragma unroll
-        for (int nt = 0; nt < 8; ++nt) st.O[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pb.h, vb[nt].h, st.O[nt], 0, 0, 0);
-      };
-
       // ---- sparse outliers, folded into the QK^T accumulators:
       //   C[t][col] += sum_e [t_e == t] * d_e * q_h[j_e],   d = (val - mean_j) * s / 2
       // with s = sm_scale * log2(e); the stored code of an outlier is the NF4
@@ -846,7 +826,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       // Stage a pass of <= 128 (token-sorted) entries: this lane's two in
       // registers, their q pairs per head into oq_s set buf.
       const float dscale = 0.5f * qscale;
-      auto stage_entries = [&](const uint2 ent, int cnt, int blk, int buf, int gslot) {
+      auto stage_entries = [&](const uint2 ent, int cnt, int blk, int gslot) {
         uint32_t tv[2], dv[2];
         int jv[2];
 #pragma unroll
@@ -876,10 +856,9 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         }
 #pragma unroll
         for (int hh = 0; hh < GQ; ++hh)
-          *reinterpret_cast<uint2*>(&oq_s[buf][w][hh][eidx]) = make_uint2(qv[0][hh], qv[1][hh]);
+          *reinterpret_cast<uint2*>(&oq_s[w][hh][eidx]) = make_uint2(qv[0][hh], qv[1][hh]);
+        *reinterpret_cast<uint16_t*>(&otb_s[w][lg][4 * (c >> 1) + 2 * (c & 1)]) = (uint16_t)(tv[0] | (tv[1] << 8));
         OutEntries oe;
-        oe.t0 = tv[0];
-        oe.t1 = tv[1];
         oe.d0 = dv[0];
         oe.d1 = dv[1];
         oe.cnt = cnt;
@@ -890,26 +869,28 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       // Apply a staged pass: one MFMA per touched tile and 16-entry chunk k
       // (lane group lg: entries 16k + 4lg + i, i < 4, held by lanes 2k, 2k + 1
       // of its row).  Every chunk's q operand is read up front.
-      auto apply_entries = [&](const OutEntries& oe, floatx4_t& CA, floatx4_t& CB, int buf) {
+      auto apply_entries = [&](const OutEntries& oe, floatx4_t& CA, floatx4_t& CB) {
         // wave-uniform counts, so the chunk tests below are plain scalar branches
         const int cnt = __builtin_amdgcn_readfirstlane(oe.cnt);
         const int nA = __builtin_amdgcn_readfirstlane(oe.nA);
+        const uint32_t zero = 0u;
+        // tokens of every chunk's four slots of this lane group (dword k = chunk k)
+        const uint4 tw03 = *reinterpret_cast<const uint4*>(&otb_s[w][lg][0]);
+        const uint4 tw47 = *reinterpret_cast<const uint4*>(&otb_s[w][lg][16]);
         uint4 qb[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) qb[k] = *reinterpret_cast<const uint4*>(&oq_s[buf][w][hq][16 * k + 4 * lg]);
+        for (int k = 0; k < 8; ++k) qb[k] = *reinterpret_cast<const uint4*>(&oq_s[w][hq][16 * k + 4 * lg]);
         auto chunk = [&](auto kc) {
           constexpr int k = decltype(kc)::value;
           if (16 * k >= cnt) return;
-          const uint32_t ta0 = row_bcast_u<2 * k>(oe.t0), ta1 = row_bcast_u<2 * k>(oe.t1);
-          const uint32_t da0 = row_bcast_u<2 * k>(oe.d0), da1 = row_bcast_u<2 * k>(oe.d1);
-          const uint32_t tb0 = row_bcast_u<2 * k + 1>(oe.t0), tb1 = row_bcast_u<2 * k + 1>(oe.t1);
-          const uint32_t db0 = row_bcast_u<2 * k + 1>(oe.d0), db1 = row_bcast_u<2 * k + 1>(oe.d1);
+          const uint32_t tw = k < 4 ? u4_word<k & 3>(tw03) : u4_word<k & 3>(tw47);
+          // slot i: entry u = i & 1 of lane 2k + (i >> 1)
           auto masked = [&](uint32_t row) {
             H8 o;
-            o.u[0] = ta0 == row ? da0 : 0u;
-            o.u[1] = ta1 == row ? da1 : 0u;
-            o.u[2] = tb0 == row ? db0 : 0u;
-            o.u[3] = tb1 == row ? db1 : 0u;
+            o.u[0] = row_select<2 * k, 0>(tw, row, oe.d0, zero);
+            o.u[1] = row_select<2 * k, 1>(tw, row, oe.d1, zero);
+            o.u[2] = row_select<2 * k + 1, 2>(tw, row, oe.d0, zero);
+            o.u[3] = row_select<2 * k + 1, 3>(tw, row, oe.d1, zero);
             return o;
           };
           H8 qv;
@@ -927,28 +908,35 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         chunk(IntC<7>{});
       };
 
-      // Block i computes with its outlier entries staged in buffer i & 1; with
-      // the skew, the entries of block i + 1 (nx1) are staged here, a whole
-      // step before they are applied, so their LDS round trips overlap work.
-      OutEntries pend;  // staged entries of the block computed next (skewed staging)
+      // Software pipeline over a wave's blocks.  Step i starts with the QK^T
+      // accumulators of block i (computed at the end of step i - 1) and the
+      // entries of block i (staged in step i - 1): it adds the outliers, runs
+      // the softmax, then interleaves block i's PV with block i + 1's QK^T so
+      // that the table reads of one overlap the MFMAs of the other.
+      OutEntries pend;          // staged outlier entries of the block computed next
+      floatx4_t CAn, CBn;       // QK^T (with the bias) of the block computed next
+      auto key_tile = [&](const uint4& k, H8 (&x)[8]) {
+#pragma unroll
+        for (int m = 0; m < 8; ++m) x[m] = key_quad(k, m);
+      };
+      auto qk_tile = [&](const H8 (&x)[8], floatx4_t& C) {
+        C = binit;
+#pragma unroll
+        for (int m = 0; m < 8; ++m) C = __builtin_amdgcn_mfma_f32_16x16x32_f16(x[m].h, Bw[m].h, C, 0, 0, 0);
+      };
+      auto val_tile = [&](const uint4& u, H8 (&v)[8]) {
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) v[nt] = val_quad(u, nt);
+      };
+      auto pv_tile = [&](const H8& pw, const H8 (&v)[8]) {
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) st.O[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pw.h, v[nt].h, st.O[nt], 0, 0, 0);
+      };
       auto process = [&](const ColdBlock<VB>& cur, int blk, const ColdBlock<VB>& nx1, int blk1,
-                         int gslot, int gslot1, int buf) {
+                         int gslot, int gslot1) {
         const int e0 = cur.e0, ne = cur.ne;
-        OutEntries oe0;
-        if constexpr (kSkew) {
-          oe0 = pend;
-        } else {
-          oe0 = stage_entries(cur.ent, min(128, ne), blk, 0, gslot);
-        }
-        floatx4_t CA, CB;
-        qk_pair(cur.kA, cur.kB, CA, CB);
-        if constexpr (!kSkew) wave_sync();
-        apply_entries(oe0, CA, CB, kSkew ? buf : 0);
-        if constexpr (kSkew) {
-          // next block's entries into the other set: independent of the
-          // rest of this step, so the scheduler interleaves it with softmax/PV
-          pend = stage_entries(nx1.ent, min(128, nx1.ne), blk1, buf ^ 1, gslot1);
-        }
+        floatx4_t CA = CAn, CB = CBn;
+        apply_entries(pend, CA, CB);
         if (ne > 128) {
           // rare (> 128 entries in one block): read each further chunk and
           // drain here, so the common path keeps exact wait counts
@@ -959,12 +947,15 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
             const uint32_t x0 = oent[min(i0, capm1)], x1 = oent[min(i0 + 1, capm1)];
             __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
             wave_sync();
-            const OutEntries ex = stage_entries(make_uint2(x0, x1), cnt, blk, kSkew ? buf : 0, gslot);
+            const OutEntries ex = stage_entries(make_uint2(x0, x1), cnt, blk, gslot);
             wave_sync();
-            apply_entries(ex, CA, CB, kSkew ? buf : 0);
+            apply_entries(ex, CA, CB);
           }
         }
+        // next block's entries: the staging buffer's reads above come first in
+        // the wave's (in-order) LDS stream
         wave_sync();
+        pend = stage_entries(nx1.ent, min(128, nx1.ne), blk1, gslot1);
         float sc[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -977,23 +968,32 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
                                p[2] * row_bcast<2>(cur.nv), p[3] * row_bcast<3>(cur.nv), lo_sel);
         const H8 pb = dup_quad(p[4] * row_bcast<4>(cur.nv), p[5] * row_bcast<5>(cur.nv),
                                p[6] * row_bcast<6>(cur.nv), p[7] * row_bcast<7>(cur.nv), lo_sel);
-        pv_pair(cur.uA, cur.uB, pa, pb);
+        H8 va[8], xa[8], vb[8], xb[8];
+        // phase order fixed for GQ <= 4 (GQ = 8 has no registers to spare)
+        val_tile(cur.uA, va);
+        key_tile(nx1.kA, xa);
+        if constexpr (GQ <= 4) __builtin_amdgcn_sched_barrier(0);
+        pv_tile(pa, va);
+        val_tile(cur.uB, vb);
+        if constexpr (GQ <= 4) __builtin_amdgcn_sched_barrier(0);
+        qk_tile(xa, CAn);
+        key_tile(nx1.kB, xb);
+        if constexpr (GQ <= 4) __builtin_amdgcn_sched_barrier(0);
+        pv_tile(pb, vb);
+        qk_tile(xb, CBn);
       };
-
-
 
     // A ring of kColdBuf buffers, kColdBuf - 1 blocks in flight: step i
     // issues the loads of block i + kColdBuf - 1 and computes block i.
-    int jp = 0, kbp = 0, ip = 0;  // computed block: wave group jp, block kbp, stream index ip
+    int jp = 0, kbp = 0;  // computed block: wave group jp, block kbp
     auto step = [&](const ColdBlock<VB>& cur, ColdBlock<VB>& nxt, const ColdBlock<VB>& nx1) {
       store_group_stats();
       load_group_stats(jl);  // group of the block load_next fetches now
       wave_sync();
-      if (kbp == 0) begin_group(jp);
+      const bool last = kbp + 1 == nblk;  // block i + 1 starts wave group jp + 1
+      if (last) begin_group(jp + 1);     // weights for the QK^T of block i + 1
       load_next(nxt);
-      const bool last = kbp + 1 == nblk;
-      process(cur, kbp, nx1, last ? 0 : kbp + 1, jp & 1, last ? (jp + 1) & 1 : jp & 1, ip & 1);
-      ++ip;
+      process(cur, kbp, nx1, last ? 0 : kbp + 1, jp & 1, last ? (jp + 1) & 1 : jp & 1);
       if (++kbp == nblk) {
         kbp = 0;
         ++jp;
@@ -1008,9 +1008,15 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       ColdBlock<VB> ring[kColdBuf];
 #pragma unroll
       for (int s = 0; s < kColdBuf - 1; ++s) load_next(ring[s]);
-      if constexpr (kSkew) {
-        wave_sync();
-        pend = stage_entries(ring[0].ent, min(128, ring[0].ne), 0, 0, 0);
+      wave_sync();
+      begin_group(0);
+      pend = stage_entries(ring[0].ent, min(128, ring[0].ne), 0, 0);
+      {
+        H8 x[8];
+        key_tile(ring[0].kA, x);
+        qk_tile(x, CAn);
+        key_tile(ring[0].kB, x);
+        qk_tile(x, CBn);
       }
       for (int i = 0; i < T; i += kColdBuf) {
 #pragma unroll
