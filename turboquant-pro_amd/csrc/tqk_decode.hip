@@ -29,6 +29,7 @@ struct DecodeArgs {
   int groups_per_split;
   int hot_per_split;
   int split_base;  // added to blockIdx.x (hot-only launches start after the coded splits)
+  int batch;
 };
 
 struct MergeArgs {
@@ -570,7 +571,25 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   constexpr int D = TQK_D;
   constexpr int VROW = D * VB / 8;
   constexpr int UNIT = VROW / 4;
-  const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  // 1-D grid: every coded split of every (seq, kv head) first, then the hot
+  // splits, so that the long workgroups fill whole rounds of CUs and the short
+  // hot ones come last
+  int split, h, b;
+  {
+    const int Hkv_ = a.d.n_kv_heads, ncs = a.n_cold_splits, nhs = a.n_hot_splits;
+    const int ncold = ncs * Hkv_ * a.batch;
+    int item = blockIdx.x;
+    if (item < ncold) {
+      split = item % ncs;
+      item /= ncs;
+    } else {
+      item -= ncold;
+      split = ncs + item % nhs;
+      item /= nhs;
+    }
+    h = item % Hkv_;
+    b = item / Hkv_;
+  }
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, lg = lane >> 4, c = lane & 15;
   const tqk_cache_desc& d = a.d;
   const int Hkv = d.n_kv_heads, Hq = d.n_q_heads, G = d.group_tokens, P = d.page_tokens;
@@ -1227,10 +1246,12 @@ hipError_t launch_split(const DecodeArgs& a, dim3 grid, hipStream_t st) {
       hipLaunchKernelGGL((tqk_decode_split_valu<GQ, 4>), grid, dim3(kThreads), 0, st, a);
     return hipGetLastError();
   }
+  // one-dimensional over (split, kv head, seq) items
+  const dim3 g1(grid.x * grid.y * grid.z);
   if (a.d.value_bits == 3)
-    hipLaunchKernelGGL((tqk_decode_split_mfma<GQ, 3>), grid, dim3(kMThreads), 0, st, a);
+    hipLaunchKernelGGL((tqk_decode_split_mfma<GQ, 3>), g1, dim3(kMThreads), 0, st, a);
   else
-    hipLaunchKernelGGL((tqk_decode_split_mfma<GQ, 4>), grid, dim3(kMThreads), 0, st, a);
+    hipLaunchKernelGGL((tqk_decode_split_mfma<GQ, 4>), g1, dim3(kMThreads), 0, st, a);
   return hipGetLastError();
 }
 
@@ -1251,6 +1272,7 @@ DecodeArgs make_args(const tqk_cache_desc* d, const tqk_cache_ptrs* p, const Pla
   a.groups_per_split = pl.groups_per_split;
   a.hot_per_split = pl.hot_per_split;
   a.split_base = 0;
+  a.batch = batch;
   return a;
 }
 
