@@ -1207,6 +1207,15 @@ struct Plan {
   size_t ws_bytes;
 };
 
+// compute units of the current device (the plan sizes the launch for them)
+int device_cus() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1)
+    n = 256;
+  return n;
+}
+
 Plan make_plan(const tqk_cache_desc* d, int batch, int max_len) {
   Plan pl{};
   const int G = d->group_tokens;
@@ -1219,12 +1228,26 @@ Plan make_plan(const tqk_cache_desc* d, int batch, int max_len) {
   const long units = (long)batch * d->n_kv_heads * (ngmax > 0 ? ngmax : 0);
   int gps;
   if (mfma_path(*d)) {
-    // MFMA kernel: eight waves per workgroup, one group per wave at a time;
-    // aim for about two workgroups per CU over the whole launch
-    int gpw = (int)((units + (long)kMWaves * 512 - 1) / ((long)kMWaves * 512));
-    if (gpw < 1) gpw = 1;
-    if (gpw > kMaxGPS / kMWaves) gpw = kMaxGPS / kMWaves;  // group metadata of a split lives in LDS
-    gps = kMWaves * gpw;
+    // MFMA kernel: one workgroup per CU at a time (its LDS), eight waves
+    // each walking every eighth group of the split.  Pick the groups per wave
+    // (<= kMaxGPS / 8: a split's group metadata lives in LDS) that minimises
+    // rounds of CUs x groups per wave in the longest split, plus about a
+    // third of a group of per-workgroup set-up (code tables, fold).
+    const int ncu = device_cus();
+    double best = 1e30;
+    int gpw_best = 1;
+    for (int gpw = 1; gpw <= kMaxGPS / kMWaves; ++gpw) {
+      const long g = (long)kMWaves * gpw;
+      const long items = (long)batch * d->n_kv_heads * ((ngmax + g - 1) / g);
+      const long rounds = (items + ncu - 1) / ncu;
+      const long per_wave = ((ngmax < g ? ngmax : g) + kMWaves - 1) / kMWaves;
+      const double cost = (double)rounds * ((double)per_wave + 0.35);
+      if (cost < best - 1e-9) {
+        best = cost;
+        gpw_best = gpw;
+      }
+    }
+    gps = kMWaves * gpw_best;
   } else {
     gps = (int)((units + 4095) / 4096);
     if (gps < 1) gps = 1;
