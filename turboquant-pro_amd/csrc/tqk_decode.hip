@@ -40,6 +40,7 @@ struct MergeArgs {
   int n_cold_splits;
   int n_splits;
   int n_q_heads;
+  int n_kv_heads;
   float* out;       // normalised output, or nullptr
   float* m_out;     // partial-state outputs (when out == nullptr)
   float* l_out;
@@ -1161,38 +1162,72 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   }
 }
 
-// One workgroup per (query head, sequence), one thread per channel.
-__global__ __launch_bounds__(TQK_D) void tqk_merge(MergeArgs a) {
+// One workgroup per (kv head, sequence): thread (half, j) merges the splits of
+// query heads half, half + 2, ... for channel j, rotates their coded part back
+// (sum_k acc[k] * Pi[k][j]) and adds the hot part (turboquant_pro/kv_fused.py:139-153).
+// Pi is staged in LDS once (every thread's wide loads issued before its
+// stores) and shared by the GQ query heads.
+constexpr int kMergeThreads = 2 * TQK_D;
+__global__ __launch_bounds__(kMergeThreads) void tqk_merge(MergeArgs a) {
   constexpr int D = TQK_D;
-  const int qh = blockIdx.x, b = blockIdx.y, j = threadIdx.x;
-  const size_t base = ((size_t)b * a.n_q_heads + qh) * a.n_splits;
-  __shared__ float crot_s[D];
-  float M = -INFINITY;
-  for (int s = 0; s < a.n_splits; ++s)
-    if (a.pl[base + s] > 0.f) M = fmaxf(M, a.pm[base + s]);
-  float den = 0.f, cr = 0.f, hr = 0.f;
-  for (int s = 0; s < a.n_splits; ++s) {
-    const float l = a.pl[base + s];
-    if (l > 0.f) {
-      const float w = __expf(a.pm[base + s] - M);
-      den += l * w;
-      const float v = a.pacc[(base + s) * D + j] * w;
-      if (s < a.n_cold_splits) cr += v; else hr += v;
+  const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  const int j = tid & (D - 1), half = tid / D;
+  const int GQ = a.n_q_heads / a.n_kv_heads;
+  __shared__ __align__(16) float pi_s[D * D];
+  __shared__ float crot_s[8][D];
+  {
+    constexpr int NV = D * D / 4 / kMergeThreads;
+    float4 v[NV];
+#pragma unroll
+    for (int r = 0; r < NV; ++r) v[r] = reinterpret_cast<const float4*>(a.pi)[tid + r * kMergeThreads];
+#pragma unroll
+    for (int r = 0; r < NV; ++r) reinterpret_cast<float4*>(pi_s)[tid + r * kMergeThreads] = v[r];
+  }
+  float hr[4], den[4], mx[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int qi = half + 2 * u;
+    hr[u] = den[u] = 0.f;
+    mx[u] = -INFINITY;
+    if (qi < GQ) {
+      const size_t base = ((size_t)b * a.n_q_heads + h * GQ + qi) * a.n_splits;
+      float M = -INFINITY;
+      for (int s = 0; s < a.n_splits; ++s)
+        if (a.pl[base + s] > 0.f) M = fmaxf(M, a.pm[base + s]);
+      float dn = 0.f, cr = 0.f, hh = 0.f;
+      for (int s = 0; s < a.n_splits; ++s) {
+        const float l = a.pl[base + s];
+        if (l > 0.f) {
+          const float wt = __expf(a.pm[base + s] - M);
+          dn += l * wt;
+          const float v = a.pacc[(base + s) * D + j] * wt;
+          if (s < a.n_cold_splits) cr += v; else hh += v;
+        }
+      }
+      crot_s[qi][j] = cr;
+      hr[u] = hh;
+      den[u] = dn;
+      mx[u] = M;
     }
   }
-  crot_s[j] = cr;
   __syncthreads();
-  float o = hr;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int qi = half + 2 * u;
+    if (qi < GQ) {
+      float o = hr[u];
 #pragma unroll 8
-  for (int k = 0; k < D; ++k) o += crot_s[k] * a.pi[k * D + j];
-  const size_t oi = ((size_t)b * a.n_q_heads + qh) * D + j;
-  if (a.out) {
-    a.out[oi] = o / den;
-  } else {
-    a.acc_out[oi] = o;
-    if (j == 0) {
-      a.m_out[(size_t)b * a.n_q_heads + qh] = M;
-      a.l_out[(size_t)b * a.n_q_heads + qh] = den;
+      for (int k = 0; k < D; ++k) o += crot_s[qi][k] * pi_s[k * D + j];
+      const size_t qh = (size_t)b * a.n_q_heads + h * GQ + qi;
+      if (a.out) {
+        a.out[qh * D + j] = o / den[u];
+      } else {
+        a.acc_out[qh * D + j] = o;
+        if (j == 0) {
+          a.m_out[qh] = mx[u];
+          a.l_out[qh] = den[u];
+        }
+      }
     }
   }
 }
@@ -1337,11 +1372,12 @@ int run_merge(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int batch, int m
   m.n_cold_splits = pl.n_cold_splits;
   m.n_splits = pl.n_cold_splits + pl.n_hot_splits;
   m.n_q_heads = d->n_q_heads;
+  m.n_kv_heads = d->n_kv_heads;
   m.out = out;
   m.m_out = m_out;
   m.l_out = l_out;
   m.acc_out = acc_out;
-  hipLaunchKernelGGL(tqk_merge, dim3(d->n_q_heads, batch), dim3(TQK_D), 0,
+  hipLaunchKernelGGL(tqk_merge, dim3(d->n_kv_heads, batch), dim3(kMergeThreads), 0,
                      reinterpret_cast<hipStream_t>(stream), m);
   return hipGetLastError() == hipSuccess ? TQK_OK : TQK_EHIP;
 }
