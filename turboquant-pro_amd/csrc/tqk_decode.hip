@@ -345,6 +345,14 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
 // current block is computed.
 // ---------------------------------------------------------------------------
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+typedef unsigned u32x3_t __attribute__((ext_vector_type(3)));
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+// dword 3 of a raw buffer resource on gfx9 (32-bit data, no swizzle)
+constexpr int kBufFlags = 0x00020000;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kBufFlags);
+}
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 union H8 {
   half8_t h;
@@ -630,7 +638,10 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       const uint32_t obase = (uint32_t)slot * (uint32_t)Hkv + (uint32_t)h;
       int v = 0;
       if (f < 16) {
-        if (f < G / 16) v = (int)page_row(a.p.block_table, d.max_pages_per_seq, b, g * G + 16 * f, P, d.n_pages, h);
+        // first row of tile f, relative to this head's page region
+        if (f < G / 16)
+          v = (int)(page_row(a.p.block_table, d.max_pages_per_seq, b, g * G + 16 * f, P, d.n_pages, h) -
+                    (size_t)h * d.n_pages * P);
       } else if (f < 16 + TQK_NOB) {
         v = min(a.p.ocount[(size_t)obase * TQK_NOB + (f - 16)], d.outlier_cap);
       } else if (f == 16 + TQK_NOB) {
@@ -709,34 +720,51 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     // 2k + 1 of the lane group's own row (DPP row broadcast reaches them)
     const int eidx = 16 * (c >> 1) + 4 * lg + 2 * (c & 1);
     auto meta = [&](int j, int f) { return __builtin_amdgcn_readfirstlane(meta_s[wu + kMWaves * j][f]); };
+    // buffer resources of this head's page regions (32-bit offsets:
+    // mfma_path() bounds a head's region below 4 GiB)
+    const uint32_t hrows = (uint32_t)d.n_pages * (uint32_t)P;
+    const __amdgpu_buffer_rsrc_t rk = buf_rsrc(a.p.kcodes + (size_t)h * hrows * (D / 2), hrows * (D / 2));
+    const __amdgpu_buffer_rsrc_t rv = buf_rsrc(a.p.vcodes + (size_t)h * hrows * VROW, hrows * VROW);
+    const __amdgpu_buffer_rsrc_t rn = buf_rsrc(a.p.vnorm + (size_t)h * hrows, hrows * 4u);
 
     // Every step issues the same loads (past the end: the last block again,
     // already in L2), so the waits on the oldest buffer stay exact.
     int jl = 0, kbl = 0, nl = 0;  // next block to load: wave group jl, block kbl, stream index nl
     auto load_next = [&](ColdBlock<VB>& cb) {
-      const size_t rowA = (size_t)(uint32_t)meta(jl, 2 * kbl);
-      const size_t rowB = (size_t)(uint32_t)meta(jl, 2 * kbl + 1);
+      // rows of the two tiles in this head's region (wave-uniform: SGPR offsets)
+      const uint32_t rowA = (uint32_t)meta(jl, 2 * kbl);
+      const uint32_t rowB = (uint32_t)meta(jl, 2 * kbl + 1);
       const uint32_t obase = (uint32_t)meta(jl, 16 + TQK_NOB);
       const int e0 = kbl == 0 ? 0 : meta(jl, 16 + kbl - 1);
       const int e1 = meta(jl, 16 + kbl);
-      cb.kA = *reinterpret_cast<const uint4*>(a.p.kcodes + rowA * (D / 2) + koffL);
-      cb.kB = *reinterpret_cast<const uint4*>(a.p.kcodes + rowB * (D / 2) + koffL);
-      const uint8_t* vA = a.p.vcodes + rowA * VROW + uoffL;
-      const uint8_t* vB = a.p.vcodes + rowB * VROW + uoffL;
-      if constexpr (VB == 3) {
-        const uint32_t* pA = reinterpret_cast<const uint32_t*>(vA);
-        const uint32_t* pB = reinterpret_cast<const uint32_t*>(vB);
-        cb.uA = make_uint4(pA[0], pA[1], pA[2], 0u);
-        cb.uB = make_uint4(pB[0], pB[1], pB[2], 0u);
-      } else {
-        cb.uA = *reinterpret_cast<const uint4*>(vA);
-        cb.uB = *reinterpret_cast<const uint4*>(vB);
+      {
+        const u32x4_t x = __builtin_amdgcn_raw_buffer_load_b128(rk, (int)koffL, (int)(rowA * (D / 2)), 0);
+        const u32x4_t y = __builtin_amdgcn_raw_buffer_load_b128(rk, (int)koffL, (int)(rowB * (D / 2)), 0);
+        cb.kA = make_uint4(x.x, x.y, x.z, x.w);
+        cb.kB = make_uint4(y.x, y.y, y.z, y.w);
       }
-      cb.nv = a.p.vnorm[((c & 4) ? rowB : rowA) + ntl];
-      const uint32_t* oe = oent_all + (size_t)obase * cap;
-      // entries past e1 are masked where they are used (the outlier pass)
-      const int i0 = e0 + eidx;
-      cb.ent = make_uint2(oe[min(i0, capm1)], oe[min(i0 + 1, capm1)]);
+      if constexpr (VB == 3) {
+        const u32x3_t x = __builtin_amdgcn_raw_buffer_load_b96(rv, (int)uoffL, (int)(rowA * VROW), 0);
+        const u32x3_t y = __builtin_amdgcn_raw_buffer_load_b96(rv, (int)uoffL, (int)(rowB * VROW), 0);
+        cb.uA = make_uint4(x.x, x.y, x.z, 0u);
+        cb.uB = make_uint4(y.x, y.y, y.z, 0u);
+      } else {
+        const u32x4_t x = __builtin_amdgcn_raw_buffer_load_b128(rv, (int)uoffL, (int)(rowA * VROW), 0);
+        const u32x4_t y = __builtin_amdgcn_raw_buffer_load_b128(rv, (int)uoffL, (int)(rowB * VROW), 0);
+        cb.uA = make_uint4(x.x, x.y, x.z, x.w);
+        cb.uB = make_uint4(y.x, y.y, y.z, y.w);
+      }
+      // (the lane's own tile row: with 16-token pages tile B may sit on a page
+      // below tile A's, so the row is picked per lane, not offset from rowA)
+      cb.nv = bitsf(__builtin_amdgcn_raw_buffer_load_b32(
+          rn, (int)(4u * (((c & 4) ? rowB : rowA) + (uint32_t)ntl)), 0, 0));
+      // the group's side-list as its own buffer: reads past its end return 0,
+      // reads past e1 are masked where they are used (the outlier pass)
+      const __amdgpu_buffer_rsrc_t ro = buf_rsrc(oent_all + (size_t)obase * cap, 4u * (uint32_t)cap);
+      {
+        const u32x2_t x = __builtin_amdgcn_raw_buffer_load_b64(ro, 4 * eidx, 4 * e0, 0);
+        cb.ent = make_uint2(x.x, x.y);
+      }
       cb.e0 = e0;
       cb.ne = e1 - e0;
       cb.obase = obase;
@@ -757,9 +785,11 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     float2 pend_s, pend_m;  // stats loaded by the previous step
     int pend_slot = 0;
     auto load_group_stats = [&](int j) {
-      const size_t mbase = (size_t)(uint32_t)meta(max(0, min(j, nw - 1)), 16 + TQK_NOB) * D;
-      pend_s = reinterpret_cast<const float2*>(a.p.gscale + mbase)[lane];
-      pend_m = reinterpret_cast<const float2*>(a.p.gmean + mbase)[lane];
+      const size_t mb = (size_t)D * (uint32_t)meta(max(0, min(j, nw - 1)), 16 + TQK_NOB);
+      const u32x2_t x = __builtin_amdgcn_raw_buffer_load_b64(buf_rsrc(a.p.gscale + mb, 4u * D), 8 * lane, 0, 0);
+      const u32x2_t y = __builtin_amdgcn_raw_buffer_load_b64(buf_rsrc(a.p.gmean + mb, 4u * D), 8 * lane, 0, 0);
+      pend_s = make_float2(bitsf(x.x), bitsf(x.y));
+      pend_m = make_float2(bitsf(y.x), bitsf(y.y));
       pend_slot = j & 1;
     };
     auto store_group_stats = [&]() {
@@ -1233,8 +1263,10 @@ __global__ __launch_bounds__(kMergeThreads) void tqk_merge(MergeArgs a) {
 }
 
 // The MFMA kernel needs tiled value codes and a hot ring of whole 32-token blocks.
+// (its loads use 32-bit buffer offsets: one head's page region stays below 4 GiB)
 __host__ __device__ inline bool mfma_path(const tqk_cache_desc& d) {
-  return v_tiled(d.group_tokens, d.page_tokens) && (d.hot_ring % 32 == 0);
+  return v_tiled(d.group_tokens, d.page_tokens) && (d.hot_ring % 32 == 0) &&
+         (long long)d.n_pages * d.page_tokens * (TQK_D / 2) < (1LL << 32);
 }
 
 struct Plan {

@@ -45,6 +45,33 @@ class CachePtrs(ctypes.Structure):
 _lib = None
 
 
+def load(path: str) -> ctypes.CDLL:
+    """Open a build of the library at ``path`` with every entry point's C
+    signature declared (pointer arguments stay 64-bit) and its ABI checked."""
+    l_ = ctypes.CDLL(path)
+    vp, i32, sz = ctypes.c_void_p, ctypes.c_int32, ctypes.c_size_t
+    pd, pp = ctypes.POINTER(CacheDesc), ctypes.POINTER(CachePtrs)
+    sig = {
+        "tqk_version": ([], ctypes.c_int),
+        "tqk_check_desc": ([pd], ctypes.c_int),
+        "tqk_decode_workspace_bytes": ([pd, i32, i32], sz),
+        "tqk_decode": ([pd, pp, i32, vp, vp, i32, vp, vp, sz, vp], ctypes.c_int),
+        "tqk_decode_partials": ([pd, pp, i32, vp, vp, i32, vp, vp, vp, vp, sz, vp], ctypes.c_int),
+        "tqk_decode_splits": ([pd, pp, i32, vp, vp, i32, vp, sz, vp], ctypes.c_int),
+        "tqk_decode_merge": ([pd, pp, i32, i32, vp, vp, sz, vp], ctypes.c_int),
+        "tqk_encode_groups": ([pd, pp, i32, i32, vp, vp, vp, vp, i32, vp, vp], ctypes.c_int),
+        "tqk_append_hot": ([pd, pp, i32, vp, vp, vp, vp, vp, i32, vp], ctypes.c_int),
+        "tqk_dequant_groups": ([pd, pp, i32, vp, vp, vp, vp], ctypes.c_int),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(l_, name)
+        fn.argtypes = args
+        fn.restype = res
+    if l_.tqk_version() != ABI_VERSION:
+        raise RuntimeError(f"libtqk ABI {l_.tqk_version()} != expected {ABI_VERSION}")
+    return l_
+
+
 def lib() -> ctypes.CDLL:
     """The loaded library (built in-tree by ``__graft_entry__.build()``)."""
     global _lib
@@ -53,28 +80,7 @@ def lib() -> ctypes.CDLL:
             raise RuntimeError(
                 f"{LIB_PATH} is missing: build the gfx950 library first "
                 "(python -c 'import __graft_entry__ as g; g.build()')")
-        l_ = ctypes.CDLL(LIB_PATH)
-        vp, i32, sz = ctypes.c_void_p, ctypes.c_int32, ctypes.c_size_t
-        pd, pp = ctypes.POINTER(CacheDesc), ctypes.POINTER(CachePtrs)
-        sig = {
-            "tqk_version": ([], ctypes.c_int),
-            "tqk_check_desc": ([pd], ctypes.c_int),
-            "tqk_decode_workspace_bytes": ([pd, i32, i32], sz),
-            "tqk_decode": ([pd, pp, i32, vp, vp, i32, vp, vp, sz, vp], ctypes.c_int),
-            "tqk_decode_partials": ([pd, pp, i32, vp, vp, i32, vp, vp, vp, vp, sz, vp], ctypes.c_int),
-            "tqk_decode_splits": ([pd, pp, i32, vp, vp, i32, vp, sz, vp], ctypes.c_int),
-            "tqk_decode_merge": ([pd, pp, i32, i32, vp, vp, sz, vp], ctypes.c_int),
-            "tqk_encode_groups": ([pd, pp, i32, i32, vp, vp, vp, vp, i32, vp, vp], ctypes.c_int),
-            "tqk_append_hot": ([pd, pp, i32, vp, vp, vp, vp, vp, i32, vp], ctypes.c_int),
-            "tqk_dequant_groups": ([pd, pp, i32, vp, vp, vp, vp], ctypes.c_int),
-        }
-        for name, (args, res) in sig.items():
-            fn = getattr(l_, name)
-            fn.argtypes = args
-            fn.restype = res
-        if l_.tqk_version() != ABI_VERSION:
-            raise RuntimeError(f"libtqk ABI {l_.tqk_version()} != expected {ABI_VERSION}")
-        _lib = l_
+        _lib = load(LIB_PATH)
     return _lib
 
 
