@@ -1196,6 +1196,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
 // Pi is staged in LDS once (every thread's wide loads issued before its
 // stores) and shared by the GQ query heads.
 constexpr int kMergeThreads = 2 * TQK_D;
+constexpr int kMergeFast = 8;  // split counts merged with all partial loads issued up front
 __global__ __launch_bounds__(kMergeThreads) void tqk_merge(MergeArgs a) {
   constexpr int D = TQK_D;
   const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
@@ -1203,6 +1204,25 @@ __global__ __launch_bounds__(kMergeThreads) void tqk_merge(MergeArgs a) {
   const int GQ = a.n_q_heads / a.n_kv_heads;
   __shared__ __align__(16) float pi_s[D * D];
   __shared__ float crot_s[8][D];
+  // every partial load of the thread's heads in flight at once when the
+  // split count allows (the partials were just written: each round trip is an
+  // L2 latency), then Pi's wide loads, then the combine
+  const bool fast = a.n_splits <= kMergeFast;
+  float vl[4][kMergeFast], vm[4][kMergeFast], va[4][kMergeFast];
+  if (fast) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int qi = half + 2 * u;
+      const size_t base = ((size_t)b * a.n_q_heads + h * GQ + qi) * a.n_splits;
+#pragma unroll
+      for (int s = 0; s < kMergeFast; ++s) {
+        const bool ok = qi < GQ && s < a.n_splits;
+        vl[u][s] = ok ? a.pl[base + s] : 0.f;
+        vm[u][s] = ok ? a.pm[base + s] : -INFINITY;
+        va[u][s] = ok ? a.pacc[(base + s) * D + j] : 0.f;
+      }
+    }
+  }
   {
     constexpr int NV = D * D / 4 / kMergeThreads;
     float4 v[NV];
@@ -1212,30 +1232,61 @@ __global__ __launch_bounds__(kMergeThreads) void tqk_merge(MergeArgs a) {
     for (int r = 0; r < NV; ++r) reinterpret_cast<float4*>(pi_s)[tid + r * kMergeThreads] = v[r];
   }
   float hr[4], den[4], mx[4];
+  // merge of query head qi's splits for channel j: M = max m over splits with
+  // l > 0, weights e^{m - M}; cold accumulators summed apart from the hot one
+  auto combine = [&](int u, int qi, const float* vl, const float* vm, const float* va, int ns) {
+    float M = -INFINITY;
+    for (int s = 0; s < ns; ++s)
+      if (vl[s] > 0.f) M = fmaxf(M, vm[s]);
+    float dn = 0.f, cr = 0.f, hh = 0.f;
+    for (int s = 0; s < ns; ++s) {
+      if (vl[s] > 0.f) {
+        const float wt = __expf(vm[s] - M);
+        dn += vl[s] * wt;
+        const float v = va[s] * wt;
+        if (s < a.n_cold_splits) cr += v; else hh += v;
+      }
+    }
+    crot_s[qi][j] = cr;
+    hr[u] = hh;
+    den[u] = dn;
+    mx[u] = M;
+  };
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
-    const int qi = half + 2 * u;
     hr[u] = den[u] = 0.f;
     mx[u] = -INFINITY;
-    if (qi < GQ) {
-      const size_t base = ((size_t)b * a.n_q_heads + h * GQ + qi) * a.n_splits;
-      float M = -INFINITY;
-      for (int s = 0; s < a.n_splits; ++s)
-        if (a.pl[base + s] > 0.f) M = fmaxf(M, a.pm[base + s]);
-      float dn = 0.f, cr = 0.f, hh = 0.f;
-      for (int s = 0; s < a.n_splits; ++s) {
-        const float l = a.pl[base + s];
-        if (l > 0.f) {
-          const float wt = __expf(a.pm[base + s] - M);
-          dn += l * wt;
-          const float v = a.pacc[(base + s) * D + j] * wt;
-          if (s < a.n_cold_splits) cr += v; else hh += v;
+  }
+  if (fast) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int qi = half + 2 * u;
+      if (qi < GQ) combine(u, qi, vl[u], vm[u], va[u], kMergeFast);
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int qi = half + 2 * u;
+      if (qi < GQ) {
+        const size_t base = ((size_t)b * a.n_q_heads + h * GQ + qi) * a.n_splits;
+        float M = -INFINITY;
+        for (int s = 0; s < a.n_splits; ++s)
+          if (a.pl[base + s] > 0.f) M = fmaxf(M, a.pm[base + s]);
+        float dn = 0.f, cr = 0.f, hh = 0.f;
+        for (int s = 0; s < a.n_splits; ++s) {
+          const float l = a.pl[base + s];
+          if (l > 0.f) {
+            const float wt = __expf(a.pm[base + s] - M);
+            dn += l * wt;
+            const float v = a.pacc[(base + s) * D + j] * wt;
+            if (s < a.n_cold_splits) cr += v; else hh += v;
+          }
         }
+        crot_s[qi][j] = cr;
+        hr[u] = hh;
+        den[u] = dn;
+        mx[u] = M;
       }
-      crot_s[qi][j] = cr;
-      hr[u] = hh;
-      den[u] = dn;
-      mx[u] = M;
     }
   }
   __syncthreads();
