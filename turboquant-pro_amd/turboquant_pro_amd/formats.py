@@ -118,3 +118,50 @@ def untile_value_rows(rows: np.ndarray, vb: int, D: int = 128) -> np.ndarray:
     vrow = D * vb // 8
     rows = np.asarray(rows, np.uint8).reshape(-1, 16 * vrow)
     return np.concatenate([untile_values(t, vb, D) for t in rows], axis=0)
+
+
+def unpack_keys(packed: np.ndarray, n_values: int) -> np.ndarray:
+    """Reference 4-bit key bytes -> flat codes (turboquant_pro/per_channel_kv.py:94-100):
+    byte n holds code 2n bit-reversed in its high nibble and code 2n + 1
+    bit-reversed in its low nibble."""
+    kp = np.asarray(packed, np.uint8).reshape(-1)
+    codes = np.empty(2 * kp.size, np.uint8)
+    codes[0::2] = _rev4(kp >> 4)
+    codes[1::2] = _rev4(kp & 0x0F)
+    return codes[:n_values]
+
+
+def mark_outlier_codes(kp: np.ndarray, idx: np.ndarray) -> np.ndarray:
+    """The stored form of reference key bytes: the NF4 zero level (code 7) at
+    every outlier position.  ``kp`` (H, G, D/2) packed codes, ``idx`` flat
+    positions into (H, G, D); the inverse of :func:`restore_outlier_codes`
+    up to the codes it recomputes."""
+    kp = np.array(kp, dtype=np.uint8, copy=True)
+    H, G, half = kp.shape
+    D = 2 * half
+    if idx.size == 0:
+        return kp
+    idx = idx.astype(np.int64)
+    h, t, j = idx // (G * D), (idx // D) % G, idx % D
+    nib = int(_rev4(np.array([NF4_ZERO_CODE]))[0])
+    for par in (0, 1):
+        m = (j % 2) == par
+        hh, tt, bb = h[m], t[m], j[m] // 2
+        byte = kp[hh, tt, bb]
+        kp[hh, tt, bb] = ((byte & 0x0F) | (nib << 4)) if par == 0 else ((byte & 0xF0) | nib)
+    return kp
+
+
+def unpack_values(packed: np.ndarray, n_values: int, bits: int) -> np.ndarray:
+    """Reference value bytes -> flat codes (turboquant_pro/core.py:400-441), the
+    inverse of :func:`pack_values`."""
+    b = np.asarray(packed, np.uint8).reshape(-1)
+    per = {2: 4, 3: 8, 4: 2}[bits]
+    if bits == 3:
+        b = np.concatenate([b, np.zeros((-b.size) % 3, np.uint8)]).reshape(-1, 3).astype(np.uint32)
+        word = b[:, 0] | (b[:, 1] << np.uint32(8)) | (b[:, 2] << np.uint32(16))
+    else:
+        word = b.astype(np.uint32)
+    mask = np.uint32((1 << bits) - 1)
+    codes = np.stack([(word >> np.uint32(bits * k)) & mask for k in range(per)], 1)
+    return codes.reshape(-1)[:n_values].astype(np.uint8)

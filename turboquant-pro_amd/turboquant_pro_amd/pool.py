@@ -23,7 +23,7 @@ import math
 import numpy as np
 
 from . import _native as N
-from .formats import pack_values, restore_outlier_codes, untile_value_rows
+from .formats import mark_outlier_codes, pack_values, restore_outlier_codes, untile_value_rows
 from .codebooks import (group_tokens_for, n_groups_for, outliers_per_channel, random_rotation,
                         value_codebook)
 
@@ -306,3 +306,57 @@ class TQKVPool:
             "vpacked": np.ascontiguousarray(vp).reshape(-1),
             "vnorms": vn.cpu().numpy(),
         }
+
+    def import_group(self, b: int, g: int, keys: dict | None = None, values: dict | None = None) -> None:
+        """Write group ``g`` of sequence ``b`` from the reference container
+        layout (the inverse of :meth:`export_group`).  ``keys``: ``kpacked``
+        (H*G*D/2 bytes), ``nf4_scale``/``nf4_mean`` (H, D), ``outlier_idx``
+        (flat over (H, G, D), token-major within a head as the reference emits
+        them) and ``outlier_val`` fp16, or ``None`` outliers; ``values``:
+        ``vpacked`` (reference pack of H*G*D codes) and ``vnorms`` (H, G).
+        Value codes stored per token only (a tiled pool raises)."""
+        torch = _torch()
+        H, G, D = self.n_kv_heads, self.group_tokens, self.head_dim
+        phys, off = self._rows(b, g)
+        slot = int(self.group_table[b, g])
+        if keys is not None:
+            kp = np.asarray(keys["kpacked"], np.uint8).reshape(H, G, D // 2)
+            oidx = keys.get("outlier_idx")
+            oval = keys.get("outlier_val")
+            oidx = np.zeros(0, np.int64) if oidx is None else np.asarray(oidx, np.int64).reshape(-1)
+            oval = np.zeros(0, np.float16) if oval is None else np.asarray(oval, np.float16).reshape(-1)
+            if oidx.size != oval.size:
+                raise ValueError("outlier_idx and outlier_val differ in length")
+            if oidx.size and (oidx.min() < 0 or oidx.max() >= H * G * D):
+                raise ValueError("outlier_idx outside the (H, G, D) block")
+            kp = mark_outlier_codes(kp, oidx)
+            self.kcodes[:, phys, off] = torch.from_numpy(kp).to(self.device)
+            self.gscale[slot] = torch.from_numpy(np.asarray(keys["nf4_scale"], np.float32).reshape(H, D)).to(self.device)
+            self.gmean[slot] = torch.from_numpy(np.asarray(keys["nf4_mean"], np.float32).reshape(H, D)).to(self.device)
+            h = oidx // (G * D)
+            pos = oidx % (G * D)  # token * D + channel within the head
+            cap = self.oent.shape[2]
+            ent = np.zeros((H, cap), np.uint32)
+            cnt = np.zeros((H, 8), np.int32)
+            for hh in range(H):
+                m = h == hh
+                ph = pos[m]
+                if ph.size > (cap if self.desc.outlier_cap > 0 else 0):
+                    raise ValueError("more outliers in a head than the pool's outlier_cap")
+                if ph.size > 1 and np.any(np.diff(ph) <= 0):
+                    raise ValueError("outliers of a head must be in ascending token-major order")
+                vals = oval[m].view(np.uint16).astype(np.uint32)
+                ent[hh, :ph.size] = ph.astype(np.uint32) | (vals << np.uint32(16))
+                tok = ph // D
+                for k in range(8):
+                    cnt[hh, k] = int(np.count_nonzero(tok < 32 * (k + 1)))
+            self.oent[slot] = torch.from_numpy(ent.view(np.int32)).to(self.device)
+            self.ocount[slot] = torch.from_numpy(cnt).to(self.device)
+        if values is not None:
+            if self.tiled:
+                raise NotImplementedError("import of value codes into a tiled pool")
+            vrow = D * self.value_bits // 8
+            vp = np.asarray(values["vpacked"], np.uint8)[: H * G * vrow].reshape(H, G, vrow)
+            self.vcodes[:, phys, off] = torch.from_numpy(np.ascontiguousarray(vp)).to(self.device)
+            self.vnorm[:, phys, off] = torch.from_numpy(
+                np.asarray(values["vnorms"], np.float32).reshape(H, G)).to(self.device)
