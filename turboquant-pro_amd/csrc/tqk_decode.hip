@@ -580,22 +580,17 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   constexpr int D = TQK_D;
   constexpr int VROW = D * VB / 8;
   constexpr int UNIT = VROW / 4;
-  // 1-D grid: every coded split of every (seq, kv head) first, then the hot
-  // splits, so that the long workgroups fill whole rounds of CUs and the short
-  // hot ones come last
+  // 1-D grid over (split, kv head, seq), split fastest.  Every workgroup
+  // streams the coded groups of its split and then its share of the fp16 hot
+  // window, and writes two partials: coded (index split) and hot (index
+  // n_cold_splits + split); a separate round of hot workgroups would only
+  // start as coded ones finish
   int split, h, b;
   {
-    const int Hkv_ = a.d.n_kv_heads, ncs = a.n_cold_splits, nhs = a.n_hot_splits;
-    const int ncold = ncs * Hkv_ * a.batch;
+    const int Hkv_ = a.d.n_kv_heads, ncs = a.n_cold_splits;
     int item = blockIdx.x;
-    if (item < ncold) {
-      split = item % ncs;
-      item /= ncs;
-    } else {
-      item -= ncold;
-      split = ncs + item % nhs;
-      item /= nhs;
-    }
+    split = item % ncs;
+    item /= ncs;
     h = item % Hkv_;
     b = item / Hkv_;
   }
@@ -606,7 +601,6 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   const int ng = n_groups_of(L, d.hot_window, G);
   // scores in the log2 domain: q * sm_scale * log2(e), softmax with exp2
   const float qscale = d.sm_scale * 1.4426950408889634f;
-  const bool hot = split >= a.n_cold_splits;
 
   __shared__ __align__(16) uint8_t lut[LutGeom<VB>::kBytes];
   __shared__ __align__(16) uint32_t qq_s[D][GQ];        // raw fp16 q twice {q, q}: [channel][head]
@@ -629,7 +623,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   // nothing but block loads: [0, 16) first row of each 16-token tile,
   // [16, 24) cumulative outlier bounds, [24] slot * Hkv + h.
   __shared__ int meta_s[kMaxGPS][kMetaInts];
-  if (!hot) {
+  {
     const int gbeg = split * a.groups_per_split;
     const int gcnt = max(0, min(ng, gbeg + a.groups_per_split) - gbeg);
     for (int x = tid; x < gcnt * kMetaInts; x += kMThreads) {
@@ -657,7 +651,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     q_h_s[i / D][i % D] = h2f((uint16_t)qr) * qscale;
   }
   __syncthreads();
-  if (!hot) {
+  {
     // unit u (8 bytes): key part first (entry u / copies, copy u % copies), then values;
     // consecutive lanes write consecutive units; levels come from LDS, so the
     // fill issues no memory loads
@@ -695,7 +689,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) st.O[nt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 
-  if (!hot) {
+  {
     constexpr int NC = LutGeom<VB>::kCopies;
     const uint32_t koff = (uint32_t)(lane % NC) * 8u;
     const uint32_t voff = LutGeom<VB>::kValOff + (uint32_t)(lane % NC) * 8u;
@@ -1074,8 +1068,18 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         }
       }
     }
-  } else {
-    // ---- fp16 hot window: tokens [n_cold, L) from the ring, 32-token blocks
+  }
+  // ---- this split's share of the fp16 hot window: tokens [n_cold, L) from
+  // the ring in 32-token blocks, block split * 8 + w onwards, in a fresh state
+  // (its partial is not rotated back, unlike the coded one).  The coded state
+  // waits in registers meanwhile: the code table, where the waves' states are
+  // folded, is still read by waves that have not finished their groups.
+  const WaveState cst = st;
+  st.m = -INFINITY;
+  st.l = 0.f;
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) st.O[nt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+  {
     const int n_cold = ng * G, R = d.hot_ring;
     const size_t hbase = ((size_t)b * Hkv + h) * R;
     const int nhb = (L - n_cold + 31) / 32;
@@ -1084,18 +1088,31 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
       Bq[ks].v = *reinterpret_cast<const uint4*>(a.q + ((size_t)b * Hq + h * GQ + hq) * D + 32 * ks + 8 * lg);
-    for (int hb = w; hb < nhb; hb += kMWaves) {
+    for (int hb = split * kMWaves + w; hb < nhb; hb += a.n_cold_splits * kMWaves) {
+      // n_cold and the ring size are multiples of 32: the block's 32 ring rows
+      // are consecutive and inside the ring, so every row is loaded (keys and
+      // values together) and rows at or past L are masked afterwards
       const int t0 = n_cold + 32 * hb;
-      const uint16_t* kr = a.p.hot_k + (hbase + (t0 % R)) * D;   // 32 consecutive ring rows
+      const uint16_t* kr = a.p.hot_k + (hbase + (t0 % R)) * D;
       const uint16_t* vr = a.p.hot_v + (hbase + (t0 % R)) * D;
+      H8 ka[4], kb[4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        ka[ks].v = *reinterpret_cast<const uint4*>(kr + (size_t)c * D + 32 * ks + 8 * lg);
+        kb[ks].v = *reinterpret_cast<const uint4*>(kr + (size_t)(16 + c) * D + 32 * ks + 8 * lg);
+      }
+      // values: token e of this lane (tile A 4lg+e, tile B 16+4lg+e), channels 8c..8c+7
+      uint4 vv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int tt = (e < 4) ? 4 * lg + e : 16 + 4 * lg + (e - 4);
+        vv[e] = *reinterpret_cast<const uint4*>(vr + (size_t)tt * D + 8 * c);
+      }
       floatx4_t CA = {0.f, 0.f, 0.f, 0.f}, CB = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        H8 ka, kb;
-        ka.v = *reinterpret_cast<const uint4*>(kr + (size_t)c * D + 32 * ks + 8 * lg);
-        kb.v = *reinterpret_cast<const uint4*>(kr + (size_t)(16 + c) * D + 32 * ks + 8 * lg);
-        CA = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka.h, Bq[ks].h, CA, 0, 0, 0);
-        CB = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb.h, Bq[ks].h, CB, 0, 0, 0);
+        CA = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[ks].h, Bq[ks].h, CA, 0, 0, 0);
+        CB = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb[ks].h, Bq[ks].h, CB, 0, 0, 0);
       }
       float s[8];
 #pragma unroll
@@ -1111,13 +1128,11 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         const _Float16 hi = (_Float16)p[e];
         pa.h[e] = is_hi ? hi : (_Float16)(p[e] - (float)hi);
       }
-      // values: token e of this lane (tile A 4lg+e, tile B 16+4lg+e), channels 8c..8c+7
-      uint4 vv[8];
+      // rows past L: zero (whatever the ring holds there, 0 * inf would be NaN)
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int tt = (e < 4) ? 4 * lg + e : 16 + 4 * lg + (e - 4);
-        vv[e] = (t0 + tt < L) ? *reinterpret_cast<const uint4*>(vr + (size_t)tt * D + 8 * c)
-                              : make_uint4(0u, 0u, 0u, 0u);
+        if (t0 + tt >= L) vv[e] = make_uint4(0u, 0u, 0u, 0u);
       }
 #pragma unroll
       for (int nt = 0; nt < 8; ++nt) {
@@ -1134,54 +1149,70 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     }
   }
 
-  // ---- fold the eight waves' states (the code table is no longer needed)
-  __syncthreads();
-  float* cm = reinterpret_cast<float*>(lut);  // [8][GQ]
-  float* cl = cm + kMWaves * GQ;              // [8][GQ]
-  float* co = cl + kMWaves * GQ;              // [8][GQ][D]
-  if (lg == 0 && c < GQ) {
-    cm[w * GQ + c] = st.m;
-    cl[w * GQ + c] = st.l;
-  }
-  // accumulator rows: r < 8 fp16-hi weights of head r, r >= 8 lo weights of head r - 8
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 4 * lg + i;
-    if (r < GQ) {
-#pragma unroll
-      for (int nt = 0; nt < 8; ++nt) co[(w * GQ + r) * D + 8 * c + nt] = st.O[nt][i];
+  // ---- the two partials.  A wave's state goes to (m_w[head], l_w[head],
+  // co_w[head][D]); accumulator rows r < 8 hold the fp16-hi weights of head r,
+  // rows r >= 8 the lo weights of head r - 8, summed onto the same row.
+  auto put_state = [&](const WaveState& x, float* m_w, float* l_w, float* co_w) {
+    if (lg == 0 && c < GQ) {
+      m_w[c] = x.m;
+      l_w[c] = x.l;
     }
-  }
-  wave_sync();
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 4 * lg + i;
-    if (r >= 8 && r < 8 + GQ) {
+    for (int i = 0; i < 4; ++i) {
+      const int r = 4 * lg + i;
+      if (r < GQ) {
 #pragma unroll
-      for (int nt = 0; nt < 8; ++nt) co[(w * GQ + r - 8) * D + 8 * c + nt] += st.O[nt][i];
+        for (int nt = 0; nt < 8; ++nt) co_w[r * D + 8 * c + nt] = x.O[nt][i];
+      }
     }
-  }
+    wave_sync();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 4 * lg + i;
+      if (r >= 8 && r < 8 + GQ) {
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) co_w[(r - 8) * D + 8 * c + nt] += x.O[nt][i];
+      }
+    }
+  };
+  // hot state: this wave's own slices of the outlier staging (no longer read)
+  float* const hm = &gsm_s[0][0][0];                        // wave ww: hm[ww * 4D + i]
+  float* const hco = reinterpret_cast<float*>(&oq_s[0][0][0]);  // wave ww: hco[ww * GQ * 132 + i * D + j]
+  constexpr int kHmStride = 4 * D, kHcoStride = GQ * 132;
+  put_state(st, hm + w * kHmStride, hm + w * kHmStride + D, hco + w * kHcoStride);
+  // coded state: the code table's area, once every wave is past its groups
   __syncthreads();
+  float* const cm = reinterpret_cast<float*>(lut);  // [8][GQ]
+  float* const cl = cm + kMWaves * GQ;              // [8][GQ]
+  float* const co = cl + kMWaves * GQ;              // [8][GQ][D]
+  put_state(cst, cm + w * GQ, cl + w * GQ, co + w * GQ * D);
+  __syncthreads();
+  // fold the eight waves of each: partial n_cold_splits * hot + split
   const int ns = a.n_cold_splits + a.n_hot_splits;
-  for (int x = tid; x < GQ * D; x += kMThreads) {
-    const int i = x / D, j = x % D;
+  for (int x = tid; x < 2 * GQ * D; x += kMThreads) {
+    const int hot = x >= GQ * D;
+    const int i = (x % (GQ * D)) / D, j = x % D;
+    const float* mp = hot ? hm + i : cm + i;
+    const float* lp = hot ? hm + D + i : cl + i;
+    const float* op = hot ? hco + i * D + j : co + i * D + j;
+    const int ms = hot ? kHmStride : GQ, os = hot ? kHcoStride : GQ * D;
     float M = -INFINITY;
 #pragma unroll
     for (int ww = 0; ww < kMWaves; ++ww)
-      if (cl[ww * GQ + i] > 0.f) M = fmaxf(M, cm[ww * GQ + i]);
+      if (lp[ww * ms] > 0.f) M = fmaxf(M, mp[ww * ms]);
     float den = 0.f, acc = 0.f;
     if (M > -INFINITY) {
 #pragma unroll
       for (int ww = 0; ww < kMWaves; ++ww) {
-        const float l = cl[ww * GQ + i];
+        const float l = lp[ww * ms];
         if (l > 0.f) {
-          const float wt = __builtin_amdgcn_exp2f(cm[ww * GQ + i] - M);
+          const float wt = __builtin_amdgcn_exp2f(mp[ww * ms] - M);
           den += l * wt;
-          acc += co[(ww * GQ + i) * D + j] * wt;
+          acc += op[ww * os] * wt;
         }
       }
     }
-    const size_t o = ((size_t)b * Hq + h * GQ + i) * ns + split;
+    const size_t o = ((size_t)b * Hq + h * GQ + i) * ns + (hot ? a.n_cold_splits : 0) + split;
     a.pacc[o * D + j] = acc;
     if (j == 0) {
       a.pm[o] = M * 0.6931471805599453f;  // back to the natural-log domain of the partials
@@ -1340,7 +1371,6 @@ Plan make_plan(const tqk_cache_desc* d, int batch, int max_len) {
   pl.hot_per_split = kThreads;
   pl.n_hot_splits = (hot_max + kThreads - 1) / kThreads;
   if (pl.n_hot_splits < 1) pl.n_hot_splits = 1;
-  if (mfma_path(*d)) pl.n_hot_splits = 1;  // one 8-wave workgroup walks the whole window
   const long units = (long)batch * d->n_kv_heads * (ngmax > 0 ? ngmax : 0);
   int gps;
   if (mfma_path(*d)) {
@@ -1370,6 +1400,12 @@ Plan make_plan(const tqk_cache_desc* d, int batch, int max_len) {
   }
   pl.groups_per_split = gps;
   pl.n_cold_splits = ngmax > 0 ? (ngmax + gps - 1) / gps : 0;
+  if (mfma_path(*d)) {
+    // every MFMA workgroup also takes a share of the hot window and writes a
+    // hot partial of its own: one split at least, as many hot partials
+    if (pl.n_cold_splits < 1) pl.n_cold_splits = 1;
+    pl.n_hot_splits = pl.n_cold_splits;
+  }
   const size_t ns = (size_t)(pl.n_cold_splits + pl.n_hot_splits);
   const size_t per = (size_t)batch * d->n_q_heads * ns;
   pl.ws_bytes = per * sizeof(float) * (2 + TQK_D) + 256;
@@ -1424,7 +1460,10 @@ int run_splits(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int batch, cons
   if (!ws || ws_bytes < pl.ws_bytes) return TQK_EWORKSPACE;
   const DecodeArgs a = make_args(d, p, pl, batch, q, seq_lens, ws);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const dim3 grid(pl.n_cold_splits + pl.n_hot_splits, d->n_kv_heads, batch);
+  // (the MFMA kernel's workgroups are the coded splits; each also covers a
+  // share of the hot window)
+  const dim3 grid(mfma_path(*d) ? pl.n_cold_splits : pl.n_cold_splits + pl.n_hot_splits,
+                  d->n_kv_heads, batch);
   hipError_t e;
   switch (d->n_q_heads / d->n_kv_heads) {
     case 1: e = launch_split<1>(a, grid, st); break;
