@@ -468,44 +468,63 @@ struct ColdBlock {
 
 // Per-wave online-softmax state for query head (c & (GQ - 1)) and the PV accumulators.
 // Scores are kept in the log2 domain (q is pre-scaled by sm_scale * log2(e)).
+// m is the head's running max (the same in every lane of its column) and
+// mt = m + kLazyMax; l is this lane's share of the denominator (the weights of
+// its own tokens), summed over the column when the state is read out.
 struct WaveState {
-  float m, l;
+  float m, mt, l;
   floatx4_t O[8];
 };
 
+__device__ __forceinline__ void reset_state(WaveState& st) {
+  st.m = -INFINITY;
+  st.mt = -INFINITY;
+  st.l = 0.f;
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) st.O[nt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+}
+
+// Slack of the lazy running max, log2 units: weights p <= 4, so p * |v| stays
+// finite in fp16 for value norms up to 16376
+constexpr float kLazyMax = 2.0f;
+
 // Online softmax over the 8 scores of this lane (tokens 4lg..4lg+3 of tiles A
-// and B of column c).  Every lane of a column holds the same state for its
-// head; accumulator row r = 4lg + i belongs to head r & (GQ - 1), whose
+// and B of column c).  Lazy running max: the heads keep their max, and the
+// accumulators their scale, until one of the wave's scores exceeds its head's
+// max by more than kLazyMax (a wave-uniform test on each lane's own scores,
+// no cross-lane reduction); then every head takes its exact max and the state
+// is rescaled.  (m, l, O) stays consistent for any m, so the softmax is the
+// same.  Accumulator row r = 4lg + i belongs to head r & (GQ - 1), whose
 // correction factor is read from that column with v_readlane.
 template <int GQ>
 __device__ __forceinline__ void softmax_block(WaveState& st, const float (&s)[8], float (&p)[8],
                                               int lg) {
   float bm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
   bm = fmaxf(bm, fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
-  bm = colgroup_max(bm);
-  const float mn = fmaxf(st.m, bm);
-  const float corr = __builtin_amdgcn_exp2f(st.m - mn);
-  st.m = mn;
-  float ps = 0.f;
+  if (__builtin_amdgcn_ballot_w64(bm > st.mt) != 0) {
+    bm = colgroup_max(bm);
+    const float mn = fmaxf(st.m, bm);
+    const float corr = __builtin_amdgcn_exp2f(st.m - mn);
+    st.m = mn;
+    st.mt = mn + kLazyMax;
+    st.l *= corr;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      // no indexed array here: a lane-dependent pick from one would live in scratch
+      const float c0 = bitsf((uint32_t)__builtin_amdgcn_readlane((int)fbits(corr), i & (GQ - 1)));
+      float ci = c0;
+      if constexpr (GQ > 4) {
+        const float c1 = bitsf((uint32_t)__builtin_amdgcn_readlane((int)fbits(corr), 4 + i));
+        ci = (lg & 1) ? c1 : c0;
+      }
+#pragma unroll
+      for (int nt = 0; nt < 8; ++nt) st.O[nt][i] *= ci;
+    }
+  }
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    p[i] = __builtin_amdgcn_exp2f(s[i] - mn);
-    ps += p[i];
-  }
-  st.l = st.l * corr + colgroup_sum(ps);
-  // the accumulators only need rescaling when some head's running max moved
-  if (__builtin_amdgcn_ballot_w64(corr < 1.0f) == 0) return;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    // no indexed array here: a lane-dependent pick from one would live in scratch
-    const float c0 = bitsf((uint32_t)__builtin_amdgcn_readlane((int)fbits(corr), i & (GQ - 1)));
-    float ci = c0;
-    if constexpr (GQ > 4) {
-      const float c1 = bitsf((uint32_t)__builtin_amdgcn_readlane((int)fbits(corr), 4 + i));
-      ci = (lg & 1) ? c1 : c0;
-    }
-#pragma unroll
-    for (int nt = 0; nt < 8; ++nt) st.O[nt][i] *= ci;
+    p[i] = __builtin_amdgcn_exp2f(s[i] - st.m);
+    st.l += p[i];
   }
 }
 
@@ -684,10 +703,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   // hi column + lo column of the same head (lane c and c ^ 8 of a row)
   auto pair_sum = [&](float x) { return x + row_ror<8>(x); };
   WaveState st;
-  st.m = -INFINITY;
-  st.l = 0.f;
-#pragma unroll
-  for (int nt = 0; nt < 8; ++nt) st.O[nt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+  reset_state(st);
 
   {
     constexpr int NC = LutGeom<VB>::kCopies;
@@ -1075,10 +1091,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   // waits in registers meanwhile: the code table, where the waves' states are
   // folded, is still read by waves that have not finished their groups.
   const WaveState cst = st;
-  st.m = -INFINITY;
-  st.l = 0.f;
-#pragma unroll
-  for (int nt = 0; nt < 8; ++nt) st.O[nt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+  reset_state(st);
   {
     const int n_cold = ng * G, R = d.hot_ring;
     const size_t hbase = ((size_t)b * Hkv + h) * R;
@@ -1153,9 +1166,10 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   // co_w[head][D]); accumulator rows r < 8 hold the fp16-hi weights of head r,
   // rows r >= 8 the lo weights of head r - 8, summed onto the same row.
   auto put_state = [&](const WaveState& x, float* m_w, float* l_w, float* co_w) {
+    const float lsum = colgroup_sum(x.l);
     if (lg == 0 && c < GQ) {
       m_w[c] = x.m;
-      l_w[c] = x.l;
+      l_w[c] = lsum;
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
