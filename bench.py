@@ -12,8 +12,9 @@ cannot serve repeat steps.
 
 Prints one JSON line.  `value` is microseconds per decode step (lower is
 better); `roofline.achieved` is the canonical compressed-KV bytes of one step
-divided by the average duration of the split-K kernel, timed with HIP events
-on the stream it runs on.
+divided by the average duration of the decode kernel (split-K over the coded
+groups and the hot window, merged by its last workgroups: the whole step is
+this one launch), timed with HIP events on the stream it runs on.
 """
 
 from __future__ import annotations
@@ -206,9 +207,8 @@ def main():
     torch.cuda.synchronize()
     ms_per_step = e0.elapsed_time(e1) / args.steps
 
-    # the dominant kernel alone: HIP events on its stream around `steps`
-    # back-to-back split-K launches (the partials of one launch are simply
-    # overwritten by the next; the merge is timed in the step above)
+    # the kernel alone: HIP events on its stream around `steps` back-to-back
+    # tqk_decode calls straight through the C ABI (one launch each)
     lib = N.lib()
     st = ctypes.c_void_p(stream.cuda_stream)
     wss = [p.workspace(B, max(p.lengths)) for p in pools]
@@ -217,9 +217,9 @@ def main():
     for i in range(args.steps):
         p = pools[i % len(pools)]
         ws, need = wss[i % len(pools)]
-        N.check(lib.tqk_decode_splits(ctypes.byref(p.desc), ctypes.byref(p.ptrs), B, q.data_ptr(),
-                                      p.seq_lens.data_ptr(), max(p.lengths), ws.data_ptr(), need, st),
-                "tqk_decode_splits")
+        N.check(lib.tqk_decode(ctypes.byref(p.desc), ctypes.byref(p.ptrs), B, q.data_ptr(),
+                               p.seq_lens.data_ptr(), max(p.lengths), outs[i % len(pools)].data_ptr(),
+                               ws.data_ptr(), need, st), "tqk_decode")
     e1.record(stream)
     torch.cuda.synchronize()
     split_ms = e0.elapsed_time(e1) / args.steps

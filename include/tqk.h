@@ -94,14 +94,18 @@ typedef struct tqk_cache_ptrs {
   const float* vbnd;    /* 2^vb - 1 fp32 value boundaries */
 } tqk_cache_ptrs;
 
-/* Library ABI version (bumped on any signature or layout change); this header is version 2. */
+/* Library ABI version (bumped on any signature or layout change); this header is version 3. */
 int tqk_version(void);
 
 /* Validate a descriptor; TQK_OK when the GPU path supports it. */
 int tqk_check_desc(const tqk_cache_desc* d);
 
 /* Bytes of decode workspace needed for `batch` sequences of at most
- * `max_len` tokens.  Host function, no GPU work. */
+ * `max_len` tokens.  Host function, no GPU work.  The workspace holds the
+ * split partials and, after them, one arrival counter per (sequence, kv head)
+ * for tqk_decode's in-kernel merge: zero-fill a new workspace once before its
+ * first tqk_decode; every completed call leaves the counters at zero again.
+ * Calls that share a workspace must not overlap. */
 size_t tqk_decode_workspace_bytes(const tqk_cache_desc* d, int32_t batch, int32_t max_len);
 
 /*

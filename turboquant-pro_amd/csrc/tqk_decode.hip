@@ -30,6 +30,10 @@ struct DecodeArgs {
   int hot_per_split;
   int split_base;  // added to blockIdx.x (hot-only launches start after the coded splits)
   int batch;
+  // in-kernel merge (MFMA kernel): the output, or nullptr to leave the
+  // partials to tqk_merge, and one arrival counter per (seq, kv head)
+  float* out;
+  uint32_t* arrive;
 };
 
 struct MergeArgs {
@@ -362,6 +366,7 @@ union H8 {
 
 constexpr int kMWaves = 8;                 // waves per workgroup (two per SIMD)
 constexpr int kMThreads = 64 * kMWaves;
+constexpr int kMergeFast = 8;  // split counts merged with all partial loads issued up front
 #ifndef TQK_COLD_BUFFERS
 #define TQK_COLD_BUFFERS 3
 #endif
@@ -526,6 +531,17 @@ __device__ __forceinline__ void softmax_block(WaveState& st, const float (&s)[8]
     p[i] = __builtin_amdgcn_exp2f(s[i] - st.m);
     st.l += p[i];
   }
+}
+
+// Partial-state stores and the merge's loads of them.  The workgroups of one
+// (seq, kv head) may run on different XCDs, each with its own L2: coherent
+// (agent-scope) accesses make the partials visible to the merging workgroup
+// without writing back or invalidating whole L2s.
+__device__ __forceinline__ void st_agent(float* p, float x) {
+  __hip_atomic_store(p, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Lane I of each 16-lane row, broadcast to the row (DPP row_newbcast).
@@ -1227,10 +1243,126 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       }
     }
     const size_t o = ((size_t)b * Hq + h * GQ + i) * ns + (hot ? a.n_cold_splits : 0) + split;
-    a.pacc[o * D + j] = acc;
+    st_agent(a.pacc + o * D + j, acc);
     if (j == 0) {
-      a.pm[o] = M * 0.6931471805599453f;  // back to the natural-log domain of the partials
-      a.pl[o] = den;
+      st_agent(a.pm + o, M * 0.6931471805599453f);  // back to the natural-log domain of the partials
+      st_agent(a.pl + o, den);
+    }
+  }
+
+  if (a.out == nullptr) return;
+
+  // ---- in-kernel merge: the last of the (seq, kv head)'s n_cold_splits
+  // workgroups to finish combines their partials (same arithmetic as
+  // tqk_merge).  The partials were stored with agent-scope coherent stores
+  // and are read with agent-scope coherent loads (the workgroups may sit on
+  // different XCDs, each with its own L2; device-scope fences would write
+  // back and invalidate whole L2s instead, measured slower).  Every thread
+  // waits for its stores to complete before the arrival is counted, and the
+  // last arrival's loads are issued after it has read the count.  The counter
+  // wraps back to zero on the last arrival, so it is zero for the next call.
+  __shared__ int last_s;
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's partial stores are done
+  __syncthreads();
+  if (tid == 0)
+    last_s = atomicInc(a.arrive + (size_t)b * Hkv + h, (uint32_t)(a.n_cold_splits - 1)) ==
+             (uint32_t)(a.n_cold_splits - 1);
+  __syncthreads();
+  if (!last_s) return;
+  {
+    // thread (u, j): query heads u, u + 4 for channel j; the coded sums go to
+    // q_h_s.  Up to kMergeFast splits, every partial load is issued before
+    // the first is used (each is a round trip to memory).
+    const int j = tid % D, u = tid / D;
+    constexpr int NH = (GQ + 3) / 4;
+    float hr[NH], den[NH];
+    auto combine = [&](int r, int qi, const float (&vl)[kMergeFast], const float (&vm)[kMergeFast],
+                       const float (&va)[kMergeFast]) {
+      float M = -INFINITY;
+#pragma unroll
+      for (int s = 0; s < kMergeFast; ++s)
+        if (vl[s] > 0.f) M = fmaxf(M, vm[s]);
+      float dn = 0.f, cr = 0.f, hh = 0.f;
+#pragma unroll
+      for (int s = 0; s < kMergeFast; ++s) {
+        if (vl[s] > 0.f) {
+          const float wt = __expf(vm[s] - M);
+          dn += vl[s] * wt;
+          const float x = va[s] * wt;
+          if (s < a.n_cold_splits) cr += x; else hh += x;
+        }
+      }
+      q_h_s[qi][j] = cr;
+      hr[r] = hh;
+      den[r] = dn;
+    };
+#pragma unroll
+    for (int r = 0; r < NH; ++r) hr[r] = den[r] = 0.f;
+    const bool fast = ns <= kMergeFast;
+    float vl[NH][kMergeFast], vm[NH][kMergeFast], va[NH][kMergeFast];
+    if (fast) {
+#pragma unroll
+      for (int r = 0; r < NH; ++r) {
+        const int qi = u + 4 * r;
+        const size_t base = ((size_t)b * Hq + h * GQ + qi) * ns;
+#pragma unroll
+        for (int s = 0; s < kMergeFast; ++s) {
+          const bool ok = qi < GQ && s < ns;
+          vl[r][s] = ok ? ld_agent(a.pl + base + s) : 0.f;
+          vm[r][s] = ok ? ld_agent(a.pm + base + s) : -INFINITY;
+          va[r][s] = ok ? ld_agent(a.pacc + (base + s) * D + j) : 0.f;
+        }
+      }
+    }
+    {
+      // Pi (64 KiB) into the code table's area, its wide loads issued behind
+      // the partial loads and before any store
+      constexpr int NV = D * D / 4 / kMThreads;
+      float4 v[NV];
+#pragma unroll
+      for (int r = 0; r < NV; ++r) v[r] = reinterpret_cast<const float4*>(a.p.pi)[tid + r * kMThreads];
+#pragma unroll
+      for (int r = 0; r < NV; ++r) reinterpret_cast<float4*>(lut)[tid + r * kMThreads] = v[r];
+    }
+    const float* const pi_s = reinterpret_cast<const float*>(lut);
+    if (fast) {
+#pragma unroll
+      for (int r = 0; r < NH; ++r)
+        if (u + 4 * r < GQ) combine(r, u + 4 * r, vl[r], vm[r], va[r]);
+    } else {
+      for (int r = 0; r < NH; ++r) {
+        const int qi = u + 4 * r;
+        if (qi < GQ) {
+          const size_t base = ((size_t)b * Hq + h * GQ + qi) * ns;
+          float M = -INFINITY;
+          for (int s = 0; s < ns; ++s)
+            if (ld_agent(a.pl + base + s) > 0.f) M = fmaxf(M, ld_agent(a.pm + base + s));
+          float dn = 0.f, cr = 0.f, hh = 0.f;
+          for (int s = 0; s < ns; ++s) {
+            const float l = ld_agent(a.pl + base + s);
+            if (l > 0.f) {
+              const float wt = __expf(ld_agent(a.pm + base + s) - M);
+              dn += l * wt;
+              const float x = ld_agent(a.pacc + (base + s) * D + j) * wt;
+              if (s < a.n_cold_splits) cr += x; else hh += x;
+            }
+          }
+          q_h_s[qi][j] = cr;
+          hr[r] = hh;
+          den[r] = dn;
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < NH; ++r) {
+      const int qi = u + 4 * r;
+      if (qi < GQ) {
+        float o = hr[r];
+#pragma unroll 8
+        for (int k = 0; k < D; ++k) o += q_h_s[qi][k] * pi_s[k * D + j];
+        a.out[((size_t)b * Hq + h * GQ + qi) * D + j] = o / den[r];
+      }
     }
   }
 }
@@ -1241,7 +1373,6 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
 // Pi is staged in LDS once (every thread's wide loads issued before its
 // stores) and shared by the GQ query heads.
 constexpr int kMergeThreads = 2 * TQK_D;
-constexpr int kMergeFast = 8;  // split counts merged with all partial loads issued up front
 __global__ __launch_bounds__(kMergeThreads) void tqk_merge(MergeArgs a) {
   constexpr int D = TQK_D;
   const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
@@ -1365,6 +1496,7 @@ __host__ __device__ inline bool mfma_path(const tqk_cache_desc& d) {
 
 struct Plan {
   int n_cold_splits, n_hot_splits, groups_per_split, hot_per_split;
+  size_t arrive_off;  // arrival counters after the partials
   size_t ws_bytes;
 };
 
@@ -1422,7 +1554,8 @@ Plan make_plan(const tqk_cache_desc* d, int batch, int max_len) {
   }
   const size_t ns = (size_t)(pl.n_cold_splits + pl.n_hot_splits);
   const size_t per = (size_t)batch * d->n_q_heads * ns;
-  pl.ws_bytes = per * sizeof(float) * (2 + TQK_D) + 256;
+  pl.arrive_off = (per * sizeof(float) * (2 + TQK_D) + 255) & ~(size_t)255;
+  pl.ws_bytes = pl.arrive_off + (size_t)batch * d->n_kv_heads * sizeof(uint32_t) + 256;
   return pl;
 }
 
@@ -1462,17 +1595,21 @@ DecodeArgs make_args(const tqk_cache_desc* d, const tqk_cache_ptrs* p, const Pla
   a.hot_per_split = pl.hot_per_split;
   a.split_base = 0;
   a.batch = batch;
+  a.out = nullptr;
+  a.arrive = reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + pl.arrive_off);
   return a;
 }
 
 int run_splits(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int batch, const uint16_t* q,
-               const int32_t* seq_lens, int max_len, void* ws, size_t ws_bytes, void* stream) {
+               const int32_t* seq_lens, int max_len, void* ws, size_t ws_bytes, void* stream,
+               float* out = nullptr) {
   int rc = tqk_check_desc(d);
   if (rc != TQK_OK) return rc;
   if (!p || !q || !seq_lens || batch <= 0 || max_len <= 0) return TQK_EINVAL;
   const Plan pl = make_plan(d, batch, max_len);
   if (!ws || ws_bytes < pl.ws_bytes) return TQK_EWORKSPACE;
-  const DecodeArgs a = make_args(d, p, pl, batch, q, seq_lens, ws);
+  DecodeArgs a = make_args(d, p, pl, batch, q, seq_lens, ws);
+  if (out && mfma_path(*d)) a.out = out;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   // (the MFMA kernel's workgroups are the coded splits; each also covers a
   // share of the hot window)
@@ -1520,7 +1657,7 @@ int run_merge(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int batch, int m
 
 extern "C" {
 
-int tqk_version(void) { return 2; }
+int tqk_version(void) { return 3; }
 
 int tqk_check_desc(const tqk_cache_desc* d) {
   if (!d) return TQK_EINVAL;
@@ -1549,8 +1686,10 @@ int tqk_decode(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t batch,
                const uint16_t* q, const int32_t* seq_lens, int32_t max_len, float* out,
                void* workspace, size_t workspace_bytes, void* stream) {
   if (!out) return TQK_EINVAL;
-  int rc = run_splits(d, p, batch, q, seq_lens, max_len, workspace, workspace_bytes, stream);
+  int rc = run_splits(d, p, batch, q, seq_lens, max_len, workspace, workspace_bytes, stream, out);
   if (rc != TQK_OK) return rc;
+  // the MFMA kernel merged in its last workgroups
+  if (mfma_path(*d)) return TQK_OK;
   return run_merge(d, p, batch, max_len, out, nullptr, nullptr, nullptr, workspace,
                    workspace_bytes, stream);
 }

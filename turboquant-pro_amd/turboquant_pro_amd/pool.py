@@ -199,7 +199,9 @@ class TQKVPool:
         torch = _torch()
         need = N.lib().tqk_decode_workspace_bytes(ctypes.byref(self.desc), batch, max_len)
         if self._ws is None or self._ws.numel() < need:
-            self._ws = torch.empty(int(need), dtype=torch.uint8, device=self.device)
+            # zero-filled once: the arrival counters of the in-kernel merge
+            # start at zero and every call leaves them there
+            self._ws = torch.zeros(int(need), dtype=torch.uint8, device=self.device)
         return self._ws, int(need)
 
     def _check_q(self, q):
