@@ -225,3 +225,23 @@ def test_quant_descriptor_names_the_bytes():
                  "value_config": {"bits": 3, "seed": 0}}
     fields, _ = _identity()
     assert fields["quant"] == q      # the golden profile describes this store's default
+
+
+def test_connector_protocol_host_side():
+    """Scheduler-side answers and eviction of the connector (vllm_v1.py:750-814),
+    over a store holding the reference's records; without vLLM, ``register``
+    reports False instead of failing."""
+    from turboquant_pro_amd.connectors import TurboQuantKVConnector
+    from turboquant_pro_amd.connectors.vllm import register
+    st, _ = _loaded_store()
+    conn = TurboQuantKVConnector(store=st)
+    req = type("Req", (), {"request_id": "req1"})()
+    assert conn.get_num_new_matched_tokens(req, 0) == (200, False)
+    assert conn.get_num_new_matched_tokens(req, 150) == (50, False)
+    assert conn.get_num_new_matched_tokens(req, 500) == (0, False)
+    assert conn.build_connector_meta() == {"version": 1}
+    assert conn.request_finished(req) == (False, None)
+    assert conn.start_load_kv(requests={"req1": 0}) == 0      # no pool bound: nothing to restore into
+    conn.get_finished({"req1"})
+    assert st.matched_tokens("req1") == 0 and st.stats()["records"] == 0
+    assert register() is False

@@ -34,6 +34,21 @@ def test_untile_inverts_tile():
         assert np.array_equal(F.untile_value_rows(tiled, vb), codes)
 
 
+def test_tile_value_rows_matches_the_definition():
+    """The vectorised tiling (used to import codes into a tiled pool) equals
+    the bit-by-bit definition, and untiling any bytes then tiling is the
+    identity (every unit bit holds a code bit)."""
+    rng = np.random.default_rng(1)
+    for vb in (3, 4):
+        codes = rng.integers(0, 2 ** vb, size=(48, 128), dtype=np.uint8)
+        want = np.concatenate([_tile(codes[16 * i:16 * (i + 1)], vb) for i in range(3)])
+        got = F.tile_value_rows(codes, vb)
+        assert got.shape == (48, 128 * vb // 8)
+        assert np.array_equal(got.reshape(-1), want)
+        raw = rng.integers(0, 256, size=(32, 128 * vb // 8), dtype=np.uint8)
+        assert np.array_equal(F.tile_value_rows(F.untile_value_rows(raw, vb), vb), raw)
+
+
 def test_pack_values_matches_oracle_pack():
     rng = np.random.default_rng(1)
     for vb in (2, 3, 4):

@@ -129,17 +129,92 @@ class TurboQuantBlockStore:
         return x.reshape((-1,) + x.shape[-3:])
 
     # ---------------------------------------------------------------- API
-    def make_record(self, keys: Any, values: Any) -> BlockRecord:
+    def make_record(self, keys: Any, values: Any, packed: bool = False) -> BlockRecord:
         """Quantize one layer block into a record (the body of ``save``)."""
         k, v = self._host_f32(keys), self._host_f32(values)
         if k.shape != v.shape:
             raise ValueError(f"keys {k.shape} and values {v.shape} differ in shape")
         k4, v4 = self._as_bhsd(k), self._as_bhsd(v)
         d, h = int(k4.shape[-1]), int(k4.shape[1])
-        return BlockRecord(key_payload=self._quantizer("key", d, h).compress(k4),
-                           value_payload=self._quantizer("value", d, h).compress(v4),
+        kw = {"packed": True} if packed else {}
+        return BlockRecord(key_payload=self._quantizer("key", d, h).compress(k4, **kw),
+                           value_payload=self._quantizer("value", d, h).compress(v4, **kw),
                            shape=tuple(int(s) for s in k.shape), dtype="float32",
                            num_tokens=int(k4.shape[-2]), head_dim=d, n_heads=h)
+
+    # ------------------------------------------------- paged (pool) records
+    @staticmethod
+    def _group_name(layer_name: str, g: int) -> str:
+        return f"{layer_name}#g{g}"
+
+    def save_sequence(self, request_id: str, layer_name: str, keys: Any, values: Any,
+                      group_tokens: int, hot_window: int) -> int:
+        """Store one sequence's layer K/V ``(H, L, D)`` the way a paged pool
+        holds it: one record per coded group of the flush cadence
+        (``<layer>#g<i>``, ``group_tokens`` tokens each, so each is exactly the
+        pool's group) and the hot tokens in records of at most 256 tokens (one
+        key group of the plugin: ``<layer>#hot<i>``).  Every record is an
+        ordinary ``tqp-kv-npz/1`` record.  Returns the groups."""
+        from ..codebooks import n_groups_for
+        k, v = self._host_f32(keys), self._host_f32(values)
+        k4, v4 = self._as_bhsd(k), self._as_bhsd(v)
+        if k4.shape[0] != 1 or k4.shape != v4.shape:
+            raise ValueError("save_sequence takes one sequence: (H, L, D) keys and values")
+        L, G = int(k4.shape[2]), int(group_tokens)
+        ng = n_groups_for(L, int(hot_window))
+        recs = {self._group_name(layer_name, g): self.make_record(
+                    k4[:, :, g * G:(g + 1) * G], v4[:, :, g * G:(g + 1) * G], packed=True)
+                for g in range(ng)}
+        for i, t0 in enumerate(range(ng * G, L, 256)):
+            recs[f"{layer_name}#hot{i}"] = self.make_record(k4[:, :, t0:t0 + 256], v4[:, :, t0:t0 + 256],
+                                                            packed=True)
+        with self._lock:
+            for name, rec in recs.items():
+                self._records[(request_id, name)] = rec
+            self._tokens[request_id] = L
+        return ng
+
+    def load_into_pool(self, request_id: str, layer_name: str, pool, b: int) -> int:
+        """Restore a sequence saved by :meth:`save_sequence` into sequence ``b``
+        of ``pool`` (empty): the coded groups go in as codes, unchanged (no
+        dequantize / re-encode), the hot tokens as their GPU dequantization
+        (the store holds nothing uncompressed).  Returns the tokens restored,
+        0 when nothing is stored (a miss)."""
+        from ..codebooks import random_rotation
+        torch = __import__("torch")
+        groups = []
+        with self._lock:
+            while (request_id, self._group_name(layer_name, len(groups))) in self._records:
+                groups.append(self._records[(request_id, self._group_name(layer_name, len(groups)))])
+            hot = []
+            while (request_id, f"{layer_name}#hot{len(hot)}") in self._records:
+                hot.append(self._records[(request_id, f"{layer_name}#hot{len(hot)}")])
+        if not groups and not hot:
+            return 0
+        H, D, G = pool.n_kv_heads, pool.head_dim, pool.group_tokens
+        vq = self._quantizer("value", D, H)
+        if getattr(vq, "value_bits", None) != pool.value_bits:
+            raise ValueError(f"stored values are {getattr(vq, 'value_bits', None)}-bit, the pool's "
+                             f"{pool.value_bits}-bit")
+        if not np.array_equal(random_rotation(getattr(vq, "seed", None), D)[0], pool.pi.cpu().numpy()):
+            raise ValueError("the pool's value rotation is not the store's (rotation seed)")
+        items = []
+        for rec in groups:
+            kp, vp = rec.key_payload, rec.value_payload
+            if rec.num_tokens != G or rec.n_heads != H or rec.head_dim != D or not kp.packed \
+                    or not vp.packed or getattr(kp, "zp_mode", "calibrated") != "calibrated":
+                raise ValueError("a stored group does not match the pool's group format")
+            items.append(({"kpacked": kp.indices, "nf4_scale": kp.nf4_scale[0], "nf4_mean": kp.nf4_mean[0],
+                           "outlier_idx": kp.outlier_idx, "outlier_val": kp.outlier_val},
+                          {"vpacked": vp.indices, "vnorms": vp.norms[0]}))
+        kq = self._quantizer("key", D, H)
+        hk = torch.zeros((H, 0, D))
+        hv = torch.zeros((H, 0, D))
+        for rec in hot:
+            hk = torch.cat([hk, torch.from_numpy(np.asarray(kq.decompress(rec.key_payload), np.float32)[0])], 1)
+            hv = torch.cat([hv, torch.from_numpy(np.asarray(vq.decompress(rec.value_payload), np.float32)[0])], 1)
+        pool.load_sequence(b, items, hk.to(torch.float16), hv.to(torch.float16))
+        return len(items) * G + int(hk.shape[1])
 
     def save(self, request_id: str, layer_name: str, keys: Any, values: Any) -> None:
         """Quantize and store one layer's KV for ``request_id``."""

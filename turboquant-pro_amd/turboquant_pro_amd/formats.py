@@ -113,6 +113,29 @@ def untile_values(tile_bytes: np.ndarray, vb: int, D: int = 128) -> np.ndarray:
     return out
 
 
+def tile_value_rows(codes: np.ndarray, vb: int) -> np.ndarray:
+    """Codes ``(n, D)`` (n % 16 == 0) -> the tiled value bytes ``(n, D*vb/8)``,
+    the inverse of :func:`untile_value_rows`: unit (lg, c) of a 16-token tile
+    holds tokens 4lg..4lg+3 x channels 8c..8c+7, code bit k of (token u,
+    channel nt) at unit bit ``unit_bit(u, nt, vb) + k``."""
+    codes = np.asarray(codes, np.uint8)
+    n, D = codes.shape
+    if n % 16 or D % 8:
+        raise ValueError("tiling needs whole 16-token tiles and D % 8 == 0")
+    vrow = D * vb // 8
+    unit_bits = vrow // 4 * 8
+    # (tile, lg, u, c, nt) view of the codes
+    t = codes.reshape(n // 16, 4, 4, D // 8, 8)
+    bits = np.zeros((n // 16, 4, D // 8, unit_bits), np.uint8)       # (tile, lg, c, bit)
+    for u in range(4):
+        for nt in range(8):
+            b0 = unit_bit(u, nt, vb)
+            for k in range(vb):
+                bits[:, :, :, b0 + k] = (t[:, :, u, :, nt] >> k) & 1
+    packed = np.packbits(bits, axis=-1, bitorder="little")           # (tile, lg, c, unit bytes)
+    return packed.reshape(n // 16, 16 * vrow).reshape(n, vrow)
+
+
 def untile_value_rows(rows: np.ndarray, vb: int, D: int = 128) -> np.ndarray:
     """Tiled value bytes of ``n`` tokens (n % 16 == 0, tile-aligned) -> codes (n, D)."""
     vrow = D * vb // 8

@@ -23,7 +23,8 @@ import math
 import numpy as np
 
 from . import _native as N
-from .formats import mark_outlier_codes, pack_values, restore_outlier_codes, untile_value_rows
+from .formats import (mark_outlier_codes, pack_values, restore_outlier_codes, tile_value_rows,
+                      unpack_values, untile_value_rows)
 from .codebooks import (group_tokens_for, n_groups_for, outliers_per_channel, random_rotation,
                         value_codebook)
 
@@ -315,8 +316,8 @@ class TQKVPool:
         (H*G*D/2 bytes), ``nf4_scale``/``nf4_mean`` (H, D), ``outlier_idx``
         (flat over (H, G, D), token-major within a head as the reference emits
         them) and ``outlier_val`` fp16, or ``None`` outliers; ``values``:
-        ``vpacked`` (reference pack of H*G*D codes) and ``vnorms`` (H, G).
-        Value codes stored per token only (a tiled pool raises)."""
+        ``vpacked`` (reference pack of H*G*D codes) and ``vnorms`` (H, G); a
+        tiled pool stores them in its MFMA-tiled order."""
         torch = _torch()
         H, G, D = self.n_kv_heads, self.group_tokens, self.head_dim
         phys, off = self._rows(b, g)
@@ -355,10 +356,40 @@ class TQKVPool:
             self.oent[slot] = torch.from_numpy(ent.view(np.int32)).to(self.device)
             self.ocount[slot] = torch.from_numpy(cnt).to(self.device)
         if values is not None:
-            if self.tiled:
-                raise NotImplementedError("import of value codes into a tiled pool")
             vrow = D * self.value_bits // 8
-            vp = np.asarray(values["vpacked"], np.uint8)[: H * G * vrow].reshape(H, G, vrow)
+            if self.tiled:
+                codes = unpack_values(np.asarray(values["vpacked"], np.uint8), H * G * D,
+                                      self.value_bits).reshape(H, G, D)
+                vp = np.stack([tile_value_rows(codes[hh], self.value_bits) for hh in range(H)])
+            else:
+                vp = np.asarray(values["vpacked"], np.uint8)[: H * G * vrow].reshape(H, G, vrow)
             self.vcodes[:, phys, off] = torch.from_numpy(np.ascontiguousarray(vp)).to(self.device)
             self.vnorm[:, phys, off] = torch.from_numpy(
                 np.asarray(values["vnorms"], np.float32).reshape(H, G)).to(self.device)
+
+    def load_sequence(self, b: int, groups, hot_k, hot_v) -> None:
+        """Restore sequence ``b`` (empty) from coded groups and hot tokens:
+        ``groups`` = ``[(keys, values), ...]`` in :meth:`import_group`'s
+        layout, written as they are (no re-encode), then ``hot_k``/``hot_v``
+        fp16 ``(Hkv, n_hot, D)`` into the hot ring.  The split must be the
+        flush cadence's: ``n_groups_for(len(groups) * G + n_hot)`` is
+        ``len(groups)``."""
+        torch = _torch()
+        if self.lengths[b] != 0:
+            raise ValueError(f"sequence {b} is not empty")
+        G, W = self.group_tokens, self.hot_window
+        n_hot = int(hot_k.shape[1])
+        L = len(groups) * G + n_hot
+        if tuple(hot_k.shape) != (self.n_kv_heads, n_hot, self.head_dim) or hot_v.shape != hot_k.shape:
+            raise ValueError(f"hot tokens must be ({self.n_kv_heads}, n, {self.head_dim}) keys and values")
+        if n_groups_for(L, W) != len(groups) or L > self.max_seq_len:
+            raise ValueError(f"{len(groups)} groups + {n_hot} hot tokens is not a state of the "
+                             f"flush cadence (hot window {W}, group {G}) within {self.max_seq_len} tokens")
+        for g, (keys, values) in enumerate(groups):
+            self.import_group(b, g, keys=keys, values=values)
+        if n_hot:
+            idx = torch.arange(L - n_hot, L, device=self.device) % W
+            self.hot_k[b][:, idx] = hot_k.to(device=self.device, dtype=torch.float16)
+            self.hot_v[b][:, idx] = hot_v.to(device=self.device, dtype=torch.float16)
+        self.lengths[b] = L
+        self.seq_lens[b] = L
