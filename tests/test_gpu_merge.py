@@ -83,3 +83,23 @@ def test_in_kernel_merge_equals_merge_kernel(gq, vbits):
     f3 = pool.decode(qd)
     torch.cuda.synchronize()
     assert torch.equal(f2, r2) and torch.equal(f3, r2)
+
+
+def test_in_kernel_merge_many_splits():
+    """A long single sequence: 10 coded splits per kv head, 20 partials, so both
+    merges take their chunked form (more than 8 splits); still bit for bit
+    equal, and within the bar of dequantize-then-attend."""
+    from turboquant_pro_amd import TQKVPool
+    B, Hkv, Hq, L = 1, 2, 8, 20000
+    print(f"[merge] long context L={L}", flush=True)
+    k, v, q = O.synthetic_kv(97, B, Hkv, Hq, L)
+    pi, pi_t = O.rotation(6, 128)
+    pool = TQKVPool(n_kv_heads=Hkv, n_q_heads=Hq, max_batch=B, max_seq_len=L, rotation=(pi, pi_t))
+    pool.append(_dev(k), _dev(v))
+    qd = _dev(q)
+    fused = [pool.decode(qd) for _ in range(2)]
+    ref = _two_phase(pool, qd)
+    torch.cuda.synchronize()
+    assert all(torch.equal(f, ref) for f in fused)
+    sc = O.SequenceCache(hot_window=512, value_bits=3, outlier_frac=0.02).build(k[0], v[0], pi, pi_t)
+    assert_attn_close(fused[0][0].cpu().numpy(), sc.attend(q[0]), what="L=20000")

@@ -544,6 +544,50 @@ __device__ __forceinline__ float ld_agent(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Merge of one query head's ns split partials for channel j when there are
+// more than kMergeFast: the two passes of the short form (the max M over the
+// partials with l > 0, then the e^{m - M}-weighted sums in split order, coded
+// and hot apart) with kMergeFast partials per round and every load of a round
+// issued before its first use -- the same arithmetic in the same order.
+template <class Load>
+__device__ __forceinline__ void merge_chunked(Load ld, const float* pl, const float* pm,
+                                              const float* pacc, size_t base, int ns, int n_cold,
+                                              int j, float& M, float& dn, float& cr, float& hh) {
+  M = -INFINITY;
+  for (int s0 = 0; s0 < ns; s0 += kMergeFast) {
+    float vl[kMergeFast], vm[kMergeFast];
+#pragma unroll
+    for (int k = 0; k < kMergeFast; ++k) {
+      const bool ok = s0 + k < ns;
+      vl[k] = ok ? ld(pl + base + s0 + k) : 0.f;
+      vm[k] = ok ? ld(pm + base + s0 + k) : -INFINITY;
+    }
+#pragma unroll
+    for (int k = 0; k < kMergeFast; ++k)
+      if (vl[k] > 0.f) M = fmaxf(M, vm[k]);
+  }
+  dn = cr = hh = 0.f;
+  for (int s0 = 0; s0 < ns; s0 += kMergeFast) {
+    float vl[kMergeFast], vm[kMergeFast], va[kMergeFast];
+#pragma unroll
+    for (int k = 0; k < kMergeFast; ++k) {
+      const bool ok = s0 + k < ns;
+      vl[k] = ok ? ld(pl + base + s0 + k) : 0.f;
+      vm[k] = ok ? ld(pm + base + s0 + k) : -INFINITY;
+      va[k] = ok ? ld(pacc + (base + s0 + k) * TQK_D + j) : 0.f;
+    }
+#pragma unroll
+    for (int k = 0; k < kMergeFast; ++k) {
+      if (vl[k] > 0.f) {
+        const float wt = __expf(vm[k] - M);
+        dn += vl[k] * wt;
+        const float x = va[k] * wt;
+        if (s0 + k < n_cold) cr += x; else hh += x;
+      }
+    }
+  }
+}
+
 // Lane I of each 16-lane row, broadcast to the row (DPP row_newbcast).
 template <int I>
 __device__ __forceinline__ float row_bcast(float x) {
@@ -1334,19 +1378,9 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         const int qi = u + 4 * r;
         if (qi < GQ) {
           const size_t base = ((size_t)b * Hq + h * GQ + qi) * ns;
-          float M = -INFINITY;
-          for (int s = 0; s < ns; ++s)
-            if (ld_agent(a.pl + base + s) > 0.f) M = fmaxf(M, ld_agent(a.pm + base + s));
-          float dn = 0.f, cr = 0.f, hh = 0.f;
-          for (int s = 0; s < ns; ++s) {
-            const float l = ld_agent(a.pl + base + s);
-            if (l > 0.f) {
-              const float wt = __expf(ld_agent(a.pm + base + s) - M);
-              dn += l * wt;
-              const float x = ld_agent(a.pacc + (base + s) * D + j) * wt;
-              if (s < a.n_cold_splits) cr += x; else hh += x;
-            }
-          }
+          float M, dn, cr, hh;
+          merge_chunked([](const float* p) { return ld_agent(p); }, a.pl, a.pm, a.pacc, base, ns,
+                        a.n_cold_splits, j, M, dn, cr, hh);
           q_h_s[qi][j] = cr;
           hr[r] = hh;
           den[r] = dn;
@@ -1445,19 +1479,9 @@ __global__ __launch_bounds__(kMergeThreads) void tqk_merge(MergeArgs a) {
       const int qi = half + 2 * u;
       if (qi < GQ) {
         const size_t base = ((size_t)b * a.n_q_heads + h * GQ + qi) * a.n_splits;
-        float M = -INFINITY;
-        for (int s = 0; s < a.n_splits; ++s)
-          if (a.pl[base + s] > 0.f) M = fmaxf(M, a.pm[base + s]);
-        float dn = 0.f, cr = 0.f, hh = 0.f;
-        for (int s = 0; s < a.n_splits; ++s) {
-          const float l = a.pl[base + s];
-          if (l > 0.f) {
-            const float wt = __expf(a.pm[base + s] - M);
-            dn += l * wt;
-            const float v = a.pacc[(base + s) * D + j] * wt;
-            if (s < a.n_cold_splits) cr += v; else hh += v;
-          }
-        }
+        float M, dn, cr, hh;
+        merge_chunked([](const float* p) { return *p; }, a.pl, a.pm, a.pacc, base, a.n_splits,
+                      a.n_cold_splits, j, M, dn, cr, hh);
         crot_s[qi][j] = cr;
         hr[u] = hh;
         den[u] = dn;
