@@ -545,39 +545,39 @@ __device__ __forceinline__ float ld_agent(const float* p) {
 }
 
 // Merge of one query head's ns split partials for channel j when there are
-// more than kMergeFast: the two passes of the short form (the max M over the
-// partials with l > 0, then the e^{m - M}-weighted sums in split order, coded
-// and hot apart) with kMergeFast partials per round and every load of a round
-// issued before its first use -- the same arithmetic in the same order.
+// more than kMergeFast: one online pass (running max M, the sums rescaled by
+// e^{M_old - M_new} when a round raises it) over rounds of 2 * kMergeFast
+// partials, every load of a round issued before its first use.  Both merges
+// (tqk_merge and the in-kernel one) use it, so they agree bit for bit.
 template <class Load>
 __device__ __forceinline__ void merge_chunked(Load ld, const float* pl, const float* pm,
                                               const float* pacc, size_t base, int ns, int n_cold,
                                               int j, float& M, float& dn, float& cr, float& hh) {
+  constexpr int C = 2 * kMergeFast;
   M = -INFINITY;
-  for (int s0 = 0; s0 < ns; s0 += kMergeFast) {
-    float vl[kMergeFast], vm[kMergeFast];
-#pragma unroll
-    for (int k = 0; k < kMergeFast; ++k) {
-      const bool ok = s0 + k < ns;
-      vl[k] = ok ? ld(pl + base + s0 + k) : 0.f;
-      vm[k] = ok ? ld(pm + base + s0 + k) : -INFINITY;
-    }
-#pragma unroll
-    for (int k = 0; k < kMergeFast; ++k)
-      if (vl[k] > 0.f) M = fmaxf(M, vm[k]);
-  }
   dn = cr = hh = 0.f;
-  for (int s0 = 0; s0 < ns; s0 += kMergeFast) {
-    float vl[kMergeFast], vm[kMergeFast], va[kMergeFast];
+  for (int s0 = 0; s0 < ns; s0 += C) {
+    float vl[C], vm[C], va[C];
 #pragma unroll
-    for (int k = 0; k < kMergeFast; ++k) {
+    for (int k = 0; k < C; ++k) {
       const bool ok = s0 + k < ns;
       vl[k] = ok ? ld(pl + base + s0 + k) : 0.f;
       vm[k] = ok ? ld(pm + base + s0 + k) : -INFINITY;
       va[k] = ok ? ld(pacc + (base + s0 + k) * TQK_D + j) : 0.f;
     }
+    float Mc = M;
 #pragma unroll
-    for (int k = 0; k < kMergeFast; ++k) {
+    for (int k = 0; k < C; ++k)
+      if (vl[k] > 0.f) Mc = fmaxf(Mc, vm[k]);
+    if (Mc > M) {
+      const float f = __expf(M - Mc);  // 0 on the first round (the sums are 0)
+      dn *= f;
+      cr *= f;
+      hh *= f;
+      M = Mc;
+    }
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
       if (vl[k] > 0.f) {
         const float wt = __expf(vm[k] - M);
         dn += vl[k] * wt;
