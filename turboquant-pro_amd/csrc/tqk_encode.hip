@@ -55,7 +55,7 @@ __global__ __launch_bounds__(kThreads) void tqk_encode_group(EncodeArgs a) {
   const int slot = a.p.group_table[(size_t)b * d.max_groups_per_seq + g];
   const int kout = d.outliers_per_channel;
 
-  __shared__ uint16_t kt_s[TQK_MAX_G][D + 8];  // key tile, fp16 bits (row padded vs bank conflicts)
+  __shared__ __align__(16) uint16_t kt_s[TQK_MAX_G][D + 8];  // key tile, fp16 bits (row padded vs bank conflicts)
   __shared__ float cent_s[D][17];            // per-channel grids (padded)
   __shared__ uint32_t thr_s[D];              // fp16 magnitude threshold per channel
   __shared__ int32_t wsum_s[4];
@@ -200,75 +200,100 @@ __global__ __launch_bounds__(kThreads) void tqk_encode_group(EncodeArgs a) {
     *reinterpret_cast<uint4*>(a.p.kcodes + row * (D / 2) + 16 * ch) =
         *reinterpret_cast<const uint4*>(&kc_s[t][16 * ch]);
   }
-  if (tid < G) {
-    const int t = g * G + tid;
-    const uint4* src = reinterpret_cast<const uint4*>(token_src(a, a.p.hot_v, a.chunk_v, b, h, t));
-    float u[D];
+  // Rotation operands: lane e of wave w owns rotated channel
+  // 64 * (w & 1) + lane and keeps column e of Pi_T (pi[e][0..D)) in
+  // registers; waves w and w ^ 1 split the channels, w >> 1 the tokens.
+  // Normalised rows u of kVBatch tokens at a time sit in LDS after the code
+  // staging area, read as wave-uniform broadcasts.  Every y_e is still the
+  // sequential, separately rounded sum over d.
+  const int lane = tid & 63, wv = tid >> 6;
+  const int ecol = 64 * (wv & 1) + lane;
+  float pcol[D];
 #pragma unroll
-    for (int c = 0; c < 16; ++c) {
-      const uint4 w4 = src[c];
-      const uint32_t wv[4] = {w4.x, w4.y, w4.z, w4.w};
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        u[c * 8 + 2 * k] = h2f((uint16_t)(wv[k] & 0xFFFFu));
-        u[c * 8 + 2 * k + 1] = h2f((uint16_t)(wv[k] >> 16));
-      }
-    }
-    float r[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) r[k] = __fmul_rn(u[k], u[k]);
-#pragma unroll
-    for (int m = 1; m < 16; ++m)
-#pragma unroll
-      for (int k = 0; k < 8; ++k) r[k] = __fadd_rn(r[k], __fmul_rn(u[8 * m + k], u[8 * m + k]));
-    const float ss = __fadd_rn(__fadd_rn(__fadd_rn(r[0], r[1]), __fadd_rn(r[2], r[3])),
-                               __fadd_rn(__fadd_rn(r[4], r[5]), __fadd_rn(r[6], r[7])));
-    const float nrm = __builtin_sqrtf(ss);  // correctly rounded (-fhip-fp32-correctly-rounded-divide-sqrt)
-    const float safe = fmaxf(nrm, 1e-30f);
-#pragma unroll
-    for (int k = 0; k < D; ++k) u[k] = __fdiv_rn(u[k], safe);
-
-    float bnd[15];
-#pragma unroll
-    for (int k = 0; k < (1 << VB) - 1; ++k) bnd[k] = a.p.vbnd[k];
-
-    const size_t row = page_row(a.p.block_table, d.max_pages_per_seq, b, t, P, d.n_pages, h);
-    uint32_t outw[VROW / 4];
-#pragma unroll
-    for (int k = 0; k < VROW / 4; ++k) outw[k] = 0u;
-    const float* __restrict__ pi = a.p.pi;  // pi[e][d] == pi_t[d][e]
-    for (int e0 = 0; e0 < D; e0 += 4) {
-      float y[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int dd = 0; dd < D; ++dd) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) y[k] = __fadd_rn(y[k], __fmul_rn(u[dd], pi[(e0 + k) * D + dd]));
-      }
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        uint32_t code = 0;
-#pragma unroll
-        for (int q = 0; q < (1 << VB) - 1; ++q) code += (bnd[q] < y[k]) ? 1u : 0u;
-        const int e = e0 + k;
-        if (tiled) {
-          vc_s[tid][e] = (uint8_t)code;
-        } else {
-          const int bitpos = e * VB;  // little-endian bit stream (3-bit: 8 codes per 24 bits)
-          outw[bitpos >> 5] |= code << (bitpos & 31);
-          if ((bitpos & 31) + VB > 32) outw[(bitpos >> 5) + 1] |= code >> (32 - (bitpos & 31));
-        }
-      }
-    }
-    if (!tiled) {
-      uint4* dst = reinterpret_cast<uint4*>(a.p.vcodes + row * VROW);
-#pragma unroll
-      for (int k = 0; k < VROW / 16; ++k)
-        dst[k] = make_uint4(outw[4 * k], outw[4 * k + 1], outw[4 * k + 2], outw[4 * k + 3]);
-    }
-    a.p.vnorm[row] = nrm;
+  for (int k = 0; k < D / 4; ++k) {
+    const float4 p4 = reinterpret_cast<const float4*>(a.p.pi + (size_t)ecol * D)[k];
+    pcol[4 * k] = p4.x;
+    pcol[4 * k + 1] = p4.y;
+    pcol[4 * k + 2] = p4.z;
+    pcol[4 * k + 3] = p4.w;
   }
-  if (tiled) {
+  float bnd[15];
+#pragma unroll
+  for (int k = 0; k < (1 << VB) - 1; ++k) bnd[k] = a.p.vbnd[k];
+  constexpr int kVBatch = 64;
+  float (*u_s)[D] = reinterpret_cast<float (*)[D]>(&kt_s[0][0] + TQK_MAX_G * D / 2);
+  static_assert(TQK_MAX_G * D + kVBatch * D * 4 <= TQK_MAX_G * (D + 8) * 2, "value staging overflows the key tile");
+  for (int t0 = 0; t0 < G; t0 += kVBatch) {
+    const int nb = min(kVBatch, G - t0);
+    // (1) norms and normalised rows, four threads per token: thread q holds
+    // the pairwise partial sums r[2q], r[2q + 1] (channels 8m + 2q, 8m + 2q + 1)
+    {
+      const int tt = tid >> 2, q = tid & 3;
+      if (tt < nb) {
+        const int t = g * G + t0 + tt;
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(token_src(a, a.p.hot_v, a.chunk_v, b, h, t));
+        float x0[16], x1[16];
+#pragma unroll
+        for (int m = 0; m < 16; ++m) {
+          const uint32_t w2 = src[4 * m + q];  // channels 8m + 2q, 8m + 2q + 1
+          x0[m] = h2f((uint16_t)(w2 & 0xFFFFu));
+          x1[m] = h2f((uint16_t)(w2 >> 16));
+        }
+        float r0 = __fmul_rn(x0[0], x0[0]), r1 = __fmul_rn(x1[0], x1[0]);
+#pragma unroll
+        for (int m = 1; m < 16; ++m) {
+          r0 = __fadd_rn(r0, __fmul_rn(x0[m], x0[m]));
+          r1 = __fadd_rn(r1, __fmul_rn(x1[m], x1[m]));
+        }
+        // pairwise tree ((r0 + r1) + (r2 + r3)) + ((r4 + r5) + (r6 + r7))
+        const float pa = __fadd_rn(r0, r1);
+        const float po = __shfl_xor(pa, 1, 4);
+        const float pb = (q & 1) ? __fadd_rn(po, pa) : __fadd_rn(pa, po);
+        const float pbo = __shfl_xor(pb, 2, 4);
+        const float ss = (q & 2) ? __fadd_rn(pbo, pb) : __fadd_rn(pb, pbo);
+        const float nrm = __builtin_sqrtf(ss);  // correctly rounded (-fhip-fp32-correctly-rounded-divide-sqrt)
+        const float safe = fmaxf(nrm, 1e-30f);
+#pragma unroll
+        for (int m = 0; m < 16; ++m) {
+          u_s[tt][8 * m + 2 * q] = __fdiv_rn(x0[m], safe);
+          u_s[tt][8 * m + 2 * q + 1] = __fdiv_rn(x1[m], safe);
+        }
+        if (q == 0)
+          a.p.vnorm[page_row(a.p.block_table, d.max_pages_per_seq, b, t, P, d.n_pages, h)] = nrm;
+      }
+    }
     __syncthreads();
+    // (2) rotation and codes: tokens j, j + 1 of the batch per step (two chains)
+    for (int j = 2 * (wv >> 1); j < nb; j += 4) {
+      const int j1 = min(j + 1, nb - 1);
+      float y0 = 0.f, y1 = 0.f;
+#pragma unroll
+      for (int d4 = 0; d4 < D / 4; ++d4) {
+        const float4 ua = *reinterpret_cast<const float4*>(&u_s[j][4 * d4]);
+        const float4 ub = *reinterpret_cast<const float4*>(&u_s[j1][4 * d4]);
+        y0 = __fadd_rn(y0, __fmul_rn(ua.x, pcol[4 * d4]));
+        y1 = __fadd_rn(y1, __fmul_rn(ub.x, pcol[4 * d4]));
+        y0 = __fadd_rn(y0, __fmul_rn(ua.y, pcol[4 * d4 + 1]));
+        y1 = __fadd_rn(y1, __fmul_rn(ub.y, pcol[4 * d4 + 1]));
+        y0 = __fadd_rn(y0, __fmul_rn(ua.z, pcol[4 * d4 + 2]));
+        y1 = __fadd_rn(y1, __fmul_rn(ub.z, pcol[4 * d4 + 2]));
+        y0 = __fadd_rn(y0, __fmul_rn(ua.w, pcol[4 * d4 + 3]));
+        y1 = __fadd_rn(y1, __fmul_rn(ub.w, pcol[4 * d4 + 3]));
+      }
+      uint32_t c0 = 0, c1 = 0;
+#pragma unroll
+      for (int k = 0; k < (1 << VB) - 1; ++k) {
+        c0 += (bnd[k] < y0) ? 1u : 0u;
+        c1 += (bnd[k] < y1) ? 1u : 0u;
+      }
+      vc_s[t0 + j][ecol] = (uint8_t)c0;
+      if (j + 1 < nb) vc_s[t0 + j + 1][ecol] = (uint8_t)c1;
+    }
+    __syncthreads();
+  }
+  // (3) the code rows: 4-token x 8-channel units of 16-token tiles, or the
+  // reference's little-endian bit stream per token
+  if (tiled) {
     // one unit = tokens [16T + 4lg, +4) x channels [8c, +8) of 16-token tile T
     for (int un = tid; un < (G / 16) * 64; un += kThreads) {
       const int T = un >> 6, lg = (un >> 4) & 3, c = un & 15;
@@ -289,8 +314,25 @@ __global__ __launch_bounds__(kThreads) void tqk_encode_group(EncodeArgs a) {
 #pragma unroll
       for (int k = 0; k < VROW / 16; ++k) dst[k] = w[k];
     }
+  } else if (tid < G) {
+    uint32_t outw[VROW / 4];
+#pragma unroll
+    for (int k = 0; k < VROW / 4; ++k) outw[k] = 0u;
+#pragma unroll
+    for (int e = 0; e < D; ++e) {
+      const uint32_t code = vc_s[tid][e];
+      const int bitpos = e * VB;  // little-endian bit stream (3-bit: 8 codes per 24 bits)
+      outw[bitpos >> 5] |= code << (bitpos & 31);
+      if ((bitpos & 31) + VB > 32) outw[(bitpos >> 5) + 1] |= code >> (32 - (bitpos & 31));
+    }
+    const size_t row = page_row(a.p.block_table, d.max_pages_per_seq, b, g * G + tid, P, d.n_pages, h);
+    uint4* dst = reinterpret_cast<uint4*>(a.p.vcodes + row * VROW);
+#pragma unroll
+    for (int k = 0; k < VROW / 16; ++k)
+      dst[k] = make_uint4(outw[4 * k], outw[4 * k + 1], outw[4 * k + 2], outw[4 * k + 3]);
   }
 }
+
 
 struct HotArgs {
   tqk_cache_desc d;
