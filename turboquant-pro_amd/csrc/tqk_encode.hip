@@ -20,6 +20,9 @@
 namespace {
 
 constexpr int kThreads = 256;
+// the group encode: eight waves, two per SIMD (its LDS allows one workgroup per CU)
+constexpr int kEncThreads = 512;
+constexpr int kEncWaves = kEncThreads / 64;
 
 struct EncodeArgs {
   tqk_cache_desc d;
@@ -46,7 +49,7 @@ __device__ __forceinline__ const uint16_t* token_src(const EncodeArgs& a, const 
 __device__ __forceinline__ uint32_t abs_h(uint16_t x) { return x & 0x7FFFu; }
 
 template <int VB>
-__global__ __launch_bounds__(kThreads) void tqk_encode_group(EncodeArgs a) {
+__global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
   constexpr int D = TQK_D;
   const int item = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
   const tqk_cache_desc& d = a.d;
@@ -58,13 +61,13 @@ __global__ __launch_bounds__(kThreads) void tqk_encode_group(EncodeArgs a) {
   __shared__ __align__(16) uint16_t kt_s[TQK_MAX_G][D + 8];  // key tile, fp16 bits (row padded vs bank conflicts)
   __shared__ float cent_s[D][17];            // per-channel grids (padded)
   __shared__ uint32_t thr_s[D];              // fp16 magnitude threshold per channel
-  __shared__ int32_t wsum_s[4];
+  __shared__ int32_t wsum_s[kEncWaves];
   // packed key codes of the group, written out after the outlier pass has put
   // the NF4 zero level (code 7) at every stored outlier position
   __shared__ __align__(16) uint8_t kc_s[TQK_MAX_G][D / 2];
 
   // ---- stage the key tile ----------------------------------------------
-  for (int idx = tid; idx < G * 16; idx += kThreads) {
+  for (int idx = tid; idx < G * 16; idx += kEncThreads) {
     const int t = idx >> 4, c = idx & 15;
     const uint4* src =
         reinterpret_cast<const uint4*>(token_src(a, a.p.hot_k, a.chunk_k, b, h, g * G + t));
@@ -92,7 +95,7 @@ __global__ __launch_bounds__(kThreads) void tqk_encode_group(EncodeArgs a) {
     for (int l = 0; l < 16; ++l) cent_s[j][l] = __fadd_rn(mu, __fmul_rn(amax, kNF4[l]));
     a.p.gscale[mbase + j] = amax;
     a.p.gmean[mbase + j] = mu;
-  } else if (kout > 0 && kout < G) {
+  } else if (tid < 2 * D && kout > 0 && kout < G) {
     // k-th largest |x| as the largest fp16 magnitude pattern T with
     // #{ |x_s| >= T } >= k (NaN patterns order above inf, as np.partition does).
     const int j = tid - D;
@@ -107,7 +110,7 @@ __global__ __launch_bounds__(kThreads) void tqk_encode_group(EncodeArgs a) {
   }
   __syncthreads();
 
-  // ---- codes: thread = (channel pair, token quarter); one byte per (token, pair)
+  // ---- codes: thread = (channel pair, token slice); one byte per (token, pair)
   {
     const int jp = tid & 63, sq = tid >> 6;
     float c0[16], c1[16];
@@ -116,7 +119,7 @@ __global__ __launch_bounds__(kThreads) void tqk_encode_group(EncodeArgs a) {
       c0[l] = cent_s[2 * jp][l];
       c1[l] = cent_s[2 * jp + 1][l];
     }
-    const int per_q = (G + 3) / 4;
+    const int per_q = (G + kEncWaves - 1) / kEncWaves;
     const int s0 = sq * per_q, s1 = min(G, s0 + per_q);
     for (int s = s0; s < s1; ++s) {
       const float x0 = h2f(kt_s[s][2 * jp]), x1 = h2f(kt_s[s][2 * jp + 1]);
@@ -158,7 +161,8 @@ __global__ __launch_bounds__(kThreads) void tqk_encode_group(EncodeArgs a) {
     __syncthreads();
     int wofs = 0;
     for (int w = 0; w < (tid >> 6); ++w) wofs += wsum_s[w];
-    const int total = wsum_s[0] + wsum_s[1] + wsum_s[2] + wsum_s[3];
+    int total = 0;
+    for (int w = 0; w < kEncWaves; ++w) total += wsum_s[w];
     int off = wofs + incl - cnt;
     // token s = TQK_OBLK*k - 1 closes block k-1: its inclusive offset is the bound
     if (tid < G && ((tid + 1) % TQK_OBLK) == 0 && (tid + 1) / TQK_OBLK <= TQK_NOB)
@@ -194,7 +198,7 @@ __global__ __launch_bounds__(kThreads) void tqk_encode_group(EncodeArgs a) {
   uint8_t (*vc_s)[D] = reinterpret_cast<uint8_t (*)[D]>(&kt_s[0][0]);
   __syncthreads();
   // key code rows, 16 bytes per thread
-  for (int idx = tid; idx < G * (D / 32); idx += kThreads) {
+  for (int idx = tid; idx < G * (D / 32); idx += kEncThreads) {
     const int t = idx / (D / 32), ch = idx % (D / 32);
     const size_t row = page_row(a.p.block_table, d.max_pages_per_seq, b, g * G + t, P, d.n_pages, h);
     *reinterpret_cast<uint4*>(a.p.kcodes + row * (D / 2) + 16 * ch) =
@@ -202,7 +206,8 @@ __global__ __launch_bounds__(kThreads) void tqk_encode_group(EncodeArgs a) {
   }
   // Rotation operands: lane e of wave w owns rotated channel
   // 64 * (w & 1) + lane and keeps column e of Pi_T (pi[e][0..D)) in
-  // registers; waves w and w ^ 1 split the channels, w >> 1 the tokens.
+  // registers; waves w and w ^ 1 split the channels, w >> 1 the tokens
+  // (two waves per SIMD).
   // Normalised rows u of kVBatch tokens at a time sit in LDS after the code
   // staging area, read as wave-uniform broadcasts.  Every y_e is still the
   // sequential, separately rounded sum over d.
@@ -264,7 +269,7 @@ __global__ __launch_bounds__(kThreads) void tqk_encode_group(EncodeArgs a) {
     }
     __syncthreads();
     // (2) rotation and codes: tokens j, j + 1 of the batch per step (two chains)
-    for (int j = 2 * (wv >> 1); j < nb; j += 4) {
+    for (int j = 2 * (wv >> 1); j < nb; j += kEncWaves) {
       const int j1 = min(j + 1, nb - 1);
       float y0 = 0.f, y1 = 0.f;
 #pragma unroll
@@ -295,7 +300,7 @@ __global__ __launch_bounds__(kThreads) void tqk_encode_group(EncodeArgs a) {
   // reference's little-endian bit stream per token
   if (tiled) {
     // one unit = tokens [16T + 4lg, +4) x channels [8c, +8) of 16-token tile T
-    for (int un = tid; un < (G / 16) * 64; un += kThreads) {
+    for (int un = tid; un < (G / 16) * 64; un += kEncThreads) {
       const int T = un >> 6, lg = (un >> 4) & 3, c = un & 15;
       uint32_t w[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
@@ -461,9 +466,9 @@ int tqk_encode_groups(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t 
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid(n_items, d->n_kv_heads);
   if (d->value_bits == 3)
-    hipLaunchKernelGGL(tqk_encode_group<3>, grid, dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL(tqk_encode_group<3>, grid, dim3(kEncThreads), 0, st, a);
   else
-    hipLaunchKernelGGL(tqk_encode_group<4>, grid, dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL(tqk_encode_group<4>, grid, dim3(kEncThreads), 0, st, a);
   return hipGetLastError() == hipSuccess ? TQK_OK : TQK_EHIP;
 }
 
