@@ -159,6 +159,43 @@ def _cpu_model():
     return "unknown"
 
 
+def encode_bench(torch, cfg, args, chunk=4096):
+    """Prefill encode: the config's batch appended in ``chunk``-token chunks up
+    to its context (group flushes through the encode kernel, hot-ring copies),
+    ``args.steps`` times after one untimed fill.  Bytes per the survey's
+    encode formula: fp16 K+V in (512 B per token-head) + the coded groups out
+    (135 B per cold token-head at K4/V3)."""
+    from turboquant_pro_amd import TQKVPool
+    B, Hkv, Hq, L, vb = cfg["B"], cfg["Hkv"], cfg["Hq"], cfg["L"], cfg["vbits"]
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(11)
+    scale = torch.exp(torch.randn((B, Hkv, 1, 128), generator=gen, device="cuda"))
+    chunks = [synth_chunk(torch, gen, scale, t, min(chunk, L - t), B, Hkv) for t in range(0, L, chunk)]
+    pool = TQKVPool(n_kv_heads=Hkv, n_q_heads=Hq, max_batch=B, max_seq_len=L, value_bits=vb, seed=0)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    times = []
+    for it in range(args.steps + 1):
+        pool.reset()
+        torch.cuda.synchronize()
+        e0.record()
+        for k, v in chunks:
+            pool.append(k, v)
+        e1.record()
+        torch.cuda.synchronize()
+        if it:
+            times.append(e0.elapsed_time(e1))
+    ms = sorted(times)[len(times) // 2]
+    n_cold = n_groups(L) * ((512 + 1) // 2)
+    nbytes = B * Hkv * (L * 2 * 128 * 2 + n_cold * (128 * 4 // 8 + 128 * vb // 8 + 4)) \
+        + B * Hkv * n_groups(L) * (2 * 128 * 4 + 640 * 6)
+    print(json.dumps({"metric": "prefill encode GB/s (fp16 K+V in + coded groups out)",
+                      "value": round(nbytes / (ms * 1e-3) / 1e9, 1), "unit": "GB/s",
+                      "ms_per_fill": round(ms, 3), "tokens_per_s": round(B * L / (ms * 1e-3)),
+                      "fills": len(times), "bytes": nbytes,
+                      "config": {"name": args.config, "batch": B, "context": L, "n_kv_heads": Hkv,
+                                 "chunk": chunk, "value_bits": vb}}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -169,6 +206,9 @@ def main():
     ap.add_argument("--config", default="headline", choices=sorted(CONFIGS))
     ap.add_argument("--replicas", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--encode", action="store_true",
+                    help="measure the prefill encode instead (quantize-on-append of 4096-token chunks "
+                         "of the chosen config; prints its own JSON line, not the decode metric)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="after timing, copy a 256 MiB buffer 3 times (calibration kernel for "
                          "the FETCH_SIZE / WRITE_SIZE counters)")
@@ -182,6 +222,9 @@ def main():
     import torch
     from turboquant_pro_amd import _native as N
 
+    if args.encode:
+        encode_bench(torch, CONFIGS[args.config], args)
+        return
     cfg = CONFIGS[args.config]
     B, Hkv, Hq, L = cfg["B"], cfg["Hkv"], cfg["Hq"], cfg["L"]
     print(f"[bench] config={args.config} {cfg} replicas={args.replicas}", file=sys.stderr, flush=True)
