@@ -101,11 +101,13 @@ int tqk_version(void);
 int tqk_check_desc(const tqk_cache_desc* d);
 
 /* Bytes of decode workspace needed for `batch` sequences of at most
- * `max_len` tokens.  Host function, no GPU work.  The workspace holds the
- * split partials and, after them, one arrival counter per (sequence, kv head)
- * for tqk_decode's in-kernel merge: zero-fill a new workspace once before its
- * first tqk_decode; every completed call leaves the counters at zero again.
- * Calls that share a workspace must not overlap. */
+ * `max_len` tokens.  Host function, no GPU work.  The workspace starts with
+ * the arrival counters of tqk_decode's in-kernel merge, one 32-bit word per
+ * (sequence, kv head) for max(batch, n_pages / max_pages_per_seq) sequences,
+ * then holds the split partials: zero-fill a new workspace once before its
+ * first tqk_decode; every completed call leaves the counters at zero again,
+ * whatever the batch and max_len of the next call.  Calls that share a
+ * workspace must not overlap. */
 size_t tqk_decode_workspace_bytes(const tqk_cache_desc* d, int32_t batch, int32_t max_len);
 
 /*

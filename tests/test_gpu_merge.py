@@ -103,3 +103,30 @@ def test_in_kernel_merge_many_splits():
     assert all(torch.equal(f, ref) for f in fused)
     sc = O.SequenceCache(hot_window=512, value_bits=3, outlier_frac=0.02).build(k[0], v[0], pi, pi_t)
     assert_attn_close(fused[0][0].cpu().numpy(), sc.attend(q[0]), what="L=20000")
+
+
+def test_in_kernel_merge_after_the_plan_shrinks():
+    """The pool keeps its workspace when a later decode needs fewer splits
+    (a shorter cache after ``reset``): the arrival counters must not sit where
+    the earlier, larger plan wrote partials."""
+    from turboquant_pro_amd import TQKVPool
+    B, Hkv, Hq = 2, 2, 8
+    print("[merge] plan shrinks: L=9000 then L=1500 on the same workspace", flush=True)
+    k, v, q = O.synthetic_kv(98, B, Hkv, Hq, 9000)
+    pi, pi_t = O.rotation(7, 128)
+    pool = TQKVPool(n_kv_heads=Hkv, n_q_heads=Hq, max_batch=B, max_seq_len=9000, rotation=(pi, pi_t))
+    qd = _dev(q)
+    pool.append(_dev(k), _dev(v))
+    big = pool.decode(qd)
+    torch.cuda.synchronize()
+    assert torch.equal(big, _two_phase(pool, qd))
+    pool.reset()
+    pool.append(_dev(k[:, :, :1500]), _dev(v[:, :, :1500]))
+    small = [pool.decode(qd) for _ in range(2)]
+    ref = _two_phase(pool, qd)
+    torch.cuda.synchronize()
+    assert all(torch.equal(s, ref) for s in small)
+    for b in range(B):
+        sc = O.SequenceCache(hot_window=512, value_bits=3, outlier_frac=0.02).build(
+            k[b, :, :1500], v[b, :, :1500], pi, pi_t)
+        assert_attn_close(small[0][b].cpu().numpy(), sc.attend(q[b]), what=f"seq {b}")

@@ -1520,7 +1520,7 @@ __host__ __device__ inline bool mfma_path(const tqk_cache_desc& d) {
 
 struct Plan {
   int n_cold_splits, n_hot_splits, groups_per_split, hot_per_split;
-  size_t arrive_off;  // arrival counters after the partials
+  size_t counter_bytes;  // arrival counters at the workspace's start, then the partials
   size_t ws_bytes;
 };
 
@@ -1578,8 +1578,13 @@ Plan make_plan(const tqk_cache_desc* d, int batch, int max_len) {
   }
   const size_t ns = (size_t)(pl.n_cold_splits + pl.n_hot_splits);
   const size_t per = (size_t)batch * d->n_q_heads * ns;
-  pl.arrive_off = (per * sizeof(float) * (2 + TQK_D) + 255) & ~(size_t)255;
-  pl.ws_bytes = pl.arrive_off + (size_t)batch * d->n_kv_heads * sizeof(uint32_t) + 256;
+  // One counter per (seq, kv head) of the cache's capacity, at a place that
+  // no plan's partials reach: the counters stay zero between calls whatever
+  // the batch and split counts of the next call.
+  const int cap_seqs = d->max_pages_per_seq > 0 ? d->n_pages / d->max_pages_per_seq : batch;
+  const size_t n_counters = (size_t)(batch > cap_seqs ? batch : cap_seqs) * d->n_kv_heads;
+  pl.counter_bytes = (n_counters * sizeof(uint32_t) + 255) & ~(size_t)255;
+  pl.ws_bytes = pl.counter_bytes + per * sizeof(float) * (2 + TQK_D) + 256;
   return pl;
 }
 
@@ -1610,7 +1615,8 @@ DecodeArgs make_args(const tqk_cache_desc* d, const tqk_cache_ptrs* p, const Pla
   a.p = *p;
   a.q = q;
   a.seq_lens = seq_lens;
-  a.pm = reinterpret_cast<float*>(ws);
+  a.arrive = reinterpret_cast<uint32_t*>(ws);
+  a.pm = reinterpret_cast<float*>(static_cast<char*>(ws) + pl.counter_bytes);
   a.pl = a.pm + per;
   a.pacc = a.pl + per;
   a.n_cold_splits = pl.n_cold_splits;
@@ -1620,7 +1626,6 @@ DecodeArgs make_args(const tqk_cache_desc* d, const tqk_cache_ptrs* p, const Pla
   a.split_base = 0;
   a.batch = batch;
   a.out = nullptr;
-  a.arrive = reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + pl.arrive_off);
   return a;
 }
 
