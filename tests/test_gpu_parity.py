@@ -212,3 +212,21 @@ def test_golden_fixture_k4v3(golden_dir):
     got = pool.decode(_dev(q[None])).cpu().numpy()[0]
     assert_attn_close(got, g["attn_out"])
     del random_rotation
+
+
+@pytest.mark.parametrize("frac", [0.1, 0.3])
+def test_decode_heavy_outliers(frac):
+    """Heavy side-lists (turboquant_pro tests/test_kv_fused_pck.py:99-103): at
+    10 % and 30 % outliers a 32-token block holds ~400 and ~1200 entries, so
+    the decode applies them in several 128-entry passes.  Codes and side-lists
+    stay bit-exact; the output stays within the bar of dequantize-then-attend."""
+    B, Hkv, Hq, L = 1, 2, 8, 1100
+    print(f"[decode heavy outliers] frac={frac}", flush=True)
+    k, v, q = O.synthetic_kv(83, B, Hkv, Hq, L)
+    seqs, rot = oracle_state(k, v, 512, 3, seed=4, outlier_frac=frac)
+    pool = _pool(n_kv_heads=Hkv, n_q_heads=Hq, max_batch=B, max_seq_len=L, rotation=rot,
+                 outlier_frac=frac)
+    _fill(pool, k, v)
+    _check_codes(pool, seqs, B)
+    got = pool.decode(_dev(q)).cpu().numpy()
+    assert_attn_close(got[0], seqs[0].attend(q[0]), what=f"frac={frac}")
