@@ -40,7 +40,18 @@ CONFIGS = {
     "c2_128k": dict(B=1, Hkv=8, Hq=32, L=131072, vbits=3),
     "c0_mha4k": dict(B=1, Hkv=32, Hq=32, L=4096, vbits=4),
     "c4_70b": dict(B=32, Hkv=8, Hq=64, L=32768, vbits=3),
+    # config 3: 64 sequences of seeded lengths U[1024, 32768], 16-token pages,
+    # block table a seeded permutation of the physical pages
+    "c3_paged_ragged": dict(B=64, Hkv=8, Hq=32, L=32768, vbits=3, ragged=True, page=16),
 }
+
+
+def config_lengths(cfg):
+    """Sequence lengths of a config: all L, or the seeded ragged draw."""
+    import numpy as np
+    if cfg.get("ragged"):
+        return [int(x) for x in np.random.default_rng(3).integers(1024, cfg["L"] + 1, size=cfg["B"])]
+    return [cfg["L"]] * cfg["B"]
 
 
 def n_groups(L, W=512):
@@ -80,9 +91,16 @@ def synth_chunk(torch, gen, scale, t0, n, B, Hkv, D=128, theta=10000.0):
 
 def build_pool(torch, cfg, seed, chunk=4096):
     from turboquant_pro_amd import TQKVPool
+    import numpy as np
     B, Hkv, Hq, L = cfg["B"], cfg["Hkv"], cfg["Hq"], cfg["L"]
+    lens = config_lengths(cfg)
+    extra = {}
+    if cfg.get("page"):
+        P = cfg["page"]
+        max_pages = n_groups(L) * 256 // P
+        extra = dict(page_tokens=P, block_table=np.random.default_rng(4).permutation(B * max_pages).astype(np.int32))
     pool = TQKVPool(n_kv_heads=Hkv, n_q_heads=Hq, max_batch=B, max_seq_len=L,
-                    value_bits=cfg["vbits"], seed=seed)
+                    value_bits=cfg["vbits"], seed=seed, **extra)
     gen = torch.Generator(device="cuda")
     gen.manual_seed(seed)
     scale = torch.exp(torch.randn((B, Hkv, 1, 128), generator=gen, device="cuda"))
@@ -95,7 +113,7 @@ def build_pool(torch, cfg, seed, chunk=4096):
     while t < L:
         n = min(chunk, L - t)
         k, v = synth_chunk(torch, gen, scale, t, n, B, Hkv)
-        pool.append(k, v)
+        pool.append(k, v, n_new=[min(n, max(0, x - t)) for x in lens])
         t += n
     torch.cuda.synchronize()
     return pool
@@ -266,7 +284,7 @@ def main():
     e1.record(stream)
     torch.cuda.synchronize()
     split_ms = e0.elapsed_time(e1) / args.steps
-    nbytes = step_bytes([L] * B, Hkv, Hq, vbits=cfg["vbits"])
+    nbytes = step_bytes(config_lengths(cfg), Hkv, Hq, vbits=cfg["vbits"])
     achieved = nbytes / (split_ms * 1e-3) / 1e9
     step_gbs = nbytes / (ms_per_step * 1e-3) / 1e9
 
@@ -297,7 +315,11 @@ def main():
         "dtype": "fp32",
         "data": "synthetic (seeded lognormal-scaled RoPE fp16 keys with 2% x10 channels, N(0,1) "
                 "values and queries), cache filled through the GPU encode path",
-        "config": {"workload": f"decode step, batch {B} x context {L}, {Hq} q-heads / {Hkv} kv-heads, "
+        "config": {"workload": f"decode step, batch {B} x context "
+                               + (f"U[1024, {L}] (seeded, mean {sum(config_lengths(cfg)) // B}), "
+                                  f"{cfg['page']}-token pages, permuted block table"
+                                  if cfg.get("ragged") else f"{L}")
+                               + f", {Hq} q-heads / {Hkv} kv-heads, "
                                f"head_dim 128, K4 asym-NF4 + 2% fp16 outliers, V{cfg['vbits']} "
                                f"PolarQuant, fp16 hot window 512",
                    "name": args.config, "batch": B, "context": L, "n_q_heads": Hq,
