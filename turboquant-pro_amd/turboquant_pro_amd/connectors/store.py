@@ -180,8 +180,9 @@ class TurboQuantBlockStore:
         dequantize / re-encode), the hot tokens as their GPU dequantization
         (the store holds nothing uncompressed).  Returns the tokens restored,
         0 when nothing is stored (a miss)."""
+        import torch
+
         from ..codebooks import random_rotation
-        torch = __import__("torch")
         groups = []
         with self._lock:
             while (request_id, self._group_name(layer_name, len(groups))) in self._records:
