@@ -683,6 +683,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
 
   __shared__ __align__(16) uint8_t lut[LutGeom<VB>::kBytes];
   __shared__ __align__(16) uint32_t qq_s[D][GQ];        // raw fp16 q twice {q, q}: [channel][head]
+  __shared__ __align__(16) uint16_t qf_s[GQ][D];        // raw fp16 q, head-major (hot-window operand)
   // scaled q, head-major; rows padded by 4 banks so that the head rows read by
   // one lane group fall in different banks
   __shared__ __align__(16) float q_h_s[GQ][D + 4];
@@ -727,6 +728,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   for (int i = tid; i < GQ * D; i += kMThreads) {
     const uint32_t qr = a.q[((size_t)b * Hq + h * GQ + i / D) * D + i % D];
     qq_s[i % D][i / D] = qr | (qr << 16);
+    qf_s[i / D][i % D] = (uint16_t)qr;
     q_h_s[i / D][i % D] = h2f((uint16_t)qr) * qscale;
   }
   __syncthreads();
@@ -1160,7 +1162,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     H8 Bq[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
-      Bq[ks].v = *reinterpret_cast<const uint4*>(a.q + ((size_t)b * Hq + h * GQ + hq) * D + 32 * ks + 8 * lg);
+      Bq[ks].v = *reinterpret_cast<const uint4*>(&qf_s[hq][32 * ks + 8 * lg]);
     for (int hb = split * kMWaves + w; hb < nhb; hb += a.n_cold_splits * kMWaves) {
       // n_cold and the ring size are multiples of 32: the block's 32 ring rows
       // are consecutive and inside the ring, so every row is loaded (keys and
