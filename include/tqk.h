@@ -65,7 +65,7 @@ typedef struct tqk_cache_desc {
   int32_t hot_window;           /* W; groups flush when the hot window exceeds W */
   int32_t group_tokens;         /* G = (W + 1) / 2, 1..256 */
   int32_t page_tokens;          /* P, divides G */
-  int32_t key_bits;             /* 4 (per-channel asym-NF4) */
+  int32_t key_bits;             /* 4 (per-channel asym-NF4 or uniform, see key_grid) */
   int32_t value_bits;           /* 3 or 4 (PolarQuant) */
   int32_t outliers_per_channel; /* k = max(1, round(G * outlier_frac)), 0 = no side-list */
   int32_t outlier_cap;          /* oent capacity per (group slot, head) */
@@ -74,6 +74,9 @@ typedef struct tqk_cache_desc {
   int32_t hot_ring;             /* ring capacity in tokens, >= W */
   int32_t n_pages;              /* physical pages in the pool (block_table entries index them) */
   float sm_scale;               /* softmax scale, 1/sqrt(D) */
+  int32_t key_grid;             /* 0: asym-NF4 (gmean = channel mean, gscale = abs-max of the
+                                   centred channel, levels NF4); 1: uniform (gmean = channel min,
+                                   gscale = max(max - min, 1e-8) / 15, levels 0..15) */
 } tqk_cache_desc;
 
 typedef struct tqk_cache_ptrs {
@@ -94,7 +97,7 @@ typedef struct tqk_cache_ptrs {
   const float* vbnd;    /* 2^vb - 1 fp32 value boundaries */
 } tqk_cache_ptrs;
 
-/* Library ABI version (bumped on any signature or layout change); this header is version 3. */
+/* Library ABI version (bumped on any signature or layout change); this header is version 4. */
 int tqk_version(void);
 
 /* Validate a descriptor; TQK_OK when the GPU path supports it. */

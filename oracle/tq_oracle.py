@@ -160,6 +160,9 @@ class KeyGroup:
     outlier_idx: np.ndarray | None   # int32 flat indices into (1, H, S, D)
     outlier_val: np.ndarray | None   # fp16 values at those indices
     shape: tuple = ()
+    # "nf4_asym", or "uniform": then nf4_scale / nf4_mean hold the reference's
+    # per-channel scale / zero (its (1, H, 1, D) arrays without the unit axes)
+    grid: str = "nf4_asym"
 
 
 @dataclass
@@ -178,6 +181,43 @@ def outlier_count_per_channel(n_tokens: int, outlier_frac: float) -> int:
     return max(1, int(round(n_tokens * outlier_frac)))
 
 
+def key_outliers(x4: np.ndarray, outlier_frac: float):
+    """Dense-sparse outliers of a (1, H, S, D) block, turboquant_pro/per_channel_kv.py:269-283:
+    the k largest |x| per (head, channel) and every tie, as flat int32
+    indices in C order and their fp16 values; (None, None) when f == 0."""
+    if outlier_frac <= 0.0:
+        return None, None
+    S = x4.shape[2]
+    k = outlier_count_per_channel(S, outlier_frac)
+    mag = np.abs(x4)
+    if k >= S:
+        sel = np.ones(x4.shape, dtype=bool)
+    else:
+        # k-th largest magnitude per (head, channel); >= keeps every tie.
+        thr = np.partition(mag, S - k, axis=2)[:, :, S - k:S - k + 1, :]
+        sel = mag >= thr
+    oidx = np.flatnonzero(sel).astype(np.int32)
+    return oidx, x4.reshape(-1)[oidx].astype(np.float16)
+
+
+def encode_keys_uniform(x: np.ndarray, outlier_frac: float) -> KeyGroup:
+    """Uniform asymmetric per-channel 4-bit key encode of one group ``x``
+    (H, S, D) fp32, turboquant_pro/per_channel_kv.py:303-317: per channel
+    ``mn``/``mx`` over the tokens, ``scale = max(mx - mn, 1e-8) / 15``,
+    ``code = clip(round_half_even((x - mn) / scale), 0, 15)``; outliers as for
+    NF4 (the codes at their positions are kept)."""
+    x4 = np.asarray(x, dtype=np.float32)[None]
+    _, H, S, D = x4.shape
+    oidx, oval = key_outliers(x4, outlier_frac)
+    mn = x4.min(axis=2, keepdims=True)
+    mx = x4.max(axis=2, keepdims=True)
+    scale = np.maximum(mx - mn, 1e-8) / 15
+    codes = np.clip(np.round((x4 - mn) / scale), 0, 15).astype(np.uint8)
+    return KeyGroup(codes=codes[0], packed=pack_key_codes(codes, 4),
+                    nf4_scale=scale[0, :, 0, :].astype(np.float32), nf4_mean=mn[0, :, 0, :].astype(np.float32),
+                    outlier_idx=oidx, outlier_val=oval, shape=(1, H, S, D), grid="uniform")
+
+
 def encode_keys(x: np.ndarray, outlier_frac: float) -> KeyGroup:
     """Asym-NF4 per-channel key encode of one group ``x`` (H, S, D) fp32.
 
@@ -188,18 +228,7 @@ def encode_keys(x: np.ndarray, outlier_frac: float) -> KeyGroup:
     """
     x4 = np.asarray(x, dtype=np.float32)[None]
     _, H, S, D = x4.shape
-    oidx = oval = None
-    if outlier_frac > 0.0:
-        k = outlier_count_per_channel(S, outlier_frac)
-        mag = np.abs(x4)
-        if k >= S:
-            sel = np.ones(x4.shape, dtype=bool)
-        else:
-            # k-th largest magnitude per (head, channel); >= keeps every tie.
-            thr = np.partition(mag, S - k, axis=2)[:, :, S - k:S - k + 1, :]
-            sel = mag >= thr
-        oidx = np.flatnonzero(sel).astype(np.int32)
-        oval = x4.reshape(-1)[oidx].astype(np.float16)
+    oidx, oval = key_outliers(x4, outlier_frac)
     mean = x4.mean(axis=2)                                   # (1, H, D)
     centred = x4 - mean[:, :, None, :]
     amax = np.maximum(np.abs(centred).max(axis=2), 1e-8)     # (1, H, D)
@@ -238,10 +267,15 @@ def decode_keys(g: KeyGroup) -> np.ndarray:
     (nf4 branch with calibrated mean, then the fp16 outlier overwrite)."""
     _, H, S, D = g.shape
     codes = unpack_key_codes(g.packed, H * S * D, 4).reshape(1, H, S, D)
-    grid = g.nf4_scale[None, ..., None] * NF4[None, None, None, :]
-    grid = grid + g.nf4_mean[None, ..., None]
-    out = np.take_along_axis(grid.astype(np.float32), np.moveaxis(codes, 2, -1), axis=-1)
-    out = np.moveaxis(out, -1, 2).astype(np.float32)
+    if g.grid == "uniform":
+        # per_channel_kv.py:529-530: idx * scale + zero, two fp32 roundings
+        out = codes.astype(np.float32) * g.nf4_scale[None, :, None, :] + g.nf4_mean[None, :, None, :]
+        out = out.astype(np.float32)
+    else:
+        grid = g.nf4_scale[None, ..., None] * NF4[None, None, None, :]
+        grid = grid + g.nf4_mean[None, ..., None]
+        out = np.take_along_axis(grid.astype(np.float32), np.moveaxis(codes, 2, -1), axis=-1)
+        out = np.moveaxis(out, -1, 2).astype(np.float32)
     if g.outlier_idx is not None:
         flat = out.reshape(-1)
         flat[g.outlier_idx] = g.outlier_val.astype(np.float32)
@@ -335,6 +369,7 @@ class SequenceCache:
     value_bits: int
     outlier_frac: float
     seed: int | None = 0
+    key_grid: str = "nf4_asym"       # or "uniform" (per_channel_kv.py:303-317)
     keys: list = field(default_factory=list)
     values: list = field(default_factory=list)
     hot_k: np.ndarray | None = None
@@ -349,7 +384,8 @@ class SequenceCache:
         self.keys, self.values = [], []
         for i in range(ng):
             sl = slice(G * i, G * (i + 1))
-            self.keys.append(encode_keys(k[:, sl].astype(np.float32), self.outlier_frac))
+            enc = encode_keys_uniform if self.key_grid == "uniform" else encode_keys
+            self.keys.append(enc(k[:, sl].astype(np.float32), self.outlier_frac))
             self.values.append(encode_values(v[:, sl].astype(np.float32), pi_t, bnd, self.value_bits))
         self.hot_k = k[:, G * ng:]
         self.hot_v = v[:, G * ng:]

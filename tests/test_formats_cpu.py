@@ -111,3 +111,22 @@ def test_clustered_block_table_is_a_permutation_with_adjacent_blocks():
                 assert pages == list(range(pages[0], pages[0] + 8))
     ident = TQKVPool._clustered_table(2, 10, 16, 256)
     assert np.array_equal(ident.reshape(-1), np.arange(20))
+
+
+def test_uniform_outlier_codes_round_trip(golden_dir):
+    """Uniform keys store code 0 at outlier positions (its level is the zero
+    term the decode's bias carries); restoring puts back the reference's own
+    codes there (tests/golden/perchannel_uniform.npz, written by
+    PerChannelKV.compress, turboquant_pro/per_channel_kv.py:303-317)."""
+    import os
+    z = np.load(os.path.join(golden_dir, "perchannel_uniform.npz"))
+    for tag in ("s256", "s200"):
+        H, S, D = z[f"{tag}_x"].shape
+        kp = z[f"{tag}_kpacked"].reshape(H, S, D // 2)
+        idx = z[f"{tag}_oidx"].astype(np.int64)
+        stored = F.mark_outlier_codes(kp, idx, grid="uniform")
+        codes = F.unpack_keys(stored, H * S * D)
+        assert np.all(codes[idx] == 0)
+        back = F.restore_outlier_codes(stored, idx, z[f"{tag}_oval"], z[f"{tag}_scale"], z[f"{tag}_zero"],
+                                       grid="uniform")
+        assert np.array_equal(back, kp)

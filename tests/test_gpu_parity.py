@@ -230,3 +230,29 @@ def test_decode_heavy_outliers(frac):
     _check_codes(pool, seqs, B)
     got = pool.decode(_dev(q)).cpu().numpy()
     assert_attn_close(got[0], seqs[0].attend(q[0]), what=f"frac={frac}")
+
+
+@pytest.mark.parametrize("vbits", [3, 4])
+def test_uniform_keys_encode_dequant_decode(vbits):
+    """Uniform per-channel keys (turboquant_pro/per_channel_kv.py:303-317,
+    529-530) through the same pool and kernels: the encode's codes, scale,
+    zero and side-list are bit-exact to the oracle (itself pinned to the
+    reference's vectors), the GPU dequant is bit-exact to the reference's
+    decompress order, and the fused decode (levels 0..15 in the code table)
+    is within the bar of dequantize-then-attend."""
+    B, Hkv, Hq, L = 2, 2, 8, 1300
+    print(f"[uniform keys] vbits={vbits}", flush=True)
+    k, v, q = O.synthetic_kv(87 + vbits, B, Hkv, Hq, L)
+    pi, pi_t = O.rotation(2, 128)
+    seqs = [O.SequenceCache(hot_window=512, value_bits=vbits, outlier_frac=0.02, key_grid="uniform")
+            .build(k[b], v[b], pi, pi_t) for b in range(B)]
+    pool = _pool(n_kv_heads=Hkv, n_q_heads=Hq, max_batch=B, max_seq_len=L, rotation=(pi, pi_t),
+                 value_bits=vbits, key_grid="uniform")
+    _fill(pool, k, v, chunks=[700, 1, 599])
+    _check_codes(pool, seqs, B)
+    kk, _ = pool.dequant_groups([(0, g) for g in range(pool.n_groups(0))])
+    for g in range(pool.n_groups(0)):
+        assert np.array_equal(kk[g].cpu().numpy(), O.decode_keys(seqs[0].keys[g]))
+    got = pool.decode(_dev(q)).cpu().numpy()
+    for b in range(B):
+        assert_attn_close(got[b], seqs[b].attend(q[b]), what=f"uniform seq {b}")

@@ -177,3 +177,21 @@ def test_n_groups_cadence():
 def test_decode_step_bytes_headline():
     b = O.decode_step_bytes([32768] * 16, 8, 32)
     assert abs(b / 1e6 - 591.2) < 0.5
+
+
+@pytest.mark.parametrize("tag", ["s256", "s200"])
+def test_uniform_keys_match_reference(golden_dir, tag):
+    """Uniform per-channel keys (turboquant_pro/per_channel_kv.py:303-317,
+    529-530) against the reference's own container and decompress
+    (tests/golden/perchannel_uniform.npz): packed codes, scale, zero,
+    outliers and the reconstruction, bit for bit."""
+    import os
+    z = np.load(os.path.join(golden_dir, "perchannel_uniform.npz"))
+    g = O.encode_keys_uniform(z[f"{tag}_x"], 0.02)
+    assert np.array_equal(g.packed, z[f"{tag}_kpacked"])
+    assert np.array_equal(g.nf4_scale, z[f"{tag}_scale"]) and np.array_equal(g.nf4_mean, z[f"{tag}_zero"])
+    assert np.array_equal(g.outlier_idx, z[f"{tag}_oidx"])
+    assert np.array_equal(g.outlier_val.view(np.uint16), z[f"{tag}_oval"].view(np.uint16))
+    assert np.array_equal(O.decode_keys(g), z[f"{tag}_decompressed"])
+    # codes are in range and the grid's ends are hit
+    assert g.codes.max() == 15 and g.codes.min() == 0

@@ -31,12 +31,17 @@ __host__ __device__ __forceinline__ int v_unit_bit(int u, int nt, int vb) {
 }
 
 // NormalFloat-4 levels, turboquant_pro/per_channel_kv.py:64-84.
+// Key level of code c: NF4 for key_grid 0, the code itself for uniform keys
+__device__ __forceinline__ float key_level(int grid, uint32_t c);
 __constant__ static const float kNF4[16] = {
     -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,
     -0.28444138169288635f, -0.18477343022823334f, -0.09105003625154495f, 0.0f,
     0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f,
     0.33791524171829224f, 0.44070982933044434f, 0.5626170039176941f,
     0.7229568362236023f, 1.0f};
+__device__ __forceinline__ float key_level(int grid, uint32_t c) {
+  return grid ? (float)c : kNF4[c];
+}
 
 __device__ __forceinline__ float h2f(uint16_t x) {
   return (float)__builtin_bit_cast(_Float16, x);

@@ -126,8 +126,8 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
 
   for (int i = tid; i < GQ * D; i += kThreads)
     q_s[i / D][i % D] = h2f(a.q[((size_t)b * Hq + h * GQ + i / D) * D + i % D]);
-  kl_s[tid][0] = kNF4[rev4(tid >> 4)];
-  kl_s[tid][1] = kNF4[rev4(tid & 15)];
+  kl_s[tid][0] = key_level(a.d.key_grid, rev4(tid >> 4));
+  kl_s[tid][1] = key_level(a.d.key_grid, rev4(tid & 15));
   if (VB == 3) {
     if (tid < 64) {
       vl_s[tid][0] = a.p.vcent[tid & 7];
@@ -220,7 +220,7 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
         const size_t row = page_row(bt, d.max_pages_per_seq, b, g * G + tt, P, d.n_pages, h);
         const uint32_t byte = a.p.kcodes[row * (D / 2) + (j >> 1)];
         const uint32_t c = (j & 1) ? rev4(byte & 15u) : rev4(byte >> 4);
-        const float delta = val - (a_s[j] * kNF4[c] + mu_s[j]);
+        const float delta = val - (a_s[j] * key_level(a.d.key_grid, c) + mu_s[j]);
 #pragma unroll
         for (int i = 0; i < GQ; ++i) atomicAdd(&sc_s[i][tt], q_s[i][j] * delta * sm);
       }
@@ -697,7 +697,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   __shared__ __align__(16) uint8_t otb_s[kMWaves][4][32];
   // NF4 levels [0, 16) and value centroids [16, 16 + 2^vb), for the table fill
   __shared__ float lvl_s[32];
-  if (tid < 16) lvl_s[tid] = kNF4[tid];
+  if (tid < 16) lvl_s[tid] = key_level(a.d.key_grid, tid);
   else if (tid < 16 + (1 << VB)) lvl_s[tid] = a.p.vcent[tid - 16];
   // Metadata of the split's groups, read once here so the block stream issues
   // nothing but block loads: [0, 16) first row of each 16-token tile,
@@ -1688,12 +1688,13 @@ int run_merge(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int batch, int m
 
 extern "C" {
 
-int tqk_version(void) { return 3; }
+int tqk_version(void) { return 4; }
 
 int tqk_check_desc(const tqk_cache_desc* d) {
   if (!d) return TQK_EINVAL;
   if (d->head_dim != TQK_D) return TQK_EUNSUPPORTED;
   if (d->key_bits != 4) return TQK_EUNSUPPORTED;
+  if (d->key_grid != 0 && d->key_grid != 1) return TQK_EINVAL;
   if (d->value_bits != 3 && d->value_bits != 4) return TQK_EUNSUPPORTED;
   if (d->n_kv_heads <= 0 || d->n_q_heads <= 0 || d->n_q_heads % d->n_kv_heads) return TQK_EINVAL;
   const int gq = d->n_q_heads / d->n_kv_heads;

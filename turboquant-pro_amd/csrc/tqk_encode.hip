@@ -77,7 +77,26 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
 
   // ---- per-channel statistics (threads 0..127) and outlier thresholds (128..255)
   const size_t mbase = ((size_t)slot * Hkv + h) * D;
-  if (tid < D) {
+  if (tid < D && d.key_grid == 1) {
+    // uniform keys (turboquant_pro/per_channel_kv.py:303-306): channel min and
+    // max over the tokens, scale = max(max - min, 1e-8) / 15 (NaN propagates)
+    const int j = tid;
+    float mn = h2f(kt_s[0][j]), mx = mn;
+    bool nan = (mn != mn);
+    for (int s = 1; s < G; ++s) {
+      const float xv = h2f(kt_s[s][j]);
+      nan |= (xv != xv);
+      mn = fminf(mn, xv);
+      mx = fmaxf(mx, xv);
+    }
+    const float rng = __fsub_rn(mx, mn);
+    const float sc = nan ? __builtin_nanf("") : __fdiv_rn(fmaxf(rng, 1e-8f), 15.0f);
+    if (nan) mn = __builtin_nanf("");
+    cent_s[j][0] = mn;
+    cent_s[j][1] = sc;
+    a.p.gscale[mbase + j] = sc;
+    a.p.gmean[mbase + j] = mn;
+  } else if (tid < D) {
     const int j = tid;
     float acc = 0.0f;
     for (int s = 0; s < G; ++s) acc = __fadd_rn(acc, h2f(kt_s[s][j]));
@@ -111,7 +130,21 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
   __syncthreads();
 
   // ---- codes: thread = (channel pair, token slice); one byte per (token, pair)
-  {
+  if (d.key_grid == 1) {
+    // uniform: clip(round_half_even((x - min) / scale), 0, 15)
+    const int jp = tid & 63, sq = tid >> 6;
+    const float mn0 = cent_s[2 * jp][0], sc0 = cent_s[2 * jp][1];
+    const float mn1 = cent_s[2 * jp + 1][0], sc1 = cent_s[2 * jp + 1][1];
+    const int per_q = (G + kEncWaves - 1) / kEncWaves;
+    const int s0 = sq * per_q, s1 = min(G, s0 + per_q);
+    for (int s = s0; s < s1; ++s) {
+      const float r0 = __builtin_rintf(__fdiv_rn(__fsub_rn(h2f(kt_s[s][2 * jp]), mn0), sc0));
+      const float r1 = __builtin_rintf(__fdiv_rn(__fsub_rn(h2f(kt_s[s][2 * jp + 1]), mn1), sc1));
+      const uint32_t b0 = (uint32_t)fminf(fmaxf(r0, 0.0f), 15.0f);
+      const uint32_t b1 = (uint32_t)fminf(fmaxf(r1, 0.0f), 15.0f);
+      kc_s[s][jp] = (uint8_t)((rev4(b0) << 4) | rev4(b1));
+    }
+  } else {
     const int jp = tid & 63, sq = tid >> 6;
     float c0[16], c1[16];
 #pragma unroll
@@ -175,11 +208,13 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
         if (sel) {
           if (off < d.outlier_cap) {
             a.p.oent[obase * d.outlier_cap + off] = (uint32_t)(tid * D + j) | ((uint32_t)xv << 16);
-            // the stored code becomes the zero level (rev4(7) = 14), so the dense
-            // part of a decode contributes only the mean here and the side-list
-            // adds val - mean; export restores the nearest-level code from val
+            // the stored code becomes the level whose value is gmean -- NF4's
+            // zero level (rev4(7) = 14), or code 0 of a uniform grid -- so the
+            // dense part of a decode contributes only gmean here and the
+            // side-list adds val - gmean; export restores the reference's code
+            const uint32_t zc = d.key_grid == 1 ? 0u : 14u;
             uint8_t& kb = kc_s[tid][j >> 1];
-            kb = (j & 1) ? (uint8_t)((kb & 0xF0u) | 14u) : (uint8_t)((kb & 0x0Fu) | (14u << 4));
+            kb = (j & 1) ? (uint8_t)((kb & 0xF0u) | zc) : (uint8_t)((kb & 0x0Fu) | (zc << 4));
           }
           ++off;
         }
@@ -398,9 +433,9 @@ __global__ __launch_bounds__(kThreads) void tqk_dequant_group(DequantArgs a) {
       const uint32_t byte = kr[jj];
       const int j0 = 2 * jj, j1 = 2 * jj + 1;
       ko[(size_t)tid * D + j0] =
-          __fadd_rn(__fmul_rn(a.p.gscale[mbase + j0], kNF4[rev4(byte >> 4)]), a.p.gmean[mbase + j0]);
+          __fadd_rn(__fmul_rn(a.p.gscale[mbase + j0], key_level(d.key_grid, rev4(byte >> 4))), a.p.gmean[mbase + j0]);
       ko[(size_t)tid * D + j1] =
-          __fadd_rn(__fmul_rn(a.p.gscale[mbase + j1], kNF4[rev4(byte & 15u)]), a.p.gmean[mbase + j1]);
+          __fadd_rn(__fmul_rn(a.p.gscale[mbase + j1], key_level(d.key_grid, rev4(byte & 15u))), a.p.gmean[mbase + j1]);
     }
     float y[D];
     if (v_tiled(G, P)) {

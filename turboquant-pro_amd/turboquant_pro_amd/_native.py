@@ -19,7 +19,7 @@ TQK_EUNSUPPORTED = 2
 TQK_EHIP = 3
 TQK_EWORKSPACE = 4
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # Every symbol include/tqk.h declares (checked by the CPU test suite).
 EXPORTS = (
@@ -33,7 +33,8 @@ class CacheDesc(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in (
         "n_kv_heads", "n_q_heads", "head_dim", "hot_window", "group_tokens", "page_tokens",
         "key_bits", "value_bits", "outliers_per_channel", "outlier_cap",
-        "max_pages_per_seq", "max_groups_per_seq", "hot_ring", "n_pages")] + [("sm_scale", ctypes.c_float)]
+        "max_pages_per_seq", "max_groups_per_seq", "hot_ring", "n_pages")] + [
+        ("sm_scale", ctypes.c_float), ("key_grid", ctypes.c_int32)]
 
 
 class CachePtrs(ctypes.Structure):

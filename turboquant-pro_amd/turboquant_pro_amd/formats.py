@@ -47,12 +47,21 @@ def nf4_codes(x: np.ndarray, scale: np.ndarray, mean: np.ndarray) -> np.ndarray:
     return np.argmin(np.abs(x - cent), axis=-1).astype(np.uint8)
 
 
+def uniform_codes(x: np.ndarray, scale: np.ndarray, zero: np.ndarray) -> np.ndarray:
+    """Uniform key code of fp32 ``x`` (turboquant_pro/per_channel_kv.py:306):
+    ``clip(round_half_even((x - zero) / scale), 0, 15)`` in fp32."""
+    x = np.asarray(x, np.float32)
+    q = (x - np.asarray(zero, np.float32)) / np.asarray(scale, np.float32)
+    return np.clip(np.round(q), 0, 15).astype(np.uint8)
+
+
 def restore_outlier_codes(kp: np.ndarray, idx: np.ndarray, val: np.ndarray,
-                          scale: np.ndarray, mean: np.ndarray) -> np.ndarray:
+                          scale: np.ndarray, mean: np.ndarray, grid: str = "nf4_asym") -> np.ndarray:
     """Put the reference's key codes back at outlier positions.
 
     ``kp`` (H, G, D/2) packed codes as stored; ``idx`` flat positions into
-    (H, G, D) and ``val`` their fp16 values; ``scale``/``mean`` (H, D)."""
+    (H, G, D) and ``val`` their fp16 values; ``scale``/``mean`` (H, D) (for
+    uniform keys ``grid="uniform"``: scale and zero)."""
     kp = np.array(kp, dtype=np.uint8, copy=True)
     H, G, half = kp.shape
     D = 2 * half
@@ -60,7 +69,7 @@ def restore_outlier_codes(kp: np.ndarray, idx: np.ndarray, val: np.ndarray,
         return kp
     idx = idx.astype(np.int64)
     h, t, j = idx // (G * D), (idx // D) % G, idx % D
-    code = nf4_codes(val.astype(np.float32), scale[h, j], mean[h, j])
+    code = (uniform_codes if grid == "uniform" else nf4_codes)(val.astype(np.float32), scale[h, j], mean[h, j])
     nib = _rev4(code)
     # even channels in the high nibble, odd in the low one; one parity at a
     # time so two outliers sharing a byte both land
@@ -154,9 +163,10 @@ def unpack_keys(packed: np.ndarray, n_values: int) -> np.ndarray:
     return codes[:n_values]
 
 
-def mark_outlier_codes(kp: np.ndarray, idx: np.ndarray) -> np.ndarray:
-    """The stored form of reference key bytes: the NF4 zero level (code 7) at
-    every outlier position.  ``kp`` (H, G, D/2) packed codes, ``idx`` flat
+def mark_outlier_codes(kp: np.ndarray, idx: np.ndarray, grid: str = "nf4_asym") -> np.ndarray:
+    """The stored form of reference key bytes: at every outlier position the
+    code whose level is the group's mean term -- NF4's zero level (code 7), or
+    code 0 of uniform keys.  ``kp`` (H, G, D/2) packed codes, ``idx`` flat
     positions into (H, G, D); the inverse of :func:`restore_outlier_codes`
     up to the codes it recomputes."""
     kp = np.array(kp, dtype=np.uint8, copy=True)
@@ -166,7 +176,7 @@ def mark_outlier_codes(kp: np.ndarray, idx: np.ndarray) -> np.ndarray:
         return kp
     idx = idx.astype(np.int64)
     h, t, j = idx // (G * D), (idx // D) % G, idx % D
-    nib = int(_rev4(np.array([NF4_ZERO_CODE]))[0])
+    nib = int(_rev4(np.array([0 if grid == "uniform" else NF4_ZERO_CODE]))[0])
     for par in (0, 1):
         m = (j % 2) == par
         hh, tt, bb = h[m], t[m], j[m] // 2

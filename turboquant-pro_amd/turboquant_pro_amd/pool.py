@@ -39,7 +39,8 @@ class TQKVPool:
                  max_batch: int = 1, max_seq_len: int = 8192, hot_window: int = 512,
                  key_bits: int = 4, value_bits: int = 3, outlier_frac: float = 0.02,
                  page_tokens: int | None = None, outlier_cap: int | None = None,
-                 seed=None, rotation: tuple | None = None, block_table=None, device=None):
+                 seed=None, rotation: tuple | None = None, block_table=None, device=None,
+                 key_grid: str = "nf4_asym"):
         torch = _torch()
         if not torch.cuda.is_available():
             raise RuntimeError("TQKVPool runs on a ROCm GPU (gfx950); none is visible")
@@ -68,7 +69,9 @@ class TQKVPool:
             group_tokens=G, page_tokens=P, key_bits=key_bits, value_bits=value_bits,
             outliers_per_channel=k_out, outlier_cap=outlier_cap,
             max_pages_per_seq=max_pages, max_groups_per_seq=max_groups,
-            hot_ring=hot_window, n_pages=max_batch * max_pages, sm_scale=1.0 / math.sqrt(head_dim))
+            hot_ring=hot_window, n_pages=max_batch * max_pages, sm_scale=1.0 / math.sqrt(head_dim),
+            key_grid={"nf4_asym": 0, "uniform": 1}[key_grid])
+        self.key_grid = key_grid
         N.check(N.lib().tqk_check_desc(ctypes.byref(self.desc)), "TQKVPool")
 
         dev = self.device
@@ -298,7 +301,7 @@ class TQKVPool:
         oidx = np.concatenate(idx) if idx else np.zeros(0, np.int64)
         oval = np.concatenate(val).view(np.float16) if val else np.zeros(0, np.float16)
         scale, mean = self.gscale[slot].cpu().numpy(), self.gmean[slot].cpu().numpy()
-        kp = restore_outlier_codes(kp, oidx, oval, scale, mean)
+        kp = restore_outlier_codes(kp, oidx, oval, scale, mean, grid=self.key_grid)
         return {
             "kpacked": kp.reshape(-1),
             "nf4_scale": scale,
@@ -332,7 +335,7 @@ class TQKVPool:
                 raise ValueError("outlier_idx and outlier_val differ in length")
             if oidx.size and (oidx.min() < 0 or oidx.max() >= H * G * D):
                 raise ValueError("outlier_idx outside the (H, G, D) block")
-            kp = mark_outlier_codes(kp, oidx)
+            kp = mark_outlier_codes(kp, oidx, grid=self.key_grid)
             self.kcodes[:, phys, off] = torch.from_numpy(kp).to(self.device)
             self.gscale[slot] = torch.from_numpy(np.asarray(keys["nf4_scale"], np.float32).reshape(H, D)).to(self.device)
             self.gmean[slot] = torch.from_numpy(np.asarray(keys["nf4_mean"], np.float32).reshape(H, D)).to(self.device)
