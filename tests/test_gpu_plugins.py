@@ -114,3 +114,28 @@ def test_polar_round_trip_across_groups():
     assert np.array_equal(dec[0], O.decode_values(g_all, cent, pi))
     cp = q.compress(v.astype(np.float32), packed=True, kind="value")
     assert np.array_equal(q.decompress(cp), dec)
+
+
+@pytest.mark.parametrize("tag", ["s256", "s200"])
+def test_per_channel_uniform_matches_reference(tag):
+    """``create("per_channel", bits=4)`` -- the reference's default, uniform
+    mode (turboquant_pro/per_channel_kv.py:303-317) -- on the GPU: the
+    container (packed codes, (1, H, 1, D) scale and zero, outliers) and the
+    decompress equal the reference's for the same block
+    (tests/golden/perchannel_uniform.npz), packed and unpacked."""
+    print(f"[plugins] per_channel uniform {tag}", flush=True)
+    PL = _pl()
+    z = np.load(os.path.join(GOLD, "perchannel_uniform.npz"), allow_pickle=False)
+    x = z[f"{tag}_x"][None]
+    q = PL.create("per_channel", n_heads=2, bits=4, outlier_frac=0.02)
+    c = q.compress(x, packed=True)
+    assert c.nf4_scale is None and c.nf4_mean is None and c.scale.shape == (1, 2, 1, 128)
+    assert np.array_equal(c.indices, z[f"{tag}_kpacked"])
+    assert np.array_equal(c.scale[0, :, 0], z[f"{tag}_scale"]) and np.array_equal(c.zero[0, :, 0], z[f"{tag}_zero"])
+    assert np.array_equal(c.outlier_idx, z[f"{tag}_oidx"])
+    assert np.array_equal(c.outlier_val.view(np.uint16), z[f"{tag}_oval"].view(np.uint16))
+    assert np.array_equal(q.decompress(c), z[f"{tag}_decompressed"][None])
+    cu = q.compress(x)
+    assert np.array_equal(q.decompress(cu), z[f"{tag}_decompressed"][None])
+    mu, w, grid = PL.affine_params(q, c)
+    assert np.array_equal(grid, np.arange(16, dtype=np.float32)) and np.array_equal(mu, z[f"{tag}_zero"])

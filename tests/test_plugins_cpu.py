@@ -66,7 +66,9 @@ def test_per_channel_constructor_validation():
         with pytest.raises(ValueError):
             PL.create("per_channel", **cfg)
     # valid reference configurations without a gfx950 encode
-    for cfg in (dict(bits=4), dict(nf4=True), dict(nuq=True),
+    uni = PL.create("per_channel", bits=4, outlier_frac=0.02)      # the reference's default mode
+    assert uni.uniform and uni.key_grid == "uniform"
+    for cfg in (dict(bits=3), dict(nf4=True), dict(nuq=True),
                 dict(nf4_asym=True, zero_point="sparse", rope_theta=1e4),
                 dict(nf4_asym=True, head_dim=64)):
         with pytest.raises(NotImplementedError):

@@ -242,7 +242,7 @@ class CompressedKV:
 
 # --------------------------------------------------------------- formats
 def _pool(H: int, S: int, value_bits: int, outlier_frac: float, B: int, seed=None, device=None,
-          outlier_cap: int | None = None):
+          outlier_cap: int | None = None, key_grid: str = "nf4_asym"):
     """A B-sequence pool whose groups are exactly S tokens, one token per page
     (value codes stored per token, in the reference's pack)."""
     from .pool import TQKVPool
@@ -251,7 +251,7 @@ def _pool(H: int, S: int, value_bits: int, outlier_frac: float, B: int, seed=Non
     assert group_tokens_for(W) == S
     return TQKVPool(n_kv_heads=H, n_q_heads=H, max_batch=B, max_seq_len=2 * S, hot_window=W,
                     value_bits=value_bits, outlier_frac=outlier_frac, page_tokens=1, seed=seed,
-                    device=device, outlier_cap=outlier_cap)
+                    device=device, outlier_cap=outlier_cap, key_grid=key_grid)
 
 
 def _fp16_tokens(x: np.ndarray):
@@ -265,14 +265,15 @@ def _fp16_tokens(x: np.ndarray):
 
 
 class PerChannelKVQuantizer:
-    """``"per_channel"`` keys on the gfx950 library: asym-NF4 4-bit with the
-    fp16 outlier side-list, one encode group per sequence.
+    """``"per_channel"`` keys on the gfx950 library: asym-NF4 4-bit or uniform
+    4-bit (the reference's default mode), with the fp16 outlier side-list,
+    one encode group per sequence.
 
     The constructor validates like ``PerChannelKV.__init__``
     (turboquant_pro/per_channel_kv.py:182-213) and raises
     ``NotImplementedError`` for the modes the library does not encode
-    (uniform, symmetric NF4, data-fit quantiles, zero-point "sparse"/"bias",
-    head_dim != 128)."""
+    (2/3-bit uniform, symmetric NF4, data-fit quantiles, zero-point
+    "sparse"/"bias", head_dim != 128)."""
 
     _ZP_MODES = ("calibrated", "sparse", "bias")
 
@@ -297,11 +298,14 @@ class PerChannelKVQuantizer:
                 raise ValueError(f"zero_point={zero_point!r} requires rope_theta")
         if zero_point == "bias" and k_bias is None:
             raise ValueError('zero_point="bias" requires k_bias')
-        if not (nf4_asym and zero_point == "calibrated") or nuq and not nf4 or head_dim != 128:
-            raise NotImplementedError("the gfx950 key encode is per-channel asym-NF4 4-bit with "
-                                      "calibrated zero points at head_dim 128")
+        uniform = bits == 4 and not nf4 and not nuq
+        if not ((nf4_asym and zero_point == "calibrated") or uniform) or head_dim != 128:
+            raise NotImplementedError("the gfx950 key encode is per-channel asym-NF4 (calibrated zero "
+                                      "points) or uniform, 4-bit, at head_dim 128")
         self.head_dim, self.n_heads, self.bits = head_dim, n_heads, bits
-        self.nuq, self.nf4, self.nf4_asym = True, True, True
+        self.uniform = uniform
+        self.key_grid = "uniform" if uniform else "nf4_asym"
+        self.nuq, self.nf4, self.nf4_asym = nuq, nf4, nf4_asym
         self.outlier_frac, self.zero_point = outlier_frac, zero_point
         self.rope_theta, self.k_bias = rope_theta, None
         self.device = device
@@ -318,7 +322,7 @@ class PerChannelKVQuantizer:
             raise ValueError(f"head_dim {D} != {self.head_dim}")
         if not 1 <= S <= _MAX_GROUP_TOKENS:
             raise NotImplementedError(f"one gfx950 key group holds 1..{_MAX_GROUP_TOKENS} tokens, got {S}")
-        pool = _pool(H, S, 3, self.outlier_frac, B, device=self.device)
+        pool = _pool(H, S, 3, self.outlier_frac, B, device=self.device, key_grid=self.key_grid)
         k = torch.cat([xt, torch.zeros_like(xt)], dim=2).to(pool.device)
         pool.append(k, torch.zeros_like(k))
         parts = [pool.export_group(b, 0) for b in range(B)]
@@ -329,6 +333,12 @@ class PerChannelKVQuantizer:
                                    for b, p in enumerate(parts)]).astype(np.int32)
             oval = np.concatenate([p["outlier_val"] for p in parts]).astype(np.float16)
         indices = kp if packed else unpack_keys(kp, B * H * S * D).reshape(B, H, S, D)
+        if self.uniform:
+            # per_channel_kv.py:303-317: (B, H, 1, D) scale and zero, no NF4 fields
+            return CompressedPerChannelKV(
+                indices, np.stack([p["nf4_scale"] for p in parts]).astype(np.float32)[:, :, None, :],
+                np.stack([p["nf4_mean"] for p in parts]).astype(np.float32)[:, :, None, :],
+                self.bits, (B, H, S, D), packed, outlier_idx=oidx, outlier_val=oval)
         return CompressedPerChannelKV(
             indices, None, None, self.bits, (B, H, S, D), packed,
             nf4_scale=np.stack([p["nf4_scale"] for p in parts]).astype(np.float32),
@@ -340,8 +350,13 @@ class PerChannelKVQuantizer:
         """fp32 ``(B, H, S, D)``: ``mean + scale * NF4[code]``, outliers overwritten
         by their fp16 values (turboquant_pro/per_channel_kv.py:497-539), on the GPU."""
         B, H, S, D = c.shape
-        if c.nf4_scale is None or c.nf4_mean is None or c.zp_mode != "calibrated":
-            raise NotImplementedError("the gfx950 dequant reads calibrated asym-NF4 containers")
+        uniform = c.nf4_scale is None and c.levels is None and c.scale is not None and c.zero is not None
+        if not uniform and (c.nf4_scale is None or c.nf4_mean is None or c.zp_mode != "calibrated"):
+            raise NotImplementedError("the gfx950 dequant reads calibrated asym-NF4 or uniform containers")
+        if uniform and c.bits != 4:
+            raise NotImplementedError("the gfx950 dequant reads 4-bit uniform containers")
+        gscale = np.asarray(c.scale)[:, :, 0, :] if uniform else np.asarray(c.nf4_scale)
+        gmean = np.asarray(c.zero)[:, :, 0, :] if uniform else np.asarray(c.nf4_mean)
         if not 1 <= S <= _MAX_GROUP_TOKENS or D != 128:
             raise NotImplementedError(f"one gfx950 key group holds 1..{_MAX_GROUP_TOKENS} tokens at head_dim 128")
         kp = c.indices if c.packed else _pack_keys(np.asarray(c.indices))
@@ -354,12 +369,11 @@ class PerChannelKVQuantizer:
         cap = max(1, int(per_head.max()))
         frac = self.outlier_frac if self.outlier_frac > 0 else 0.02
         pool = _pool(H, S, 3, frac if has_out else 0.0, B, device=self.device,
-                     outlier_cap=cap if has_out else 0)
+                     outlier_cap=cap if has_out else 0, key_grid="uniform" if uniform else "nf4_asym")
         for b in range(B):
             m = (flat // (H * S * D)) == b
             pool.import_group(b, 0, keys={
-                "kpacked": kp[b], "nf4_scale": np.asarray(c.nf4_scale)[b],
-                "nf4_mean": np.asarray(c.nf4_mean)[b],
+                "kpacked": kp[b], "nf4_scale": gscale[b], "nf4_mean": gmean[b],
                 "outlier_idx": flat[m] - b * H * S * D, "outlier_val": vals[m]})
         keys, _ = pool.dequant_groups([(b, 0) for b in range(B)])
         return keys.cpu().numpy().reshape(B, H, S, D)
@@ -371,8 +385,12 @@ class PerChannelKVQuantizer:
         B = c.shape[0]
         if B != 1:
             raise ValueError("fused decode operates on single-batch blocks (B=1)")
+        if c.nf4_scale is None and c.levels is None and c.scale is not None:
+            # uniform: dequant = zero + scale * code
+            return (np.asarray(c.zero)[0, :, 0, :].astype(np.float32),
+                    np.asarray(c.scale)[0, :, 0, :].astype(np.float32), np.arange(16, dtype=np.float32))
         if c.nf4_scale is None:
-            raise NotImplementedError("only NF4-family containers carry the affine grid here")
+            raise NotImplementedError("only NF4-family and uniform containers carry the affine grid here")
         mu = (np.asarray(c.nf4_mean)[0] if c.nf4_mean is not None
               else np.zeros(np.asarray(c.nf4_scale)[0].shape, np.float32))
         return mu.astype(np.float32), np.asarray(c.nf4_scale)[0].astype(np.float32), NF4.copy()
