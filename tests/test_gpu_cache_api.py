@@ -125,3 +125,29 @@ def test_stats_clear_and_errors():
         cache.append(np.zeros((3, 128), np.float16), np.zeros((3, 128), np.float16))
     with pytest.raises(NotImplementedError):
         TurboQuantKVCache(head_dim=128, n_heads=2, bits=3)          # uniform keys: no GPU form
+
+
+def test_uniform_key_cache():
+    """``TurboQuantKVCache(per_channel_keys=True)`` without NF4 flags keeps the
+    reference's uniform 4-bit keys (turboquant_pro/core.py:1011-1038 with
+    PerChannelKV's uniform branch, per_channel_kv.py:303-317): every flushed
+    group bit-exact to the oracle (itself pinned to the reference's uniform
+    vectors), ``get_keys`` bit-exact, ``fused_decode`` within the bar."""
+    from oracle import tq_oracle as O
+    from turboquant_pro_amd import TurboQuantKVCache
+    print("[cache] uniform keys", flush=True)
+    H, L = 2, 1100
+    k, v, q = O.synthetic_kv(91, 1, H, H, L)
+    k, v, q = k[0], v[0], q[0]
+    cache = TurboQuantKVCache(head_dim=128, n_heads=H, key_bits=4, value_bits=3, hot_window=512,
+                              per_channel_keys=True, key_outlier_frac=0.02, seed=0)
+    assert cache.key_grid == "uniform"
+    cache.extend(k[:, :600], v[:, :600])
+    for t in range(600, L):
+        cache.append(k[:, t], v[:, t])
+    pi, pi_t = O.rotation(0, 128)
+    sc = O.SequenceCache(hot_window=512, value_bits=3, outlier_frac=0.02, key_grid="uniform").build(k, v, pi, pi_t)
+    assert cache.length == L and cache.cold_length == len(sc.keys) * 256
+    assert np.array_equal(cache.get_keys(0, L)[0], sc.get_keys())
+    assert np.array_equal(cache.get_values(0, L)[0], sc.get_values())
+    assert_attn_close(cache.fused_decode(q), sc.attend(q))

@@ -80,11 +80,15 @@ class TurboQuantKVCache:
             key_nf4 = True
         if key_nf4 and self.key_bits != 4:
             raise ValueError("nf4=True requires bits=4")
-        if not per_channel_keys or key_nuq or not key_nf4_asym:
+        # per-channel keys: asym-NF4 (robust / build_cache) or, without any NF4
+        # or quantile flag, the reference's uniform 4-bit mode
+        uniform = per_channel_keys and not key_nuq and not key_nf4 and self.key_bits == 4
+        if not per_channel_keys or key_nuq or not (key_nf4_asym or uniform):
             raise NotImplementedError(
                 "the gfx950 cache codes keys as per-channel asym-NF4 (TurboQuantKVCache.robust / "
-                "AutoConfig.build_cache); PolarQuant, uniform, symmetric-NF4 and quantile keys "
-                "have no GPU form here")
+                "AutoConfig.build_cache) or uniform 4-bit; PolarQuant, 2/3-bit uniform, "
+                "symmetric-NF4 and quantile keys have no GPU form here")
+        self.key_grid = "uniform" if uniform else "nf4_asym"
         if key_zero_point != "calibrated":
             raise NotImplementedError(f"zero_point={key_zero_point!r} has no gfx950 form yet")
         if self.value_bits not in (3, 4):
@@ -103,7 +107,7 @@ class TurboQuantKVCache:
                         max_batch=1, max_seq_len=capacity, hot_window=self.hot_window,
                         key_bits=self.key_bits, value_bits=self.value_bits,
                         outlier_frac=self.key_outlier_frac, seed=self.seed, rotation=rotation,
-                        device=self._device)
+                        device=self._device, key_grid=self.key_grid)
 
     def _grow(self, need: int) -> None:
         """Reallocate to hold ``need`` tokens, copying the coded groups and the
