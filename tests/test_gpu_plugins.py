@@ -139,3 +139,40 @@ def test_per_channel_uniform_matches_reference(tag):
     assert np.array_equal(q.decompress(cu), z[f"{tag}_decompressed"][None])
     mu, w, grid = PL.affine_params(q, c)
     assert np.array_equal(grid, np.arange(16, dtype=np.float32)) and np.array_equal(mu, z[f"{tag}_zero"])
+
+
+def test_polar_unseeded_rotation_is_the_instances():
+    """``create("polar")`` with no seed (the reference's default,
+    turboquant_pro/core.py:178-228) draws one random rotation per instance:
+    compress and decompress of that instance -- across two groups -- equal
+    the oracle under ``q.rotation``."""
+    print("[plugins] polar seed=None", flush=True)
+    PL = _pl()
+    _, v, _ = O.synthetic_kv(79, 1, 2, 2, 300)
+    q = PL.create("polar", n_heads=2, bits=3)
+    assert q.seed is None
+    pi, pi_t = q.rotation
+    cent, bnd = O.polar_codebook(3, 128)
+    c = q.compress(v.astype(np.float32), packed=True, kind="value")
+    g = O.encode_values(v[0].astype(np.float32), pi_t, bnd, 3)
+    assert np.array_equal(c.norms[0], g.norms)
+    assert np.array_equal(q.decompress(c)[0], O.decode_values(g, cent, pi))
+
+
+def test_per_channel_uniform_without_outliers():
+    """``create("per_channel")`` with no arguments -- the reference's default:
+    uniform 4-bit keys, ``outlier_frac=0`` (turboquant_pro/per_channel_kv.py:
+    183-200,303-317) -- on the GPU equals the oracle's uniform encode (pinned
+    to the reference's uniform vectors) and its decode, with no side-list."""
+    print("[plugins] per_channel default (uniform, no outliers)", flush=True)
+    PL = _pl()
+    z = np.load(os.path.join(GOLD, "perchannel_uniform.npz"), allow_pickle=False)
+    for tag in ("s256", "s200"):
+        x = z[f"{tag}_x"]
+        q = PL.create("per_channel", n_heads=2)
+        c = q.compress(x[None], packed=True)
+        g = O.encode_keys_uniform(x, 0.0)
+        assert c.outlier_idx is None and g.outlier_idx is None
+        assert np.array_equal(c.indices.reshape(-1), g.packed.reshape(-1))
+        assert np.array_equal(c.scale[0, :, 0], g.nf4_scale) and np.array_equal(c.zero[0, :, 0], g.nf4_mean)
+        assert np.array_equal(q.decompress(c)[0], O.decode_keys(g))

@@ -62,10 +62,11 @@ class TurboQuantBlockStore:
     ``quantizer_config`` goes to both plugins, as in the reference (a plugin
     that refuses a keyword gets its defaults); ``key_config`` and
     ``value_config`` are applied on top, per plugin.  Without any of them the
-    store uses the configuration the gfx950 encode serves: asym-NF4 keys with
-    2 % outliers, 3-bit values with rotation seed 0 (the reference's plugin
-    defaults -- uniform 4-bit keys, a random rotation -- have no gfx950
-    encode, and a random rotation could not be decoded by another process).
+    store uses the cache's own format: asym-NF4 keys with 2 % outliers, 3-bit
+    values with rotation seed 0.  ``quantizer_config={}`` gives the reference's
+    plugin defaults instead (uniform 4-bit keys without outliers, a rotation
+    drawn per store), which the gfx950 plugins also serve; records of an
+    unseeded rotation decode only in the process that wrote them.
     """
 
     DEFAULT_KEY_CONFIG = {"nf4_asym": True, "outlier_frac": 0.02}

@@ -36,7 +36,7 @@ from typing import Any, Protocol, runtime_checkable
 
 import numpy as np
 
-from .codebooks import group_tokens_for
+from .codebooks import group_tokens_for, random_rotation
 from .formats import NF4, pack_values, unpack_keys, unpack_values
 
 logger = logging.getLogger(__name__)
@@ -242,7 +242,7 @@ class CompressedKV:
 
 # --------------------------------------------------------------- formats
 def _pool(H: int, S: int, value_bits: int, outlier_frac: float, B: int, seed=None, device=None,
-          outlier_cap: int | None = None, key_grid: str = "nf4_asym"):
+          outlier_cap: int | None = None, key_grid: str = "nf4_asym", rotation=None):
     """A B-sequence pool whose groups are exactly S tokens, one token per page
     (value codes stored per token, in the reference's pack)."""
     from .pool import TQKVPool
@@ -251,7 +251,7 @@ def _pool(H: int, S: int, value_bits: int, outlier_frac: float, B: int, seed=Non
     assert group_tokens_for(W) == S
     return TQKVPool(n_kv_heads=H, n_q_heads=H, max_batch=B, max_seq_len=2 * S, hot_window=W,
                     value_bits=value_bits, outlier_frac=outlier_frac, page_tokens=1, seed=seed,
-                    device=device, outlier_cap=outlier_cap, key_grid=key_grid)
+                    rotation=rotation, device=device, outlier_cap=outlier_cap, key_grid=key_grid)
 
 
 def _fp16_tokens(x: np.ndarray):
@@ -460,6 +460,9 @@ class PolarQuantizer:
             raise NotImplementedError("the gfx950 value encode serves head_dim 128")
         self.head_dim, self.n_heads, self.bits, self.seed = head_dim, n_heads, bits, seed
         self.device = device
+        # drawn once, as TurboQuantKV does (core.py:178-228): with seed=None the
+        # instance's compress and decompress still share one rotation
+        self.rotation = random_rotation(seed, head_dim)
 
     def _width(self, kind: str | None) -> int:
         if kind == "key":
@@ -485,7 +488,7 @@ class PolarQuantizer:
         norms = np.zeros((B, H, S), np.float32)
         for t0 in range(0, S, _MAX_GROUP_TOKENS):
             n = min(_MAX_GROUP_TOKENS, S - t0)
-            pool = _pool(H, n, bits, 0.0, B, seed=self.seed, device=self.device)
+            pool = _pool(H, n, bits, 0.0, B, rotation=self.rotation, device=self.device)
             chunk = vt[:, :, t0:t0 + n]
             v = torch.cat([chunk, torch.zeros_like(chunk)], dim=2).to(pool.device)
             pool.append(torch.zeros_like(v), v)
@@ -512,7 +515,7 @@ class PolarQuantizer:
         out = np.zeros((B, H, S, D), np.float32)
         for t0 in range(0, S, _MAX_GROUP_TOKENS):
             n = min(_MAX_GROUP_TOKENS, S - t0)
-            pool = _pool(H, n, bits, 0.0, B, seed=self.seed, device=self.device)
+            pool = _pool(H, n, bits, 0.0, B, rotation=self.rotation, device=self.device)
             for b in range(B):
                 pool.import_group(b, 0, values={
                     "vpacked": pack_values(codes[b, :, t0:t0 + n], bits),
