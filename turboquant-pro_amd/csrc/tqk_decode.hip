@@ -30,6 +30,9 @@ struct DecodeArgs {
   int hot_per_split;
   int split_base;  // added to blockIdx.x (hot-only launches start after the coded splits)
   int batch;
+  // MFMA kernel: 1 when the grid takes more than one round of CUs, so that
+  // the order in which (seq, split) items start matters (longest first)
+  int reorder;
   // in-kernel merge (MFMA kernel): the output, or nullptr to leave the
   // partials to tqk_merge, and one arrival counter per (seq, kv head)
   float* out;
@@ -672,6 +675,39 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     item /= ncs;
     h = item % Hkv_;
     b = item / Hkv_;
+    // Batches: take the (seq, split) items longest first -- most coded groups
+    // first, ties in index order -- so that in a ragged batch the long items
+    // start in the first rounds of workgroups and the short ones fill in
+    // behind them.  Every workgroup ranks the same items the same way, so
+    // (rank, kv head) <-> blockIdx.x is a bijection.  More items than the
+    // workgroup has threads keep the plain order.
+    const int n_items = a.batch * ncs;
+    if (a.reorder && a.batch > 1 && n_items <= kMWaves * 64) {
+      __shared__ int work_s[kMWaves * 64];
+      __shared__ int pick_s;
+      const int t = threadIdx.x;
+      int wk = 0;
+      if (t < n_items) {
+        const int ng_t = n_groups_of(a.seq_lens[t / ncs], a.d.hot_window, a.d.group_tokens);
+        wk = min(max(ng_t - (t % ncs) * a.groups_per_split, 0), a.groups_per_split);
+        work_s[t] = wk;
+      }
+      __syncthreads();
+      const int want = blockIdx.x / Hkv_;
+      if (t < n_items) {
+        int rank = 0;
+        for (int j = 0; j < n_items; ++j) {
+          const int wj = work_s[j];
+          rank += (wj > wk) | ((wj == wk) & (j < t));
+        }
+        if (rank == want) pick_s = t;
+      }
+      __syncthreads();
+      const int it = pick_s;
+      b = it / ncs;
+      split = it % ncs;
+      h = blockIdx.x % Hkv_;
+    }
   }
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, lg = lane >> 4, c = lane & 15;
   const tqk_cache_desc& d = a.d;
@@ -1627,6 +1663,7 @@ DecodeArgs make_args(const tqk_cache_desc* d, const tqk_cache_ptrs* p, const Pla
   a.hot_per_split = pl.hot_per_split;
   a.split_base = 0;
   a.batch = batch;
+  a.reorder = mfma_path(*d) && (long)pl.n_cold_splits * d->n_kv_heads * batch > device_cus();
   a.out = nullptr;
   return a;
 }
