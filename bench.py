@@ -11,10 +11,14 @@ replicas (>= 1 GB together) are used round-robin so the 256 MB Infinity Cache
 cannot serve repeat steps.
 
 Prints one JSON line.  `value` is microseconds per decode step (lower is
-better); `roofline.achieved` is the canonical compressed-KV bytes of one step
-divided by the average duration of the decode kernel (split-K over the coded
-groups and the hot window, merged by its last workgroups: the whole step is
-this one launch), timed with HIP events on the stream it runs on.
+better), averaged over `--steps` back-to-back steps after a time-based
+pre-roll (GPU clock ramp) and `--warmup` steps.  `roofline.achieved` is the
+canonical compressed-KV bytes of one step divided by the median duration of
+one decode-kernel launch (split-K over the coded groups and the hot window,
+merged by its last workgroups: the whole step is this one launch), from a HIP
+event pair around each launch on the stream it runs on.  `encode` holds the
+prefill encode of the same workload and `cpu_baseline` the reference's CPU
+decode path (oracle restatement) on this host's cores.
 """
 
 from __future__ import annotations
@@ -137,33 +141,65 @@ def measured_traffic(config):
     return int(m.group(1)) if m else None
 
 
-def cpu_baseline(cfg, budget_s=12.0):
-    """The oracle's NumPy dequantize-then-attend (the reference CPU decode path)
-    timed on this host on a bounded sample: whole-cache decode of single
-    (sequence, kv head) pairs at the workload's context, scaled to the step."""
+_CPU_STATE = {}
+
+
+def _cpu_pair_attend(i):
+    """One (sequence, kv head) pair's dequantize-then-attend (pool worker)."""
+    sc, q = _CPU_STATE["cache"], _CPU_STATE["q"]
+    out = sc.attend(q)
+    return float(out[0, 0])
+
+
+def cpu_workers():
+    """Worker processes for the CPU baseline: the host cores this process may
+    run on, at most 16 (one GPU's share of a box)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def cpu_baseline(cfg, steps=3):
+    """The reference CPU decode path as the oracle restates it (NumPy
+    dequantize-then-attend, turboquant_pro/core.py:1040-1117 +
+    per_channel_kv.py:497-539 + core.py:619-654), timed on this host for whole
+    decode steps: every (sequence, kv head) pair of the batch attends over its
+    full-context cache, the pairs spread over a pool of single-threaded worker
+    processes (NumPy/BLAS one thread each).  All pairs use one synthetic pair
+    cache of the workload's context (the cost of a pair does not depend on its
+    data).  Median of ``steps`` whole steps.  Runs before the GPU is touched:
+    the workers are forked from a process that has not initialised HIP."""
+    import multiprocessing as mp
     import numpy as np
     sys.path.insert(0, ROOT)
     from oracle import tq_oracle as O
     L, g = cfg["L"], cfg["Hq"] // cfg["Hkv"]
+    t0 = time.perf_counter()
     k, v, q = O.synthetic_kv(1, 1, 1, g, L)
     pi, pi_t = O.rotation(0, 128)
     sc = O.SequenceCache(hot_window=512, value_bits=cfg["vbits"], outlier_frac=0.02).build(
         k[0], v[0], pi, pi_t)
-    times = []
-    t_start = time.perf_counter()
-    while True:
-        t0 = time.perf_counter()
-        out = sc.attend(q[0])
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start > budget_s or len(times) >= 5:
-            break
-    assert np.isfinite(out).all()
-    per_pair = float(np.median(times))
+    build_s = time.perf_counter() - t0
+    _CPU_STATE["cache"], _CPU_STATE["q"] = sc, q[0]
     pairs = cfg["B"] * cfg["Hkv"]
-    return {"value": per_pair * pairs * 1e6, "unit": "us/step", "cores": 1, "kind": "port",
-            "sample": f"{len(times)} runs of one (sequence, kv head) pair at L={L} with {g} q-heads, "
-                      f"median {per_pair * 1e3:.1f} ms x {pairs} pairs; NumPy single thread, "
-                      f"cpu={_cpu_model()}, os.cpu_count()={os.cpu_count()}"}
+    nw = cpu_workers()
+    times = []
+    with mp.get_context("fork").Pool(nw) as pool:
+        pool.map(_cpu_pair_attend, range(nw))  # workers up and warm
+        for _ in range(steps):
+            t1 = time.perf_counter()
+            res = pool.map(_cpu_pair_attend, range(pairs), chunksize=1)
+            times.append(time.perf_counter() - t1)
+    assert np.isfinite(res).all()
+    step_s = float(np.median(times))
+    return {"value": round(step_s * 1e6, 1), "unit": "us/step", "cores": nw, "kind": "port",
+            "sample": f"median of {steps} whole decode steps: {pairs} (sequence, kv head) pairs x "
+                      f"L={L} with {g} q-heads each, over {nw} worker processes x 1 NumPy/BLAS "
+                      f"thread (steps {', '.join(f'{t * 1e3:.0f}' for t in times)} ms; pair cache "
+                      f"built once in {build_s:.1f} s, encode excluded); cpu={_cpu_model()}, "
+                      f"os.cpu_count()={os.cpu_count()}"}
 
 
 def _cpu_model():
@@ -177,12 +213,18 @@ def _cpu_model():
     return "unknown"
 
 
-def encode_bench(torch, cfg, args, chunk=4096):
+VALU_OPS_PEAK = 256 * 4 * 16 * 2.4e9  # separately rounded fp32 ops/s: 256 CUs x 4 SIMD x 16 lanes x 2.4 GHz
+
+
+def encode_bench(torch, cfg, fills, chunk=4096):
     """Prefill encode: the config's batch appended in ``chunk``-token chunks up
     to its context (group flushes through the encode kernel, hot-ring copies),
-    ``args.steps`` times after one untimed fill.  Bytes per the survey's
-    encode formula: fp16 K+V in (512 B per token-head) + the coded groups out
-    (135 B per cold token-head at K4/V3)."""
+    ``fills`` times after one untimed fill; median fill.  Bytes per the
+    survey's encode formula: fp16 K+V in (512 B per token-head) + the coded
+    groups out (135 B per cold token-head at K4/V3).  The encode is bound by
+    the value rotation's 2 * 128^2 separately rounded fp32 operations per
+    token-head (no FMA, no packed math: the bit-exactness contract), reported
+    against the chip's unpacked VALU issue rate."""
     from turboquant_pro_amd import TQKVPool
     B, Hkv, Hq, L, vb = cfg["B"], cfg["Hkv"], cfg["Hq"], cfg["L"], cfg["vbits"]
     gen = torch.Generator(device="cuda")
@@ -192,7 +234,7 @@ def encode_bench(torch, cfg, args, chunk=4096):
     pool = TQKVPool(n_kv_heads=Hkv, n_q_heads=Hq, max_batch=B, max_seq_len=L, value_bits=vb, seed=0)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     times = []
-    for it in range(args.steps + 1):
+    for it in range(fills + 1):
         pool.reset()
         torch.cuda.synchronize()
         e0.record()
@@ -206,24 +248,48 @@ def encode_bench(torch, cfg, args, chunk=4096):
     n_cold = n_groups(L) * ((512 + 1) // 2)
     nbytes = B * Hkv * (L * 2 * 128 * 2 + n_cold * (128 * 4 // 8 + 128 * vb // 8 + 4)) \
         + B * Hkv * n_groups(L) * (2 * 128 * 4 + 640 * 6)
-    print(json.dumps({"metric": "prefill encode GB/s (fp16 K+V in + coded groups out)",
-                      "value": round(nbytes / (ms * 1e-3) / 1e9, 1), "unit": "GB/s",
-                      "ms_per_fill": round(ms, 3), "tokens_per_s": round(B * L / (ms * 1e-3)),
-                      "fills": len(times), "bytes": nbytes,
-                      "config": {"name": args.config, "batch": B, "context": L, "n_kv_heads": Hkv,
-                                 "chunk": chunk, "value_bits": vb}}), flush=True)
+    rot_ops = B * Hkv * n_cold * 2 * 128 * 128
+    return {"metric": "prefill encode GB/s (fp16 K+V in + coded groups out)",
+            "value": round(nbytes / (ms * 1e-3) / 1e9, 1), "unit": "GB/s",
+            "ms_per_fill": round(ms, 3), "tokens_per_s": round(B * L / (ms * 1e-3)),
+            "fills": len(times), "bytes": nbytes,
+            "rotation_ops_per_s": round(rot_ops / (ms * 1e-3) / 1e12, 2),
+            "valu_frac": round(rot_ops / (ms * 1e-3) / VALU_OPS_PEAK, 3),
+            "config": {"name": cfg.get("name", ""), "batch": B, "context": L, "n_kv_heads": Hkv,
+                       "chunk": chunk, "value_bits": vb}}
+
+
+def preroll(fn, min_ms):
+    """Untimed decode launches until ``min_ms`` of wall time have passed (and
+    the GPU has drained them): the GPU clocks ramp over the first tens of ms of
+    sustained work, so the timed steps start at steady state whatever
+    ``--warmup`` is.  Returns (launches, elapsed ms)."""
+    import torch
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        for _ in range(20):
+            fn(n)
+            n += 1
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3
+        if ms >= min_ms:
+            return n, ms
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    # the GPU's clocks ramp over the first ~50 ms of sustained work: the default
-    # warm-up covers that, so the timed steps are steady state
     ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=300)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--preroll-ms", type=float, default=300.0,
+                    help="untimed, time-based run of decode launches before the warm-up "
+                         "(GPU clock ramp), reported as preroll_ms")
     ap.add_argument("--config", default="headline", choices=sorted(CONFIGS))
     ap.add_argument("--replicas", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-encode", action="store_true",
+                    help="skip the prefill-encode sub-record of the decode line")
     ap.add_argument("--encode", action="store_true",
                     help="measure the prefill encode instead (quantize-on-append of 4096-token chunks "
                          "of the chosen config; prints its own JSON line, not the decode metric)")
@@ -237,13 +303,22 @@ def main():
                           "out of scope here", "n_gpus": args.gpus}))
         sys.exit(2)
 
+    cfg = CONFIGS[args.config]
+    cpu = None
+    if not args.encode and not args.no_cpu_baseline:
+        # single-threaded BLAS in each worker process; set before NumPy loads
+        for var in ("OPENBLAS_NUM_THREADS", "MKL_NUM_THREADS"):
+            os.environ[var] = "1"
+        t0 = time.time()
+        cpu = cpu_baseline(cfg)
+        print(f"[bench] cpu baseline done in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+
     import torch
     from turboquant_pro_amd import _native as N
 
     if args.encode:
-        encode_bench(torch, CONFIGS[args.config], args)
+        print(json.dumps(encode_bench(torch, dict(cfg, name=args.config), args.steps)), flush=True)
         return
-    cfg = CONFIGS[args.config]
     B, Hkv, Hq, L = cfg["B"], cfg["Hkv"], cfg["Hq"], cfg["L"]
     print(f"[bench] config={args.config} {cfg} replicas={args.replicas}", file=sys.stderr, flush=True)
     t0 = time.time()
@@ -254,8 +329,12 @@ def main():
     q = torch.randn((B, Hq, 128), generator=gen, device="cuda").half()
     outs = [torch.empty((B, Hq, 128), dtype=torch.float32, device="cuda") for _ in pools]
 
-    for i in range(args.warmup):
+    def step(i):
         pools[i % len(pools)].decode(q, out=outs[i % len(pools)])
+
+    n_pre, pre_ms = preroll(step, args.preroll_ms)
+    for i in range(args.warmup):
+        step(i)
     torch.cuda.synchronize()
 
     stream = torch.cuda.current_stream()
@@ -263,29 +342,33 @@ def main():
     torch.cuda.synchronize()
     e0.record(stream)
     for i in range(args.steps):
-        pools[i % len(pools)].decode(q, out=outs[i % len(pools)])
+        step(i)
     e1.record(stream)
     torch.cuda.synchronize()
     ms_per_step = e0.elapsed_time(e1) / args.steps
 
-    # the kernel alone: HIP events on its stream around `steps` back-to-back
-    # tqk_decode calls straight through the C ABI (one launch each)
+    # the kernel alone: a HIP event pair on its stream around each of `steps`
+    # back-to-back tqk_decode calls straight through the C ABI (one launch
+    # each); kernel_us is the median launch
     lib = N.lib()
     st = ctypes.c_void_p(stream.cuda_stream)
     wss = [p.workspace(B, max(p.lengths)) for p in pools]
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(args.steps)]
     torch.cuda.synchronize()
-    e0.record(stream)
     for i in range(args.steps):
         p = pools[i % len(pools)]
         ws, need = wss[i % len(pools)]
+        ev[i][0].record(stream)
         N.check(lib.tqk_decode(ctypes.byref(p.desc), ctypes.byref(p.ptrs), B, q.data_ptr(),
                                p.seq_lens.data_ptr(), max(p.lengths), outs[i % len(pools)].data_ptr(),
                                ws.data_ptr(), need, st), "tqk_decode")
-    e1.record(stream)
+        ev[i][1].record(stream)
     torch.cuda.synchronize()
-    split_ms = e0.elapsed_time(e1) / args.steps
+    launch_ms = sorted(a.elapsed_time(b) for a, b in ev)
+    kernel_ms = launch_ms[len(launch_ms) // 2]
     nbytes = step_bytes(config_lengths(cfg), Hkv, Hq, vbits=cfg["vbits"])
-    achieved = nbytes / (split_ms * 1e-3) / 1e9
+    achieved = nbytes / (kernel_ms * 1e-3) / 1e9
     step_gbs = nbytes / (ms_per_step * 1e-3) / 1e9
 
     if args.copy_probe:
@@ -297,9 +380,11 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes": COPY_PROBE_BYTES, "copies": 3}), file=sys.stderr, flush=True)
 
-    cpu = None
-    if not args.no_cpu_baseline:
-        cpu = cpu_baseline(cfg)
+    enc = None
+    if not args.no_encode:
+        del pools, wss
+        torch.cuda.empty_cache()
+        enc = encode_bench(torch, dict(cfg, name=args.config), 5)
 
     line = {
         "metric": METRIC,
@@ -308,6 +393,8 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "preroll_ms": round(pre_ms, 1),
+        "preroll_launches": n_pre,
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": False,
         "scaling": "weak",
@@ -329,7 +416,10 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(args.config),
-                     "kernel": "tqk_decode_split_mfma", "kernel_us": round(split_ms * 1e3, 2)},
+                     "kernel": "tqk_decode_split_mfma", "kernel_us": round(kernel_ms * 1e3, 2),
+                     "kernel_us_p10_p90": [round(launch_ms[len(launch_ms) // 10] * 1e3, 2),
+                                           round(launch_ms[(9 * len(launch_ms)) // 10] * 1e3, 2)]},
+        "encode": enc,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -104,13 +104,14 @@ int tqk_version(void);
 int tqk_check_desc(const tqk_cache_desc* d);
 
 /* Bytes of decode workspace needed for `batch` sequences of at most
- * `max_len` tokens.  Host function, no GPU work.  The workspace starts with
+ * `max_len` tokens (0 when batch > n_pages: a decode call takes at most
+ * n_pages sequences).  Host function, no GPU work.  The workspace starts with
  * the arrival counters of tqk_decode's in-kernel merge, one 32-bit word per
- * (sequence, kv head) for max(batch, n_pages / max_pages_per_seq) sequences,
- * then holds the split partials: zero-fill a new workspace once before its
- * first tqk_decode; every completed call leaves the counters at zero again,
- * whatever the batch and max_len of the next call.  Calls that share a
- * workspace must not overlap. */
+ * (sequence, kv head) for n_pages sequences -- a region that depends on the
+ * descriptor only, so it never moves between calls -- then holds the split
+ * partials: zero-fill a new workspace once before its first tqk_decode; every
+ * completed call leaves the counters at zero again, whatever the batch and
+ * max_len of the next call.  Calls that share a workspace must not overlap. */
 size_t tqk_decode_workspace_bytes(const tqk_cache_desc* d, int32_t batch, int32_t max_len);
 
 /*
@@ -162,8 +163,11 @@ int tqk_decode_merge(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t b
  * Writes K/V codes, norms, group scale/mean and the outlier side-list
  * bit-exactly as PerChannelKV.compress (turboquant_pro/per_channel_kv.py:285-401)
  * and TurboQuantKV.compress (turboquant_pro/core.py:542-617) would.
- * `overflow` (device i32, caller zeroes it) is set non-zero when a (group, head)
- * has more outliers than outlier_cap; the side-list is then truncated.
+ * `overflow` (device i32, caller zeroes it) gets bit 0 when a (group, head)
+ * has more outliers than outlier_cap (the side-list is then truncated) and
+ * bit 1 when a value vector's norm exceeds 16376 (the decode keeps softmax
+ * weights <= 4 and carries weight * norm in fp16, whose largest value is
+ * 65504: such a cache cannot be decoded).
  * Replaces TurboQuantKVCache._flush_to_cold (turboquant_pro/core.py:1011-1038).
  */
 int tqk_encode_groups(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t batch,

@@ -77,3 +77,38 @@ def test_error_mapping():
         N.check(N.TQK_EINVAL, "x")
     with pytest.raises(RuntimeError):
         N.check(N.TQK_EHIP, "x")
+
+
+def _header_signatures():
+    """{name: [param declarations]} for every entry point include/tqk.h declares."""
+    with open(os.path.join(ROOT, "include", "tqk.h")) as f:
+        hdr = re.sub(r"/\*.*?\*/", "", f.read(), flags=re.S)
+    sigs = {}
+    for m in re.finditer(r"^(?:int|size_t)\s+(tqk_\w+)\(([^)]*)\);", hdr, re.M):
+        params = [p.strip() for p in m.group(2).replace("\n", " ").split(",")]
+        sigs[m.group(1)] = [] if params == ["void"] else params
+    return sigs
+
+
+def test_binding_declares_every_signature_with_64bit_pointers():
+    """Every entry point gets argtypes matching the header's parameter count,
+    and every pointer parameter is bound as c_void_p or a POINTER type: an
+    undeclared ctypes call passes Python ints as 32-bit C ints, which
+    truncates 64-bit device pointers (the cause of a GPU memory fault in a
+    scratch harness that opened the library without this binding)."""
+    N, lib = _lib()
+    sigs = _header_signatures()
+    assert set(sigs) == set(N.EXPORTS)
+    for name, params in sigs.items():
+        fn = getattr(lib, name)
+        assert fn.argtypes is not None, f"{name}: argtypes not declared"
+        assert len(fn.argtypes) == len(params), f"{name}: {len(fn.argtypes)} argtypes for {len(params)} params"
+        for decl, ty in zip(params, fn.argtypes):
+            if "*" in decl:
+                ok = ty is ctypes.c_void_p or (isinstance(ty, type) and issubclass(ty, ctypes._Pointer))
+                assert ok, f"{name}: pointer parameter '{decl}' bound as {ty}"
+            elif "size_t" in decl:
+                assert ty is ctypes.c_size_t, f"{name}: '{decl}' bound as {ty}"
+            else:
+                assert ty in (ctypes.c_int32, ctypes.c_int), f"{name}: '{decl}' bound as {ty}"
+        assert fn.restype in (ctypes.c_int, ctypes.c_size_t), f"{name}: restype {fn.restype}"

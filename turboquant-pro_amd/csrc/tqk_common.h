@@ -10,6 +10,12 @@
 #define TQK_MAX_G 256      // largest group (flush) size
 #define TQK_OBLK 32        // outlier side-list bound granularity (tokens)
 #define TQK_NOB 8          // cumulative outlier counts kept per (group slot, head)
+// Largest value norm the decode's fp16 PV weights carry: the online softmax
+// keeps every weight p <= 4, and p * norm must stay below fp16's 65504.
+#define TQK_MAX_VNORM 16376.0f
+// Bits of tqk_encode_groups' overflow word
+#define TQK_OVF_OUTLIERS 1  // a (group, head) side-list exceeded outlier_cap
+#define TQK_OVF_VNORM 2     // a value norm exceeded TQK_MAX_VNORM
 
 // Value codes use the MFMA-tiled byte order when every 16-token tile lies in
 // one page and groups are whole 32-token blocks; otherwise per-token rows.

@@ -12,6 +12,8 @@
 // (turboquant_pro/kv_fused_pck.py:196-236).  tqk_merge then combines the
 // splits, rotates the coded part back with one D x D product per query head
 // and adds the hot-window part (turboquant_pro/kv_fused.py:139-153).
+#include <atomic>
+
 #include "tqk_common.h"
 
 namespace {
@@ -1346,9 +1348,13 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   __shared__ int last_s;
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's partial stores are done
   __syncthreads();
+  // acquire-release at agent scope: the workgroup's partial stores (ordered
+  // before this RMW by the barrier above) are released to the last arrival,
+  // whose loads below are ordered after its acquire
   if (tid == 0)
-    last_s = atomicInc(a.arrive + (size_t)b * Hkv + h, (uint32_t)(a.n_cold_splits - 1)) ==
-             (uint32_t)(a.n_cold_splits - 1);
+    last_s = __builtin_amdgcn_atomic_inc32(a.arrive + (size_t)b * Hkv + h,
+                                           (uint32_t)(a.n_cold_splits - 1), __ATOMIC_ACQ_REL,
+                                           "agent") == (uint32_t)(a.n_cold_splits - 1);
   __syncthreads();
   if (!last_s) return;
   {
@@ -1556,18 +1562,29 @@ __host__ __device__ inline bool mfma_path(const tqk_cache_desc& d) {
          (long long)d.n_pages * d.page_tokens * (TQK_D / 2) < (1LL << 32);
 }
 
+// Sequences the arrival counters of a workspace cover: the page pool's page
+// count (a pool of whole sequences holds at least one page per sequence).  A
+// decode call may take at most this many sequences.
+inline int counter_seqs(const tqk_cache_desc& d) { return d.n_pages; }
+
 struct Plan {
   int n_cold_splits, n_hot_splits, groups_per_split, hot_per_split;
   size_t counter_bytes;  // arrival counters at the workspace's start, then the partials
   size_t ws_bytes;
 };
 
-// compute units of the current device (the plan sizes the launch for them)
+// compute units of the current device (the plan sizes the launch for them),
+// queried once per device and process
+constexpr int kMaxDevices = 64;
 int device_cus() {
-  int dev = 0, n = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1)
+  static std::atomic<int> cus[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n > 0) return n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1)
     n = 256;
+  cus[dev].store(n, std::memory_order_relaxed);
   return n;
 }
 
@@ -1616,11 +1633,11 @@ Plan make_plan(const tqk_cache_desc* d, int batch, int max_len) {
   }
   const size_t ns = (size_t)(pl.n_cold_splits + pl.n_hot_splits);
   const size_t per = (size_t)batch * d->n_q_heads * ns;
-  // One counter per (seq, kv head) of the cache's capacity, at a place that
-  // no plan's partials reach: the counters stay zero between calls whatever
-  // the batch and split counts of the next call.
-  const int cap_seqs = d->max_pages_per_seq > 0 ? d->n_pages / d->max_pages_per_seq : batch;
-  const size_t n_counters = (size_t)(batch > cap_seqs ? batch : cap_seqs) * d->n_kv_heads;
+  // One counter per (seq, kv head) for counter_seqs() sequences, a bound that
+  // depends on the descriptor only: the counter region never moves or grows
+  // between calls, so no plan's partials ever land on a counter and the
+  // counters stay zero between calls whatever the batch and split counts.
+  const size_t n_counters = (size_t)counter_seqs(*d) * d->n_kv_heads;
   pl.counter_bytes = (n_counters * sizeof(uint32_t) + 255) & ~(size_t)255;
   pl.ws_bytes = pl.counter_bytes + per * sizeof(float) * (2 + TQK_D) + 256;
   return pl;
@@ -1674,6 +1691,7 @@ int run_splits(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int batch, cons
   int rc = tqk_check_desc(d);
   if (rc != TQK_OK) return rc;
   if (!p || !q || !seq_lens || batch <= 0 || max_len <= 0) return TQK_EINVAL;
+  if (batch > counter_seqs(*d)) return TQK_EINVAL;
   const Plan pl = make_plan(d, batch, max_len);
   if (!ws || ws_bytes < pl.ws_bytes) return TQK_EWORKSPACE;
   DecodeArgs a = make_args(d, p, pl, batch, q, seq_lens, ws);
@@ -1700,6 +1718,7 @@ int run_merge(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int batch, int m
   if (rc != TQK_OK) return rc;
   if (!p || batch <= 0 || max_len <= 0) return TQK_EINVAL;
   if (!out && !(m_out && l_out && acc_out)) return TQK_EINVAL;
+  if (batch > counter_seqs(*d)) return TQK_EINVAL;
   const Plan pl = make_plan(d, batch, max_len);
   if (!ws || ws_bytes < pl.ws_bytes) return TQK_EWORKSPACE;
   const DecodeArgs a = make_args(d, p, pl, batch, nullptr, nullptr, ws);
@@ -1747,7 +1766,7 @@ int tqk_check_desc(const tqk_cache_desc* d) {
 }
 
 size_t tqk_decode_workspace_bytes(const tqk_cache_desc* d, int32_t batch, int32_t max_len) {
-  if (!d || batch <= 0 || max_len <= 0) return 0;
+  if (!d || batch <= 0 || max_len <= 0 || batch > counter_seqs(*d)) return 0;
   return make_plan(d, batch, max_len).ws_bytes;
 }
 

@@ -220,7 +220,7 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
         }
       }
     }
-    if (tid == 0 && total > d.outlier_cap && a.overflow) atomicOr(a.overflow, 1);
+    if (tid == 0 && total > d.outlier_cap && a.overflow) atomicOr(a.overflow, TQK_OVF_OUTLIERS);
   } else if (tid < TQK_NOB) {
     a.p.ocount[obase * TQK_NOB + tid] = 0;
   }
@@ -298,8 +298,10 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
           u_s[tt][8 * m + 2 * q] = __fdiv_rn(x0[m], safe);
           u_s[tt][8 * m + 2 * q + 1] = __fdiv_rn(x1[m], safe);
         }
-        if (q == 0)
+        if (q == 0) {
           a.p.vnorm[page_row(a.p.block_table, d.max_pages_per_seq, b, t, P, d.n_pages, h)] = nrm;
+          if (nrm > TQK_MAX_VNORM && a.overflow) atomicOr(a.overflow, TQK_OVF_VNORM);
+        }
       }
     }
     __syncthreads();

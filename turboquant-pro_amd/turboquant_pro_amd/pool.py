@@ -194,7 +194,11 @@ class TQKVPool:
                                      k.data_ptr(), v.data_ptr(), T, st), "tqk_append_hot")
         self.lengths = new
         self.seq_lens.copy_(torch.tensor(new, dtype=torch.int32), non_blocking=False)
-        if items and check_overflow and int(self._overflow.item()) != 0:
+        ovf = int(self._overflow.item()) if items and check_overflow else 0
+        if ovf & 2:
+            raise ValueError("a value vector's norm exceeds 16376, the largest the gfx950 decode "
+                             "carries (softmax weight <= 4 times the norm in fp16)")
+        if ovf & 1:
             raise RuntimeError("outlier side-list exceeded outlier_cap for a group; "
                                "rebuild the pool with a larger outlier_cap")
 
