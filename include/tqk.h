@@ -97,7 +97,7 @@ typedef struct tqk_cache_ptrs {
   const float* vbnd;    /* 2^vb - 1 fp32 value boundaries */
 } tqk_cache_ptrs;
 
-/* Library ABI version (bumped on any signature or layout change); this header is version 4. */
+/* Library ABI version (bumped on any signature or layout change); this header is version 5. */
 int tqk_version(void);
 
 /* Validate a descriptor; TQK_OK when the GPU path supports it. */
@@ -128,6 +128,24 @@ size_t tqk_decode_workspace_bytes(const tqk_cache_desc* d, int32_t batch, int32_
 int tqk_decode(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t batch,
                const uint16_t* q, const int32_t* seq_lens, int32_t max_len, float* out,
                void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * tqk_decode without a caller workspace, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  No counterpart in the reference.  The split
+ * partials and arrival counters live in the library's own device scratch
+ * array, 32 MiB per GPU, held until the process ends; the call allocates
+ * nothing.  Limits: batch * n_kv_heads <= 65536, and the partials
+ * (batch * n_q_heads * splits * (head_dim + 2) floats, the part of
+ * tqk_decode_workspace_bytes after the counters) must fit the rest of the
+ * 32 MiB; otherwise TQK_EWORKSPACE.  Every call on one GPU shares that GPU's
+ * scratch: calls that overlap on one GPU (other streams, other threads) race.
+ * The first call on a device resolves the array's address and zeroes its
+ * counters on `stream`.
+ */
+int tqk_decode_noalloc(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t batch,
+                       const uint16_t* q, const int32_t* seq_lens, int32_t max_len, float* out,
+                       void* stream);
 
 /*
  * Same step, returning the unnormalised online-softmax state instead of the

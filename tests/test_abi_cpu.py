@@ -112,3 +112,17 @@ def test_binding_declares_every_signature_with_64bit_pointers():
             else:
                 assert ty in (ctypes.c_int32, ctypes.c_int), f"{name}: '{decl}' bound as {ty}"
         assert fn.restype in (ctypes.c_int, ctypes.c_size_t), f"{name}: restype {fn.restype}"
+
+
+def test_noalloc_rejects_plans_beyond_its_scratch():
+    """tqk_decode_noalloc returns TQK_EWORKSPACE for a step whose partials do
+    not fit the 32 MiB scratch, before any GPU work (pointers are never
+    dereferenced on this path)."""
+    N, lib = _lib()
+    d = _desc(N, n_pages=1 << 17, max_pages_per_seq=1 << 17, max_groups_per_seq=1 << 17)
+    fake = ctypes.c_void_p(0x1000)
+    ptrs = N.CachePtrs()
+    rc = lib.tqk_decode_noalloc(ctypes.byref(d), ctypes.byref(ptrs), 1, fake, fake, 1 << 30, fake, None)
+    assert rc == N.TQK_EWORKSPACE
+    rc = lib.tqk_decode_noalloc(ctypes.byref(d), ctypes.byref(ptrs), 0, fake, fake, 100, fake, None)
+    assert rc == N.TQK_EINVAL

@@ -13,6 +13,7 @@
 // splits, rotates the coded part back with one D x D product per query head
 // and adds the hot-window part (turboquant_pro/kv_fused.py:139-153).
 #include <atomic>
+#include <mutex>
 
 #include "tqk_common.h"
 
@@ -1570,7 +1571,15 @@ inline int counter_seqs(const tqk_cache_desc& d) { return d.n_pages; }
 struct Plan {
   int n_cold_splits, n_hot_splits, groups_per_split, hot_per_split;
   size_t counter_bytes;  // arrival counters at the workspace's start, then the partials
+  size_t partial_bytes;  // the split partials (m, l, acc)
   size_t ws_bytes;
+};
+
+// Where one call's arrival counters and split partials live: the caller's
+// workspace, or the library's scratch array for tqk_decode_noalloc.
+struct WsView {
+  uint32_t* arrive;
+  void* partials;
 };
 
 // compute units of the current device (the plan sizes the launch for them),
@@ -1639,7 +1648,8 @@ Plan make_plan(const tqk_cache_desc* d, int batch, int max_len) {
   // counters stay zero between calls whatever the batch and split counts.
   const size_t n_counters = (size_t)counter_seqs(*d) * d->n_kv_heads;
   pl.counter_bytes = (n_counters * sizeof(uint32_t) + 255) & ~(size_t)255;
-  pl.ws_bytes = pl.counter_bytes + per * sizeof(float) * (2 + TQK_D) + 256;
+  pl.partial_bytes = per * sizeof(float) * (2 + TQK_D);
+  pl.ws_bytes = pl.counter_bytes + pl.partial_bytes + 256;
   return pl;
 }
 
@@ -1662,7 +1672,7 @@ hipError_t launch_split(const DecodeArgs& a, dim3 grid, hipStream_t st) {
 }
 
 DecodeArgs make_args(const tqk_cache_desc* d, const tqk_cache_ptrs* p, const Plan& pl, int batch,
-                     const uint16_t* q, const int32_t* seq_lens, void* ws) {
+                     const uint16_t* q, const int32_t* seq_lens, const WsView& w) {
   const int ns = pl.n_cold_splits + pl.n_hot_splits;
   const size_t per = (size_t)batch * d->n_q_heads * ns;
   DecodeArgs a;
@@ -1670,8 +1680,8 @@ DecodeArgs make_args(const tqk_cache_desc* d, const tqk_cache_ptrs* p, const Pla
   a.p = *p;
   a.q = q;
   a.seq_lens = seq_lens;
-  a.arrive = reinterpret_cast<uint32_t*>(ws);
-  a.pm = reinterpret_cast<float*>(static_cast<char*>(ws) + pl.counter_bytes);
+  a.arrive = w.arrive;
+  a.pm = reinterpret_cast<float*>(w.partials);
   a.pl = a.pm + per;
   a.pacc = a.pl + per;
   a.n_cold_splits = pl.n_cold_splits;
@@ -1685,16 +1695,25 @@ DecodeArgs make_args(const tqk_cache_desc* d, const tqk_cache_ptrs* p, const Pla
   return a;
 }
 
-int run_splits(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int batch, const uint16_t* q,
-               const int32_t* seq_lens, int max_len, void* ws, size_t ws_bytes, void* stream,
-               float* out = nullptr) {
+WsView caller_ws(const Plan& pl, void* ws) {
+  return WsView{reinterpret_cast<uint32_t*>(ws), static_cast<char*>(ws) + pl.counter_bytes};
+}
+
+// Arguments every decode entry point validates the same way.
+int check_decode_args(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int batch, int max_len) {
   int rc = tqk_check_desc(d);
   if (rc != TQK_OK) return rc;
-  if (!p || !q || !seq_lens || batch <= 0 || max_len <= 0) return TQK_EINVAL;
+  if (!p || batch <= 0 || max_len <= 0) return TQK_EINVAL;
   if (batch > counter_seqs(*d)) return TQK_EINVAL;
-  const Plan pl = make_plan(d, batch, max_len);
-  if (!ws || ws_bytes < pl.ws_bytes) return TQK_EWORKSPACE;
-  DecodeArgs a = make_args(d, p, pl, batch, q, seq_lens, ws);
+  return TQK_OK;
+}
+
+// The split kernel (validated arguments); `out` non-null selects the MFMA
+// kernel's in-kernel merge.
+int launch_splits(const tqk_cache_desc* d, const tqk_cache_ptrs* p, const Plan& pl, int batch,
+                  const uint16_t* q, const int32_t* seq_lens, const WsView& w, void* stream,
+                  float* out) {
+  DecodeArgs a = make_args(d, p, pl, batch, q, seq_lens, w);
   if (out && mfma_path(*d)) a.out = out;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   // (the MFMA kernel's workgroups are the coded splits; each also covers a
@@ -1712,16 +1731,11 @@ int run_splits(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int batch, cons
   return e == hipSuccess ? TQK_OK : TQK_EHIP;
 }
 
-int run_merge(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int batch, int max_len, float* out,
-              float* m_out, float* l_out, float* acc_out, void* ws, size_t ws_bytes, void* stream) {
-  int rc = tqk_check_desc(d);
-  if (rc != TQK_OK) return rc;
-  if (!p || batch <= 0 || max_len <= 0) return TQK_EINVAL;
-  if (!out && !(m_out && l_out && acc_out)) return TQK_EINVAL;
-  if (batch > counter_seqs(*d)) return TQK_EINVAL;
-  const Plan pl = make_plan(d, batch, max_len);
-  if (!ws || ws_bytes < pl.ws_bytes) return TQK_EWORKSPACE;
-  const DecodeArgs a = make_args(d, p, pl, batch, nullptr, nullptr, ws);
+// tqk_merge over the partials the split kernel left (validated arguments).
+int launch_merge(const tqk_cache_desc* d, const tqk_cache_ptrs* p, const Plan& pl, int batch,
+                 const WsView& w, float* out, float* m_out, float* l_out, float* acc_out,
+                 void* stream) {
+  const DecodeArgs a = make_args(d, p, pl, batch, nullptr, nullptr, w);
   MergeArgs m;
   m.pm = a.pm;
   m.pl = a.pl;
@@ -1740,11 +1754,73 @@ int run_merge(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int batch, int m
   return hipGetLastError() == hipSuccess ? TQK_OK : TQK_EHIP;
 }
 
+int run_splits(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int batch, const uint16_t* q,
+               const int32_t* seq_lens, int max_len, void* ws, size_t ws_bytes, void* stream,
+               float* out = nullptr) {
+  int rc = check_decode_args(d, p, batch, max_len);
+  if (rc != TQK_OK) return rc;
+  if (!q || !seq_lens) return TQK_EINVAL;
+  const Plan pl = make_plan(d, batch, max_len);
+  if (!ws || ws_bytes < pl.ws_bytes) return TQK_EWORKSPACE;
+  return launch_splits(d, p, pl, batch, q, seq_lens, caller_ws(pl, ws), stream, out);
+}
+
+int run_merge(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int batch, int max_len, float* out,
+              float* m_out, float* l_out, float* acc_out, void* ws, size_t ws_bytes, void* stream) {
+  int rc = check_decode_args(d, p, batch, max_len);
+  if (rc != TQK_OK) return rc;
+  if (!out && !(m_out && l_out && acc_out)) return TQK_EINVAL;
+  const Plan pl = make_plan(d, batch, max_len);
+  if (!ws || ws_bytes < pl.ws_bytes) return TQK_EWORKSPACE;
+  return launch_merge(d, p, pl, batch, caller_ws(pl, ws), out, m_out, l_out, acc_out, stream);
+}
+
+// ---- the no-allocation decode's scratch ------------------------------------
+// One zero-fill kernel for the scratch array's counter region (a kernel, not
+// hipMemsetAsync, so that no memset node is recorded if a caller captures it).
+__global__ void tqk_zero_words(uint32_t* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+}  // namespace
+
+// Device scratch of tqk_decode_noalloc, one copy per GPU for the life of the
+// process: kNoAllocCounters arrival counters, then the split partials.  The
+// array's name is a host-side stand-in: host code only ever uses the address
+// hipGetSymbolAddress returns for the current device (noalloc_scratch()).
+constexpr int kNoAllocCounters = 1 << 16;         // (sequence, kv head) pairs per call
+constexpr size_t kNoAllocBytes = (size_t)32 << 20;  // 32 MiB per GPU
+static __device__ __align__(256) uint8_t scratch[kNoAllocBytes];
+
+namespace {
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+// The current device's scratch address, resolved (and its counters zeroed,
+// on `stream`) at the first call on that device.
+int noalloc_scratch(hipStream_t stream, void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return TQK_EHIP;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return TQK_EHIP;
+    hipLaunchKernelGGL(tqk_zero_words, dim3(kNoAllocCounters / 256), dim3(256), 0, stream,
+                       static_cast<uint32_t*>(ptr), kNoAllocCounters);
+    if (hipGetLastError() != hipSuccess) return TQK_EHIP;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return TQK_OK;
+}
+
 }  // namespace
 
 extern "C" {
 
-int tqk_version(void) { return 4; }
+int tqk_version(void) { return 5; }
 
 int tqk_check_desc(const tqk_cache_desc* d) {
   if (!d) return TQK_EINVAL;
@@ -1780,6 +1856,27 @@ int tqk_decode(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t batch,
   if (mfma_path(*d)) return TQK_OK;
   return run_merge(d, p, batch, max_len, out, nullptr, nullptr, nullptr, workspace,
                    workspace_bytes, stream);
+}
+
+int tqk_decode_noalloc(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t batch,
+                       const uint16_t* q, const int32_t* seq_lens, int32_t max_len, float* out,
+                       void* stream) {
+  int rc = check_decode_args(d, p, batch, max_len);
+  if (rc != TQK_OK) return rc;
+  if (!q || !seq_lens || !out) return TQK_EINVAL;
+  const Plan pl = make_plan(d, batch, max_len);
+  constexpr size_t kCounterBytes = (size_t)kNoAllocCounters * sizeof(uint32_t);
+  if ((size_t)batch * d->n_kv_heads > (size_t)kNoAllocCounters ||
+      pl.partial_bytes > kNoAllocBytes - kCounterBytes)
+    return TQK_EWORKSPACE;
+  void* base = nullptr;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  rc = noalloc_scratch(st, &base);
+  if (rc != TQK_OK) return rc;
+  const WsView w{static_cast<uint32_t*>(base), static_cast<char*>(base) + kCounterBytes};
+  rc = launch_splits(d, p, pl, batch, q, seq_lens, w, stream, out);
+  if (rc != TQK_OK || mfma_path(*d)) return rc;
+  return launch_merge(d, p, pl, batch, w, out, nullptr, nullptr, nullptr, stream);
 }
 
 int tqk_decode_partials(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t batch,

@@ -19,12 +19,12 @@ TQK_EUNSUPPORTED = 2
 TQK_EHIP = 3
 TQK_EWORKSPACE = 4
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # Every symbol include/tqk.h declares (checked by the CPU test suite).
 EXPORTS = (
     "tqk_version", "tqk_check_desc", "tqk_decode_workspace_bytes", "tqk_decode",
-    "tqk_decode_partials", "tqk_decode_splits", "tqk_decode_merge", "tqk_encode_groups",
+    "tqk_decode_noalloc", "tqk_decode_partials", "tqk_decode_splits", "tqk_decode_merge", "tqk_encode_groups",
     "tqk_append_hot", "tqk_dequant_groups",
 )
 
@@ -57,6 +57,7 @@ def load(path: str) -> ctypes.CDLL:
         "tqk_check_desc": ([pd], ctypes.c_int),
         "tqk_decode_workspace_bytes": ([pd, i32, i32], sz),
         "tqk_decode": ([pd, pp, i32, vp, vp, i32, vp, vp, sz, vp], ctypes.c_int),
+        "tqk_decode_noalloc": ([pd, pp, i32, vp, vp, i32, vp, vp], ctypes.c_int),
         "tqk_decode_partials": ([pd, pp, i32, vp, vp, i32, vp, vp, vp, vp, sz, vp], ctypes.c_int),
         "tqk_decode_splits": ([pd, pp, i32, vp, vp, i32, vp, sz, vp], ctypes.c_int),
         "tqk_decode_merge": ([pd, pp, i32, i32, vp, vp, sz, vp], ctypes.c_int),
