@@ -2,8 +2,9 @@
  * tqk.h -- C ABI of the MI355X (gfx950) TurboQuant Pro KV-cache kernels.
  *
  * One hot path: the two-tier TurboQuant KV cache (fp16 hot window + flushed
- * groups of per-channel asym-NF4 4-bit keys with an fp16 outlier side-list and
- * PolarQuant 3/4-bit values) and the fused decode-step attention over it.
+ * groups of per-channel 4-bit keys -- asym-NF4 with a calibrated, sparse or
+ * bias zero point, or uniform -- with an fp16 outlier side-list, and
+ * PolarQuant 2/3/4-bit values) and the fused decode-step attention over it.
  *
  * Conventions
  *   - Every pointer is a DEVICE pointer unless its comment says host.
@@ -32,10 +33,12 @@
  * (turboquant_pro/per_channel_kv.py:87-93 and turboquant_pro/core.py:350-398):
  * the key bytes of one (group, head) in page order are the reference
  * container's `indices` slice for that head, except that every position held
- * in oent stores the NF4 zero level (code 7, nibble 0xE): the dense part of a
- * decode then contributes exactly the channel mean there and the side-list
- * adds val - mean.  The reference's code at such a position is the nearest
- * NF4 level to the stored fp16 value (recomputed on export).  Value bytes are the reference's
+ * in oent stores the code whose level is 0 -- NF4's code 7 (nibble 0xE) for
+ * key_grid 0, code 0 for key_grid 1 -- so that the dense part of a decode
+ * contributes exactly gmean there and the side-list adds val - gmean (exact
+ * only because the stored level's reconstruction equals gmean).  The
+ * reference's code at such a position is the nearest level to the stored
+ * fp16 value (recomputed on export).  Value bytes are the reference's
  * per-token pack when page_tokens % 16 != 0 or group_tokens % 32 != 0; otherwise
  * each 16-token tile of a page holds 64 units of head_dim*vb/32 bytes, unit
  * (lg, c) = tokens [4lg, 4lg+4) x channels [8c, 8c+8) with the code of token u,
@@ -66,7 +69,7 @@ typedef struct tqk_cache_desc {
   int32_t group_tokens;         /* G = (W + 1) / 2, 1..256 */
   int32_t page_tokens;          /* P, divides G */
   int32_t key_bits;             /* 4 (per-channel asym-NF4 or uniform, see key_grid) */
-  int32_t value_bits;           /* 3 or 4 (PolarQuant) */
+  int32_t value_bits;           /* 2, 3 or 4 (PolarQuant) */
   int32_t outliers_per_channel; /* k = max(1, round(G * outlier_frac)), 0 = no side-list */
   int32_t outlier_cap;          /* oent capacity per (group slot, head) */
   int32_t max_pages_per_seq;    /* block_table row stride */
@@ -74,9 +77,14 @@ typedef struct tqk_cache_desc {
   int32_t hot_ring;             /* ring capacity in tokens, >= W */
   int32_t n_pages;              /* physical pages in the pool (block_table entries index them) */
   float sm_scale;               /* softmax scale, 1/sqrt(D) */
-  int32_t key_grid;             /* 0: asym-NF4 (gmean = channel mean, gscale = abs-max of the
-                                   centred channel, levels NF4); 1: uniform (gmean = channel min,
+  int32_t key_grid;             /* 0: asym-NF4 (gmean = the zero point, gscale = abs-max of the
+                                   channel centred on it, levels NF4); 1: uniform (gmean = channel min,
                                    gscale = max(max - min, 1e-8) / 15, levels 0..15) */
+  int32_t zero_point;           /* asym-NF4 zero point (turboquant_pro/per_channel_kv.py:327-345):
+                                   0 "calibrated", the channel mean over the group;
+                                   1 "sparse", the channel mean on the dc_mask channels, 0 elsewhere;
+                                   2 "bias", zp_mean[g] of the group's index g (host-computed) */
+  uint32_t dc_mask[4];          /* sparse: channel j is a DC channel when bit j % 32 of word j / 32 is set */
 } tqk_cache_desc;
 
 typedef struct tqk_cache_ptrs {
@@ -95,9 +103,11 @@ typedef struct tqk_cache_ptrs {
   const float* pi_t;    /* (D, D) row-major: rotate x -> x @ pi_t */
   const float* vcent;   /* 2^vb fp32 value centroids (already / sqrt(D)) */
   const float* vbnd;    /* 2^vb - 1 fp32 value boundaries */
+  const float* zp_mean; /* zero_point 2: [max_groups_per_seq][n_kv_heads][head_dim] zero points of
+                           the groups starting at token g * group_tokens; unused otherwise */
 } tqk_cache_ptrs;
 
-/* Library ABI version (bumped on any signature or layout change); this header is version 5. */
+/* Library ABI version (bumped on any signature or layout change); this header is version 6. */
 int tqk_version(void);
 
 /* Validate a descriptor; TQK_OK when the GPU path supports it. */
@@ -213,6 +223,69 @@ int tqk_append_hot(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t bat
  */
 int tqk_dequant_groups(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t n_items,
                        const int32_t* items, float* kout, float* vout, void* stream);
+
+/*
+ * Stateless block quantizers: one (B, H, S, D) block, every (b, h) pair one
+ * quantization group of S tokens (any S >= 1), fp16 or fp32 input, outputs in
+ * the reference containers' layouts.  The plugin / block-store path
+ * (PerChannelKV.compress on whole layer blocks, turboquant_pro/connectors/
+ * vllm_v1.py:298-322).
+ */
+typedef struct tqk_block_desc {
+  int32_t batch;                /* B */
+  int32_t n_heads;              /* H */
+  int32_t tokens;               /* S >= 1 */
+  int32_t head_dim;             /* D = 128 */
+  int32_t bits;                 /* keys: 4; values: 2, 3 or 4 */
+  int32_t key_grid;             /* keys: 0 asym-NF4, 1 uniform */
+  int32_t zero_point;           /* asym-NF4 keys: 0 calibrated, 1 sparse, 2 given (zp), as in tqk_cache_desc */
+  int32_t outliers_per_channel; /* keys: k = max(1, round(S * outlier_frac)), 0 = no side-list */
+  int32_t outlier_cap;          /* keys: side-list capacity per (b, h) */
+  int32_t input_f32;            /* 1: x is fp32, 0: x is fp16 */
+  uint32_t dc_mask[4];          /* sparse: DC channels, as in tqk_cache_desc */
+} tqk_block_desc;
+
+/*
+ * Per-channel key quantization of x [B][H][S][D] (PerChannelKV.compress,
+ * turboquant_pro/per_channel_kv.py:269-401): packed [B*H*S*D/2] u8 (the
+ * reference's packed indices, true codes at outlier positions), scale and
+ * zero [B][H][D] f32 (asym-NF4: nf4_scale and the zero point; uniform: scale
+ * and channel min), the side-list of each (b, h) in (s, j) order as
+ * out_pos [B*H][outlier_cap] u32 (s * D + j) and out_val [B*H][outlier_cap]
+ * fp16, and out_count [B*H] i32 (may exceed outlier_cap: the list is then
+ * truncated).  zp [H][D] f32 for zero_point 2, else unused.
+ */
+int tqk_encode_key_block(const tqk_block_desc* d, const void* x, const float* zp, uint8_t* packed,
+                         float* scale, float* zero, uint32_t* out_pos, uint16_t* out_val,
+                         int32_t* out_count, void* stream);
+
+/*
+ * PolarQuant of x [B][H][S][D] (TurboQuantKV.compress(kind="value"),
+ * turboquant_pro/core.py:542-617): packed [B*H*S][D*bits/8] u8 (the
+ * reference's little-endian bit stream per token) and norms [B*H*S] f32.
+ * pi is the cache's (D, D) row-major Pi (rotation y_e = sum_d u_d * pi[e][d],
+ * i.e. u @ pi_t), vbnd the 2^bits - 1 boundaries.
+ */
+int tqk_encode_value_block(const tqk_block_desc* d, const void* x, const float* pi,
+                           const float* vbnd, uint8_t* packed, float* norms, void* stream);
+
+/*
+ * Key reconstruction (PerChannelKV.decompress, turboquant_pro/per_channel_kv.py:
+ * 497-539): out [B][H][S][D] f32 = zero + scale * level[code] (level NF4 or
+ * the code itself for key_grid 1), then out[out_idx[i]] = fp32(out_val[i])
+ * for the n_out flat indices of the reference's side-list (an index outside
+ * [0, B*H*S*D) is skipped; callers validate the list beforehand).
+ */
+int tqk_dequant_key_block(const tqk_block_desc* d, const uint8_t* packed, const float* scale,
+                          const float* zero, int32_t n_out, const int32_t* out_idx,
+                          const uint16_t* out_val, float* out, void* stream);
+
+/*
+ * Value reconstruction (TurboQuantKV.decompress, turboquant_pro/core.py:
+ * 619-654): out [B][H][S][D] f32 = (vcent[code] @ pi) * norm per token.
+ */
+int tqk_dequant_value_block(const tqk_block_desc* d, const uint8_t* packed, const float* norms,
+                            const float* pi, const float* vcent, float* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -218,18 +218,51 @@ def encode_keys_uniform(x: np.ndarray, outlier_frac: float) -> KeyGroup:
                     outlier_idx=oidx, outlier_val=oval, shape=(1, H, S, D), grid="uniform")
 
 
-def encode_keys(x: np.ndarray, outlier_frac: float) -> KeyGroup:
+def dc_channel_mask(rope_theta: float, head_dim: int, window: int) -> np.ndarray:
+    """Channels whose rotary wavelength exceeds ``window`` tokens,
+    turboquant_pro/per_channel_kv.py:234-243 (float64)."""
+    half = head_dim // 2
+    inv = rope_theta ** (-2.0 * np.arange(half) / head_dim)
+    return np.tile(2.0 * np.pi / inv, 2)[:head_dim] > float(window)
+
+
+def rope_averaged_bias(k_bias: np.ndarray, rope_theta: float, head_dim: int, start: int,
+                       n: int) -> np.ndarray:
+    """Position-averaged rotation of the k_proj bias over ``[start, start + n)``,
+    turboquant_pro/per_channel_kv.py:245-267: float64 mean cos/sin per
+    frequency, rounded to fp32, then ``b * c + rotate_half(b) * s`` in fp32."""
+    half = head_dim // 2
+    inv = rope_theta ** (-2.0 * np.arange(half, dtype=np.float64) / head_dim)
+    ang = np.arange(start, start + n, dtype=np.float64)[:, None] * inv[None, :]
+    c = np.tile(np.cos(ang).mean(axis=0), 2).astype(np.float32)
+    sn = np.tile(np.sin(ang).mean(axis=0), 2).astype(np.float32)
+    b = np.asarray(k_bias, dtype=np.float32).reshape(-1, head_dim)
+    return b * c[None, :] + np.concatenate([-b[:, half:], b[:, :half]], axis=1) * sn[None, :]
+
+
+def encode_keys(x: np.ndarray, outlier_frac: float, zero_point: str = "calibrated",
+                rope_theta: float | None = None, k_bias=None, position_start: int = 0) -> KeyGroup:
     """Asym-NF4 per-channel key encode of one group ``x`` (H, S, D) fp32.
 
     Restates turboquant_pro/per_channel_kv.py:269-283 (outliers) and
-    :285-401 (nf4_asym, zero_point="calibrated").  The reference works on a
-    ``(1, H, S, D)`` array; the same shape is used here so NumPy's reduction
-    order (and therefore every rounding) is the same.
+    :285-401 (nf4_asym) with the zero point of :327-345: the channel mean
+    ("calibrated"), the mean on the DC channels only ("sparse"), or the
+    RoPE-averaged k_proj bias of positions ``[position_start, +S)`` ("bias").
+    ``nf4_mean`` holds the zero point of every channel (the reference stores
+    only the DC channels for "sparse" and nothing for "bias").  The reference
+    works on a ``(1, H, S, D)`` array; the same shape is used here so NumPy's
+    reduction order (and therefore every rounding) is the same.
     """
     x4 = np.asarray(x, dtype=np.float32)[None]
     _, H, S, D = x4.shape
     oidx, oval = key_outliers(x4, outlier_frac)
-    mean = x4.mean(axis=2)                                   # (1, H, D)
+    if zero_point == "bias":
+        mean = np.broadcast_to(rope_averaged_bias(k_bias, rope_theta, D, position_start, S)[None],
+                               (1, H, D))
+    elif zero_point == "sparse":
+        mean = x4.mean(axis=2) * dc_channel_mask(rope_theta, D, S)[None, None, :]
+    else:
+        mean = x4.mean(axis=2)                               # (1, H, D)
     centred = x4 - mean[:, :, None, :]
     amax = np.maximum(np.abs(centred).max(axis=2), 1e-8)     # (1, H, D)
     grid = (mean[..., None] + amax[..., None] * NF4[None, None, None, :]).astype(np.float32)
@@ -370,6 +403,9 @@ class SequenceCache:
     outlier_frac: float
     seed: int | None = 0
     key_grid: str = "nf4_asym"       # or "uniform" (per_channel_kv.py:303-317)
+    zero_point: str = "calibrated"   # asym-NF4: or "sparse" / "bias" (per_channel_kv.py:327-345)
+    rope_theta: float | None = None
+    k_bias: np.ndarray | None = None
     keys: list = field(default_factory=list)
     values: list = field(default_factory=list)
     hot_k: np.ndarray | None = None
@@ -384,8 +420,12 @@ class SequenceCache:
         self.keys, self.values = [], []
         for i in range(ng):
             sl = slice(G * i, G * (i + 1))
-            enc = encode_keys_uniform if self.key_grid == "uniform" else encode_keys
-            self.keys.append(enc(k[:, sl].astype(np.float32), self.outlier_frac))
+            if self.key_grid == "uniform":
+                self.keys.append(encode_keys_uniform(k[:, sl].astype(np.float32), self.outlier_frac))
+            else:
+                # the flushed block's position_start is the cold length before it
+                self.keys.append(encode_keys(k[:, sl].astype(np.float32), self.outlier_frac,
+                                             self.zero_point, self.rope_theta, self.k_bias, G * i))
             self.values.append(encode_values(v[:, sl].astype(np.float32), pi_t, bnd, self.value_bits))
         self.hot_k = k[:, G * ng:]
         self.hot_v = v[:, G * ng:]

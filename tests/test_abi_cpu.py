@@ -47,8 +47,16 @@ def test_check_desc_status_codes():
     ok = _desc(N)
     assert lib.tqk_check_desc(ctypes.byref(ok)) == N.TQK_OK
     assert lib.tqk_check_desc(ctypes.byref(_desc(N, head_dim=64))) == N.TQK_EUNSUPPORTED
-    assert lib.tqk_check_desc(ctypes.byref(_desc(N, value_bits=2))) == N.TQK_EUNSUPPORTED
+    assert lib.tqk_check_desc(ctypes.byref(_desc(N, value_bits=2))) == N.TQK_OK
+    assert lib.tqk_check_desc(ctypes.byref(_desc(N, value_bits=5))) == N.TQK_EUNSUPPORTED
+    assert lib.tqk_check_desc(ctypes.byref(_desc(N, zero_point=2))) == N.TQK_OK
+    assert lib.tqk_check_desc(ctypes.byref(_desc(N, zero_point=3))) == N.TQK_EINVAL
+    # zero points belong to asym-NF4 keys
+    assert lib.tqk_check_desc(ctypes.byref(_desc(N, zero_point=1, key_grid=1))) == N.TQK_EINVAL
     assert lib.tqk_check_desc(ctypes.byref(_desc(N, n_q_heads=12))) == N.TQK_EINVAL
+    # any 1..8 query heads per kv head (Qwen2.5-7B: 28 over 4)
+    assert lib.tqk_check_desc(ctypes.byref(_desc(N, n_q_heads=56))) == N.TQK_OK
+    assert lib.tqk_check_desc(ctypes.byref(_desc(N, n_q_heads=72))) == N.TQK_EUNSUPPORTED
     assert lib.tqk_check_desc(ctypes.byref(_desc(N, group_tokens=128))) == N.TQK_EINVAL
     assert lib.tqk_check_desc(ctypes.byref(_desc(N, page_tokens=24))) == N.TQK_EINVAL
     assert lib.tqk_check_desc(ctypes.byref(_desc(N, hot_window=1023, group_tokens=512))) == \
@@ -111,6 +119,7 @@ def test_binding_declares_every_signature_with_64bit_pointers():
                 assert ty is ctypes.c_size_t, f"{name}: '{decl}' bound as {ty}"
             else:
                 assert ty in (ctypes.c_int32, ctypes.c_int), f"{name}: '{decl}' bound as {ty}"
+                assert "int32_t" in decl, f"{name}: '{decl}' is not a 32-bit integer"
         assert fn.restype in (ctypes.c_int, ctypes.c_size_t), f"{name}: restype {fn.restype}"
 
 

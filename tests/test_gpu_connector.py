@@ -86,7 +86,7 @@ def test_store_save_export_load():
         "blob": blobs["packed"], "sha256": hashlib.sha256(blobs["packed"]).hexdigest()}}}) == 1
     k2, v2 = other.load("r", "l")
     assert np.array_equal(k2, ok) and np.array_equal(v2, ov)
-    # an undecodable record is a miss, and is dropped
+    # an undecodable record (its code bytes cut short) is a miss, and is dropped
     rec = other.record("r", "l")
-    rec.key_payload.nf4_mean = None
+    rec.key_payload.indices = np.asarray(rec.key_payload.indices).reshape(-1)[:10]
     assert other.load("r", "l") is None and other.record("r", "l") is None

@@ -6,11 +6,12 @@ Two requests (1100 and 700 tokens, GQA 8:2) are appended to a pool, saved
 through ``save_kv_layer`` in the pool's group cadence, and restored with
 ``start_load_kv`` into the two slots of a fresh pool.  Every coded group of
 the restored pool is bit-identical to the original's (imported as codes,
-including the MFMA-tiled value order, no re-encode); the hot tokens are the
-GPU dequantization of their records; the restored pool decodes within the
-north-star bar of dequantize-then-attend over its own contents, before and
-after further appends; the scheduler side reports the stored tokens and a
-finished request is evicted.
+including the MFMA-tiled value order, no re-encode) and so is the hot window
+(kept as fp16): the restored pool decodes exactly as the original does, and
+within the north-star bar of dequantize-then-attend over its own contents;
+after the same further appends both pools hold the same codes and decode
+alike.  The scheduler side reports the stored tokens and a finished request
+is evicted.  A pool of another key grid refuses the records.
 """
 
 import numpy as np
@@ -90,13 +91,27 @@ def test_start_load_kv_restores_codes():
             a, c = src.export_group(b, g), dst.export_group(b, g)
             for key in a:
                 assert np.array_equal(np.asarray(a[key]), np.asarray(c[key])), f"seq {b} group {g} {key}"
-        hs, hd = src.hot_window_tokens(b)[0].float(), dst.hot_window_tokens(b)[0].float()
-        assert hs.shape == hd.shape
-        assert (hs - hd).abs().max().item() < 0.25 * hs.abs().max().item()   # a dequantization
+        for x_s, x_d in zip(src.hot_window_tokens(b), dst.hot_window_tokens(b)):
+            assert torch.equal(x_s, x_d)                                      # kept as fp16
+    assert torch.equal(dst.decode(qd), src.decode(qd))
     _check_decode(dst, qd)
-    # decoding continues on the restored pool: more tokens, a flush in each sequence
+    # decoding continues on the restored pool: more tokens, a flush in each
+    # sequence, the same codes as the original pool gets from the same tokens
     dst.append(kd[:, :, 1100:1400], vd[:, :, 1100:1400], n_new=[300, 300])
-    assert dst.n_groups(0) == src.n_groups(0) + 1 and dst.n_groups(1) == src.n_groups(1) + 1
+    src.append(kd[:, :, 1100:1400], vd[:, :, 1100:1400], n_new=[300, 300])
+    assert dst.n_groups(0) == src.n_groups(0) and dst.n_groups(1) == src.n_groups(1)
+    for b in range(2):
+        for g in range(src.n_groups(b)):
+            a, c = src.export_group(b, g), dst.export_group(b, g)
+            for key in ("kpacked", "vpacked", "vnorms", "outlier_idx"):
+                assert np.array_equal(np.asarray(a[key]), np.asarray(c[key])), f"seq {b} group {g} {key}"
+    assert torch.equal(dst.decode(qd), src.decode(qd))
     _check_decode(dst, qd)
+    # a pool of another key grid refuses the records
+    from turboquant_pro_amd import TQKVPool
+    uni = TQKVPool(n_kv_heads=2, n_q_heads=8, max_batch=2, max_seq_len=2048, value_bits=3, seed=0,
+                   key_grid="uniform")
+    with pytest.raises(ValueError, match="asym-NF4"):
+        conn.store.load_into_pool("reqA", "layers.0.attn", uni, 0)
     conn.get_finished({"reqA"})
     assert conn.store.matched_tokens("reqA") == 0 and conn.store.matched_tokens("reqB") == 700

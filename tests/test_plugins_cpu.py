@@ -68,11 +68,14 @@ def test_per_channel_constructor_validation():
     # valid reference configurations without a gfx950 encode
     uni = PL.create("per_channel", bits=4, outlier_frac=0.02)      # the reference's default mode
     assert uni.uniform and uni.key_grid == "uniform"
-    for cfg in (dict(bits=3), dict(nf4=True), dict(nuq=True),
-                dict(nf4_asym=True, zero_point="sparse", rope_theta=1e4),
-                dict(nf4_asym=True, head_dim=64)):
+    for cfg in (dict(bits=3), dict(nf4=True), dict(nuq=True), dict(nf4_asym=True, head_dim=64)):
         with pytest.raises(NotImplementedError):
             PL.create("per_channel", **cfg)
+    # every asym-NF4 zero point has a gfx950 encode
+    sp = PL.create("per_channel", nf4_asym=True, zero_point="sparse", rope_theta=1e4)
+    bi = PL.create("per_channel", nf4_asym=True, zero_point="bias", rope_theta=1e6,
+                   k_bias=np.ones((32, 128), np.float32), n_heads=32)
+    assert sp.zero_point == "sparse" and bi.k_bias.shape == (32, 128)
 
 
 def test_polar_constructor_validation():
@@ -83,11 +86,11 @@ def test_polar_constructor_validation():
         PL.create("polar", value_bits=1)
     with pytest.raises(NotImplementedError):
         PL.create("polar", head_dim=64)
-    x = np.zeros((1, 2, 4, 128), np.float32)
-    with pytest.raises(NotImplementedError, match="keys"):
-        q.compress(x, kind="key")
-    with pytest.raises(NotImplementedError):
-        PL.create("polar", bits=2).compress(x)
+    # widths per kind, as TurboQuantKV._resolve_bits (turboquant_pro/core.py:528-540)
+    kv = PL.create("polar", bits=3, key_bits=4, value_bits=2, seed=0)
+    assert (kv._width(None), kv._width("key"), kv._width("value")) == (3, 4, 2)
+    with pytest.raises(ValueError):
+        kv._width("query")
     assert PL.affine_params(q, None) is None and PL.outlier_csr(q, None) is None
 
 

@@ -1,0 +1,472 @@
+// Stateless block quantizers and their reconstruction (gfx950).
+//
+// One (B, H, S, D) block per call, every (b, h) pair one quantization group of
+// S tokens (any S >= 1), fp16 or fp32 input, outputs in the reference
+// containers' layouts: the whole-layer records of the plugin / block-store
+// path, which the cache's 256-token group encode does not cover.
+//
+// Bit-exactness contract (compiled with -ffp-contract=off, explicitly rounded
+// __f*_rn operations), the same NumPy operation order as the group encode:
+//   keys   (turboquant_pro/per_channel_kv.py:269-401)
+//     asym-NF4: mu = token-order sequential fp32 sum / S (a float64 division,
+//               then fp32), times the DC mask ("sparse") or given ("bias");
+//               amax = max(max_s |x_s - mu|, 1e-8); cent = mu + amax * NF4[l];
+//               code = first argmin_l |x - cent_l|
+//     uniform:  scale = max(max - min, 1e-8) / 15; code = clip(rint((x - min) / scale), 0, 15)
+//     outliers: threshold = k-th largest |x| over s; every |x| >= it, (s, j) order
+//   values (turboquant_pro/core.py:569-606): pairwise-8 norm, u = x / max(norm, 1e-30),
+//     y_e = sequential over d of u_d * Pi[e][d], code = #{ boundaries < y_e }
+#include "tqk_common.h"
+
+namespace {
+
+constexpr int kKbThreads = 256;  // key block: one workgroup per (b, h)
+constexpr int kVbThreads = 512;  // value block: 64 tokens per workgroup
+constexpr int kVbTokens = 64;
+
+__device__ __forceinline__ float load_x(const void* x, int f32, size_t i) {
+  return f32 ? reinterpret_cast<const float*>(x)[i] : h2f(reinterpret_cast<const uint16_t*>(x)[i]);
+}
+__device__ __forceinline__ bool dc_channel(const tqk_block_desc& d, int j) {
+  return (d.dc_mask[j >> 5] >> (j & 31)) & 1u;
+}
+
+struct KeyBlockArgs {
+  tqk_block_desc d;
+  const void* x;
+  const float* zp;
+  uint8_t* packed;
+  float* scale;
+  float* zero;
+  uint32_t* out_pos;
+  uint16_t* out_val;
+  int32_t* out_count;
+};
+
+__global__ __launch_bounds__(kKbThreads) void tqk_key_block(KeyBlockArgs a) {
+  constexpr int D = TQK_D;
+  const tqk_block_desc& d = a.d;
+  const int bh = blockIdx.x, h = bh % d.n_heads, tid = threadIdx.x;
+  const int S = d.tokens, f32 = d.input_f32, kout = d.outliers_per_channel;
+  const size_t base = (size_t)bh * S * D;
+  auto X = [&](int s, int j) { return load_x(a.x, f32, base + (size_t)s * D + j); };
+
+  __shared__ float cent_s[D][17];  // per-channel grid (uniform: min, scale)
+  __shared__ float thr_s[D];       // outlier threshold magnitude per channel
+  __shared__ int32_t wsum_s[kKbThreads / 64];
+
+  // ---- per-channel statistics (threads 0..127) and thresholds (128..255)
+  if (tid < D) {
+    const int j = tid;
+    if (d.key_grid == 1) {
+      float mn = X(0, j), mx = mn;
+      bool nan = (mn != mn);
+      for (int s = 1; s < S; ++s) {
+        const float xv = X(s, j);
+        nan |= (xv != xv);
+        mn = fminf(mn, xv);
+        mx = fmaxf(mx, xv);
+      }
+      const float sc = nan ? __builtin_nanf("") : __fdiv_rn(fmaxf(__fsub_rn(mx, mn), 1e-8f), 15.0f);
+      if (nan) mn = __builtin_nanf("");
+      cent_s[j][0] = mn;
+      cent_s[j][1] = sc;
+      a.scale[(size_t)bh * D + j] = sc;
+      a.zero[(size_t)bh * D + j] = mn;
+    } else {
+      float mu;
+      if (d.zero_point == 2) {
+        mu = a.zp[(size_t)h * D + j];
+      } else {
+        float acc = 0.0f;
+        for (int s = 0; s < S; ++s) acc = __fadd_rn(acc, X(s, j));
+        mu = (float)((double)acc / (double)S);
+        if (d.zero_point == 1) mu = __fmul_rn(mu, dc_channel(d, j) ? 1.0f : 0.0f);
+      }
+      float amax = 0.0f;
+      bool nan = (mu != mu);
+      for (int s = 0; s < S; ++s) {
+        const float dv = fabsf(__fsub_rn(X(s, j), mu));
+        nan |= (dv != dv);
+        amax = fmaxf(amax, dv);
+      }
+      amax = nan ? __builtin_nanf("") : fmaxf(amax, 1e-8f);
+#pragma unroll
+      for (int l = 0; l < 16; ++l) cent_s[j][l] = __fadd_rn(mu, __fmul_rn(amax, kNF4[l]));
+      a.scale[(size_t)bh * D + j] = amax;
+      a.zero[(size_t)bh * D + j] = mu;
+    }
+  } else if (tid < 2 * D && kout > 0 && kout < S) {
+    // k-th largest |x| as the largest fp32 magnitude pattern T with
+    // #{ |x_s| >= T } >= k (NaN patterns order above inf, as np.partition does)
+    const int j = tid - D;
+    uint32_t T = 0;
+    for (int bit = 30; bit >= 0; --bit) {
+      const uint32_t cand = T | (1u << bit);
+      int cnt = 0;
+      for (int s = 0; s < S; ++s) cnt += (__float_as_uint(fabsf(X(s, j))) >= cand);
+      if (cnt >= kout) T = cand;
+    }
+    thr_s[j] = __uint_as_float(T);
+  }
+  __syncthreads();
+
+  // ---- codes: thread = (channel pair, token slice), one byte per (token, pair)
+  {
+    const int jp = tid & 63, sq = tid >> 6;
+    const int per = (S + 3) / 4, s0 = sq * per, s1 = min(S, s0 + per);
+    uint8_t* out = a.packed + base / 2 + jp;
+    if (d.key_grid == 1) {
+      const float mn0 = cent_s[2 * jp][0], sc0 = cent_s[2 * jp][1];
+      const float mn1 = cent_s[2 * jp + 1][0], sc1 = cent_s[2 * jp + 1][1];
+      for (int s = s0; s < s1; ++s) {
+        const float r0 = __builtin_rintf(__fdiv_rn(__fsub_rn(X(s, 2 * jp), mn0), sc0));
+        const float r1 = __builtin_rintf(__fdiv_rn(__fsub_rn(X(s, 2 * jp + 1), mn1), sc1));
+        const uint32_t b0 = (uint32_t)fminf(fmaxf(r0, 0.0f), 15.0f);
+        const uint32_t b1 = (uint32_t)fminf(fmaxf(r1, 0.0f), 15.0f);
+        out[(size_t)s * (D / 2)] = (uint8_t)((rev4(b0) << 4) | rev4(b1));
+      }
+    } else {
+      float c0[16], c1[16];
+#pragma unroll
+      for (int l = 0; l < 16; ++l) {
+        c0[l] = cent_s[2 * jp][l];
+        c1[l] = cent_s[2 * jp + 1][l];
+      }
+      for (int s = s0; s < s1; ++s) {
+        const float x0 = X(s, 2 * jp), x1 = X(s, 2 * jp + 1);
+        int b0 = 0, b1 = 0;
+        float d0 = fabsf(__fsub_rn(x0, c0[0])), d1 = fabsf(__fsub_rn(x1, c1[0]));
+#pragma unroll
+        for (int l = 1; l < 16; ++l) {
+          const float e0 = fabsf(__fsub_rn(x0, c0[l])), e1 = fabsf(__fsub_rn(x1, c1[l]));
+          // np.argmin: strictly smaller wins; the first NaN wins over any number
+          if (e0 < d0 || (e0 != e0 && d0 == d0)) { d0 = e0; b0 = l; }
+          if (e1 < d1 || (e1 != e1 && d1 == d1)) { d1 = e1; b1 = l; }
+        }
+        out[(size_t)s * (D / 2)] = (uint8_t)((rev4(b0) << 4) | rev4(b1));
+      }
+    }
+  }
+
+  // ---- outlier side-list in (s, j) order: thread t owns a contiguous token
+  // range, counts its entries, takes its offset from a block scan, writes
+  if (kout > 0) {
+    const bool all = kout >= S;
+    const int chunk = (S + kKbThreads - 1) / kKbThreads;
+    const int s0 = min(S, tid * chunk), s1 = min(S, s0 + chunk);
+    int cnt = 0;
+    for (int s = s0; s < s1; ++s)
+      for (int j = 0; j < D; ++j) cnt += all || (fabsf(X(s, j)) >= thr_s[j]);
+    int incl = cnt;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int v = __shfl_up(incl, o, 64);
+      if ((tid & 63) >= o) incl += v;
+    }
+    if ((tid & 63) == 63) wsum_s[tid >> 6] = incl;
+    __syncthreads();
+    int off = incl - cnt, total = 0;
+    for (int w = 0; w < kKbThreads / 64; ++w) {
+      if (w < (tid >> 6)) off += wsum_s[w];
+      total += wsum_s[w];
+    }
+    if (tid == 0) a.out_count[bh] = total;
+    const size_t lb = (size_t)bh * d.outlier_cap;
+    for (int s = s0; s < s1 && off < d.outlier_cap; ++s) {
+      for (int j = 0; j < D; ++j) {
+        const float xv = X(s, j);
+        if (all || fabsf(xv) >= thr_s[j]) {
+          if (off < d.outlier_cap) {
+            a.out_pos[lb + off] = (uint32_t)s * D + (uint32_t)j;
+            a.out_val[lb + off] = f2h(xv);  // fp16, round to nearest even
+          }
+          ++off;
+        }
+      }
+    }
+  } else if (tid == 0) {
+    a.out_count[bh] = 0;
+  }
+}
+
+struct ValueBlockArgs {
+  tqk_block_desc d;
+  const void* x;
+  const float* pi;
+  const float* vbnd;
+  uint8_t* packed;
+  float* norms;
+};
+
+// 64 tokens of one (b, h) per workgroup.  Four threads per token compute the
+// norm in the reference's pairwise order and stage the normalised row in LDS;
+// then lane e of wave w owns rotated channel 64 * (w & 1) + e with its column
+// of Pi_T (row e of Pi) in registers, waves w >> 1 split the tokens, and each
+// y_e is the sequential, separately rounded sum over d.
+template <int VB>
+__global__ __launch_bounds__(kVbThreads) void tqk_value_block(ValueBlockArgs a) {
+  constexpr int D = TQK_D;
+  constexpr int VROW = D * VB / 8;
+  const tqk_block_desc& d = a.d;
+  const int S = d.tokens, bh = blockIdx.y, t0 = blockIdx.x * kVbTokens, tid = threadIdx.x;
+  const int nb = min(kVbTokens, S - t0);
+  const size_t tok0 = (size_t)bh * S + t0;  // flat token index of the first token
+  __shared__ __align__(16) float u_s[kVbTokens][D];
+  __shared__ uint8_t vc_s[kVbTokens][D];
+
+  {
+    const int tt = tid >> 2, q = tid & 3;
+    if (tt < nb) {
+      const size_t row = (tok0 + tt) * D;
+      float x0[16], x1[16];
+#pragma unroll
+      for (int m = 0; m < 16; ++m) {  // channels 8m + 2q, 8m + 2q + 1
+        x0[m] = load_x(a.x, d.input_f32, row + 8 * m + 2 * q);
+        x1[m] = load_x(a.x, d.input_f32, row + 8 * m + 2 * q + 1);
+      }
+      float r0 = __fmul_rn(x0[0], x0[0]), r1 = __fmul_rn(x1[0], x1[0]);
+#pragma unroll
+      for (int m = 1; m < 16; ++m) {
+        r0 = __fadd_rn(r0, __fmul_rn(x0[m], x0[m]));
+        r1 = __fadd_rn(r1, __fmul_rn(x1[m], x1[m]));
+      }
+      // pairwise tree ((r0 + r1) + (r2 + r3)) + ((r4 + r5) + (r6 + r7))
+      const float pa = __fadd_rn(r0, r1);
+      const float po = __shfl_xor(pa, 1, 4);
+      const float pb = (q & 1) ? __fadd_rn(po, pa) : __fadd_rn(pa, po);
+      const float pbo = __shfl_xor(pb, 2, 4);
+      const float ss = (q & 2) ? __fadd_rn(pbo, pb) : __fadd_rn(pb, pbo);
+      const float nrm = __builtin_sqrtf(ss);  // correctly rounded (-fhip-fp32-correctly-rounded-divide-sqrt)
+      const float safe = fmaxf(nrm, 1e-30f);
+#pragma unroll
+      for (int m = 0; m < 16; ++m) {
+        u_s[tt][8 * m + 2 * q] = __fdiv_rn(x0[m], safe);
+        u_s[tt][8 * m + 2 * q + 1] = __fdiv_rn(x1[m], safe);
+      }
+      if (q == 0) a.norms[tok0 + tt] = nrm;
+    }
+  }
+  const int lane = tid & 63, wv = tid >> 6;
+  const int ecol = 64 * (wv & 1) + lane;
+  float pcol[D];
+#pragma unroll
+  for (int k = 0; k < D / 4; ++k) {
+    const float4 p4 = reinterpret_cast<const float4*>(a.pi + (size_t)ecol * D)[k];
+    pcol[4 * k] = p4.x;
+    pcol[4 * k + 1] = p4.y;
+    pcol[4 * k + 2] = p4.z;
+    pcol[4 * k + 3] = p4.w;
+  }
+  float bnd[15];
+#pragma unroll
+  for (int k = 0; k < (1 << VB) - 1; ++k) bnd[k] = a.vbnd[k];
+  __syncthreads();
+  for (int j = 2 * (wv >> 1); j < nb; j += kVbThreads / 64) {
+    const int j1 = min(j + 1, nb - 1);
+    float y0 = 0.f, y1 = 0.f;
+#pragma unroll
+    for (int d4 = 0; d4 < D / 4; ++d4) {
+      const float4 ua = *reinterpret_cast<const float4*>(&u_s[j][4 * d4]);
+      const float4 ub = *reinterpret_cast<const float4*>(&u_s[j1][4 * d4]);
+      y0 = __fadd_rn(y0, __fmul_rn(ua.x, pcol[4 * d4]));
+      y1 = __fadd_rn(y1, __fmul_rn(ub.x, pcol[4 * d4]));
+      y0 = __fadd_rn(y0, __fmul_rn(ua.y, pcol[4 * d4 + 1]));
+      y1 = __fadd_rn(y1, __fmul_rn(ub.y, pcol[4 * d4 + 1]));
+      y0 = __fadd_rn(y0, __fmul_rn(ua.z, pcol[4 * d4 + 2]));
+      y1 = __fadd_rn(y1, __fmul_rn(ub.z, pcol[4 * d4 + 2]));
+      y0 = __fadd_rn(y0, __fmul_rn(ua.w, pcol[4 * d4 + 3]));
+      y1 = __fadd_rn(y1, __fmul_rn(ub.w, pcol[4 * d4 + 3]));
+    }
+    uint32_t c0 = 0, c1 = 0;
+#pragma unroll
+    for (int k = 0; k < (1 << VB) - 1; ++k) {
+      c0 += (bnd[k] < y0) ? 1u : 0u;
+      c1 += (bnd[k] < y1) ? 1u : 0u;
+    }
+    vc_s[j][ecol] = (uint8_t)c0;
+    if (j + 1 < nb) vc_s[j + 1][ecol] = (uint8_t)c1;
+  }
+  __syncthreads();
+  // the reference's little-endian bit stream, one token per thread
+  if (tid < nb) {
+    uint32_t outw[VROW / 4];
+#pragma unroll
+    for (int k = 0; k < VROW / 4; ++k) outw[k] = 0u;
+#pragma unroll
+    for (int e = 0; e < D; ++e) {
+      const uint32_t code = vc_s[tid][e];
+      const int bitpos = e * VB;
+      outw[bitpos >> 5] |= code << (bitpos & 31);
+      if ((bitpos & 31) + VB > 32) outw[(bitpos >> 5) + 1] |= code >> (32 - (bitpos & 31));
+    }
+    uint32_t* dst = reinterpret_cast<uint32_t*>(a.packed + (tok0 + tid) * VROW);
+#pragma unroll
+    for (int k = 0; k < VROW / 4; ++k) dst[k] = outw[k];
+  }
+}
+
+struct KeyDequantArgs {
+  tqk_block_desc d;
+  const uint8_t* packed;
+  const float* scale;
+  const float* zero;
+  float* out;
+};
+
+// one thread per code byte (two channels): zero + scale * level[code]
+__global__ __launch_bounds__(kKbThreads) void tqk_key_block_dequant(KeyDequantArgs a) {
+  constexpr int D = TQK_D;
+  const tqk_block_desc& d = a.d;
+  const size_t n = (size_t)d.batch * d.n_heads * d.tokens * (D / 2);
+  const size_t i = (size_t)blockIdx.x * kKbThreads + threadIdx.x;
+  if (i >= n) return;
+  const size_t bh = i / ((size_t)d.tokens * (D / 2));
+  const int j0 = 2 * (int)(i % (D / 2));
+  const uint32_t byte = a.packed[i];
+  const float* sc = a.scale + bh * D;
+  const float* zr = a.zero + bh * D;
+  a.out[2 * i] = __fadd_rn(__fmul_rn(sc[j0], key_level(d.key_grid, rev4(byte >> 4))), zr[j0]);
+  a.out[2 * i + 1] = __fadd_rn(__fmul_rn(sc[j0 + 1], key_level(d.key_grid, rev4(byte & 15u))), zr[j0 + 1]);
+}
+
+// the side-list overwrite (after the dense pass on the same stream); an index
+// outside [0, total) is skipped here and reported by the host-side check
+__global__ __launch_bounds__(kKbThreads) void tqk_key_block_outliers(float* out, int n,
+                                                                   int64_t total,
+                                                                   const int32_t* idx,
+                                                                   const uint16_t* val) {
+  const int i = blockIdx.x * kKbThreads + threadIdx.x;
+  if (i < n) {
+    const int64_t p = idx[i];
+    if (p >= 0 && p < total) out[p] = h2f(val[i]);
+  }
+}
+
+struct ValueDequantArgs {
+  tqk_block_desc d;
+  const uint8_t* packed;
+  const float* norms;
+  const float* pi;
+  const float* vcent;
+  float* out;
+};
+
+// one thread per token: y = vcent[code]; x_e = sequential over j of y_j * Pi[j][e]; x * norm
+template <int VB>
+__global__ __launch_bounds__(kKbThreads) void tqk_value_block_dequant(ValueDequantArgs a) {
+  constexpr int D = TQK_D;
+  constexpr int VROW = D * VB / 8;
+  const tqk_block_desc& d = a.d;
+  const size_t n = (size_t)d.batch * d.n_heads * d.tokens;
+  const size_t t = (size_t)blockIdx.x * kKbThreads + threadIdx.x;
+  if (t >= n) return;
+  const uint8_t* vr = a.packed + t * VROW;
+  float y[D];
+#pragma unroll
+  for (int j = 0; j < D; ++j) {
+    const int bitpos = j * VB;
+    const uint32_t w = vr[bitpos >> 3] | ((uint32_t)vr[min((bitpos >> 3) + 1, VROW - 1)] << 8);
+    y[j] = a.vcent[(w >> (bitpos & 7)) & ((1u << VB) - 1)];
+  }
+  const float nrm = a.norms[t];
+  float* o = a.out + t * D;
+  for (int e = 0; e < D; ++e) {
+    float x = 0.f;
+#pragma unroll
+    for (int j = 0; j < D; ++j) x = __fadd_rn(x, __fmul_rn(y[j], a.pi[j * D + e]));
+    o[e] = __fmul_rn(x, nrm);
+  }
+}
+
+int check_block(const tqk_block_desc* d, bool key) {
+  if (!d) return TQK_EINVAL;
+  if (d->head_dim != TQK_D) return TQK_EUNSUPPORTED;
+  if (d->batch <= 0 || d->n_heads <= 0 || d->tokens <= 0) return TQK_EINVAL;
+  if ((long long)d->batch * d->n_heads * d->tokens * TQK_D >= (1LL << 40)) return TQK_EINVAL;
+  if (key) {
+    if (d->bits != 4) return TQK_EUNSUPPORTED;
+    if (d->key_grid != 0 && d->key_grid != 1) return TQK_EINVAL;
+    if (d->zero_point < 0 || d->zero_point > 2 || (d->zero_point != 0 && d->key_grid != 0))
+      return TQK_EINVAL;
+    if (d->outliers_per_channel < 0 || d->outlier_cap < 0) return TQK_EINVAL;
+    // side-list positions s * D + j are 32-bit
+    if ((long long)d->tokens * TQK_D >= (1LL << 32)) return TQK_EUNSUPPORTED;
+  } else if (d->bits < 2 || d->bits > 4) {
+    return TQK_EUNSUPPORTED;
+  }
+  return TQK_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tqk_encode_key_block(const tqk_block_desc* d, const void* x, const float* zp, uint8_t* packed,
+                         float* scale, float* zero, uint32_t* out_pos, uint16_t* out_val,
+                         int32_t* out_count, void* stream) {
+  int rc = check_block(d, true);
+  if (rc != TQK_OK) return rc;
+  if (!x || !packed || !scale || !zero || !out_count) return TQK_EINVAL;
+  if (d->key_grid == 0 && d->zero_point == 2 && !zp) return TQK_EINVAL;
+  if (d->outliers_per_channel > 0 && d->outlier_cap > 0 && (!out_pos || !out_val)) return TQK_EINVAL;
+  KeyBlockArgs a{*d, x, zp, packed, scale, zero, out_pos, out_val, out_count};
+  hipLaunchKernelGGL(tqk_key_block, dim3(d->batch * d->n_heads), dim3(kKbThreads), 0,
+                     reinterpret_cast<hipStream_t>(stream), a);
+  return hipGetLastError() == hipSuccess ? TQK_OK : TQK_EHIP;
+}
+
+int tqk_encode_value_block(const tqk_block_desc* d, const void* x, const float* pi,
+                           const float* vbnd, uint8_t* packed, float* norms, void* stream) {
+  int rc = check_block(d, false);
+  if (rc != TQK_OK) return rc;
+  if (!x || !pi || !vbnd || !packed || !norms) return TQK_EINVAL;
+  ValueBlockArgs a{*d, x, pi, vbnd, packed, norms};
+  const dim3 grid((d->tokens + kVbTokens - 1) / kVbTokens, d->batch * d->n_heads);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (d->bits == 2)
+    hipLaunchKernelGGL(tqk_value_block<2>, grid, dim3(kVbThreads), 0, st, a);
+  else if (d->bits == 3)
+    hipLaunchKernelGGL(tqk_value_block<3>, grid, dim3(kVbThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL(tqk_value_block<4>, grid, dim3(kVbThreads), 0, st, a);
+  return hipGetLastError() == hipSuccess ? TQK_OK : TQK_EHIP;
+}
+
+int tqk_dequant_key_block(const tqk_block_desc* d, const uint8_t* packed, const float* scale,
+                          const float* zero, int32_t n_out, const int32_t* out_idx,
+                          const uint16_t* out_val, float* out, void* stream) {
+  int rc = check_block(d, true);
+  if (rc != TQK_OK) return rc;
+  if (!packed || !scale || !zero || !out || n_out < 0 || (n_out > 0 && (!out_idx || !out_val)))
+    return TQK_EINVAL;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const size_t n = (size_t)d->batch * d->n_heads * d->tokens * (TQK_D / 2);
+  KeyDequantArgs a{*d, packed, scale, zero, out};
+  hipLaunchKernelGGL(tqk_key_block_dequant, dim3((unsigned)((n + kKbThreads - 1) / kKbThreads)),
+                     dim3(kKbThreads), 0, st, a);
+  if (n_out > 0)
+    hipLaunchKernelGGL(tqk_key_block_outliers, dim3((n_out + kKbThreads - 1) / kKbThreads),
+                       dim3(kKbThreads), 0, st, out, n_out, (int64_t)(2 * n), out_idx, out_val);
+  return hipGetLastError() == hipSuccess ? TQK_OK : TQK_EHIP;
+}
+
+int tqk_dequant_value_block(const tqk_block_desc* d, const uint8_t* packed, const float* norms,
+                            const float* pi, const float* vcent, float* out, void* stream) {
+  int rc = check_block(d, false);
+  if (rc != TQK_OK) return rc;
+  if (!packed || !norms || !pi || !vcent || !out) return TQK_EINVAL;
+  const size_t n = (size_t)d->batch * d->n_heads * d->tokens;
+  ValueDequantArgs a{*d, packed, norms, pi, vcent, out};
+  const dim3 grid((unsigned)((n + kKbThreads - 1) / kKbThreads));
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (d->bits == 2)
+    hipLaunchKernelGGL(tqk_value_block_dequant<2>, grid, dim3(kKbThreads), 0, st, a);
+  else if (d->bits == 3)
+    hipLaunchKernelGGL(tqk_value_block_dequant<3>, grid, dim3(kKbThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL(tqk_value_block_dequant<4>, grid, dim3(kKbThreads), 0, st, a);
+  return hipGetLastError() == hipSuccess ? TQK_OK : TQK_EHIP;
+}
+
+}  // extern "C"

@@ -125,23 +125,22 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
   __shared__ float w_s[GQ][D];
   __shared__ float sc_s[GQ][kThreads];
   __shared__ float kl_s[256][2];
-  __shared__ float vl_s[(VB == 3) ? 64 : 256][2];
+  __shared__ float vl_s[1 << (2 * VB)][2];
   __shared__ float red_s[4][GQ];
   __shared__ float a_s[D], mu_s[D];
   __shared__ float accr_s[4][GQ][D];
 
+  // GQ is the kernel's power-of-two head count; the last GQ - gq heads are
+  // zero-query padding whose states are never written
+  const int gq = Hq / Hkv;
   for (int i = tid; i < GQ * D; i += kThreads)
-    q_s[i / D][i % D] = h2f(a.q[((size_t)b * Hq + h * GQ + i / D) * D + i % D]);
+    q_s[i / D][i % D] = (i / D < gq) ? h2f(a.q[((size_t)b * Hq + h * gq + i / D) * D + i % D]) : 0.f;
   kl_s[tid][0] = key_level(a.d.key_grid, rev4(tid >> 4));
   kl_s[tid][1] = key_level(a.d.key_grid, rev4(tid & 15));
-  if (VB == 3) {
-    if (tid < 64) {
-      vl_s[tid][0] = a.p.vcent[tid & 7];
-      vl_s[tid][1] = a.p.vcent[tid >> 3];
-    }
-  } else {
-    vl_s[tid & 255][0] = a.p.vcent[tid & 15];
-    vl_s[tid & 255][1] = a.p.vcent[(tid >> 4) & 15];
+  // value pair table: field f of two channels' codes -> their two centroids
+  if (tid < (1 << (2 * VB))) {
+    vl_s[tid][0] = a.p.vcent[tid & ((1 << VB) - 1)];
+    vl_s[tid][1] = a.p.vcent[tid >> VB];
   }
 
   float m_run[GQ], l_run[GQ], acc0[GQ], acc1[GQ];
@@ -238,16 +237,12 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
       const int tend = min(G, tq * 64 + 64);
       for (int tt = tq * 64; tt < tend; ++tt) {
         const size_t row = page_row(bt, d.max_pages_per_seq, b, g * G + tt, P, d.n_pages, h);
-        uint32_t f;
-        if (VB == 3) {
-          const uint32_t* vr = reinterpret_cast<const uint32_t*>(a.p.vcodes + row * VROW);
-          const int bit = 6 * jp, wd = bit >> 5, sh = bit & 31;
-          const uint32_t lo = vr[wd];
-          const uint32_t hi = (sh > 26) ? vr[wd + 1] : 0u;
-          f = (uint32_t)(((((uint64_t)hi) << 32) | lo) >> sh) & 63u;
-        } else {
-          f = a.p.vcodes[row * VROW + jp];
-        }
+        // the 2*VB-bit field of channels 2jp, 2jp + 1 in the token's bit stream
+        const uint32_t* vr = reinterpret_cast<const uint32_t*>(a.p.vcodes + row * VROW);
+        const int bit = 2 * VB * jp, wd = bit >> 5, sh = bit & 31;
+        const uint32_t lo = vr[wd];
+        const uint32_t hi = (sh + 2 * VB > 32) ? vr[wd + 1] : 0u;
+        const uint32_t f = (uint32_t)(((((uint64_t)hi) << 32) | lo) >> sh) & ((1u << (2 * VB)) - 1u);
         const float c0 = vl_s[f][0], c1 = vl_s[f][1];
 #pragma unroll
         for (int i = 0; i < GQ; ++i) {
@@ -313,15 +308,15 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
   }
   __syncthreads();
   const int ns = a.n_cold_splits + a.n_hot_splits;
-  for (int x = tid; x < GQ * D; x += kThreads) {
+  for (int x = tid; x < gq * D; x += kThreads) {
     const int i = x / D, j = x % D;
     const float s4 = (accr_s[0][i][j] + accr_s[1][i][j]) + (accr_s[2][i][j] + accr_s[3][i][j]);
-    a.pacc[(((size_t)b * Hq + h * GQ + i) * ns + split) * D + j] = s4;
+    a.pacc[(((size_t)b * Hq + h * gq + i) * ns + split) * D + j] = s4;
   }
 #pragma unroll
   for (int i = 0; i < GQ; ++i) {
-    if (tid == i) {
-      const size_t o = ((size_t)b * Hq + h * GQ + i) * ns + split;
+    if (tid == i && i < gq) {
+      const size_t o = ((size_t)b * Hq + h * gq + i) * ns + split;
       a.pm[o] = m_run[i];
       a.pl[o] = l_run[i];
     }
@@ -383,10 +378,18 @@ constexpr int kLutEntry = 256;   // bytes per table entry
 
 // Code tables in LDS.  Every entry holds one 8-byte {hi pair, lo pair} copy
 // per lane of an LDS pass so that random lookups never share a bank:
+//   2-bit values: value table [16 entries x 32 copies] at 0, key table
+//                 [256 entries x 32 copies] after it (68 KiB);
 //   3-bit values: value table [64 entries x 32 copies] at 0, key table
 //                 [256 entries x 32 copies] at kKeyBase3 (80 KiB);
 //   4-bit values: 256 entries x (16 key copies | 16 value copies) (64 KiB).
 template <int VB> struct LutGeom;
+template <> struct LutGeom<2> {
+  static constexpr int kBytes = 16 * 256 + 256 * 256;
+  static constexpr uint32_t kKeyBase = 16 * 256;
+  static constexpr int kCopies = 32;
+  static constexpr uint32_t kValOff = 0;  // value entry e at e*256 + copy*8
+};
 template <> struct LutGeom<3> {
   static constexpr int kBytes = 64 * 256 + 256 * 256;
   static constexpr uint32_t kKeyBase = 64 * 256;
@@ -600,36 +603,34 @@ __device__ __forceinline__ float row_bcast(float x) {
   return bitsf((uint32_t)__builtin_amdgcn_update_dpp(0, (int)fbits(x), 0x150 + I, 0xF, 0xF, false));
 }
 
-// (row_newbcast reads a valid lane for every lane, so no "old" value is needed)
-template <int I>
-__device__ __forceinline__ uint32_t row_bcast_u(uint32_t x) {
-  return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x150 + I, 0xF, 0xF, false);
-}
-// d of lane L of this lane's 16-lane row if byte I of tw equals row, else 0:
-// a byte-select (SDWA) compare, then a select whose data operand is read
-// from lane L by DPP; the s_nop covers the VALU write of VCC before its use
-// as a lane mask.
-template <int L, int I>
-__device__ __forceinline__ uint32_t row_select(uint32_t tw, uint32_t row, uint32_t d, uint32_t zero) {
-  uint32_t out;
-  asm("v_cmp_ne_u32_sdwa vcc, %1, %2 src0_sel:BYTE_%5 src1_sel:DWORD\n\t"
-      "s_nop 1\n\t"
-      "v_cndmask_b32_dpp %0, %3, %4, vcc row_newbcast:%6 row_mask:0xf bank_mask:0xf"
-      : "=v"(out)
-      : "v"(tw), "v"(row), "v"(d), "v"(zero), "i"(I), "i"(L)
-      : "vcc");
-  return out;
+// Outlier A operand of one tile row: dword i = dq[i] when byte i of tw
+// (the token of slot i) equals row, else 0.  Four byte compares into four
+// SGPR pairs, then four selects, each four instructions after its compare:
+// independent operations with no dependency chain through VCC and no DPP.
+__device__ __forceinline__ void onehot_operand(uint32_t tw, uint32_t row, const uint4& dq,
+                                               uint32_t (&o)[4]) {
+  uint64_t m0, m1, m2, m3;
+  asm("v_cmp_eq_u32_sdwa %4, %8, %9 src0_sel:BYTE_0 src1_sel:DWORD\n\t"
+      "v_cmp_eq_u32_sdwa %5, %8, %9 src0_sel:BYTE_1 src1_sel:DWORD\n\t"
+      "v_cmp_eq_u32_sdwa %6, %8, %9 src0_sel:BYTE_2 src1_sel:DWORD\n\t"
+      "v_cmp_eq_u32_sdwa %7, %8, %9 src0_sel:BYTE_3 src1_sel:DWORD\n\t"
+      "v_cndmask_b32_e64 %0, 0, %10, %4\n\t"
+      "v_cndmask_b32_e64 %1, 0, %11, %5\n\t"
+      "v_cndmask_b32_e64 %2, 0, %12, %6\n\t"
+      "v_cndmask_b32_e64 %3, 0, %13, %7"
+      : "=&v"(o[0]), "=&v"(o[1]), "=&v"(o[2]), "=&v"(o[3]), "=&s"(m0), "=&s"(m1), "=&s"(m2),
+        "=&s"(m3)
+      : "v"(tw), "v"(row), "v"(dq.x), "v"(dq.y), "v"(dq.z), "v"(dq.w));
 }
 template <int K>
 struct IntC {
   static constexpr int value = K;
 };
 
-// Outlier entries of one block as this lane holds them (two entries): fp16
-// {hi, lo} of (val - mean) * s / 2 (their tokens are staged in LDS), plus the
-// block's entry count (<= 128 per pass) and how many fall in tile A.
+// Outlier entries of one block as staged for the apply: the block's entry
+// count (<= 128 per pass) and how many fall in tile A (the tokens, operand
+// values and q pairs are in LDS).
 struct OutEntries {
-  uint32_t d0, d1;
   int cnt, nA;
 };
 
@@ -731,9 +732,11 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   // outlier correction B operand of the block computed next: per head, each
   // entry's raw fp16 q twice (rows 4 banks apart)
   __shared__ __align__(16) uint32_t oq_s[kMWaves][GQ][132];
-  // ... and each entry's token in the block (255 = none): byte 4k + i of row
+  // ... each entry's token in the block (255 = none): byte 4k + i of row
   // lg is slot i of lane group lg in 16-entry chunk k
   __shared__ __align__(16) uint8_t otb_s[kMWaves][4][32];
+  // ... and each entry's A-operand value, fp16 {hi, lo} of (val - mean) * s / 2
+  __shared__ __align__(16) uint32_t od_s[kMWaves][128];
   // NF4 levels [0, 16) and value centroids [16, 16 + 2^vb), for the table fill
   __shared__ float lvl_s[32];
   if (tid < 16) lvl_s[tid] = key_level(a.d.key_grid, tid);
@@ -764,8 +767,11 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     }
   }
 
+  // GQ is the kernel's power-of-two head count; the last GQ - gq heads are
+  // zero-query padding (their columns score 0) whose states are never written
+  const int gq = Hq / Hkv;
   for (int i = tid; i < GQ * D; i += kMThreads) {
-    const uint32_t qr = a.q[((size_t)b * Hq + h * GQ + i / D) * D + i % D];
+    const uint32_t qr = (i / D < gq) ? a.q[((size_t)b * Hq + h * gq + i / D) * D + i % D] : 0u;
     qq_s[i % D][i / D] = qr | (qr << 16);
     qf_s[i / D][i % D] = (uint16_t)qr;
     q_h_s[i / D][i % D] = h2f((uint16_t)qr) * qscale;
@@ -854,7 +860,12 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         cb.kA = make_uint4(x.x, x.y, x.z, x.w);
         cb.kB = make_uint4(y.x, y.y, y.z, y.w);
       }
-      if constexpr (VB == 3) {
+      if constexpr (VB == 2) {
+        const u32x2_t x = __builtin_amdgcn_raw_buffer_load_b64(rv, (int)uoffL, (int)(rowA * VROW), 0);
+        const u32x2_t y = __builtin_amdgcn_raw_buffer_load_b64(rv, (int)uoffL, (int)(rowB * VROW), 0);
+        cb.uA = make_uint4(x.x, x.y, 0u, 0u);
+        cb.uB = make_uint4(y.x, y.y, 0u, 0u);
+      } else if constexpr (VB == 3) {
         const u32x3_t x = __builtin_amdgcn_raw_buffer_load_b96(rv, (int)uoffL, (int)(rowA * VROW), 0);
         const u32x3_t y = __builtin_amdgcn_raw_buffer_load_b96(rv, (int)uoffL, (int)(rowB * VROW), 0);
         cb.uA = make_uint4(x.x, x.y, x.z, 0u);
@@ -957,7 +968,12 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       // lo t1, hi t2, hi t3, lo t2, lo t3], matching the weight quad.
       auto val_quad = [&](const uint4& un, int nt) {
         uint32_t f0, f1;
-        if constexpr (VB == 3) {
+        if constexpr (VB == 2) {
+          // 4-bit fields 2nt, 2nt + 1 at bits 8nt, 8nt + 4 of the 64-bit unit
+          const uint32_t word = nt < 4 ? un.x : un.y;
+          f0 = (word >> (8 * (nt & 3))) & 15u;
+          f1 = (word >> (8 * (nt & 3) + 4)) & 15u;
+        } else if constexpr (VB == 3) {
           switch (nt) {
 #define TQK_V3(NT) case NT: f0 = v3_field<2 * NT>(un); f1 = v3_field<2 * NT + 1>(un); break;
             TQK_V3(0) TQK_V3(1) TQK_V3(2) TQK_V3(3) TQK_V3(4) TQK_V3(5) TQK_V3(6) TQK_V3(7)
@@ -1019,45 +1035,41 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         for (int hh = 0; hh < GQ; ++hh)
           *reinterpret_cast<uint2*>(&oq_s[w][hh][eidx]) = make_uint2(qv[0][hh], qv[1][hh]);
         *reinterpret_cast<uint16_t*>(&otb_s[w][lg][4 * (c >> 1) + 2 * (c & 1)]) = (uint16_t)(tv[0] | (tv[1] << 8));
+        *reinterpret_cast<uint2*>(&od_s[w][eidx]) = make_uint2(dv[0], dv[1]);
         OutEntries oe;
-        oe.d0 = dv[0];
-        oe.d1 = dv[1];
         oe.cnt = cnt;
         // token-sorted: the entries of tile A (tokens 0..15) come first
         oe.nA = (int)__popcll(__ballot(tv[0] < 16u)) + (int)__popcll(__ballot(tv[1] < 16u));
         return oe;
       };
       // Apply a staged pass: one MFMA per touched tile and 16-entry chunk k
-      // (lane group lg: entries 16k + 4lg + i, i < 4, held by lanes 2k, 2k + 1
-      // of its row).  Every chunk's q operand is read up front.
+      // (lane group lg: entries 16k + 4lg + i, i < 4).  The operands of every
+      // chunk the pass holds are read up front.
       auto apply_entries = [&](const OutEntries& oe, floatx4_t& CA, floatx4_t& CB) {
         // wave-uniform counts, so the chunk tests below are plain scalar branches
         const int cnt = __builtin_amdgcn_readfirstlane(oe.cnt);
         const int nA = __builtin_amdgcn_readfirstlane(oe.nA);
-        const uint32_t zero = 0u;
         // tokens of every chunk's four slots of this lane group (dword k = chunk k)
         const uint4 tw03 = *reinterpret_cast<const uint4*>(&otb_s[w][lg][0]);
         const uint4 tw47 = *reinterpret_cast<const uint4*>(&otb_s[w][lg][16]);
-        uint4 qb[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) qb[k] = *reinterpret_cast<const uint4*>(&oq_s[w][hq][16 * k + 4 * lg]);
         auto chunk = [&](auto kc) {
           constexpr int k = decltype(kc)::value;
           if (16 * k >= cnt) return;
+          uint4 dq[8];
+          dq[k] = *reinterpret_cast<const uint4*>(&od_s[w][16 * k + 4 * lg]);
           const uint32_t tw = k < 4 ? u4_word<k & 3>(tw03) : u4_word<k & 3>(tw47);
-          // slot i: entry u = i & 1 of lane 2k + (i >> 1)
-          auto masked = [&](uint32_t row) {
-            H8 o;
-            o.u[0] = row_select<2 * k, 0>(tw, row, oe.d0, zero);
-            o.u[1] = row_select<2 * k, 1>(tw, row, oe.d1, zero);
-            o.u[2] = row_select<2 * k + 1, 2>(tw, row, oe.d0, zero);
-            o.u[3] = row_select<2 * k + 1, 3>(tw, row, oe.d1, zero);
-            return o;
-          };
           H8 qv;
-          qv.v = qb[k];
-          if (16 * k < nA) CA = __builtin_amdgcn_mfma_f32_16x16x32_f16(masked((uint32_t)c).h, qv.h, CA, 0, 0, 0);
-          if (16 * k + 16 > nA) CB = __builtin_amdgcn_mfma_f32_16x16x32_f16(masked((uint32_t)(16 + c)).h, qv.h, CB, 0, 0, 0);
+          qv.v = *reinterpret_cast<const uint4*>(&oq_s[w][hq][16 * k + 4 * lg]);
+          if (16 * k < nA) {
+            H8 o;
+            onehot_operand(tw, (uint32_t)c, dq[k], o.u);
+            CA = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.h, qv.h, CA, 0, 0, 0);
+          }
+          if (16 * k + 16 > nA) {
+            H8 o;
+            onehot_operand(tw, (uint32_t)(16 + c), dq[k], o.u);
+            CB = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.h, qv.h, CB, 0, 0, 0);
+          }
         };
         chunk(IntC<0>{});
         chunk(IntC<1>{});
@@ -1070,10 +1082,11 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       };
 
       // Software pipeline over a wave's blocks.  Step i starts with the QK^T
-      // accumulators of block i (computed at the end of step i - 1) and the
-      // entries of block i (staged in step i - 1): it adds the outliers, runs
-      // the softmax, then interleaves block i's PV with block i + 1's QK^T so
-      // that the table reads of one overlap the MFMAs of the other.
+      // accumulators of block i, outliers included (computed at the end of
+      // step i - 1): it stages block i + 1's outlier entries, runs block i's
+      // softmax, interleaves block i's PV with block i + 1's QK^T so that the
+      // table reads of one overlap the MFMAs of the other, and adds block
+      // i + 1's outlier corrections.
       OutEntries pend;          // staged outlier entries of the block computed next
       floatx4_t CAn, CBn;       // QK^T (with the bias) of the block computed next
       auto key_tile = [&](const uint4& k, H8 (&x)[8]) {
@@ -1093,18 +1106,18 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
 #pragma unroll
         for (int nt = 0; nt < 8; ++nt) st.O[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pw.h, v[nt].h, st.O[nt], 0, 0, 0);
       };
-      auto process = [&](const ColdBlock<VB>& cur, int blk, const ColdBlock<VB>& nx1, int blk1,
-                         int gslot, int gslot1) {
-        const int e0 = cur.e0, ne = cur.ne;
-        floatx4_t CA = CAn, CB = CBn;
+      // Outlier corrections of block blk (its first pass staged in pend) into
+      // that block's QK^T accumulators; passes beyond the first 128 entries
+      // (rare) read the side-list here and drain, so the common path keeps
+      // exact wait counts.  Applied right after the block's QK^T, a step
+      // before its scores are read, so the MFMA chain's latency is hidden.
+      auto apply_block = [&](const ColdBlock<VB>& cb, int blk, int gslot, floatx4_t& CA, floatx4_t& CB) {
         apply_entries(pend, CA, CB);
-        if (ne > 128) {
-          // rare (> 128 entries in one block): read each further chunk and
-          // drain here, so the common path keeps exact wait counts
-          const uint32_t* __restrict__ oent = oent_all + (size_t)cur.obase * cap;
-          for (int base = 128; base < ne; base += 128) {
-            const int cnt = min(128, ne - base);
-            const int i0 = e0 + base + eidx;
+        if (cb.ne > 128) {
+          const uint32_t* __restrict__ oent = oent_all + (size_t)cb.obase * cap;
+          for (int base = 128; base < cb.ne; base += 128) {
+            const int cnt = min(128, cb.ne - base);
+            const int i0 = cb.e0 + base + eidx;
             const uint32_t x0 = oent[min(i0, capm1)], x1 = oent[min(i0 + 1, capm1)];
             __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
             wave_sync();
@@ -1113,8 +1126,10 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
             apply_entries(ex, CA, CB);
           }
         }
-        // next block's entries: the staging buffer's reads above come first in
-        // the wave's (in-order) LDS stream
+      };
+      auto process = [&](const ColdBlock<VB>& cur, const ColdBlock<VB>& nx1, int blk1, int gslot1) {
+        const floatx4_t CA = CAn, CB = CBn;
+        // next block's entries (this block's were applied in the previous step)
         wave_sync();
         pend = stage_entries(nx1.ent, min(128, nx1.ne), blk1, gslot1);
         float sc[8];
@@ -1140,6 +1155,8 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         key_tile(nx1.kB, xb);
         pv_tile(pb, vb);
         qk_tile(xb, CBn);
+        wave_sync();
+        apply_block(nx1, blk1, gslot1, CAn, CBn);
       };
 
     // A ring of kColdBuf buffers, kColdBuf - 1 blocks in flight: step i
@@ -1152,7 +1169,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       const bool last = kbp + 1 == nblk;  // block i + 1 starts wave group jp + 1
       if (last) begin_group(jp + 1);     // weights for the QK^T of block i + 1
       load_next(nxt);
-      process(cur, kbp, nx1, last ? 0 : kbp + 1, jp & 1, last ? (jp + 1) & 1 : jp & 1);
+      process(cur, nx1, last ? 0 : kbp + 1, last ? (jp + 1) & 1 : jp & 1);
       if (++kbp == nblk) {
         kbp = 0;
         ++jp;
@@ -1177,6 +1194,8 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         key_tile(ring[0].kB, x);
         qk_tile(x, CBn);
       }
+      wave_sync();
+      apply_block(ring[0], 0, 0, CAn, CBn);
       for (int i = 0; i < T; i += kColdBuf) {
 #pragma unroll
         for (int s = 0; s < kColdBuf; ++s) {
@@ -1307,6 +1326,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   for (int x = tid; x < 2 * GQ * D; x += kMThreads) {
     const int hot = x >= GQ * D;
     const int i = (x % (GQ * D)) / D, j = x % D;
+    if (i >= gq) continue;
     const float* mp = hot ? hm + i : cm + i;
     const float* lp = hot ? hm + D + i : cl + i;
     const float* op = hot ? hco + i * D + j : co + i * D + j;
@@ -1327,7 +1347,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         }
       }
     }
-    const size_t o = ((size_t)b * Hq + h * GQ + i) * ns + (hot ? a.n_cold_splits : 0) + split;
+    const size_t o = ((size_t)b * Hq + h * gq + i) * ns + (hot ? a.n_cold_splits : 0) + split;
     st_agent(a.pacc + o * D + j, acc);
     if (j == 0) {
       st_agent(a.pm + o, M * 0.6931471805599453f);  // back to the natural-log domain of the partials
@@ -1393,10 +1413,10 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
 #pragma unroll
       for (int r = 0; r < NH; ++r) {
         const int qi = u + 4 * r;
-        const size_t base = ((size_t)b * Hq + h * GQ + qi) * ns;
+        const size_t base = ((size_t)b * Hq + h * gq + qi) * ns;
 #pragma unroll
         for (int s = 0; s < kMergeFast; ++s) {
-          const bool ok = qi < GQ && s < ns;
+          const bool ok = qi < gq && s < ns;
           vl[r][s] = ok ? ld_agent(a.pl + base + s) : 0.f;
           vm[r][s] = ok ? ld_agent(a.pm + base + s) : -INFINITY;
           va[r][s] = ok ? ld_agent(a.pacc + (base + s) * D + j) : 0.f;
@@ -1417,12 +1437,12 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     if (fast) {
 #pragma unroll
       for (int r = 0; r < NH; ++r)
-        if (u + 4 * r < GQ) combine(r, u + 4 * r, vl[r], vm[r], va[r]);
+        if (u + 4 * r < gq) combine(r, u + 4 * r, vl[r], vm[r], va[r]);
     } else {
       for (int r = 0; r < NH; ++r) {
         const int qi = u + 4 * r;
-        if (qi < GQ) {
-          const size_t base = ((size_t)b * Hq + h * GQ + qi) * ns;
+        if (qi < gq) {
+          const size_t base = ((size_t)b * Hq + h * gq + qi) * ns;
           float M, dn, cr, hh;
           merge_chunked([](const float* p) { return ld_agent(p); }, a.pl, a.pm, a.pacc, base, ns,
                         a.n_cold_splits, j, M, dn, cr, hh);
@@ -1436,11 +1456,11 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
 #pragma unroll
     for (int r = 0; r < NH; ++r) {
       const int qi = u + 4 * r;
-      if (qi < GQ) {
+      if (qi < gq) {
         float o = hr[r];
 #pragma unroll 8
         for (int k = 0; k < D; ++k) o += q_h_s[qi][k] * pi_s[k * D + j];
-        a.out[((size_t)b * Hq + h * GQ + qi) * D + j] = o / den[r];
+        a.out[((size_t)b * Hq + h * gq + qi) * D + j] = o / den[r];
       }
     }
   }
@@ -1656,7 +1676,9 @@ Plan make_plan(const tqk_cache_desc* d, int batch, int max_len) {
 template <int GQ>
 hipError_t launch_split(const DecodeArgs& a, dim3 grid, hipStream_t st) {
   if (!mfma_path(a.d)) {
-    if (a.d.value_bits == 3)
+    if (a.d.value_bits == 2)
+      hipLaunchKernelGGL((tqk_decode_split_valu<GQ, 2>), grid, dim3(kThreads), 0, st, a);
+    else if (a.d.value_bits == 3)
       hipLaunchKernelGGL((tqk_decode_split_valu<GQ, 3>), grid, dim3(kThreads), 0, st, a);
     else
       hipLaunchKernelGGL((tqk_decode_split_valu<GQ, 4>), grid, dim3(kThreads), 0, st, a);
@@ -1664,7 +1686,9 @@ hipError_t launch_split(const DecodeArgs& a, dim3 grid, hipStream_t st) {
   }
   // one-dimensional over (split, kv head, seq) items
   const dim3 g1(grid.x * grid.y * grid.z);
-  if (a.d.value_bits == 3)
+  if (a.d.value_bits == 2)
+    hipLaunchKernelGGL((tqk_decode_split_mfma<GQ, 2>), g1, dim3(kMThreads), 0, st, a);
+  else if (a.d.value_bits == 3)
     hipLaunchKernelGGL((tqk_decode_split_mfma<GQ, 3>), g1, dim3(kMThreads), 0, st, a);
   else
     hipLaunchKernelGGL((tqk_decode_split_mfma<GQ, 4>), g1, dim3(kMThreads), 0, st, a);
@@ -1721,11 +1745,13 @@ int launch_splits(const tqk_cache_desc* d, const tqk_cache_ptrs* p, const Plan& 
   const dim3 grid(mfma_path(*d) ? pl.n_cold_splits : pl.n_cold_splits + pl.n_hot_splits,
                   d->n_kv_heads, batch);
   hipError_t e;
+  // kernels exist for 1, 2, 4 and 8 query heads per kv head; other counts
+  // run on the next larger one with zero-query padding heads
   switch (d->n_q_heads / d->n_kv_heads) {
     case 1: e = launch_split<1>(a, grid, st); break;
     case 2: e = launch_split<2>(a, grid, st); break;
-    case 4: e = launch_split<4>(a, grid, st); break;
-    case 8: e = launch_split<8>(a, grid, st); break;
+    case 3: case 4: e = launch_split<4>(a, grid, st); break;
+    case 5: case 6: case 7: case 8: e = launch_split<8>(a, grid, st); break;
     default: return TQK_EUNSUPPORTED;
   }
   return e == hipSuccess ? TQK_OK : TQK_EHIP;
@@ -1820,17 +1846,19 @@ int noalloc_scratch(hipStream_t stream, void** out) {
 
 extern "C" {
 
-int tqk_version(void) { return 5; }
+int tqk_version(void) { return 6; }
 
 int tqk_check_desc(const tqk_cache_desc* d) {
   if (!d) return TQK_EINVAL;
   if (d->head_dim != TQK_D) return TQK_EUNSUPPORTED;
   if (d->key_bits != 4) return TQK_EUNSUPPORTED;
   if (d->key_grid != 0 && d->key_grid != 1) return TQK_EINVAL;
-  if (d->value_bits != 3 && d->value_bits != 4) return TQK_EUNSUPPORTED;
+  if (d->value_bits < 2 || d->value_bits > 4) return TQK_EUNSUPPORTED;
+  if (d->zero_point < 0 || d->zero_point > 2 || (d->zero_point != 0 && d->key_grid != 0))
+    return TQK_EINVAL;
   if (d->n_kv_heads <= 0 || d->n_q_heads <= 0 || d->n_q_heads % d->n_kv_heads) return TQK_EINVAL;
   const int gq = d->n_q_heads / d->n_kv_heads;
-  if (gq != 1 && gq != 2 && gq != 4 && gq != 8) return TQK_EUNSUPPORTED;
+  if (gq < 1 || gq > 8) return TQK_EUNSUPPORTED;
   if (d->hot_window < 1) return TQK_EINVAL;
   if (d->group_tokens != (d->hot_window + 1) / 2) return TQK_EINVAL;
   if (d->group_tokens < 1 || d->group_tokens > TQK_MAX_G) return TQK_EUNSUPPORTED;

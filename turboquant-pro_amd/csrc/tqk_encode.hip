@@ -4,8 +4,9 @@
 // uses explicitly rounded __f*_rn operations): every code, scale, mean, norm
 // and outlier entry equals what the reference's NumPy encoder produces for the
 // same fp16 inputs.  NumPy's operation order is restated exactly:
-//   keys   (turboquant_pro/per_channel_kv.py:269-401, nf4_asym "calibrated")
-//     mean  = token-order sequential fp32 sum / G
+//   keys   (turboquant_pro/per_channel_kv.py:269-401, nf4_asym)
+//     mean  = token-order sequential fp32 sum / G ("calibrated"; "sparse"
+//             multiplies it by the DC-channel mask, "bias" takes it given)
 //     amax  = max(max_s |x_s - mean|, 1e-8)            (NaN propagates)
 //     cent  = mean + amax * NF4[l]
 //     code  = first argmin_l |x - cent_l|               (NaN counts as minimal)
@@ -98,10 +99,20 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
     a.p.gmean[mbase + j] = mn;
   } else if (tid < D) {
     const int j = tid;
-    float acc = 0.0f;
-    for (int s = 0; s < G; ++s) acc = __fadd_rn(acc, h2f(kt_s[s][j]));
-    // np.mean divides the fp32 sum by an intp count: a float64 division, then fp32
-    const float mu = (float)((double)acc / (double)G);
+    // the zero point (turboquant_pro/per_channel_kv.py:327-345)
+    float mu;
+    if (d.zero_point == 2) {
+      // "bias": the RoPE-averaged k_proj bias of the group's positions
+      mu = a.p.zp_mean[((size_t)g * Hkv + h) * D + j];
+    } else {
+      float acc = 0.0f;
+      for (int s = 0; s < G; ++s) acc = __fadd_rn(acc, h2f(kt_s[s][j]));
+      // np.mean divides the fp32 sum by an intp count: a float64 division, then fp32
+      mu = (float)((double)acc / (double)G);
+      // "sparse": the mean times the DC-channel mask (a float product, so a
+      // non-DC channel gets a signed zero, or NaN from a NaN mean)
+      if (d.zero_point == 1) mu = __fmul_rn(mu, ((d.dc_mask[j >> 5] >> (j & 31)) & 1u) ? 1.0f : 0.0f);
+    }
     float amax = 0.0f;
     bool nan = (mu != mu);
     for (int s = 0; s < G; ++s) {
@@ -501,8 +512,11 @@ int tqk_encode_groups(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t 
   a.chunk_tokens = chunk_tokens;
   a.overflow = overflow;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (d->key_grid == 0 && d->zero_point == 2 && !p->zp_mean) return TQK_EINVAL;
   const dim3 grid(n_items, d->n_kv_heads);
-  if (d->value_bits == 3)
+  if (d->value_bits == 2)
+    hipLaunchKernelGGL(tqk_encode_group<2>, grid, dim3(kEncThreads), 0, st, a);
+  else if (d->value_bits == 3)
     hipLaunchKernelGGL(tqk_encode_group<3>, grid, dim3(kEncThreads), 0, st, a);
   else
     hipLaunchKernelGGL(tqk_encode_group<4>, grid, dim3(kEncThreads), 0, st, a);
@@ -547,7 +561,9 @@ int tqk_dequant_groups(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t
   a.vout = vout;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid(n_items, d->n_kv_heads);
-  if (d->value_bits == 3)
+  if (d->value_bits == 2)
+    hipLaunchKernelGGL(tqk_dequant_group<2>, grid, dim3(kThreads), 0, st, a);
+  else if (d->value_bits == 3)
     hipLaunchKernelGGL(tqk_dequant_group<3>, grid, dim3(kThreads), 0, st, a);
   else
     hipLaunchKernelGGL(tqk_dequant_group<4>, grid, dim3(kThreads), 0, st, a);

@@ -2,8 +2,8 @@
 
 Each ``csrc/*.hip`` translation unit is compiled for gfx950 only and linked
 into one shared library that exports the C ABI declared in ``include/tqk.h``.
-The encode unit is built with ``-ffp-contract=off`` and correctly rounded
-division/sqrt: its results must match NumPy bit for bit.
+The encode and block units are built with ``-ffp-contract=off`` and correctly
+rounded division/sqrt: their results must match NumPy bit for bit.
 """
 
 from __future__ import annotations
@@ -28,6 +28,7 @@ COMMON = [
 ]
 PER_UNIT = {
     "tqk_encode.hip": ["-ffp-contract=off"],
+    "tqk_block.hip": ["-ffp-contract=off"],
     "tqk_decode.hip": [],
 }
 
@@ -44,14 +45,18 @@ def build(verbose: bool = False) -> str:
     os.makedirs(LIB_DIR, exist_ok=True)
     objs = []
     cc = hipcc()
+    procs = []
     for unit, extra in PER_UNIT.items():
         src = os.path.join(CSRC, unit)
         obj = os.path.join(LIB_DIR, unit.replace(".hip", ".o"))
         cmd = [cc, *COMMON, *extra, "-c", src, "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)
-        subprocess.run(cmd, check=True)
+        procs.append((cmd, subprocess.Popen(cmd)))
         objs.append(obj)
+    for cmd, p in procs:  # the units compile side by side
+        if p.wait() != 0:
+            raise subprocess.CalledProcessError(p.returncode, cmd)
     tmp = LIB_PATH + ".tmp"
     cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     if verbose:

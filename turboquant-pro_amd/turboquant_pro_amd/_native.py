@@ -19,13 +19,14 @@ TQK_EUNSUPPORTED = 2
 TQK_EHIP = 3
 TQK_EWORKSPACE = 4
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # Every symbol include/tqk.h declares (checked by the CPU test suite).
 EXPORTS = (
     "tqk_version", "tqk_check_desc", "tqk_decode_workspace_bytes", "tqk_decode",
     "tqk_decode_noalloc", "tqk_decode_partials", "tqk_decode_splits", "tqk_decode_merge", "tqk_encode_groups",
-    "tqk_append_hot", "tqk_dequant_groups",
+    "tqk_append_hot", "tqk_dequant_groups", "tqk_encode_key_block", "tqk_encode_value_block",
+    "tqk_dequant_key_block", "tqk_dequant_value_block",
 )
 
 
@@ -34,13 +35,21 @@ class CacheDesc(ctypes.Structure):
         "n_kv_heads", "n_q_heads", "head_dim", "hot_window", "group_tokens", "page_tokens",
         "key_bits", "value_bits", "outliers_per_channel", "outlier_cap",
         "max_pages_per_seq", "max_groups_per_seq", "hot_ring", "n_pages")] + [
-        ("sm_scale", ctypes.c_float), ("key_grid", ctypes.c_int32)]
+        ("sm_scale", ctypes.c_float), ("key_grid", ctypes.c_int32), ("zero_point", ctypes.c_int32),
+        ("dc_mask", ctypes.c_uint32 * 4)]
 
 
 class CachePtrs(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in (
         "kcodes", "vcodes", "vnorm", "gscale", "gmean", "ocount", "oent", "hot_k", "hot_v",
-        "block_table", "group_table", "pi", "pi_t", "vcent", "vbnd")]
+        "block_table", "group_table", "pi", "pi_t", "vcent", "vbnd", "zp_mean")]
+
+
+class BlockDesc(ctypes.Structure):
+    """``tqk_block_desc``: one (B, H, S, D) block for the stateless quantizers."""
+    _fields_ = [(n, ctypes.c_int32) for n in (
+        "batch", "n_heads", "tokens", "head_dim", "bits", "key_grid", "zero_point",
+        "outliers_per_channel", "outlier_cap", "input_f32")] + [("dc_mask", ctypes.c_uint32 * 4)]
 
 
 _lib = None
@@ -51,7 +60,7 @@ def load(path: str) -> ctypes.CDLL:
     signature declared (pointer arguments stay 64-bit) and its ABI checked."""
     l_ = ctypes.CDLL(path)
     vp, i32, sz = ctypes.c_void_p, ctypes.c_int32, ctypes.c_size_t
-    pd, pp = ctypes.POINTER(CacheDesc), ctypes.POINTER(CachePtrs)
+    pd, pp, pb = ctypes.POINTER(CacheDesc), ctypes.POINTER(CachePtrs), ctypes.POINTER(BlockDesc)
     sig = {
         "tqk_version": ([], ctypes.c_int),
         "tqk_check_desc": ([pd], ctypes.c_int),
@@ -64,6 +73,10 @@ def load(path: str) -> ctypes.CDLL:
         "tqk_encode_groups": ([pd, pp, i32, i32, vp, vp, vp, vp, i32, vp, vp], ctypes.c_int),
         "tqk_append_hot": ([pd, pp, i32, vp, vp, vp, vp, vp, i32, vp], ctypes.c_int),
         "tqk_dequant_groups": ([pd, pp, i32, vp, vp, vp, vp], ctypes.c_int),
+        "tqk_encode_key_block": ([pb, vp, vp, vp, vp, vp, vp, vp, vp, vp], ctypes.c_int),
+        "tqk_encode_value_block": ([pb, vp, vp, vp, vp, vp, vp], ctypes.c_int),
+        "tqk_dequant_key_block": ([pb, vp, vp, vp, i32, vp, vp, vp, vp], ctypes.c_int),
+        "tqk_dequant_value_block": ([pb, vp, vp, vp, vp, vp, vp], ctypes.c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(l_, name)

@@ -132,10 +132,11 @@ class AutoConfig:
                     robust: bool = True, outlier_frac: float = 0.02, k_bias=None, *,
                     n_q_heads: int | None = None, capacity: int = 4096):
         """The GPU cache with this config's K/V bits (turboquant_pro/autoconfig.py:439-486):
-        asym-NF4 keys + ``outlier_frac`` fp16 outliers.  ``n_q_heads`` (default:
+        asym-NF4 keys with the resolved zero point (``bias`` needs this layer's
+        ``k_bias``) + ``outlier_frac`` fp16 outliers.  ``n_q_heads`` (default:
         one query per kv-head, as the reference's cache) serves GQA queries.
-        ``robust=False`` (uniform keys) and the ``bias``/``sparse`` zero points
-        raise ``NotImplementedError``: they have no gfx950 form."""
+        ``robust=False`` (uniform keys) builds 4-bit uniform keys and raises
+        ``NotImplementedError`` at other key widths: they have no gfx950 form."""
         from .core import TurboQuantKVCache
         zp = self.resolve_key_zero_point(k_bias is not None) if robust else "calibrated"
         return TurboQuantKVCache(

@@ -1,5 +1,6 @@
-"""Host-side constants of the codecs: PolarQuant value codebooks and the
-seeded random rotation.  Computed once per cache on the host (NumPy) and
+"""Host-side constants of the codecs: PolarQuant value codebooks, the seeded
+random rotation, and the config-derived key zero points (RoPE-averaged k_proj
+bias, DC-channel mask).  Computed once per cache on the host (NumPy) and
 uploaded; every per-token operation runs in the gfx950 kernels.
 
 The tables and their fp32 rounding have to be identical to the reference's for
@@ -61,3 +62,44 @@ def n_groups_for(length: int, hot_window: int) -> int:
     if G == 0 or length <= hot_window:
         return 0
     return (length - (hot_window + 1)) // G + 1
+
+
+# --------------------------------------------------------------------------- #
+# Zero points of asym-NF4 keys that come from the model config, not the data   #
+# (turboquant_pro/per_channel_kv.py:234-267).  Computed on the host in float64 #
+# NumPy with the reference's operation order, rounded to fp32 where it does.   #
+# --------------------------------------------------------------------------- #
+
+
+def dc_channel_mask(rope_theta: float, head_dim: int, window: int) -> np.ndarray:
+    """``(head_dim,)`` bool: channels whose rotary wavelength exceeds ``window``
+    tokens (``zero_point="sparse"`` keeps the channel mean only there)."""
+    half = head_dim // 2
+    inv = rope_theta ** (-2.0 * np.arange(half) / head_dim)
+    wl = 2.0 * np.pi / inv
+    return np.tile(wl, 2)[:head_dim] > float(window)
+
+
+def dc_mask_words(mask: np.ndarray) -> list[int]:
+    """A ``(128,)`` bool channel mask as the descriptor's four uint32 words:
+    channel j is bit j % 32 of word j // 32."""
+    m = np.asarray(mask, bool).reshape(-1)
+    return [int(sum(1 << b for b in range(32) if m[32 * w + b])) for w in range(len(m) // 32)]
+
+
+def rope_averaged_bias(k_bias: np.ndarray, rope_theta: float, head_dim: int, start: int,
+                       n: int) -> np.ndarray:
+    """``(H, head_dim)`` fp32 zero point of ``zero_point="bias"``: the k_proj
+    bias rotated by RoPE and averaged over positions ``[start, start + n)``,
+    ``b * mean(cos) + rotate_half(b) * mean(sin)``."""
+    half = head_dim // 2
+    inv = rope_theta ** (-2.0 * np.arange(half, dtype=np.float64) / head_dim)
+    pos = np.arange(start, start + n, dtype=np.float64)
+    ang = pos[:, None] * inv[None, :]
+    mc = np.cos(ang).mean(axis=0)
+    ms = np.sin(ang).mean(axis=0)
+    c_full = np.concatenate([mc, mc]).astype(np.float32)
+    s_full = np.concatenate([ms, ms]).astype(np.float32)
+    b = np.asarray(k_bias, dtype=np.float32).reshape(-1, head_dim)
+    rh = np.concatenate([-b[:, half:], b[:, :half]], axis=1)
+    return (b * c_full[None, :] + rh * s_full[None, :]).astype(np.float32)

@@ -29,7 +29,7 @@ from typing import Any
 
 import numpy as np
 
-__all__ = ["BLOB_CODEC", "BlockRecord", "payload_to_state", "payload_from_state",
+__all__ = ["BLOB_CODEC", "BlockRecord", "RawTokens", "payload_to_state", "payload_from_state",
            "rec_to_blob", "rec_from_blob", "payload_nbytes"]
 
 BLOB_CODEC = "tqp-kv-npz/1"
@@ -48,6 +48,17 @@ class BlockRecord:
     num_tokens: int
     head_dim: int
     n_heads: int
+
+
+@dataclasses.dataclass
+class RawTokens:
+    """Tokens kept as they are, fp16 ``(1, H, n, D)``: the payload of the hot
+    window's records in a pool's live-path save (``<layer>#hot<i>``), so a
+    restore gives back exactly what the pool held.  Its blob member is
+    ``k.data`` / ``v.data``; a reader without this payload type sees a record
+    its quantizer cannot decode, which the store treats as a miss."""
+
+    data: np.ndarray
 
 
 def payload_nbytes(payload: Any) -> int:

@@ -38,7 +38,7 @@ from typing import Any
 import numpy as np
 
 from .identity import IncompatibleProfile, KVIdentityProfile
-from .records import BlockRecord, payload_nbytes, rec_from_blob, rec_to_blob
+from .records import BlockRecord, RawTokens, payload_nbytes, rec_from_blob, rec_to_blob
 
 logger = logging.getLogger(__name__)
 
@@ -153,9 +153,9 @@ class TurboQuantBlockStore:
         """Store one sequence's layer K/V ``(H, L, D)`` the way a paged pool
         holds it: one record per coded group of the flush cadence
         (``<layer>#g<i>``, ``group_tokens`` tokens each, so each is exactly the
-        pool's group) and the hot tokens in records of at most 256 tokens (one
-        key group of the plugin: ``<layer>#hot<i>``).  Every record is an
-        ordinary ``tqp-kv-npz/1`` record.  Returns the groups."""
+        pool's group) and the hot window as it is, fp16 (``<layer>#hot0``, a
+        :class:`RawTokens` payload), so that a restore is the pool it came
+        from.  Every record is a ``tqp-kv-npz/1`` record.  Returns the groups."""
         from ..codebooks import n_groups_for
         k, v = self._host_f32(keys), self._host_f32(values)
         k4, v4 = self._as_bhsd(k), self._as_bhsd(v)
@@ -166,9 +166,13 @@ class TurboQuantBlockStore:
         recs = {self._group_name(layer_name, g): self.make_record(
                     k4[:, :, g * G:(g + 1) * G], v4[:, :, g * G:(g + 1) * G], packed=True)
                 for g in range(ng)}
-        for i, t0 in enumerate(range(ng * G, L, 256)):
-            recs[f"{layer_name}#hot{i}"] = self.make_record(k4[:, :, t0:t0 + 256], v4[:, :, t0:t0 + 256],
-                                                            packed=True)
+        if L > ng * G:
+            hk = np.ascontiguousarray(k4[:, :, ng * G:], dtype=np.float16)
+            hv = np.ascontiguousarray(v4[:, :, ng * G:], dtype=np.float16)
+            recs[f"{layer_name}#hot0"] = BlockRecord(
+                key_payload=RawTokens(hk), value_payload=RawTokens(hv), shape=tuple(hk.shape[1:]),
+                dtype="float16", num_tokens=int(hk.shape[2]), head_dim=int(hk.shape[3]),
+                n_heads=int(hk.shape[1]))
         with self._lock:
             for name, rec in recs.items():
                 self._records[(request_id, name)] = rec
@@ -178,44 +182,54 @@ class TurboQuantBlockStore:
     def load_into_pool(self, request_id: str, layer_name: str, pool, b: int) -> int:
         """Restore a sequence saved by :meth:`save_sequence` into sequence ``b``
         of ``pool`` (empty): the coded groups go in as codes, unchanged (no
-        dequantize / re-encode), the hot tokens as their GPU dequantization
-        (the store holds nothing uncompressed).  Returns the tokens restored,
-        0 when nothing is stored (a miss)."""
+        dequantize / re-encode), the hot window as the fp16 tokens it held.
+        Returns the tokens restored, 0 when nothing is stored (a miss).
+        Raises ``ValueError`` when the records are not in the pool's format
+        (key grid, zero point, value width, rotation, group size)."""
         import torch
 
-        from ..codebooks import random_rotation
         groups = []
         with self._lock:
             while (request_id, self._group_name(layer_name, len(groups))) in self._records:
                 groups.append(self._records[(request_id, self._group_name(layer_name, len(groups)))])
-            hot = []
-            while (request_id, f"{layer_name}#hot{len(hot)}") in self._records:
-                hot.append(self._records[(request_id, f"{layer_name}#hot{len(hot)}")])
-        if not groups and not hot:
+            hot = self._records.get((request_id, f"{layer_name}#hot0"))
+        if not groups and hot is None:
             return 0
         H, D, G = pool.n_kv_heads, pool.head_dim, pool.group_tokens
         vq = self._quantizer("value", D, H)
         if getattr(vq, "value_bits", None) != pool.value_bits:
             raise ValueError(f"stored values are {getattr(vq, 'value_bits', None)}-bit, the pool's "
                              f"{pool.value_bits}-bit")
-        if not np.array_equal(random_rotation(getattr(vq, "seed", None), D)[0], pool.pi.cpu().numpy()):
-            raise ValueError("the pool's value rotation is not the store's (rotation seed)")
+        # the instance's own rotation (drawn once, also for an unseeded store)
+        if not np.array_equal(np.asarray(vq.rotation[0], np.float32), pool.pi.cpu().numpy()):
+            raise ValueError("the pool's value rotation is not the store's")
         items = []
         for rec in groups:
             kp, vp = rec.key_payload, rec.value_payload
             if rec.num_tokens != G or rec.n_heads != H or rec.head_dim != D or not kp.packed \
-                    or not vp.packed or getattr(kp, "zp_mode", "calibrated") != "calibrated":
+                    or not vp.packed:
                 raise ValueError("a stored group does not match the pool's group format")
-            items.append(({"kpacked": kp.indices, "nf4_scale": kp.nf4_scale[0], "nf4_mean": kp.nf4_mean[0],
+            uniform = getattr(kp, "nf4_scale", None) is None and getattr(kp, "scale", None) is not None
+            if ("uniform" if uniform else "nf4_asym") != pool.key_grid:
+                raise ValueError(f"stored keys are {'uniform' if uniform else 'asym-NF4'}, the pool's "
+                                 f"{pool.key_grid}")
+            zp = "calibrated" if uniform else getattr(kp, "zp_mode", "calibrated")
+            if zp != pool.zero_point:
+                raise ValueError(f"stored key zero point {zp!r}, the pool's {pool.zero_point!r}")
+            if uniform:
+                scale, mean = np.asarray(kp.scale)[0, :, 0, :], np.asarray(kp.zero)[0, :, 0, :]
+            else:
+                scale = np.asarray(kp.nf4_scale)[0]
+                mean = None if kp.nf4_mean is None else np.asarray(kp.nf4_mean)[0]
+            items.append(({"kpacked": kp.indices, "nf4_scale": scale, "nf4_mean": mean,
                            "outlier_idx": kp.outlier_idx, "outlier_val": kp.outlier_val},
                           {"vpacked": vp.indices, "vnorms": vp.norms[0]}))
-        kq = self._quantizer("key", D, H)
-        hk = torch.zeros((H, 0, D))
-        hv = torch.zeros((H, 0, D))
-        for rec in hot:
-            hk = torch.cat([hk, torch.from_numpy(np.asarray(kq.decompress(rec.key_payload), np.float32)[0])], 1)
-            hv = torch.cat([hv, torch.from_numpy(np.asarray(vq.decompress(rec.value_payload), np.float32)[0])], 1)
-        pool.load_sequence(b, items, hk.to(torch.float16), hv.to(torch.float16))
+        if hot is not None:
+            hk = torch.from_numpy(np.asarray(hot.key_payload.data, np.float16)[0])
+            hv = torch.from_numpy(np.asarray(hot.value_payload.data, np.float16)[0])
+        else:
+            hk = hv = torch.zeros((H, 0, D), dtype=torch.float16)
+        pool.load_sequence(b, items, hk, hv)
         return len(items) * G + int(hk.shape[1])
 
     def save(self, request_id: str, layer_name: str, keys: Any, values: Any) -> None:
@@ -235,6 +249,10 @@ class TurboQuantBlockStore:
         rec = self.record(request_id, layer_name)
         if rec is None:
             return None
+        if hasattr(rec.key_payload, "data") and not hasattr(rec.key_payload, "indices"):
+            # a live-path hot window, stored as it is
+            return (np.asarray(rec.key_payload.data, np.float32).reshape(rec.shape),
+                    np.asarray(rec.value_payload.data, np.float32).reshape(rec.shape))
         try:
             k = self._quantizer("key", rec.head_dim, rec.n_heads).decompress(rec.key_payload)
             v = self._quantizer("value", rec.head_dim, rec.n_heads).decompress(rec.value_payload)

@@ -3,8 +3,9 @@
 Same constructor, methods and return conventions as the reference's
 ``TurboQuantKVCache`` (turboquant_pro/core.py:818-1307): one sequence, an fp16
 hot window of ``hot_window`` tokens, and flushed groups of
-``(hot_window + 1) // 2`` tokens coded as per-channel asym-NF4 keys with an fp16
-outlier side-list plus PolarQuant values.  Storage and compute live on the GPU:
+``(hot_window + 1) // 2`` tokens coded as per-channel 4-bit keys (asym-NF4
+with a calibrated, sparse or bias zero point, or uniform) with an fp16
+outlier side-list plus 2/3/4-bit PolarQuant values.  Storage and compute live on the GPU:
 ``append`` runs the quantize-on-flush kernel when a group completes,
 ``fused_decode`` runs the fused split-K kernel, ``get_keys``/``get_values``
 reconstruct on the GPU.
@@ -15,9 +16,9 @@ Differences from the reference, all deliberate:
     AutoConfig default and the point of this build);
   * keys/values/queries are converted to fp16 on entry (the serving dtype the
     kernels consume); codes are bit-exact with the reference for fp16 inputs;
-  * configurations without a gfx950 form (non-NF4 keys, zero-point modes other
-    than "calibrated", head_dim != 128) raise NotImplementedError at
-    construction instead of silently running on the CPU;
+  * configurations without a gfx950 form (PolarQuant, 2/3-bit uniform,
+    symmetric-NF4 and quantile keys; head_dim != 128) raise
+    NotImplementedError at construction instead of silently running on the CPU;
   * an optional ``n_q_heads`` (a multiple of ``n_heads``) serves GQA queries.
 """
 
@@ -80,6 +81,17 @@ class TurboQuantKVCache:
             key_nf4 = True
         if key_nf4 and self.key_bits != 4:
             raise ValueError("nf4=True requires bits=4")
+        # zero-point checks of PerChannelKV.__init__ (turboquant_pro/per_channel_kv.py:199-213)
+        if key_zero_point != "calibrated":
+            if not key_nf4_asym:
+                raise ValueError(f"zero_point={key_zero_point!r} requires nf4_asym=True")
+            if key_rope_theta is None:
+                raise ValueError(f"zero_point={key_zero_point!r} requires rope_theta")
+        if key_zero_point == "bias":
+            if key_k_bias is None:
+                raise ValueError('zero_point="bias" requires k_bias')
+            key_k_bias = np.asarray(key_k_bias, dtype=np.float32).reshape(n_heads, head_dim)
+        self.key_rope_theta, self.key_k_bias = key_rope_theta, key_k_bias
         # per-channel keys: asym-NF4 (robust / build_cache) or, without any NF4
         # or quantile flag, the reference's uniform 4-bit mode
         uniform = per_channel_keys and not key_nuq and not key_nf4 and self.key_bits == 4
@@ -89,10 +101,6 @@ class TurboQuantKVCache:
                 "AutoConfig.build_cache) or uniform 4-bit; PolarQuant, 2/3-bit uniform, "
                 "symmetric-NF4 and quantile keys have no GPU form here")
         self.key_grid = "uniform" if uniform else "nf4_asym"
-        if key_zero_point != "calibrated":
-            raise NotImplementedError(f"zero_point={key_zero_point!r} has no gfx950 form yet")
-        if self.value_bits not in (3, 4):
-            raise NotImplementedError("gfx950 value codes are 3- or 4-bit PolarQuant")
         if head_dim != 128:
             raise NotImplementedError("the gfx950 kernels are built for head_dim=128")
         if group_tokens_for(hot_window) > 256 or hot_window < 1:
@@ -107,29 +115,15 @@ class TurboQuantKVCache:
                         max_batch=1, max_seq_len=capacity, hot_window=self.hot_window,
                         key_bits=self.key_bits, value_bits=self.value_bits,
                         outlier_frac=self.key_outlier_frac, seed=self.seed, rotation=rotation,
-                        device=self._device, key_grid=self.key_grid)
+                        device=self._device, key_grid=self.key_grid,
+                        zero_point=self.key_zero_point, rope_theta=self.key_rope_theta,
+                        k_bias=self.key_k_bias)
 
     def _grow(self, need: int) -> None:
-        """Reallocate to hold ``need`` tokens, copying the coded groups and the
-        hot ring (identity tables: page p and slot g keep their index)."""
+        """Reallocate to hold ``need`` tokens (at least doubling), moving the
+        coded groups and the hot ring as they are."""
         cap = max(need, 2 * self._capacity)
-        new = self._new_pool(cap, rotation=self._rotation)
-        old = self._pool
-        npg, nsl = old.kcodes.shape[1], old.gscale.shape[0]
-        # pages are head-major and the default table of a single sequence does
-        # not depend on the capacity, so page p keeps its index
-        new.kcodes[:, :npg] = old.kcodes
-        new.vcodes[:, :npg] = old.vcodes
-        new.vnorm[:, :npg] = old.vnorm
-        new.gscale[:nsl] = old.gscale
-        new.gmean[:nsl] = old.gmean
-        new.ocount[:nsl] = old.ocount
-        new.oent[:nsl, :, :old.oent.shape[2]] = old.oent
-        new.hot_k.copy_(old.hot_k)
-        new.hot_v.copy_(old.hot_v)
-        new.lengths = list(old.lengths)
-        new.seq_lens.copy_(old.seq_lens)
-        self._pool, self._capacity = new, cap
+        self._pool, self._capacity = self._pool.grown(cap), cap
 
     # ---------------------------------------------------------------- sizes --
     @property
@@ -234,7 +228,11 @@ class TurboQuantKVCache:
         H, D, G = self.n_heads, self.head_dim, self._pool.group_tokens
         ng = self._pool.n_groups(0)
         n_out = int(self._pool.ocount[:ng, :, -1].sum().item()) if ng else 0
-        key_bytes = ng * (H * G * D * self.key_bits // 8 + 2 * H * D * 4) + n_out * 6
+        # stored zero point: every channel, the DC channels ("sparse") or none ("bias")
+        zp_ch = {"calibrated": D, "bias": 0}.get(self.key_zero_point, None)
+        if zp_ch is None:
+            zp_ch = int(self._pool.dc_mask.sum())
+        key_bytes = ng * (H * G * D * self.key_bits // 8 + H * D * 4 + H * zp_ch * 4) + n_out * 6
         val_bytes = ng * (H * G * D * self.value_bits // 8 + H * G * 4)
         cold = float(key_bytes + val_bytes)
         hot = float(self.hot_length * H * D * 2 * 2)

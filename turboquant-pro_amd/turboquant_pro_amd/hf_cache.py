@@ -20,9 +20,10 @@ GPU (quantize-on-append in the encode kernel) and:
 Differences from the reference layer, by design of the pool: tokens leave
 the hot window in groups of ``(hot_window + 1) // 2`` (the cadence of
 ``TurboQuantKVCache``, turboquant_pro/core.py:1015-1038) instead of
-overflow-sized spills; the hot window is kept in fp16; head_dim is 128; the
-capacity per sequence is fixed when the layer is created (``max_cache_len``,
-else the model config's ``max_position_embeddings``, else 4096).
+overflow-sized spills; the hot window is kept in fp16; head_dim is 128; a
+layer starts with room for 4096 tokens per sequence (or twice its first
+chunk) and doubles on demand, moving its codes, up to ``max_cache_len`` (else
+the model config's ``max_position_embeddings``) as a bound only.
 ``crop``/``reorder_cache``/batch edits re-ingest dense K/V, as the reference
 does (hf_cache.py:247-299).
 """
@@ -49,7 +50,8 @@ __all__ = ["TurboQuantCache", "TurboQuantLayer", "enable_turboquant_cache", "tqk
            "ATTN_IMPLEMENTATION"]
 
 ATTN_IMPLEMENTATION = "tqk_gfx950"
-_DEFAULT_CAPACITY = 4096
+# first allocation per layer, in tokens per sequence; layers grow by doubling
+_INITIAL_CAPACITY = 4096
 
 
 class TurboQuantLayer(CacheLayerMixin):
@@ -78,12 +80,16 @@ class TurboQuantLayer(CacheLayerMixin):
         self.dtype, self.device = key_states.dtype, key_states.device
         b, h, _, d = key_states.shape
         self.batch, self.n_kv_heads, self.head_dim = int(b), int(h), int(d)
+        # start small and grow on demand (max_cache_len is an upper bound only)
+        first = int(key_states.shape[-2])
+        cap = max(_INITIAL_CAPACITY, 2 * first)
+        if self.max_cache_len:
+            cap = min(cap, int(self.max_cache_len))
         self.pool = TQKVPool(
             n_kv_heads=self.n_kv_heads, n_q_heads=self.n_q_heads or self.n_kv_heads,
-            head_dim=self.head_dim, max_batch=self.batch,
-            max_seq_len=int(self.max_cache_len or _DEFAULT_CAPACITY), hot_window=self.hot_window,
-            key_bits=self.key_bits, value_bits=self.value_bits, outlier_frac=self.outlier_frac,
-            seed=self.seed, device=self.device)
+            head_dim=self.head_dim, max_batch=self.batch, max_seq_len=max(cap, first),
+            hot_window=self.hot_window, key_bits=self.key_bits, value_bits=self.value_bits,
+            outlier_frac=self.outlier_frac, seed=self.seed, device=self.device)
         self.is_initialized = True
 
     def _ingest(self, key_states, value_states) -> None:
@@ -93,9 +99,14 @@ class TurboQuantLayer(CacheLayerMixin):
         if tuple(key_states.shape[:2]) != (self.batch, self.n_kv_heads):
             raise ValueError(f"cache layer holds (batch, kv heads) = ({self.batch}, {self.n_kv_heads}); "
                              f"got {tuple(key_states.shape[:2])}")
-        if self.get_seq_length() + n > self.pool.max_seq_len:
-            raise ValueError(f"sequence length {self.get_seq_length() + n} exceeds the layer's capacity "
-                             f"{self.pool.max_seq_len} (pass max_cache_len)")
+        need = self.get_seq_length() + n
+        if need > self.pool.max_seq_len:
+            if self.max_cache_len and need > int(self.max_cache_len):
+                raise ValueError(f"sequence length {need} exceeds max_cache_len={self.max_cache_len}")
+            cap = max(need, 2 * self.pool.max_seq_len)
+            if self.max_cache_len:
+                cap = min(cap, int(self.max_cache_len))
+            self.pool = self.pool.grown(cap)
         self.pool.append(key_states.to(torch.float16).contiguous(),
                          value_states.to(torch.float16).contiguous())
 

@@ -10,17 +10,17 @@ probes :func:`affine_params` / :func:`affine_codes` / :func:`outlier_csr` /
 
 In-tree formats:
 
-* ``"per_channel"`` -- :class:`PerChannelKVQuantizer`, asym-NF4 4-bit keys with
-  the fp16 outlier side-list (turboquant_pro/per_channel_kv.py:182-401).
-  ``compress`` runs the GPU encode of one group per sequence (up to 256 tokens,
-  the cache's group size bound) and returns the reference container, bit for
-  bit for fp16-valued input (keys enter the cache as fp16); ``decompress``
-  runs the GPU dequant.  The affine capability (``grid_params`` / ``codes`` /
-  ``outlier_csr``) reads the container on the host, as the reference's
-  (turboquant_pro/kv_fused_pck.py:47-127).
-* ``"polar"`` -- :class:`PolarQuantizer`, PolarQuant values
-  (turboquant_pro/core.py:139-654) at 3 or 4 bits: ``compress`` /
-  ``decompress`` on the GPU, any number of tokens.
+* ``"per_channel"`` -- :class:`PerChannelKVQuantizer`, per-channel 4-bit keys
+  (asym-NF4 with a calibrated, sparse or bias zero point, or uniform) with the
+  fp16 outlier side-list (turboquant_pro/per_channel_kv.py:182-401).
+  ``compress`` runs the GPU block encode, every (b, h) pair one group of any
+  length S, and returns the reference container bit for bit for fp32 or fp16
+  input; ``decompress`` runs the GPU block dequant.  The affine capability
+  (``grid_params`` / ``codes`` / ``outlier_csr``) reads the container on the
+  host, as the reference's (turboquant_pro/kv_fused_pck.py:47-127).
+* ``"polar"`` -- :class:`PolarQuantizer`, PolarQuant
+  (turboquant_pro/core.py:139-654) at 2, 3 or 4 bits, of values or keys:
+  ``compress`` / ``decompress`` on the GPU, any number of tokens.
 
 Configurations the library has no gfx950 form for raise
 ``NotImplementedError`` at construction.
@@ -28,6 +28,7 @@ Configurations the library has no gfx950 form for raise
 
 from __future__ import annotations
 
+import ctypes
 import logging
 from collections.abc import Callable
 from dataclasses import dataclass, field
@@ -36,7 +37,7 @@ from typing import Any, Protocol, runtime_checkable
 
 import numpy as np
 
-from .codebooks import group_tokens_for, random_rotation
+from .codebooks import outliers_per_channel, random_rotation
 from .formats import NF4, pack_values, unpack_keys, unpack_values
 
 logger = logging.getLogger(__name__)
@@ -56,8 +57,6 @@ _TARGETS = frozenset({TARGET_KV_KEY, TARGET_KV_VALUE, TARGET_WEIGHT, TARGET_EMBE
 _TIERS = frozenset({"stable", "beta", "experimental"})
 ENTRY_POINT_GROUP = "turboquant_pro.plugins"
 
-# one encode group holds at most this many tokens (the library's group bound)
-_MAX_GROUP_TOKENS = 256
 
 
 @runtime_checkable
@@ -241,39 +240,60 @@ class CompressedKV:
 
 
 # --------------------------------------------------------------- formats
-def _pool(H: int, S: int, value_bits: int, outlier_frac: float, B: int, seed=None, device=None,
-          outlier_cap: int | None = None, key_grid: str = "nf4_asym", rotation=None):
-    """A B-sequence pool whose groups are exactly S tokens, one token per page
-    (value codes stored per token, in the reference's pack)."""
-    from .pool import TQKVPool
-
-    W = 2 * S - 1
-    assert group_tokens_for(W) == S
-    return TQKVPool(n_kv_heads=H, n_q_heads=H, max_batch=B, max_seq_len=2 * S, hot_window=W,
-                    value_bits=value_bits, outlier_frac=outlier_frac, page_tokens=1, seed=seed,
-                    rotation=rotation, device=device, outlier_cap=outlier_cap, key_grid=key_grid)
+def _torch():
+    import torch
+    return torch
 
 
-def _fp16_tokens(x: np.ndarray):
-    from .pool import _torch
-
+def _device_tokens(x, device):
+    """A ``(B, H, S, D)`` block on the GPU as the block kernels read it, and
+    whether it is fp32: fp16 input stays fp16 (exact either way, half the
+    bytes); anything else becomes fp32, as ``np.asarray(x, dtype=np.float32)``
+    makes it in the reference (turboquant_pro/per_channel_kv.py:293)."""
     torch = _torch()
-    x = np.asarray(x)
-    if x.ndim != 4:
-        raise ValueError(f"expected (B,H,S,D), got shape {x.shape}")
-    return torch.from_numpy(np.ascontiguousarray(x, dtype=np.float16))
+    dev = torch.device(device if device is not None else "cuda")
+    if isinstance(x, torch.Tensor):
+        t = x.detach()
+        if t.dtype != torch.float16:
+            t = t.to(torch.float32)
+    else:
+        a = np.asarray(x)
+        a = a if a.dtype == np.float16 else np.asarray(a, dtype=np.float32)
+        t = torch.from_numpy(np.ascontiguousarray(a))
+    if t.dim() != 4:
+        raise ValueError(f"expected (B,H,S,D), got shape {tuple(t.shape)}")
+    return t.to(dev).contiguous(), int(t.dtype == torch.float32)
+
+
+def _block_desc(shape, bits: int, key_grid: int = 0, zero_point: int = 0, k: int = 0, cap: int = 0,
+                f32: int = 1, dc=None):
+    from . import _native as N
+    from .codebooks import dc_mask_words
+    B, H, S, D = (int(v) for v in shape)
+    d = N.BlockDesc(batch=B, n_heads=H, tokens=S, head_dim=D, bits=bits, key_grid=key_grid,
+                    zero_point=zero_point, outliers_per_channel=k, outlier_cap=cap, input_f32=f32)
+    if dc is not None:
+        d.dc_mask[:] = dc_mask_words(dc)
+    return d
+
+
+def _stream():
+    return ctypes.c_void_p(_torch().cuda.current_stream().cuda_stream)
+
+
+_ZERO_POINTS = {"calibrated": 0, "sparse": 1, "bias": 2}
 
 
 class PerChannelKVQuantizer:
-    """``"per_channel"`` keys on the gfx950 library: asym-NF4 4-bit or uniform
-    4-bit (the reference's default mode), with the fp16 outlier side-list,
-    one encode group per sequence.
+    """``"per_channel"`` keys on the gfx950 library: asym-NF4 4-bit (zero
+    point "calibrated", "sparse" or "bias") or uniform 4-bit (the reference's
+    default mode), with the fp16 outlier side-list; every (b, h) pair of a
+    block is one group.
 
     The constructor validates like ``PerChannelKV.__init__``
     (turboquant_pro/per_channel_kv.py:182-213) and raises
     ``NotImplementedError`` for the modes the library does not encode
-    (2/3-bit uniform, symmetric NF4, data-fit quantiles, zero-point
-    "sparse"/"bias", head_dim != 128)."""
+    (2/3-bit uniform, symmetric NF4, data-fit quantiles, head_dim != 128)."""
 
     _ZP_MODES = ("calibrated", "sparse", "bias")
 
@@ -299,84 +319,129 @@ class PerChannelKVQuantizer:
         if zero_point == "bias" and k_bias is None:
             raise ValueError('zero_point="bias" requires k_bias')
         uniform = bits == 4 and not nf4 and not nuq
-        if not ((nf4_asym and zero_point == "calibrated") or uniform) or head_dim != 128:
-            raise NotImplementedError("the gfx950 key encode is per-channel asym-NF4 (calibrated zero "
-                                      "points) or uniform, 4-bit, at head_dim 128")
+        if not (nf4_asym or uniform) or head_dim != 128:
+            raise NotImplementedError("the gfx950 key encode is per-channel 4-bit, asym-NF4 (any zero "
+                                      "point) or uniform, at head_dim 128")
         self.head_dim, self.n_heads, self.bits = head_dim, n_heads, bits
         self.uniform = uniform
         self.key_grid = "uniform" if uniform else "nf4_asym"
         self.nuq, self.nf4, self.nf4_asym = nuq, nf4, nf4_asym
         self.outlier_frac, self.zero_point = outlier_frac, zero_point
-        self.rope_theta, self.k_bias = rope_theta, None
+        self.rope_theta = rope_theta
+        self.k_bias = (np.asarray(k_bias, dtype=np.float32).reshape(n_heads, head_dim)
+                       if zero_point == "bias" else None)
         self.device = device
 
-    def compress(self, x: np.ndarray, packed: bool = False, position_start: int = 0) -> CompressedPerChannelKV:
-        """``(B, H, S, D)`` keys, S <= 256, as one group per sequence; the
-        values are taken as fp16 (the form the cache stores)."""
-        from .pool import _torch
+    def compress(self, x, packed: bool = False, position_start: int = 0) -> CompressedPerChannelKV:
+        """``(B, H, S, D)`` keys, any S, each (b, h) one group, on the GPU
+        (turboquant_pro/per_channel_kv.py:285-401); fp32 (or fp16) input is
+        encoded as given, bit for bit."""
+        from . import _native as N
+        from .codebooks import dc_channel_mask, rope_averaged_bias
 
         torch = _torch()
-        xt = _fp16_tokens(x)
+        xt, f32 = _device_tokens(x, self.device)
         B, H, S, D = xt.shape
         if D != self.head_dim:
             raise ValueError(f"head_dim {D} != {self.head_dim}")
-        if not 1 <= S <= _MAX_GROUP_TOKENS:
-            raise NotImplementedError(f"one gfx950 key group holds 1..{_MAX_GROUP_TOKENS} tokens, got {S}")
-        pool = _pool(H, S, 3, self.outlier_frac, B, device=self.device, key_grid=self.key_grid)
-        k = torch.cat([xt, torch.zeros_like(xt)], dim=2).to(pool.device)
-        pool.append(k, torch.zeros_like(k))
-        parts = [pool.export_group(b, 0) for b in range(B)]
-        kp = np.concatenate([p["kpacked"] for p in parts])
+        k = outliers_per_channel(S, self.outlier_frac)
+        zp_mode = "calibrated" if self.uniform else self.zero_point
+        dc = dc_channel_mask(self.rope_theta, D, S) if zp_mode == "sparse" else None
+        zp = None
+        if zp_mode == "bias":
+            if H != self.n_heads:
+                raise ValueError(f"input has {H} heads but k_bias was given for {self.n_heads}; "
+                                 "zero_point='bias' needs them equal")
+            zp = torch.from_numpy(rope_averaged_bias(self.k_bias, self.rope_theta, D, position_start, S)
+                                  ).to(xt.device)
+        u8, f32t, i32 = torch.uint8, torch.float32, torch.int32
+        kp = torch.empty(B * H * S * D // 2, dtype=u8, device=xt.device)
+        scale = torch.empty((B, H, D), dtype=f32t, device=xt.device)
+        zero = torch.empty_like(scale)
+        count = torch.zeros(B * H, dtype=i32, device=xt.device)
+        cap = min(S * D, 4 * k * D) if k else 0
+        while True:
+            pos = torch.empty((B * H, max(cap, 1)), dtype=torch.int32, device=xt.device)
+            val = torch.empty((B * H, max(cap, 1)), dtype=torch.float16, device=xt.device)
+            d = _block_desc(xt.shape, 4, int(self.uniform), _ZERO_POINTS[zp_mode], k, cap, f32, dc)
+            N.check(N.lib().tqk_encode_key_block(
+                ctypes.byref(d), xt.data_ptr(), zp.data_ptr() if zp is not None else None,
+                kp.data_ptr(), scale.data_ptr(), zero.data_ptr(), pos.data_ptr(), val.data_ptr(),
+                count.data_ptr(), _stream()), "tqk_encode_key_block")
+            cnt = count.cpu().numpy()
+            if k == 0 or int(cnt.max()) <= cap:
+                break
+            cap = int(cnt.max())  # magnitude ties: more than k per channel
+        kp_np = kp.cpu().numpy()
         oidx = oval = None
-        if self.outlier_frac > 0:
-            oidx = np.concatenate([p["outlier_idx"].astype(np.int64) + b * H * S * D
-                                   for b, p in enumerate(parts)]).astype(np.int32)
-            oval = np.concatenate([p["outlier_val"] for p in parts]).astype(np.float16)
-        indices = kp if packed else unpack_keys(kp, B * H * S * D).reshape(B, H, S, D)
+        if k:
+            pos_np = pos.cpu().numpy().view(np.uint32)
+            val_np = val.cpu().numpy()
+            oidx = np.concatenate([pos_np[i, :cnt[i]].astype(np.int64) + i * S * D
+                                   for i in range(B * H)]).astype(np.int32)
+            oval = np.concatenate([val_np[i, :cnt[i]] for i in range(B * H)]).astype(np.float16)
+        indices = kp_np if packed else unpack_keys(kp_np, B * H * S * D).reshape(B, H, S, D)
+        sc, zr = scale.cpu().numpy(), zero.cpu().numpy()
         if self.uniform:
             # per_channel_kv.py:303-317: (B, H, 1, D) scale and zero, no NF4 fields
-            return CompressedPerChannelKV(
-                indices, np.stack([p["nf4_scale"] for p in parts]).astype(np.float32)[:, :, None, :],
-                np.stack([p["nf4_mean"] for p in parts]).astype(np.float32)[:, :, None, :],
-                self.bits, (B, H, S, D), packed, outlier_idx=oidx, outlier_val=oval)
+            return CompressedPerChannelKV(indices, sc[:, :, None, :], zr[:, :, None, :], self.bits,
+                                          (B, H, S, D), packed, outlier_idx=oidx, outlier_val=oval)
+        # the stored zero point: every channel's, the DC channels', or none
+        mean = {"calibrated": zr, "sparse": zr[:, :, dc] if dc is not None else None, "bias": None}[zp_mode]
         return CompressedPerChannelKV(
-            indices, None, None, self.bits, (B, H, S, D), packed,
-            nf4_scale=np.stack([p["nf4_scale"] for p in parts]).astype(np.float32),
-            nf4_mean=np.stack([p["nf4_mean"] for p in parts]).astype(np.float32),
-            outlier_idx=oidx, outlier_val=oval, zp_mode="calibrated", rope_theta=None,
+            indices, None, None, self.bits, (B, H, S, D), packed, nf4_scale=sc, nf4_mean=mean,
+            outlier_idx=oidx, outlier_val=oval, zp_mode=zp_mode,
+            rope_theta=self.rope_theta if zp_mode != "calibrated" else None,
             position_start=position_start)
 
     def decompress(self, c: CompressedPerChannelKV) -> np.ndarray:
-        """fp32 ``(B, H, S, D)``: ``mean + scale * NF4[code]``, outliers overwritten
-        by their fp16 values (turboquant_pro/per_channel_kv.py:497-539), on the GPU."""
+        """fp32 ``(B, H, S, D)``: ``zero point + scale * NF4[code]`` (or
+        ``zero + scale * code``), outliers overwritten by their fp16 values
+        (turboquant_pro/per_channel_kv.py:497-539), on the GPU."""
+        from . import _native as N
+        from .codebooks import dc_channel_mask, rope_averaged_bias
+
+        torch = _torch()
         B, H, S, D = c.shape
         uniform = c.nf4_scale is None and c.levels is None and c.scale is not None and c.zero is not None
-        if not uniform and (c.nf4_scale is None or c.nf4_mean is None or c.zp_mode != "calibrated"):
-            raise NotImplementedError("the gfx950 dequant reads calibrated asym-NF4 or uniform containers")
-        if uniform and c.bits != 4:
-            raise NotImplementedError("the gfx950 dequant reads 4-bit uniform containers")
-        gscale = np.asarray(c.scale)[:, :, 0, :] if uniform else np.asarray(c.nf4_scale)
-        gmean = np.asarray(c.zero)[:, :, 0, :] if uniform else np.asarray(c.nf4_mean)
-        if not 1 <= S <= _MAX_GROUP_TOKENS or D != 128:
-            raise NotImplementedError(f"one gfx950 key group holds 1..{_MAX_GROUP_TOKENS} tokens at head_dim 128")
-        kp = c.indices if c.packed else _pack_keys(np.asarray(c.indices))
-        kp = np.asarray(kp, np.uint8).reshape(B, H * S * D // 2)
+        if c.levels is not None or (not uniform and c.nf4_scale is None):
+            raise NotImplementedError("data-fit (quantile) key grids have no gfx950 dequant")
+        if c.bits != 4 or D != 128:
+            raise NotImplementedError("the gfx950 dequant reads 4-bit keys at head_dim 128")
+        if uniform:
+            scale = np.asarray(c.scale, np.float32)[:, :, 0, :]
+            zero = np.asarray(c.zero, np.float32)[:, :, 0, :]
+        else:
+            scale = np.asarray(c.nf4_scale, np.float32)
+            if c.zp_mode == "bias":
+                if self.k_bias is None:
+                    raise ValueError('container was compressed with zero_point="bias"; decompress '
+                                     "needs a quantizer built with the same k_bias")
+                zero = np.broadcast_to(rope_averaged_bias(self.k_bias, c.rope_theta, D, c.position_start, S)[None],
+                                       (B, H, D))
+            elif c.zp_mode == "sparse":
+                zero = np.zeros((B, H, D), np.float32)
+                zero[:, :, dc_channel_mask(c.rope_theta, D, S)] = c.nf4_mean
+            elif c.nf4_mean is not None:
+                zero = np.asarray(c.nf4_mean, np.float32)
+            else:  # symmetric NF4 container: no zero point
+                zero = np.zeros((B, H, D), np.float32)
+        kp = np.asarray(c.indices if c.packed else _pack_keys(np.asarray(c.indices)), np.uint8).reshape(-1)
         has_out = c.outlier_idx is not None and c.outlier_val is not None
-        flat = np.asarray(c.outlier_idx, np.int64).reshape(-1) if has_out else np.zeros(0, np.int64)
-        vals = np.asarray(c.outlier_val, np.float16).reshape(-1) if has_out else np.zeros(0, np.float16)
-        # side-list sized for the container's own counts (ties can exceed k per channel)
-        per_head = np.bincount(flat // (S * D), minlength=B * H) if flat.size else np.zeros(1, np.int64)
-        cap = max(1, int(per_head.max()))
-        frac = self.outlier_frac if self.outlier_frac > 0 else 0.02
-        pool = _pool(H, S, 3, frac if has_out else 0.0, B, device=self.device,
-                     outlier_cap=cap if has_out else 0, key_grid="uniform" if uniform else "nf4_asym")
-        for b in range(B):
-            m = (flat // (H * S * D)) == b
-            pool.import_group(b, 0, keys={
-                "kpacked": kp[b], "nf4_scale": gscale[b], "nf4_mean": gmean[b],
-                "outlier_idx": flat[m] - b * H * S * D, "outlier_val": vals[m]})
-        keys, _ = pool.dequant_groups([(b, 0) for b in range(B)])
-        return keys.cpu().numpy().reshape(B, H, S, D)
+        _check_key_container(kp, scale, zero, c, B * H * S * D, (B, H, D), has_out)
+        dev = torch.device(self.device if self.device is not None else "cuda")
+        t = lambda a, dt: torch.from_numpy(np.ascontiguousarray(a, dt)).to(dev)  # noqa: E731
+        kp_d, sc_d, zr_d = t(kp, np.uint8), t(scale, np.float32), t(zero, np.float32)
+        n_out = int(np.asarray(c.outlier_idx).size) if has_out else 0
+        idx_d = t(np.asarray(c.outlier_idx, np.int32).reshape(-1), np.int32) if n_out else None
+        val_d = t(np.asarray(c.outlier_val, np.float16).reshape(-1).view(np.int16), np.int16) if n_out else None
+        out = torch.empty((B, H, S, D), dtype=torch.float32, device=dev)
+        d = _block_desc(c.shape, 4, int(uniform))
+        N.check(N.lib().tqk_dequant_key_block(
+            ctypes.byref(d), kp_d.data_ptr(), sc_d.data_ptr(), zr_d.data_ptr(), n_out,
+            idx_d.data_ptr() if n_out else None, val_d.data_ptr() if n_out else None, out.data_ptr(),
+            _stream()), "tqk_dequant_key_block")
+        return out.cpu().numpy()
 
     # affine capability (turboquant_pro/kv_fused_pck.py:47-127), on the container
     def grid_params(self, c: CompressedPerChannelKV):
@@ -439,14 +504,13 @@ def _pack_keys(codes: np.ndarray) -> np.ndarray:
 
 
 class PolarQuantizer:
-    """``"polar"`` values on the gfx950 library: PolarQuant (norm + rotated
-    direction on the Lloyd-Max grid) at 3 or 4 bits.
+    """``"polar"`` on the gfx950 library: PolarQuant (norm + rotated direction
+    on the Lloyd-Max grid) at 2, 3 or 4 bits.
 
     Constructor as ``TurboQuantKV.__init__`` (turboquant_pro/core.py:178-228):
     ``bits`` is the default width, ``key_bits`` / ``value_bits`` override it
-    per kind; the rotation is the reference's ``seed`` recipe.  Widths other
-    than 3 and 4, ``head_dim`` other than 128, and PolarQuant *keys* have no
-    gfx950 form."""
+    per kind (``compress(kind=...)``); the rotation is the reference's
+    ``seed`` recipe.  ``head_dim`` other than 128 has no gfx950 form."""
 
     def __init__(self, head_dim: int = 128, n_heads: int = 32, bits: int = 3,
                  key_bits: int | None = None, value_bits: int | None = None, use_gpu: bool = True,
@@ -457,72 +521,98 @@ class PolarQuantizer:
             if v not in (2, 3, 4):
                 raise ValueError(f"Unsupported {name}={v}; choose from [2, 3, 4]")
         if head_dim != 128:
-            raise NotImplementedError("the gfx950 value encode serves head_dim 128")
+            raise NotImplementedError("the gfx950 PolarQuant encode serves head_dim 128")
         self.head_dim, self.n_heads, self.bits, self.seed = head_dim, n_heads, bits, seed
         self.device = device
         # drawn once, as TurboQuantKV does (core.py:178-228): with seed=None the
         # instance's compress and decompress still share one rotation
         self.rotation = random_rotation(seed, head_dim)
+        self._dev_consts: dict = {}
 
     def _width(self, kind: str | None) -> int:
-        if kind == "key":
-            raise NotImplementedError("PolarQuant keys have no gfx950 form (the cache's keys are asym-NF4)")
-        if kind not in (None, "value"):
+        if kind not in (None, "key", "value"):
             raise ValueError(f"kind must be 'key', 'value' or None, got {kind!r}")
-        w = self.value_bits if kind == "value" else self.bits
-        if w not in (3, 4):
-            raise NotImplementedError(f"the gfx950 value encode is 3 or 4 bits, not {w}")
-        return w
+        return self.key_bits if kind == "key" else self.value_bits if kind == "value" else self.bits
 
-    def compress(self, tensor: np.ndarray, packed: bool = False, kind: str | None = None) -> CompressedKV:
-        """``(B, H, S, D)`` values (taken as fp16) -> codes + fp32 norms, in
-        groups of up to 256 tokens (PolarQuant is per token)."""
-        from .pool import _torch
+    def _consts(self, bits: int):
+        """Device copies of Pi and the bits-wide codebook."""
+        torch = _torch()
+        got = self._dev_consts.get(bits)
+        if got is None:
+            from .codebooks import value_codebook
+            dev = torch.device(self.device if self.device is not None else "cuda")
+            cent, bnd = value_codebook(bits, self.head_dim)
+            got = tuple(torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev)
+                        for a in (self.rotation[0], cent, bnd))
+            self._dev_consts[bits] = got
+        return got
+
+    def compress(self, tensor, packed: bool = False, kind: str | None = None) -> CompressedKV:
+        """``(B, H, S, D)`` -> codes + fp32 norms (turboquant_pro/core.py:542-617),
+        any S, on the GPU; fp32 (or fp16) input is encoded as given, bit for bit."""
+        from . import _native as N
 
         torch = _torch()
         bits = self._width(kind)
-        orig = np.asarray(tensor).dtype
-        vt = _fp16_tokens(tensor)
-        B, H, S, D = vt.shape
-        codes = np.zeros((B, H, S, D), np.uint8)
-        norms = np.zeros((B, H, S), np.float32)
-        for t0 in range(0, S, _MAX_GROUP_TOKENS):
-            n = min(_MAX_GROUP_TOKENS, S - t0)
-            pool = _pool(H, n, bits, 0.0, B, rotation=self.rotation, device=self.device)
-            chunk = vt[:, :, t0:t0 + n]
-            v = torch.cat([chunk, torch.zeros_like(chunk)], dim=2).to(pool.device)
-            pool.append(torch.zeros_like(v), v)
-            for b in range(B):
-                e = pool.export_group(b, 0)
-                codes[b, :, t0:t0 + n] = unpack_values(e["vpacked"], H * n * D, bits).reshape(H, n, D)
-                norms[b, :, t0:t0 + n] = e["vnorms"]
-        shape = (B, H, S, D)
+        orig = np.dtype(str(tensor.dtype).replace("torch.", "")) if isinstance(tensor, torch.Tensor) \
+            else np.asarray(tensor).dtype
+        xt, f32 = _device_tokens(tensor, self.device)
+        B, H, S, D = xt.shape
+        pi, _, bnd = self._consts(bits)
+        out = torch.empty(B * H * S * D * bits // 8, dtype=torch.uint8, device=xt.device)
+        norms = torch.empty((B, H, S), dtype=torch.float32, device=xt.device)
+        d = _block_desc(xt.shape, bits, f32=f32)
+        N.check(N.lib().tqk_encode_value_block(ctypes.byref(d), xt.data_ptr(), pi.data_ptr(),
+                                               bnd.data_ptr(), out.data_ptr(), norms.data_ptr(),
+                                               _stream()), "tqk_encode_value_block")
+        pk, nv = out.cpu().numpy(), norms.cpu().numpy()
+        shape, n = (B, H, S, D), B * H * S * D
         if packed:
-            return CompressedKV(pack_values(codes, bits), norms, bits, np.dtype(orig), True,
-                                int(codes.size), shape)
-        return CompressedKV(codes, norms, bits, np.dtype(orig), False, int(codes.size), shape)
+            return CompressedKV(pk, nv, bits, orig, True, n, shape)
+        return CompressedKV(unpack_values(pk, n, bits).reshape(shape), nv, bits, orig, False, n, shape)
 
     def decompress(self, compressed: CompressedKV) -> np.ndarray:
         """fp32 ``(B, H, S, D)`` = norm * (centroids[code] @ Pi), on the GPU
         (turboquant_pro/core.py:619-654)."""
+        from . import _native as N
+
+        torch = _torch()
         bits = compressed.bits
-        if bits not in (3, 4):
-            raise NotImplementedError(f"the gfx950 value dequant is 3 or 4 bits, not {bits}")
+        if bits not in (2, 3, 4):
+            raise NotImplementedError(f"the gfx950 PolarQuant dequant is 2, 3 or 4 bits, not {bits}")
         B, H, S, D = compressed.shape
-        codes = (unpack_values(compressed.indices, compressed.n_values, bits) if compressed.packed
-                 else np.asarray(compressed.indices, np.uint8)).reshape(B, H, S, D)
-        norms = np.asarray(compressed.norms, np.float32).reshape(B, H, S)
-        out = np.zeros((B, H, S, D), np.float32)
-        for t0 in range(0, S, _MAX_GROUP_TOKENS):
-            n = min(_MAX_GROUP_TOKENS, S - t0)
-            pool = _pool(H, n, bits, 0.0, B, rotation=self.rotation, device=self.device)
-            for b in range(B):
-                pool.import_group(b, 0, values={
-                    "vpacked": pack_values(codes[b, :, t0:t0 + n], bits),
-                    "vnorms": norms[b, :, t0:t0 + n]})
-            _, vals = pool.dequant_groups([(b, 0) for b in range(B)])
-            out[:, :, t0:t0 + n] = vals.cpu().numpy().reshape(B, H, n, D)
-        return out
+        n = B * H * S * D
+        pk = (np.asarray(compressed.indices, np.uint8).reshape(-1)[: n * bits // 8] if compressed.packed
+              else pack_values(np.asarray(compressed.indices, np.uint8), bits))
+        norms = np.ascontiguousarray(compressed.norms, np.float32).reshape(-1)
+        if pk.size != n * bits // 8 or norms.size != B * H * S:
+            raise ValueError(f"value container holds {pk.size} code bytes and {norms.size} norms, "
+                             f"shape {compressed.shape} needs {n * bits // 8} and {B * H * S}")
+        pi, cent, _ = self._consts(bits)
+        dev = pi.device
+        pk_d = torch.from_numpy(np.ascontiguousarray(pk)).to(dev)
+        nv_d = torch.from_numpy(norms).to(dev)
+        out = torch.empty((B, H, S, D), dtype=torch.float32, device=dev)
+        d = _block_desc(compressed.shape, bits)
+        N.check(N.lib().tqk_dequant_value_block(ctypes.byref(d), pk_d.data_ptr(), nv_d.data_ptr(),
+                                                pi.data_ptr(), cent.data_ptr(), out.data_ptr(),
+                                                _stream()), "tqk_dequant_value_block")
+        return out.cpu().numpy()
+
+
+def _check_key_container(kp, scale, zero, c, n, bhd, has_out) -> None:
+    """Sizes and side-list indices of a key container before its arrays go to
+    the GPU (a container read from a store may be damaged or foreign)."""
+    if kp.size != n // 2:
+        raise ValueError(f"key container holds {kp.size} code bytes, shape {c.shape} needs {n // 2}")
+    if scale.shape != bhd or zero.shape != bhd:
+        raise ValueError(f"key container scale {scale.shape} / zero point {zero.shape}, expected {bhd}")
+    if has_out:
+        idx = np.asarray(c.outlier_idx).reshape(-1)
+        if idx.size != np.asarray(c.outlier_val).size:
+            raise ValueError("outlier index and value lists differ in length")
+        if idx.size and (int(idx.min()) < 0 or int(idx.max()) >= n):
+            raise ValueError(f"outlier index outside [0, {n})")
 
 
 def _per_channel_factory(**config: Any) -> PerChannelKVQuantizer:
@@ -535,9 +625,9 @@ def _polar_factory(**config: Any) -> PolarQuantizer:
 
 register(PluginSpec(
     name="per_channel", factory=_per_channel_factory, targets=frozenset({TARGET_KV_KEY}), tier="beta",
-    description="per-channel asym-NF4 4-bit keys with the fp16 outlier side-list on the gfx950 "
+    description="per-channel 4-bit keys (asym-NF4, any zero point, or uniform) with the fp16 outlier side-list on the gfx950 "
                 "library; full affine contract"))
 register(PluginSpec(
     name="polar", factory=_polar_factory, targets=frozenset({TARGET_KV_VALUE}), tier="stable",
-    description="PolarQuant values (rotation + norm/direction codes) at 3 or 4 bits on the gfx950 "
+    description="PolarQuant values (rotation + norm/direction codes) at 2, 3 or 4 bits on the gfx950 "
                 "library"))

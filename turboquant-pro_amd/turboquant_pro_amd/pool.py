@@ -25,8 +25,10 @@ import numpy as np
 from . import _native as N
 from .formats import (mark_outlier_codes, pack_values, restore_outlier_codes, tile_value_rows,
                       unpack_values, untile_value_rows)
-from .codebooks import (group_tokens_for, n_groups_for, outliers_per_channel, random_rotation,
-                        value_codebook)
+from .codebooks import (dc_channel_mask, dc_mask_words, group_tokens_for, n_groups_for,
+                        outliers_per_channel, random_rotation, rope_averaged_bias, value_codebook)
+
+ZERO_POINTS = {"calibrated": 0, "sparse": 1, "bias": 2}
 
 
 def _torch():
@@ -40,8 +42,25 @@ class TQKVPool:
                  key_bits: int = 4, value_bits: int = 3, outlier_frac: float = 0.02,
                  page_tokens: int | None = None, outlier_cap: int | None = None,
                  seed=None, rotation: tuple | None = None, block_table=None, device=None,
-                 key_grid: str = "nf4_asym"):
+                 key_grid: str = "nf4_asym", zero_point: str = "calibrated",
+                 rope_theta: float | None = None, k_bias=None):
         torch = _torch()
+        self._init_args = dict(n_kv_heads=n_kv_heads, n_q_heads=n_q_heads, head_dim=head_dim,
+                               max_batch=max_batch, hot_window=hot_window, key_bits=key_bits,
+                               value_bits=value_bits, outlier_frac=outlier_frac,
+                               page_tokens=page_tokens, outlier_cap=outlier_cap, device=device,
+                               key_grid=key_grid, zero_point=zero_point, rope_theta=rope_theta,
+                               k_bias=k_bias)
+        self._custom_table = block_table is not None
+        if zero_point not in ZERO_POINTS:
+            raise ValueError(f"zero_point must be one of {tuple(ZERO_POINTS)}")
+        if zero_point != "calibrated":
+            if key_grid != "nf4_asym":
+                raise ValueError(f"zero_point={zero_point!r} requires asym-NF4 keys")
+            if rope_theta is None:
+                raise ValueError(f"zero_point={zero_point!r} requires rope_theta")
+        if zero_point == "bias" and k_bias is None:
+            raise ValueError('zero_point="bias" requires k_bias')
         if not torch.cuda.is_available():
             raise RuntimeError("TQKVPool runs on a ROCm GPU (gfx950); none is visible")
         self.device = torch.device(device if device is not None else "cuda")
@@ -70,8 +89,14 @@ class TQKVPool:
             outliers_per_channel=k_out, outlier_cap=outlier_cap,
             max_pages_per_seq=max_pages, max_groups_per_seq=max_groups,
             hot_ring=hot_window, n_pages=max_batch * max_pages, sm_scale=1.0 / math.sqrt(head_dim),
-            key_grid={"nf4_asym": 0, "uniform": 1}[key_grid])
+            key_grid={"nf4_asym": 0, "uniform": 1}[key_grid], zero_point=ZERO_POINTS[zero_point])
         self.key_grid = key_grid
+        self.zero_point, self.rope_theta = zero_point, rope_theta
+        # "sparse": the channels whose rotary wavelength exceeds a group
+        self.dc_mask = dc_channel_mask(rope_theta, head_dim, G) if zero_point == "sparse" else None
+        if self.dc_mask is not None:
+            self.desc.dc_mask[:] = dc_mask_words(self.dc_mask)
+        self.k_bias = None if k_bias is None else np.asarray(k_bias, np.float32).reshape(n_kv_heads, head_dim)
         N.check(N.lib().tqk_check_desc(ctypes.byref(self.desc)), "TQKVPool")
 
         dev = self.device
@@ -106,6 +131,13 @@ class TQKVPool:
         self.pi_t = torch.from_numpy(np.ascontiguousarray(pi_t, np.float32)).to(dev)
         self.vcent = torch.from_numpy(cent).to(dev)
         self.vbnd = torch.from_numpy(bnd).to(dev)
+        # "bias": the zero point of group g, whose block starts at token g * G
+        # (turboquant_pro/per_channel_kv.py:245-267 with position_start = g * G)
+        self.zp_mean = None
+        if zero_point == "bias":
+            zp = np.stack([rope_averaged_bias(self.k_bias, rope_theta, head_dim, g * G, G)
+                           for g in range(max_groups)])
+            self.zp_mean = torch.from_numpy(np.ascontiguousarray(zp, np.float32)).to(dev)
         self.ptrs = N.CachePtrs(
             kcodes=self.kcodes.data_ptr(), vcodes=self.vcodes.data_ptr(),
             vnorm=self.vnorm.data_ptr(), gscale=self.gscale.data_ptr(),
@@ -113,7 +145,8 @@ class TQKVPool:
             oent=self.oent.data_ptr(), hot_k=self.hot_k.data_ptr(), hot_v=self.hot_v.data_ptr(),
             block_table=self.block_table.data_ptr(), group_table=self.group_table.data_ptr(),
             pi=self.pi.data_ptr(), pi_t=self.pi_t.data_ptr(), vcent=self.vcent.data_ptr(),
-            vbnd=self.vbnd.data_ptr())
+            vbnd=self.vbnd.data_ptr(),
+            zp_mean=self.zp_mean.data_ptr() if self.zp_mean is not None else None)
         self.lengths = [0] * max_batch
         self.seq_lens = torch.zeros(max_batch, dtype=i32, device=dev)
         self._overflow = torch.zeros(1, dtype=i32, device=dev)
@@ -148,6 +181,41 @@ class TQKVPool:
     def reset(self) -> None:
         self.lengths = [0] * self.max_batch
         self.seq_lens.zero_()
+
+    def grown(self, max_seq_len: int) -> "TQKVPool":
+        """A pool of the same format holding up to ``max_seq_len`` tokens per
+        sequence, with this pool's contents: every sequence's pages copied
+        through both block tables, its group slots and its hot ring (the
+        codes are moved, never re-encoded).  Pools with a caller's block
+        table cannot grow."""
+        torch = _torch()
+        if self._custom_table:
+            raise ValueError("a pool with a caller's block table cannot grow")
+        if max_seq_len <= self.max_seq_len:
+            return self
+        new = TQKVPool(max_seq_len=max_seq_len, rotation=(self.pi.cpu().numpy(), self.pi_t.cpu().numpy()),
+                       **self._init_args)
+        if new.oent.shape[2] < self.oent.shape[2]:
+            raise ValueError("the grown pool's outlier_cap is smaller")
+        B, mp_old, mg_old = self.max_batch, self.max_pages, self.max_groups
+        dev = self.device
+        old_bt = self.block_table.long()[:, :mp_old]
+        new_bt = new.block_table.long()[:, :mp_old]
+        src, dst = old_bt.reshape(-1), new_bt.reshape(-1)
+        for name in ("kcodes", "vcodes", "vnorm"):
+            getattr(new, name)[:, dst] = getattr(self, name)[:, src]
+        so = self.group_table.long()[:, :mg_old].reshape(-1)
+        sn = new.group_table.long()[:, :mg_old].reshape(-1)
+        new.gscale[sn] = self.gscale[so]
+        new.gmean[sn] = self.gmean[so]
+        new.ocount[sn] = self.ocount[so]
+        new.oent[sn, :, :self.oent.shape[2]] = self.oent[so]
+        new.hot_k.copy_(self.hot_k)
+        new.hot_v.copy_(self.hot_v)
+        new.lengths = list(self.lengths)
+        new.seq_lens.copy_(self.seq_lens)
+        torch.cuda.synchronize(dev)
+        return new
 
     # ------------------------------------------------------------------ #
     def append(self, k, v, n_new=None, check_overflow: bool = True) -> None:
@@ -306,10 +374,16 @@ class TQKVPool:
         oval = np.concatenate(val).view(np.float16) if val else np.zeros(0, np.float16)
         scale, mean = self.gscale[slot].cpu().numpy(), self.gmean[slot].cpu().numpy()
         kp = restore_outlier_codes(kp, oidx, oval, scale, mean, grid=self.key_grid)
+        # the reference's stored zero point: every channel's ("calibrated"),
+        # the DC channels' ("sparse") or none ("bias": recomputed from the bias)
+        stored_mean = (mean[:, self.dc_mask] if self.zero_point == "sparse"
+                       else None if self.zero_point == "bias" else mean)
         return {
             "kpacked": kp.reshape(-1),
             "nf4_scale": scale,
-            "nf4_mean": mean,
+            "nf4_mean": stored_mean,
+            "zp_mode": self.zero_point,
+            "position_start": g * G,
             "outlier_idx": oidx.astype(np.int32),
             "outlier_val": oval,
             "outlier_count": cnt.astype(np.int64),
@@ -342,7 +416,14 @@ class TQKVPool:
             kp = mark_outlier_codes(kp, oidx, grid=self.key_grid)
             self.kcodes[:, phys, off] = torch.from_numpy(kp).to(self.device)
             self.gscale[slot] = torch.from_numpy(np.asarray(keys["nf4_scale"], np.float32).reshape(H, D)).to(self.device)
-            self.gmean[slot] = torch.from_numpy(np.asarray(keys["nf4_mean"], np.float32).reshape(H, D)).to(self.device)
+            if self.zero_point == "bias":
+                self.gmean[slot] = self.zp_mean[g]
+            elif self.zero_point == "sparse":
+                full = np.zeros((H, D), np.float32)
+                full[:, self.dc_mask] = np.asarray(keys["nf4_mean"], np.float32).reshape(H, -1)
+                self.gmean[slot] = torch.from_numpy(full).to(self.device)
+            else:
+                self.gmean[slot] = torch.from_numpy(np.asarray(keys["nf4_mean"], np.float32).reshape(H, D)).to(self.device)
             h = oidx // (G * D)
             pos = oidx % (G * D)  # token * D + channel within the head
             cap = self.oent.shape[2]
