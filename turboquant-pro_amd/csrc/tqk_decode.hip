@@ -837,6 +837,13 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     // 2k + 1 of the lane group's own row (DPP row broadcast reaches them)
     const int eidx = 16 * (c >> 1) + 4 * lg + 2 * (c & 1);
     auto meta = [&](int j, int f) { return __builtin_amdgcn_readfirstlane(meta_s[wu + kMWaves * j][f]); };
+    // the metadata of the wave group being loaded (jl below), field f in lane
+    // f: the block loads read it with v_readlane, with no LDS round trip per block
+    int mv = 0;
+    auto load_meta = [&](int j) {
+      mv = (lane < kMetaInts && nw > 0) ? meta_s[wu + kMWaves * min(j, nw - 1)][lane] : 0;
+    };
+    auto meta_l = [&](int f) { return __builtin_amdgcn_readlane(mv, f); };
     // buffer resources of this head's page regions (32-bit offsets:
     // mfma_path() bounds a head's region below 4 GiB)
     const uint32_t hrows = (uint32_t)d.n_pages * (uint32_t)P;
@@ -847,13 +854,14 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     // Every step issues the same loads (past the end: the last block again,
     // already in L2), so the waits on the oldest buffer stay exact.
     int jl = 0, kbl = 0, nl = 0;  // next block to load: wave group jl, block kbl, stream index nl
+    load_meta(0);
     auto load_next = [&](ColdBlock<VB>& cb) {
       // rows of the two tiles in this head's region (wave-uniform: SGPR offsets)
-      const uint32_t rowA = (uint32_t)meta(jl, 2 * kbl);
-      const uint32_t rowB = (uint32_t)meta(jl, 2 * kbl + 1);
-      const uint32_t obase = (uint32_t)meta(jl, 16 + TQK_NOB);
-      const int e0 = kbl == 0 ? 0 : meta(jl, 16 + kbl - 1);
-      const int e1 = meta(jl, 16 + kbl);
+      const uint32_t rowA = (uint32_t)meta_l(2 * kbl);
+      const uint32_t rowB = (uint32_t)meta_l(2 * kbl + 1);
+      const uint32_t obase = (uint32_t)meta_l(16 + TQK_NOB);
+      const int e0 = kbl == 0 ? 0 : meta_l(16 + kbl - 1);
+      const int e1 = meta_l(16 + kbl);
       {
         const u32x4_t x = __builtin_amdgcn_raw_buffer_load_b128(rk, (int)koffL, (int)(rowA * (D / 2)), 0);
         const u32x4_t y = __builtin_amdgcn_raw_buffer_load_b128(rk, (int)koffL, (int)(rowB * (D / 2)), 0);
@@ -895,6 +903,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         if (++kbl == nblk) {
           kbl = 0;
           ++jl;
+          load_meta(jl);
         }
       }
     };
@@ -906,8 +915,9 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     // the next step writes them, a step before that group can start.
     float2 pend_s, pend_m;  // stats loaded by the previous step
     int pend_slot = 0;
-    auto load_group_stats = [&](int j) {
-      const size_t mb = (size_t)D * (uint32_t)meta(max(0, min(j, nw - 1)), 16 + TQK_NOB);
+    // (obase: slot * Hkv + h of wave group j)
+    auto load_group_stats = [&](int obase, int j) {
+      const size_t mb = (size_t)D * (uint32_t)obase;
       const u32x2_t x = __builtin_amdgcn_raw_buffer_load_b64(buf_rsrc(a.p.gscale + mb, 4u * D), 8 * lane, 0, 0);
       const u32x2_t y = __builtin_amdgcn_raw_buffer_load_b64(buf_rsrc(a.p.gmean + mb, 4u * D), 8 * lane, 0, 0);
       pend_s = make_float2(bitsf(x.x), bitsf(x.y));
@@ -1052,33 +1062,45 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         // tokens of every chunk's four slots of this lane group (dword k = chunk k)
         const uint4 tw03 = *reinterpret_cast<const uint4*>(&otb_s[w][lg][0]);
         const uint4 tw47 = *reinterpret_cast<const uint4*>(&otb_s[w][lg][16]);
+        // chunk operands four at a time, read before the first of them is used
+        // (one LDS round trip per four chunks; the staged arrays hold 128
+        // entries, so the reads stay inside them whatever cnt is)
+        uint4 dq[4];
+        H8 qv[4];
+        auto read4 = [&](int k0) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            dq[i] = *reinterpret_cast<const uint4*>(&od_s[w][16 * (k0 + i) + 4 * lg]);
+            qv[i].v = *reinterpret_cast<const uint4*>(&oq_s[w][hq][16 * (k0 + i) + 4 * lg]);
+          }
+        };
         auto chunk = [&](auto kc) {
           constexpr int k = decltype(kc)::value;
           if (16 * k >= cnt) return;
-          uint4 dq[8];
-          dq[k] = *reinterpret_cast<const uint4*>(&od_s[w][16 * k + 4 * lg]);
           const uint32_t tw = k < 4 ? u4_word<k & 3>(tw03) : u4_word<k & 3>(tw47);
-          H8 qv;
-          qv.v = *reinterpret_cast<const uint4*>(&oq_s[w][hq][16 * k + 4 * lg]);
           if (16 * k < nA) {
             H8 o;
-            onehot_operand(tw, (uint32_t)c, dq[k], o.u);
-            CA = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.h, qv.h, CA, 0, 0, 0);
+            onehot_operand(tw, (uint32_t)c, dq[k & 3], o.u);
+            CA = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.h, qv[k & 3].h, CA, 0, 0, 0);
           }
           if (16 * k + 16 > nA) {
             H8 o;
-            onehot_operand(tw, (uint32_t)(16 + c), dq[k], o.u);
-            CB = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.h, qv.h, CB, 0, 0, 0);
+            onehot_operand(tw, (uint32_t)(16 + c), dq[k & 3], o.u);
+            CB = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.h, qv[k & 3].h, CB, 0, 0, 0);
           }
         };
+        read4(0);
         chunk(IntC<0>{});
         chunk(IntC<1>{});
         chunk(IntC<2>{});
         chunk(IntC<3>{});
-        chunk(IntC<4>{});
-        chunk(IntC<5>{});
-        chunk(IntC<6>{});
-        chunk(IntC<7>{});
+        if (cnt > 64) {
+          read4(4);
+          chunk(IntC<4>{});
+          chunk(IntC<5>{});
+          chunk(IntC<6>{});
+          chunk(IntC<7>{});
+        }
       };
 
       // Software pipeline over a wave's blocks.  Step i starts with the QK^T
@@ -1164,7 +1186,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     int jp = 0, kbp = 0;  // computed block: wave group jp, block kbp
     auto step = [&](const ColdBlock<VB>& cur, ColdBlock<VB>& nxt, const ColdBlock<VB>& nx1) {
       store_group_stats();
-      load_group_stats(jl);  // group of the block load_next fetches now
+      load_group_stats(meta_l(16 + TQK_NOB), jl);  // group of the block load_next fetches now
       wave_sync();
       const bool last = kbp + 1 == nblk;  // block i + 1 starts wave group jp + 1
       if (last) begin_group(jp + 1);     // weights for the QK^T of block i + 1
@@ -1177,9 +1199,10 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     };
     if (T > 0) {
       // groups of the first two blocks, synchronously
-      load_group_stats(0);
+      const int j1 = min(1, T - 1) / nblk;
+      load_group_stats(meta(0, 16 + TQK_NOB), 0);
       store_group_stats();
-      load_group_stats(min(1, T - 1) / nblk);
+      load_group_stats(meta(j1, 16 + TQK_NOB), j1);
       store_group_stats();
       ColdBlock<VB> ring[kColdBuf];
 #pragma unroll
