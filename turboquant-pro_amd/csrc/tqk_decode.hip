@@ -522,6 +522,9 @@ __device__ __forceinline__ void softmax_block(WaveState& st, const float (&s)[8]
     st.m = mn;
     st.mt = mn + kLazyMax;
     st.l *= corr;
+    // one factor per accumulator row, the rows as one vector (whole-vector
+    // multiplies keep the accumulators in their registers)
+    float cv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       // no indexed array here: a lane-dependent pick from one would live in scratch
@@ -531,9 +534,11 @@ __device__ __forceinline__ void softmax_block(WaveState& st, const float (&s)[8]
         const float c1 = bitsf((uint32_t)__builtin_amdgcn_readlane((int)fbits(corr), 4 + i));
         ci = (lg & 1) ? c1 : c0;
       }
-#pragma unroll
-      for (int nt = 0; nt < 8; ++nt) st.O[nt][i] *= ci;
+      cv[i] = ci;
     }
+    const floatx4_t cvec = {cv[0], cv[1], cv[2], cv[3]};
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) st.O[nt] = st.O[nt] * cvec;
   }
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
