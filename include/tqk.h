@@ -44,6 +44,12 @@
  * (lg, c) = tokens [4lg, 4lg+4) x channels [8c, 8c+8) with the code of token u,
  * channel nt at bit (2*nt + u/2)*2*vb + (u%2)*vb -- a lossless permutation of
  * the same bits that lets one MFMA lane load its operand with one access.
+ * kcodes rows are head_dim*key_bits/8 bytes.  4-bit keys use the reference's
+ * pack as above; 3- and 2-bit keys (uniform) a permutation of it: each row is
+ * four 32-channel chunks of head_dim*key_bits/32 bytes, and in chunk c the
+ * little-endian field i (2*key_bits bits at bit 2*key_bits*i) holds
+ * code(32c + 2i) | code(32c + 2i + 1) << key_bits, so one MFMA lane loads its
+ * 32 channels with one access and reads a channel pair with one field.
  */
 #ifndef TQK_H_
 #define TQK_H_
@@ -68,7 +74,7 @@ typedef struct tqk_cache_desc {
   int32_t hot_window;           /* W; groups flush when the hot window exceeds W */
   int32_t group_tokens;         /* G = (W + 1) / 2, 1..256 */
   int32_t page_tokens;          /* P, divides G */
-  int32_t key_bits;             /* 4 (per-channel asym-NF4 or uniform, see key_grid) */
+  int32_t key_bits;             /* 4 (asym-NF4 or uniform, see key_grid); 3 or 2 (uniform only) */
   int32_t value_bits;           /* 2, 3 or 4 (PolarQuant) */
   int32_t outliers_per_channel; /* k = max(1, round(G * outlier_frac)), 0 = no side-list */
   int32_t outlier_cap;          /* oent capacity per (group slot, head) */
@@ -107,7 +113,7 @@ typedef struct tqk_cache_ptrs {
                            the groups starting at token g * group_tokens; unused otherwise */
 } tqk_cache_ptrs;
 
-/* Library ABI version (bumped on any signature or layout change); this header is version 6. */
+/* Library ABI version (bumped on any signature or layout change); this header is version 7. */
 int tqk_version(void);
 
 /* Validate a descriptor; TQK_OK when the GPU path supports it. */
@@ -236,7 +242,7 @@ typedef struct tqk_block_desc {
   int32_t n_heads;              /* H */
   int32_t tokens;               /* S >= 1 */
   int32_t head_dim;             /* D = 128 */
-  int32_t bits;                 /* keys: 4; values: 2, 3 or 4 */
+  int32_t bits;                 /* keys: 4, 3 or 2 (3 and 2 uniform only); values: 2, 3 or 4 */
   int32_t key_grid;             /* keys: 0 asym-NF4, 1 uniform */
   int32_t zero_point;           /* asym-NF4 keys: 0 calibrated, 1 sparse, 2 given (zp), as in tqk_cache_desc */
   int32_t outliers_per_channel; /* keys: k = max(1, round(S * outlier_frac)), 0 = no side-list */
@@ -247,7 +253,7 @@ typedef struct tqk_block_desc {
 
 /*
  * Per-channel key quantization of x [B][H][S][D] (PerChannelKV.compress,
- * turboquant_pro/per_channel_kv.py:269-401): packed [B*H*S*D/2] u8 (the
+ * turboquant_pro/per_channel_kv.py:269-401): packed [B*H*S*D*bits/8] u8 (the
  * reference's packed indices, true codes at outlier positions), scale and
  * zero [B][H][D] f32 (asym-NF4: nf4_scale and the zero point; uniform: scale
  * and channel min), the side-list of each (b, h) in (s, j) order as

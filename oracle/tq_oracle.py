@@ -163,6 +163,7 @@ class KeyGroup:
     # "nf4_asym", or "uniform": then nf4_scale / nf4_mean hold the reference's
     # per-channel scale / zero (its (1, H, 1, D) arrays without the unit axes)
     grid: str = "nf4_asym"
+    bits: int = 4                # code width (2 or 3 only with the uniform grid)
 
 
 @dataclass
@@ -200,22 +201,24 @@ def key_outliers(x4: np.ndarray, outlier_frac: float):
     return oidx, x4.reshape(-1)[oidx].astype(np.float16)
 
 
-def encode_keys_uniform(x: np.ndarray, outlier_frac: float) -> KeyGroup:
-    """Uniform asymmetric per-channel 4-bit key encode of one group ``x``
-    (H, S, D) fp32, turboquant_pro/per_channel_kv.py:303-317: per channel
-    ``mn``/``mx`` over the tokens, ``scale = max(mx - mn, 1e-8) / 15``,
-    ``code = clip(round_half_even((x - mn) / scale), 0, 15)``; outliers as for
+def encode_keys_uniform(x: np.ndarray, outlier_frac: float, bits: int = 4) -> KeyGroup:
+    """Uniform asymmetric per-channel key encode of one group ``x`` (H, S, D)
+    fp32, turboquant_pro/per_channel_kv.py:303-317 with ``qmax = 2**bits - 1``
+    (:179): per channel ``mn``/``mx`` over the tokens,
+    ``scale = max(mx - mn, 1e-8) / qmax``,
+    ``code = clip(round_half_even((x - mn) / scale), 0, qmax)``; outliers as for
     NF4 (the codes at their positions are kept)."""
     x4 = np.asarray(x, dtype=np.float32)[None]
     _, H, S, D = x4.shape
+    qmax = (1 << bits) - 1
     oidx, oval = key_outliers(x4, outlier_frac)
     mn = x4.min(axis=2, keepdims=True)
     mx = x4.max(axis=2, keepdims=True)
-    scale = np.maximum(mx - mn, 1e-8) / 15
-    codes = np.clip(np.round((x4 - mn) / scale), 0, 15).astype(np.uint8)
-    return KeyGroup(codes=codes[0], packed=pack_key_codes(codes, 4),
+    scale = np.maximum(mx - mn, 1e-8) / qmax
+    codes = np.clip(np.round((x4 - mn) / scale), 0, qmax).astype(np.uint8)
+    return KeyGroup(codes=codes[0], packed=pack_key_codes(codes, bits),
                     nf4_scale=scale[0, :, 0, :].astype(np.float32), nf4_mean=mn[0, :, 0, :].astype(np.float32),
-                    outlier_idx=oidx, outlier_val=oval, shape=(1, H, S, D), grid="uniform")
+                    outlier_idx=oidx, outlier_val=oval, shape=(1, H, S, D), grid="uniform", bits=bits)
 
 
 def dc_channel_mask(rope_theta: float, head_dim: int, window: int) -> np.ndarray:
@@ -299,7 +302,7 @@ def decode_keys(g: KeyGroup) -> np.ndarray:
     """Reconstruct (H, S, D) fp32 keys, turboquant_pro/per_channel_kv.py:497-539
     (nf4 branch with calibrated mean, then the fp16 outlier overwrite)."""
     _, H, S, D = g.shape
-    codes = unpack_key_codes(g.packed, H * S * D, 4).reshape(1, H, S, D)
+    codes = unpack_key_codes(g.packed, H * S * D, g.bits).reshape(1, H, S, D)
     if g.grid == "uniform":
         # per_channel_kv.py:529-530: idx * scale + zero, two fp32 roundings
         out = codes.astype(np.float32) * g.nf4_scale[None, :, None, :] + g.nf4_mean[None, :, None, :]
@@ -403,6 +406,7 @@ class SequenceCache:
     outlier_frac: float
     seed: int | None = 0
     key_grid: str = "nf4_asym"       # or "uniform" (per_channel_kv.py:303-317)
+    key_bits: int = 4                # uniform keys: 2, 3 or 4
     zero_point: str = "calibrated"   # asym-NF4: or "sparse" / "bias" (per_channel_kv.py:327-345)
     rope_theta: float | None = None
     k_bias: np.ndarray | None = None
@@ -421,7 +425,8 @@ class SequenceCache:
         for i in range(ng):
             sl = slice(G * i, G * (i + 1))
             if self.key_grid == "uniform":
-                self.keys.append(encode_keys_uniform(k[:, sl].astype(np.float32), self.outlier_frac))
+                self.keys.append(encode_keys_uniform(k[:, sl].astype(np.float32), self.outlier_frac,
+                                                     self.key_bits))
             else:
                 # the flushed block's position_start is the cold length before it
                 self.keys.append(encode_keys(k[:, sl].astype(np.float32), self.outlier_frac,

@@ -12,7 +12,11 @@
 //               then fp32), times the DC mask ("sparse") or given ("bias");
 //               amax = max(max_s |x_s - mu|, 1e-8); cent = mu + amax * NF4[l];
 //               code = first argmin_l |x - cent_l|
-//     uniform:  scale = max(max - min, 1e-8) / 15; code = clip(rint((x - min) / scale), 0, 15)
+//     uniform:  scale = max(max - min, 1e-8) / (2^bits - 1);
+//               code = clip(rint((x - min) / scale), 0, 2^bits - 1)
+//   key packing (per_channel_kv.py:87-100): each code's bits LSB first, in
+//   MSB-first bytes, codes in (b, h, s, j) order (4-bit: byte n =
+//   rev4(code[2n]) << 4 | rev4(code[2n+1]); a token row is 16 * bits bytes)
 //     outliers: threshold = k-th largest |x| over s; every |x| >= it, (s, j) order
 //   values (turboquant_pro/core.py:569-606): pairwise-8 norm, u = x / max(norm, 1e-30),
 //     y_e = sequential over d of u_d * Pi[e][d], code = #{ boundaries < y_e }
@@ -29,6 +33,24 @@ __device__ __forceinline__ float load_x(const void* x, int f32, size_t i) {
 }
 __device__ __forceinline__ bool dc_channel(const tqk_block_desc& d, int j) {
   return (d.dc_mask[j >> 5] >> (j & 31)) & 1u;
+}
+// code c of channel j into a token row of little-endian dwords, in the
+// reference's bit order (bit k of c at stream position j * bits + k, streams
+// filling bytes from their most significant bit)
+__device__ __forceinline__ void put_code_ref(uint32_t* rw, int j, int bits, uint32_t c) {
+  for (int k = 0; k < bits; ++k) {
+    const int p = j * bits + k;
+    rw[p >> 5] |= ((c >> k) & 1u) << (8 * ((p >> 3) & 3) + 7 - (p & 7));
+  }
+}
+// code n of a packed key stream (the reference's bit order)
+__device__ __forceinline__ uint32_t get_code_ref(const uint8_t* packed, size_t n, int bits, size_t nbytes) {
+  const size_t p = n * (size_t)bits, b0 = p >> 3;
+  const uint32_t win = ((uint32_t)packed[b0] << 8) | (b0 + 1 < nbytes ? packed[b0 + 1] : 0u);
+  const int o = (int)(p & 7);
+  uint32_t c = 0;
+  for (int k = 0; k < bits; ++k) c |= ((win >> (15 - o - k)) & 1u) << k;
+  return c;
 }
 
 struct KeyBlockArgs {
@@ -67,7 +89,8 @@ __global__ __launch_bounds__(kKbThreads) void tqk_key_block(KeyBlockArgs a) {
         mn = fminf(mn, xv);
         mx = fmaxf(mx, xv);
       }
-      const float sc = nan ? __builtin_nanf("") : __fdiv_rn(fmaxf(__fsub_rn(mx, mn), 1e-8f), 15.0f);
+      const float sc = nan ? __builtin_nanf("") : __fdiv_rn(fmaxf(__fsub_rn(mx, mn), 1e-8f),
+                                                            (float)((1 << d.bits) - 1));
       if (nan) mn = __builtin_nanf("");
       cent_s[j][0] = mn;
       cent_s[j][1] = sc;
@@ -111,8 +134,22 @@ __global__ __launch_bounds__(kKbThreads) void tqk_key_block(KeyBlockArgs a) {
   }
   __syncthreads();
 
-  // ---- codes: thread = (channel pair, token slice), one byte per (token, pair)
-  {
+  // ---- codes of 3- and 2-bit (uniform) keys: one token row per thread
+  if (d.bits != 4) {
+    const int bits = d.bits, rwords = 4 * bits;  // 16 * bits bytes per token
+    const float qmax = (float)((1 << bits) - 1);
+    for (int s = tid; s < S; s += kKbThreads) {
+      uint32_t rw[16] = {0u};
+      for (int j = 0; j < D; ++j) {
+        const float r = __builtin_rintf(__fdiv_rn(__fsub_rn(X(s, j), cent_s[j][0]), cent_s[j][1]));
+        put_code_ref(rw, j, bits, (uint32_t)fminf(fmaxf(r, 0.0f), qmax));
+      }
+      uint32_t* dst = reinterpret_cast<uint32_t*>(a.packed + ((size_t)bh * S + s) * (size_t)(16 * bits));
+      for (int w = 0; w < rwords; ++w) dst[w] = rw[w];
+    }
+  }
+  // ---- 4-bit codes: thread = (channel pair, token slice), one byte per (token, pair)
+  else {
     const int jp = tid & 63, sq = tid >> 6;
     const int per = (S + 3) / 4, s0 = sq * per, s1 = min(S, s0 + per);
     uint8_t* out = a.packed + base / 2 + jp;
@@ -314,10 +351,21 @@ struct KeyDequantArgs {
   float* out;
 };
 
-// one thread per code byte (two channels): zero + scale * level[code]
+// one thread per code byte (two channels): zero + scale * level[code]; 3- and
+// 2-bit keys one thread per code
 __global__ __launch_bounds__(kKbThreads) void tqk_key_block_dequant(KeyDequantArgs a) {
   constexpr int D = TQK_D;
   const tqk_block_desc& d = a.d;
+  if (d.bits != 4) {
+    const size_t n = (size_t)d.batch * d.n_heads * d.tokens * D;
+    const size_t i = (size_t)blockIdx.x * kKbThreads + threadIdx.x;
+    if (i >= n) return;
+    const size_t bh = i / ((size_t)d.tokens * D);
+    const int j = (int)(i % D);
+    const uint32_t c = get_code_ref(a.packed, i, d.bits, (n * d.bits + 7) / 8);
+    a.out[i] = __fadd_rn(__fmul_rn(a.scale[bh * D + j], (float)c), a.zero[bh * D + j]);
+    return;
+  }
   const size_t n = (size_t)d.batch * d.n_heads * d.tokens * (D / 2);
   const size_t i = (size_t)blockIdx.x * kKbThreads + threadIdx.x;
   if (i >= n) return;
@@ -385,8 +433,9 @@ int check_block(const tqk_block_desc* d, bool key) {
   if (d->batch <= 0 || d->n_heads <= 0 || d->tokens <= 0) return TQK_EINVAL;
   if ((long long)d->batch * d->n_heads * d->tokens * TQK_D >= (1LL << 40)) return TQK_EINVAL;
   if (key) {
-    if (d->bits != 4) return TQK_EUNSUPPORTED;
+    if (d->bits < 2 || d->bits > 4) return TQK_EUNSUPPORTED;
     if (d->key_grid != 0 && d->key_grid != 1) return TQK_EINVAL;
+    if (d->bits != 4 && d->key_grid != 1) return TQK_EUNSUPPORTED;  // NF4 is 4-bit
     if (d->zero_point < 0 || d->zero_point > 2 || (d->zero_point != 0 && d->key_grid != 0))
       return TQK_EINVAL;
     if (d->outliers_per_channel < 0 || d->outlier_cap < 0) return TQK_EINVAL;
@@ -441,13 +490,14 @@ int tqk_dequant_key_block(const tqk_block_desc* d, const uint8_t* packed, const 
   if (!packed || !scale || !zero || !out || n_out < 0 || (n_out > 0 && (!out_idx || !out_val)))
     return TQK_EINVAL;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const size_t n = (size_t)d->batch * d->n_heads * d->tokens * (TQK_D / 2);
+  const size_t total = (size_t)d->batch * d->n_heads * d->tokens * TQK_D;
+  const size_t n = d->bits == 4 ? total / 2 : total;  // threads: code bytes, or codes
   KeyDequantArgs a{*d, packed, scale, zero, out};
   hipLaunchKernelGGL(tqk_key_block_dequant, dim3((unsigned)((n + kKbThreads - 1) / kKbThreads)),
                      dim3(kKbThreads), 0, st, a);
   if (n_out > 0)
     hipLaunchKernelGGL(tqk_key_block_outliers, dim3((n_out + kKbThreads - 1) / kKbThreads),
-                       dim3(kKbThreads), 0, st, out, n_out, (int64_t)(2 * n), out_idx, out_val);
+                       dim3(kKbThreads), 0, st, out, n_out, (int64_t)total, out_idx, out_val);
   return hipGetLastError() == hipSuccess ? TQK_OK : TQK_EHIP;
 }
 

@@ -63,6 +63,31 @@ __host__ __device__ __forceinline__ uint32_t rev4(uint32_t x) {
   return ((x & 1u) << 3) | ((x & 2u) << 1) | ((x & 4u) >> 1) | ((x & 8u) >> 3);
 }
 
+// Key code rows: k_row_bytes(kb) bytes per token.  4-bit keys are the
+// reference's byte stream (byte n = rev4(code[2n]) << 4 | rev4(code[2n+1])).
+// 3- and 2-bit keys (uniform grid) are four 32-channel chunks of
+// k_row_bytes(kb) / 4 bytes; in chunk c the little-endian field i (2*kb bits
+// at bit 2*kb*i) is code(32c + 2i) | code(32c + 2i + 1) << kb.  Either way a
+// channel pair has one table index: the byte, or the field.
+__host__ __device__ __forceinline__ int k_row_bytes(int kb) { return TQK_D * kb / 8; }
+// table index of channel pair `pair` (channels 2*pair, 2*pair + 1) of a row
+// given as little-endian dwords
+__device__ __forceinline__ uint32_t k_pair_index(const uint32_t* rw, int kb, int pair) {
+  if (kb == 4) return (rw[pair >> 2] >> (8 * (pair & 3))) & 0xFFu;
+  const int o = (pair >> 4) * (32 * kb) + 2 * kb * (pair & 15);  // bit offset in the row (32 channels a chunk)
+  const int w = o >> 5, sh = o & 31;
+  uint32_t v = rw[w] >> sh;
+  if (sh + 2 * kb > 32) v |= rw[w + 1] << (32 - sh);
+  return v & ((1u << (2 * kb)) - 1u);
+}
+// the two codes of a table index
+__host__ __device__ __forceinline__ uint32_t k_code_even(uint32_t f, int kb) {
+  return kb == 4 ? rev4(f >> 4) : (f & ((1u << kb) - 1u));
+}
+__host__ __device__ __forceinline__ uint32_t k_code_odd(uint32_t f, int kb) {
+  return kb == 4 ? rev4(f & 15u) : (f >> kb);
+}
+
 // Number of flushed groups after `len` appends: the first flush fires at
 // hot_window + 1 tokens, then every G tokens (turboquant_pro/core.py:1006-1016).
 __host__ __device__ __forceinline__ int n_groups_of(int len, int hot_window, int G) {

@@ -135,8 +135,10 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
   const int gq = Hq / Hkv;
   for (int i = tid; i < GQ * D; i += kThreads)
     q_s[i / D][i % D] = (i / D < gq) ? h2f(a.q[((size_t)b * Hq + h * gq + i / D) * D + i % D]) : 0.f;
-  kl_s[tid][0] = key_level(a.d.key_grid, rev4(tid >> 4));
-  kl_s[tid][1] = key_level(a.d.key_grid, rev4(tid & 15));
+  // key pair table: index of a channel pair (the code byte, or the 3-/2-bit
+  // pair field) -> its two levels
+  kl_s[tid][0] = key_level(a.d.key_grid, k_code_even((uint32_t)tid & 0xFFu, a.d.key_bits) & 15u);
+  kl_s[tid][1] = key_level(a.d.key_grid, k_code_odd((uint32_t)tid & 0xFFu, a.d.key_bits) & 15u);
   // value pair table: field f of two channels' codes -> their two centroids
   if (tid < (1 << (2 * VB))) {
     vl_s[tid][0] = a.p.vcent[tid & ((1 << VB) - 1)];
@@ -188,25 +190,19 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
       float norm_t = 0.f;
       if (tid < G) {
         const size_t row = page_row(bt, d.max_pages_per_seq, b, g * G + tid, P, d.n_pages, h);
-        const uint4* kr = reinterpret_cast<const uint4*>(a.p.kcodes + row * (D / 2));
+        const int kb = d.key_bits;
+        const uint32_t* kr = reinterpret_cast<const uint32_t*>(a.p.kcodes + row * k_row_bytes(kb));
+        uint32_t rw[D / 8];
+        for (int w2 = 0; w2 < k_row_bytes(kb) / 4; ++w2) rw[w2] = kr[w2];
         float s[GQ];
 #pragma unroll
         for (int i = 0; i < GQ; ++i) s[i] = 0.f;
+        for (int jp2 = 0; jp2 < D / 2; ++jp2) {
+          const uint32_t f = k_pair_index(rw, kb, jp2);
+          const int j = 2 * jp2;
+          const float k0 = kl_s[f][0], k1 = kl_s[f][1];
 #pragma unroll
-        for (int c4 = 0; c4 < 4; ++c4) {
-          const uint4 w4 = kr[c4];
-          const uint32_t wv[4] = {w4.x, w4.y, w4.z, w4.w};
-#pragma unroll
-          for (int wi = 0; wi < 4; ++wi) {
-#pragma unroll
-            for (int bi = 0; bi < 4; ++bi) {
-              const uint32_t byte = (wv[wi] >> (8 * bi)) & 0xFFu;
-              const int j = (c4 * 16 + wi * 4 + bi) * 2;
-              const float k0 = kl_s[byte][0], k1 = kl_s[byte][1];
-#pragma unroll
-              for (int i = 0; i < GQ; ++i) s[i] += w_s[i][j] * k0 + w_s[i][j + 1] * k1;
-            }
-          }
+          for (int i = 0; i < GQ; ++i) s[i] += w_s[i][j] * k0 + w_s[i][j + 1] * k1;
         }
 #pragma unroll
         for (int i = 0; i < GQ; ++i) sc_s[i][tid] = (s[i] + bias[i]) * sm;
@@ -223,8 +219,12 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
         const float val = h2f((uint16_t)(ent >> 16));
         const int tt = pos >> 7, j = pos & (D - 1);
         const size_t row = page_row(bt, d.max_pages_per_seq, b, g * G + tt, P, d.n_pages, h);
-        const uint32_t byte = a.p.kcodes[row * (D / 2) + (j >> 1)];
-        const uint32_t c = (j & 1) ? rev4(byte & 15u) : rev4(byte >> 4);
+        const int kb = d.key_bits;
+        const uint32_t* kr = reinterpret_cast<const uint32_t*>(a.p.kcodes + row * k_row_bytes(kb));
+        uint32_t rw[D / 8];
+        for (int w2 = 0; w2 < k_row_bytes(kb) / 4; ++w2) rw[w2] = kr[w2];
+        const uint32_t f = k_pair_index(rw, kb, j >> 1);
+        const uint32_t c = (j & 1) ? k_code_odd(f, kb) : k_code_even(f, kb);
         const float delta = val - (a_s[j] * key_level(a.d.key_grid, c) + mu_s[j]);
 #pragma unroll
         for (int i = 0; i < GQ; ++i) atomicAdd(&sc_s[i][tt], q_s[i][j] * delta * sm);
@@ -383,24 +383,24 @@ constexpr int kLutEntry = 256;   // bytes per table entry
 //   3-bit values: value table [64 entries x 32 copies] at 0, key table
 //                 [256 entries x 32 copies] at kKeyBase3 (80 KiB);
 //   4-bit values: 256 entries x (16 key copies | 16 value copies) (64 KiB).
-template <int VB> struct LutGeom;
-template <> struct LutGeom<2> {
-  static constexpr int kBytes = 16 * 256 + 256 * 256;
-  static constexpr uint32_t kKeyBase = 16 * 256;
-  static constexpr int kCopies = 32;
-  static constexpr uint32_t kValOff = 0;  // value entry e at e*256 + copy*8
-};
-template <> struct LutGeom<3> {
-  static constexpr int kBytes = 64 * 256 + 256 * 256;
-  static constexpr uint32_t kKeyBase = 64 * 256;
-  static constexpr int kCopies = 32;
-  static constexpr uint32_t kValOff = 0;  // value entry e at e*256 + copy*8
-};
-template <> struct LutGeom<4> {
-  static constexpr int kBytes = 256 * 256;
-  static constexpr uint32_t kKeyBase = 0;
-  static constexpr int kCopies = 16;
-  static constexpr uint32_t kValOff = 128;  // value copies after the 16 key copies
+// LDS code tables: entry e holds {fp16 hi pair, fp16 lo pair} (8 bytes) of
+// its two levels in kCopies bank-spread copies (copy c at byte 8c of the
+// entry's 256-byte row).  Key entries: 256 bytes of 4-bit codes, or the
+// 2^(2kb) pair fields of 3-/2-bit codes; value entries: the 2^(2vb) fields.
+// With 4-bit keys and 4-bit values (256 entries each) both share the rows,
+// 16 copies each; otherwise the value rows come first, then the key rows.
+template <int KB, int VB>
+struct LutGeom {
+  static constexpr int kKeyEntries = KB == 4 ? 256 : 1 << (2 * KB);
+  static constexpr int kValEntries = 1 << (2 * VB);
+  static constexpr bool kShared = KB == 4 && VB == 4;
+  static constexpr int kCopies = kShared ? 16 : 32;
+  // at least 64 KiB: after the stream the area holds the waves' coded states
+  // (8 x GQ x (D + 2) floats) and then Pi (D x D floats) for the merge
+  static constexpr int kTableBytes = kShared ? 256 * 256 : (kKeyEntries + kValEntries) * 256;
+  static constexpr int kBytes = kTableBytes > 65536 ? kTableBytes : 65536;
+  static constexpr uint32_t kKeyBase = kShared ? 0u : (uint32_t)kValEntries * 256u;
+  static constexpr uint32_t kValOff = kShared ? 128u : 0u;  // value copy base inside a row
 };
 
 __device__ __forceinline__ uint2 split_pair(float x0, float x1) {
@@ -666,10 +666,11 @@ __device__ __forceinline__ H8 dup_quad(float x0, float x1, float x2, float x3, f
   return r;
 }
 
-template <int GQ, int VB>
+template <int GQ, int VB, int KB>
 __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs a) {
   constexpr int D = TQK_D;
   constexpr int VROW = D * VB / 8;
+  constexpr int KROW = D * KB / 8;  // key code bytes per token (tqk_common.h layout)
   constexpr int UNIT = VROW / 4;
   // 1-D grid over (split, kv head, seq), split fastest.  Every workgroup
   // streams the coded groups of its split and then its share of the fp16 hot
@@ -726,7 +727,10 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   // scores in the log2 domain: q * sm_scale * log2(e), softmax with exp2
   const float qscale = d.sm_scale * 1.4426950408889634f;
 
-  __shared__ __align__(16) uint8_t lut[LutGeom<VB>::kBytes];
+  __shared__ __align__(16) uint8_t lut[LutGeom<KB, VB>::kBytes];
+  // the area's later uses: the coded wave states of the fold, Pi in the merge
+  static_assert(LutGeom<KB, VB>::kBytes >= (int)sizeof(float) * kMWaves * GQ * (D + 2), "fold area");
+  static_assert(LutGeom<KB, VB>::kBytes >= (int)sizeof(float) * D * D, "Pi area");
   __shared__ __align__(16) uint32_t qq_s[D][GQ];        // raw fp16 q twice {q, q}: [channel][head]
   __shared__ __align__(16) uint16_t qf_s[GQ][D];        // raw fp16 q, head-major (hot-window operand)
   // scaled q, head-major; rows padded by 4 banks so that the head rows read by
@@ -786,18 +790,19 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     // unit u (8 bytes): key part first (entry u / copies, copy u % copies), then values;
     // consecutive lanes write consecutive units; levels come from LDS, so the
     // fill issues no memory loads
-    using LG = LutGeom<VB>;
+    using LG = LutGeom<KB, VB>;
     constexpr int NC = LG::kCopies;
-    constexpr int NV = 1 << (2 * VB);
-    for (int u = tid; u < 256 * NC + NV * NC; u += kMThreads) {
+    constexpr int NK = LG::kKeyEntries;
+    constexpr int NV = LG::kValEntries;
+    for (int u = tid; u < NK * NC + NV * NC; u += kMThreads) {
       uint2 val;
       uint32_t off;
-      if (u < 256 * NC) {
-        const int e = u / NC;
-        val = split_pair(lvl_s[rev4((uint32_t)e >> 4)], lvl_s[rev4((uint32_t)e & 15u)]);
+      if (u < NK * NC) {
+        const uint32_t e = (uint32_t)(u / NC);
+        val = split_pair(lvl_s[k_code_even(e, KB)], lvl_s[k_code_odd(e, KB)]);
         off = LG::kKeyBase + (uint32_t)e * kLutEntry + (uint32_t)(u % NC) * 8u;
       } else {
-        const int v = u - 256 * NC, e = v / NC, m = (1 << VB) - 1;
+        const int v = u - NK * NC, e = v / NC, m = (1 << VB) - 1;
         val = split_pair(lvl_s[16 + (e & m)], lvl_s[16 + (e >> VB)]);
         off = (uint32_t)e * kLutEntry + LG::kValOff + (uint32_t)(v % NC) * 8u;
       }
@@ -818,10 +823,10 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   reset_state(st);
 
   {
-    constexpr int NC = LutGeom<VB>::kCopies;
+    constexpr int NC = LutGeom<KB, VB>::kCopies;
     const uint32_t koff = (uint32_t)(lane % NC) * 8u;
-    const uint32_t voff = LutGeom<VB>::kValOff + (uint32_t)(lane % NC) * 8u;
-    const uint8_t* __restrict__ klut = lut + LutGeom<VB>::kKeyBase;
+    const uint32_t voff = LutGeom<KB, VB>::kValOff + (uint32_t)(lane % NC) * 8u;
+    const uint8_t* __restrict__ klut = lut + LutGeom<KB, VB>::kKeyBase;
     const int cap = d.outlier_cap;
     // outlier entries are read at clamped indices (never past the group's list)
     const uint32_t* __restrict__ oent_all = cap > 0 ? a.p.oent : reinterpret_cast<const uint32_t*>(a.p.ocount);
@@ -834,7 +839,8 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     const int nblk = G / 32;
     const int T = nw * nblk;
     // per-lane parts of the block addresses (the row parts are wave-uniform)
-    const uint32_t koffL = (uint32_t)c * (D / 2) + 16u * (uint32_t)lg;
+    // (the lane's token row c, its 32-channel chunk lg)
+    const uint32_t koffL = (uint32_t)c * KROW + (uint32_t)(KROW / 4) * (uint32_t)lg;
     const uint32_t uoffL = (uint32_t)(16 * lg + c) * UNIT;
     const int ntl = 4 * lg + (c & 3);  // token (of tile A if c & 4 == 0, else B) whose norm this lane reads
     // outlier entries eidx, eidx + 1 of a block are this lane's: the four
@@ -852,7 +858,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     // buffer resources of this head's page regions (32-bit offsets:
     // mfma_path() bounds a head's region below 4 GiB)
     const uint32_t hrows = (uint32_t)d.n_pages * (uint32_t)P;
-    const __amdgpu_buffer_rsrc_t rk = buf_rsrc(a.p.kcodes + (size_t)h * hrows * (D / 2), hrows * (D / 2));
+    const __amdgpu_buffer_rsrc_t rk = buf_rsrc(a.p.kcodes + (size_t)h * hrows * KROW, hrows * KROW);
     const __amdgpu_buffer_rsrc_t rv = buf_rsrc(a.p.vcodes + (size_t)h * hrows * VROW, hrows * VROW);
     const __amdgpu_buffer_rsrc_t rn = buf_rsrc(a.p.vnorm + (size_t)h * hrows, hrows * 4u);
 
@@ -867,11 +873,21 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       const uint32_t obase = (uint32_t)meta_l(16 + TQK_NOB);
       const int e0 = kbl == 0 ? 0 : meta_l(16 + kbl - 1);
       const int e1 = meta_l(16 + kbl);
-      {
-        const u32x4_t x = __builtin_amdgcn_raw_buffer_load_b128(rk, (int)koffL, (int)(rowA * (D / 2)), 0);
-        const u32x4_t y = __builtin_amdgcn_raw_buffer_load_b128(rk, (int)koffL, (int)(rowB * (D / 2)), 0);
+      if constexpr (KB == 4) {
+        const u32x4_t x = __builtin_amdgcn_raw_buffer_load_b128(rk, (int)koffL, (int)(rowA * KROW), 0);
+        const u32x4_t y = __builtin_amdgcn_raw_buffer_load_b128(rk, (int)koffL, (int)(rowB * KROW), 0);
         cb.kA = make_uint4(x.x, x.y, x.z, x.w);
         cb.kB = make_uint4(y.x, y.y, y.z, y.w);
+      } else if constexpr (KB == 3) {
+        const u32x3_t x = __builtin_amdgcn_raw_buffer_load_b96(rk, (int)koffL, (int)(rowA * KROW), 0);
+        const u32x3_t y = __builtin_amdgcn_raw_buffer_load_b96(rk, (int)koffL, (int)(rowB * KROW), 0);
+        cb.kA = make_uint4(x.x, x.y, x.z, 0u);
+        cb.kB = make_uint4(y.x, y.y, y.z, 0u);
+      } else {
+        const u32x2_t x = __builtin_amdgcn_raw_buffer_load_b64(rk, (int)koffL, (int)(rowA * KROW), 0);
+        const u32x2_t y = __builtin_amdgcn_raw_buffer_load_b64(rk, (int)koffL, (int)(rowB * KROW), 0);
+        cb.kA = make_uint4(x.x, x.y, 0u, 0u);
+        cb.kB = make_uint4(y.x, y.y, 0u, 0u);
       }
       if constexpr (VB == 2) {
         const u32x2_t x = __builtin_amdgcn_raw_buffer_load_b64(rv, (int)uoffL, (int)(rowA * VROW), 0);
@@ -964,12 +980,32 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       // A operand of QK^T MFMA m from the lane's key bytes (a table row of a code
       // byte is {fp16 hi pair, fp16 lo pair} of its two channels)
       auto key_quad = [&](const uint4& k, int m) {
-        const uint32_t word = (m >> 1) == 0 ? k.x : (m >> 1) == 1 ? k.y : (m >> 1) == 2 ? k.z : k.w;
-        const uint32_t q0 = 2u * (uint32_t)(m & 1);
-        const uint2 t0 = *reinterpret_cast<const uint2*>(
-            klut + __builtin_amdgcn_perm(word, koff, 0x0C0C0000u | ((4u + q0) << 8)));
-        const uint2 t1 = *reinterpret_cast<const uint2*>(
-            klut + __builtin_amdgcn_perm(word, koff, 0x0C0C0000u | ((5u + q0) << 8)));
+        uint32_t a0, a1;  // table addresses of channel pairs 2m, 2m + 1 of the chunk
+        if constexpr (KB == 4) {
+          // a code byte is the index: one v_perm puts it above the copy offset
+          const uint32_t word = (m >> 1) == 0 ? k.x : (m >> 1) == 1 ? k.y : (m >> 1) == 2 ? k.z : k.w;
+          const uint32_t q0 = 2u * (uint32_t)(m & 1);
+          a0 = __builtin_amdgcn_perm(word, koff, 0x0C0C0000u | ((4u + q0) << 8));
+          a1 = __builtin_amdgcn_perm(word, koff, 0x0C0C0000u | ((5u + q0) << 8));
+        } else {
+          uint32_t f0 = 0, f1 = 0;
+          if constexpr (KB == 3) {
+            switch (m) {
+#define TQK_K3(M) case M: f0 = v3_field<2 * M>(k); f1 = v3_field<2 * M + 1>(k); break;
+              TQK_K3(0) TQK_K3(1) TQK_K3(2) TQK_K3(3) TQK_K3(4) TQK_K3(5) TQK_K3(6) TQK_K3(7)
+#undef TQK_K3
+            }
+          } else {
+            // 4-bit fields 2m, 2m + 1 at bits 8m, 8m + 4 of the 64-bit chunk
+            const uint32_t word = m < 4 ? k.x : k.y;
+            f0 = (word >> (8 * (m & 3))) & 15u;
+            f1 = (word >> (8 * (m & 3) + 4)) & 15u;
+          }
+          a0 = (f0 << 8) | koff;
+          a1 = (f1 << 8) | koff;
+        }
+        const uint2 t0 = *reinterpret_cast<const uint2*>(klut + a0);
+        const uint2 t1 = *reinterpret_cast<const uint2*>(klut + a1);
         H8 r;
         r.u[0] = t0.x;
         r.u[1] = t0.y;
@@ -1701,6 +1737,16 @@ Plan make_plan(const tqk_cache_desc* d, int batch, int max_len) {
   return pl;
 }
 
+template <int GQ, int KB>
+void launch_mfma_kb(const DecodeArgs& a, dim3 g1, hipStream_t st) {
+  if (a.d.value_bits == 2)
+    hipLaunchKernelGGL((tqk_decode_split_mfma<GQ, 2, KB>), g1, dim3(kMThreads), 0, st, a);
+  else if (a.d.value_bits == 3)
+    hipLaunchKernelGGL((tqk_decode_split_mfma<GQ, 3, KB>), g1, dim3(kMThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL((tqk_decode_split_mfma<GQ, 4, KB>), g1, dim3(kMThreads), 0, st, a);
+}
+
 template <int GQ>
 hipError_t launch_split(const DecodeArgs& a, dim3 grid, hipStream_t st) {
   if (!mfma_path(a.d)) {
@@ -1714,12 +1760,12 @@ hipError_t launch_split(const DecodeArgs& a, dim3 grid, hipStream_t st) {
   }
   // one-dimensional over (split, kv head, seq) items
   const dim3 g1(grid.x * grid.y * grid.z);
-  if (a.d.value_bits == 2)
-    hipLaunchKernelGGL((tqk_decode_split_mfma<GQ, 2>), g1, dim3(kMThreads), 0, st, a);
-  else if (a.d.value_bits == 3)
-    hipLaunchKernelGGL((tqk_decode_split_mfma<GQ, 3>), g1, dim3(kMThreads), 0, st, a);
+  if (a.d.key_bits == 4)
+    launch_mfma_kb<GQ, 4>(a, g1, st);
+  else if (a.d.key_bits == 3)
+    launch_mfma_kb<GQ, 3>(a, g1, st);
   else
-    hipLaunchKernelGGL((tqk_decode_split_mfma<GQ, 4>), g1, dim3(kMThreads), 0, st, a);
+    launch_mfma_kb<GQ, 2>(a, g1, st);
   return hipGetLastError();
 }
 
@@ -1874,13 +1920,15 @@ int noalloc_scratch(hipStream_t stream, void** out) {
 
 extern "C" {
 
-int tqk_version(void) { return 6; }
+int tqk_version(void) { return 7; }
 
 int tqk_check_desc(const tqk_cache_desc* d) {
   if (!d) return TQK_EINVAL;
   if (d->head_dim != TQK_D) return TQK_EUNSUPPORTED;
-  if (d->key_bits != 4) return TQK_EUNSUPPORTED;
+  if (d->key_bits < 2 || d->key_bits > 4) return TQK_EUNSUPPORTED;
   if (d->key_grid != 0 && d->key_grid != 1) return TQK_EINVAL;
+  // NF4 is a 4-bit grid; 3- and 2-bit keys are uniform
+  if (d->key_bits != 4 && d->key_grid != 1) return TQK_EUNSUPPORTED;
   if (d->value_bits < 2 || d->value_bits > 4) return TQK_EUNSUPPORTED;
   if (d->zero_point < 0 || d->zero_point > 2 || (d->zero_point != 0 && d->key_grid != 0))
     return TQK_EINVAL;

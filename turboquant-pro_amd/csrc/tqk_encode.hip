@@ -80,7 +80,7 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
   const size_t mbase = ((size_t)slot * Hkv + h) * D;
   if (tid < D && d.key_grid == 1) {
     // uniform keys (turboquant_pro/per_channel_kv.py:303-306): channel min and
-    // max over the tokens, scale = max(max - min, 1e-8) / 15 (NaN propagates)
+    // max over the tokens, scale = max(max - min, 1e-8) / (2^bits - 1) (NaN propagates)
     const int j = tid;
     float mn = h2f(kt_s[0][j]), mx = mn;
     bool nan = (mn != mn);
@@ -91,7 +91,7 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
       mx = fmaxf(mx, xv);
     }
     const float rng = __fsub_rn(mx, mn);
-    const float sc = nan ? __builtin_nanf("") : __fdiv_rn(fmaxf(rng, 1e-8f), 15.0f);
+    const float sc = nan ? __builtin_nanf("") : __fdiv_rn(fmaxf(rng, 1e-8f), (float)((1 << d.key_bits) - 1));
     if (nan) mn = __builtin_nanf("");
     cent_s[j][0] = mn;
     cent_s[j][1] = sc;
@@ -142,8 +142,9 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
 
   // ---- codes: thread = (channel pair, token slice); one byte per (token, pair)
   if (d.key_grid == 1) {
-    // uniform: clip(round_half_even((x - min) / scale), 0, 15)
-    const int jp = tid & 63, sq = tid >> 6;
+    // uniform: clip(round_half_even((x - min) / scale), 0, 2^bits - 1)
+    const int jp = tid & 63, sq = tid >> 6, kb = d.key_bits;
+    const float qmax = (float)((1 << kb) - 1);
     const float mn0 = cent_s[2 * jp][0], sc0 = cent_s[2 * jp][1];
     const float mn1 = cent_s[2 * jp + 1][0], sc1 = cent_s[2 * jp + 1][1];
     const int per_q = (G + kEncWaves - 1) / kEncWaves;
@@ -151,9 +152,10 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
     for (int s = s0; s < s1; ++s) {
       const float r0 = __builtin_rintf(__fdiv_rn(__fsub_rn(h2f(kt_s[s][2 * jp]), mn0), sc0));
       const float r1 = __builtin_rintf(__fdiv_rn(__fsub_rn(h2f(kt_s[s][2 * jp + 1]), mn1), sc1));
-      const uint32_t b0 = (uint32_t)fminf(fmaxf(r0, 0.0f), 15.0f);
-      const uint32_t b1 = (uint32_t)fminf(fmaxf(r1, 0.0f), 15.0f);
-      kc_s[s][jp] = (uint8_t)((rev4(b0) << 4) | rev4(b1));
+      const uint32_t b0 = (uint32_t)fminf(fmaxf(r0, 0.0f), qmax);
+      const uint32_t b1 = (uint32_t)fminf(fmaxf(r1, 0.0f), qmax);
+      // one table index per channel pair (the key row layout of tqk_common.h)
+      kc_s[s][jp] = (uint8_t)(kb == 4 ? ((rev4(b0) << 4) | rev4(b1)) : (b0 | (b1 << kb)));
     }
   } else {
     const int jp = tid & 63, sq = tid >> 6;
@@ -223,9 +225,15 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
             // zero level (rev4(7) = 14), or code 0 of a uniform grid -- so the
             // dense part of a decode contributes only gmean here and the
             // side-list adds val - gmean; export restores the reference's code
-            const uint32_t zc = d.key_grid == 1 ? 0u : 14u;
-            uint8_t& kb = kc_s[tid][j >> 1];
-            kb = (j & 1) ? (uint8_t)((kb & 0xF0u) | zc) : (uint8_t)((kb & 0x0Fu) | (zc << 4));
+            uint8_t& kp = kc_s[tid][j >> 1];
+            if (d.key_bits == 4) {
+              const uint32_t zc = d.key_grid == 1 ? 0u : 14u;
+              kp = (j & 1) ? (uint8_t)((kp & 0xF0u) | zc) : (uint8_t)((kp & 0x0Fu) | (zc << 4));
+            } else {
+              // 3- and 2-bit keys are uniform: the pair field's code of channel j to 0
+              const uint32_t m = (1u << d.key_bits) - 1u;
+              kp = (uint8_t)(kp & ~((j & 1) ? (m << d.key_bits) : m));
+            }
           }
           ++off;
         }
@@ -243,12 +251,28 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
   // re-assembled into 4-token x 8-channel units below
   uint8_t (*vc_s)[D] = reinterpret_cast<uint8_t (*)[D]>(&kt_s[0][0]);
   __syncthreads();
-  // key code rows, 16 bytes per thread
+  // key code rows, one 32-channel chunk (16 pair indices) per thread
+  const int KROW = k_row_bytes(d.key_bits);
   for (int idx = tid; idx < G * (D / 32); idx += kEncThreads) {
     const int t = idx / (D / 32), ch = idx % (D / 32);
     const size_t row = page_row(a.p.block_table, d.max_pages_per_seq, b, g * G + t, P, d.n_pages, h);
-    *reinterpret_cast<uint4*>(a.p.kcodes + row * (D / 2) + 16 * ch) =
-        *reinterpret_cast<const uint4*>(&kc_s[t][16 * ch]);
+    const uint4 f16 = *reinterpret_cast<const uint4*>(&kc_s[t][16 * ch]);
+    if (d.key_bits == 4) {
+      *reinterpret_cast<uint4*>(a.p.kcodes + row * KROW + 16 * ch) = f16;
+    } else {
+      // 16 fields of 2*kb bits, little-endian, into kb dwords
+      const int kb = d.key_bits;
+      const uint32_t fw[4] = {f16.x, f16.y, f16.z, f16.w};
+      uint32_t o[3] = {0u, 0u, 0u};
+      for (int i = 0; i < 16; ++i) {
+        const uint32_t f = (fw[i >> 2] >> (8 * (i & 3))) & 0xFFu;
+        const int bo = 2 * kb * i, w = bo >> 5, sh = bo & 31;
+        o[w] |= f << sh;
+        if (sh + 2 * kb > 32) o[w + 1] |= f >> (32 - sh);
+      }
+      uint32_t* dst = reinterpret_cast<uint32_t*>(a.p.kcodes + row * KROW + (KROW / 4) * ch);
+      for (int w = 0; w < kb; ++w) dst[w] = o[w];
+    }
   }
   // Rotation operands: lane e of wave w owns rotated channel
   // 64 * (w & 1) + lane and keeps column e of Pi_T (pi[e][0..D)) in
@@ -441,14 +465,17 @@ __global__ __launch_bounds__(kThreads) void tqk_dequant_group(DequantArgs a) {
   float* vo = a.vout + ((size_t)item * Hkv + h) * G * D;
   if (tid < G) {
     const size_t row = page_row(a.p.block_table, d.max_pages_per_seq, b, g * G + tid, P, d.n_pages, h);
-    const uint8_t* kr = a.p.kcodes + row * (D / 2);
+    const int kb = d.key_bits, KROW = k_row_bytes(kb);
+    uint32_t rw[TQK_D / 8];
+    const uint32_t* kr = reinterpret_cast<const uint32_t*>(a.p.kcodes + row * KROW);
+    for (int w = 0; w < KROW / 4; ++w) rw[w] = kr[w];
     for (int jj = 0; jj < D / 2; ++jj) {
-      const uint32_t byte = kr[jj];
+      const uint32_t f = k_pair_index(rw, kb, jj);
       const int j0 = 2 * jj, j1 = 2 * jj + 1;
       ko[(size_t)tid * D + j0] =
-          __fadd_rn(__fmul_rn(a.p.gscale[mbase + j0], key_level(d.key_grid, rev4(byte >> 4))), a.p.gmean[mbase + j0]);
+          __fadd_rn(__fmul_rn(a.p.gscale[mbase + j0], key_level(d.key_grid, k_code_even(f, kb))), a.p.gmean[mbase + j0]);
       ko[(size_t)tid * D + j1] =
-          __fadd_rn(__fmul_rn(a.p.gscale[mbase + j1], key_level(d.key_grid, rev4(byte & 15u))), a.p.gmean[mbase + j1]);
+          __fadd_rn(__fmul_rn(a.p.gscale[mbase + j1], key_level(d.key_grid, k_code_odd(f, kb))), a.p.gmean[mbase + j1]);
     }
     float y[D];
     if (v_tiled(G, P)) {

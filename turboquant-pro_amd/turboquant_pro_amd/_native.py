@@ -19,7 +19,7 @@ TQK_EUNSUPPORTED = 2
 TQK_EHIP = 3
 TQK_EWORKSPACE = 4
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 # Every symbol include/tqk.h declares (checked by the CPU test suite).
 EXPORTS = (

@@ -135,8 +135,8 @@ class AutoConfig:
         asym-NF4 keys with the resolved zero point (``bias`` needs this layer's
         ``k_bias``) + ``outlier_frac`` fp16 outliers.  ``n_q_heads`` (default:
         one query per kv-head, as the reference's cache) serves GQA queries.
-        ``robust=False`` (uniform keys) builds 4-bit uniform keys and raises
-        ``NotImplementedError`` at other key widths: they have no gfx950 form."""
+        ``robust=False`` builds uniform keys at the config's key width, as the
+        reference's plain per-channel cache."""
         from .core import TurboQuantKVCache
         zp = self.resolve_key_zero_point(k_bias is not None) if robust else "calibrated"
         return TurboQuantKVCache(

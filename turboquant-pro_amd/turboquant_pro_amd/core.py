@@ -3,9 +3,10 @@
 Same constructor, methods and return conventions as the reference's
 ``TurboQuantKVCache`` (turboquant_pro/core.py:818-1307): one sequence, an fp16
 hot window of ``hot_window`` tokens, and flushed groups of
-``(hot_window + 1) // 2`` tokens coded as per-channel 4-bit keys (asym-NF4
-with a calibrated, sparse or bias zero point, or uniform) with an fp16
-outlier side-list plus 2/3/4-bit PolarQuant values.  Storage and compute live on the GPU:
+``(hot_window + 1) // 2`` tokens coded as per-channel keys (4-bit asym-NF4
+with a calibrated, sparse or bias zero point, or uniform 2/3/4-bit -- the
+reference's default) with an fp16 outlier side-list plus 2/3/4-bit PolarQuant
+values.  Storage and compute live on the GPU:
 ``append`` runs the quantize-on-flush kernel when a group completes,
 ``fused_decode`` runs the fused split-K kernel, ``get_keys``/``get_values``
 reconstruct on the GPU.
@@ -16,8 +17,8 @@ Differences from the reference, all deliberate:
     AutoConfig default and the point of this build);
   * keys/values/queries are converted to fp16 on entry (the serving dtype the
     kernels consume); codes are bit-exact with the reference for fp16 inputs;
-  * configurations without a gfx950 form (PolarQuant, 2/3-bit uniform,
-    symmetric-NF4 and quantile keys; head_dim != 128) raise
+  * configurations without a gfx950 form (PolarQuant, symmetric-NF4 and
+    quantile keys; head_dim != 128) raise
     NotImplementedError at construction instead of silently running on the CPU;
   * an optional ``n_q_heads`` (a multiple of ``n_heads``) serves GQA queries.
 """
@@ -93,13 +94,14 @@ class TurboQuantKVCache:
             key_k_bias = np.asarray(key_k_bias, dtype=np.float32).reshape(n_heads, head_dim)
         self.key_rope_theta, self.key_k_bias = key_rope_theta, key_k_bias
         # per-channel keys: asym-NF4 (robust / build_cache) or, without any NF4
-        # or quantile flag, the reference's uniform 4-bit mode
-        uniform = per_channel_keys and not key_nuq and not key_nf4 and self.key_bits == 4
+        # or quantile flag, the reference's uniform mode (its default, at 2, 3 or
+        # 4 bits)
+        uniform = per_channel_keys and not key_nuq and not key_nf4
         if not per_channel_keys or key_nuq or not (key_nf4_asym or uniform):
             raise NotImplementedError(
-                "the gfx950 cache codes keys as per-channel asym-NF4 (TurboQuantKVCache.robust / "
-                "AutoConfig.build_cache) or uniform 4-bit; PolarQuant, 2/3-bit uniform, "
-                "symmetric-NF4 and quantile keys have no GPU form here")
+                "the gfx950 cache codes keys per channel, as asym-NF4 (TurboQuantKVCache.robust / "
+                "AutoConfig.build_cache) or uniform 2/3/4-bit; PolarQuant, symmetric-NF4 and "
+                "quantile keys have no GPU form here")
         self.key_grid = "uniform" if uniform else "nf4_asym"
         if head_dim != 128:
             raise NotImplementedError("the gfx950 kernels are built for head_dim=128")

@@ -8,6 +8,10 @@ container byte layouts (host side, NumPy; used for export and inspection).
   exactly the channel mean there and the side-list adds ``val - mean``.  The
   reference's code at such a position is the nearest level to the stored fp16
   value; :func:`restore_outlier_codes` puts it back on export.
+* 3- and 2-bit key codes (uniform grid) are stored as 32-channel chunks of
+  pair fields (:func:`key_rows_from_codes`), a permutation of the reference's
+  bit stream (:func:`pack_key_codes`) that gives every decode lane its 32
+  channels in one load and a channel pair in one field.
 * Value codes are the reference's little-endian pack
   (turboquant_pro/core.py:350-398) when stored per token; with the MFMA-tiled
   order (page_tokens % 16 == 0 and group_tokens % 32 == 0) each 16-token tile
@@ -47,12 +51,56 @@ def nf4_codes(x: np.ndarray, scale: np.ndarray, mean: np.ndarray) -> np.ndarray:
     return np.argmin(np.abs(x - cent), axis=-1).astype(np.uint8)
 
 
-def uniform_codes(x: np.ndarray, scale: np.ndarray, zero: np.ndarray) -> np.ndarray:
+def uniform_codes(x: np.ndarray, scale: np.ndarray, zero: np.ndarray, bits: int = 4) -> np.ndarray:
     """Uniform key code of fp32 ``x`` (turboquant_pro/per_channel_kv.py:306):
-    ``clip(round_half_even((x - zero) / scale), 0, 15)`` in fp32."""
+    ``clip(round_half_even((x - zero) / scale), 0, 2**bits - 1)`` in fp32."""
     x = np.asarray(x, np.float32)
     q = (x - np.asarray(zero, np.float32)) / np.asarray(scale, np.float32)
-    return np.clip(np.round(q), 0, 15).astype(np.uint8)
+    return np.clip(np.round(q), 0, (1 << bits) - 1).astype(np.uint8)
+
+
+def pack_key_codes(codes: np.ndarray, bits: int) -> np.ndarray:
+    """Flat key codes -> the reference's key bytes (turboquant_pro/per_channel_kv.py:87-93):
+    each code's ``bits`` low bits least significant first, the bit stream
+    filling every byte from its most significant bit."""
+    c = np.ascontiguousarray(codes, dtype=np.uint8).reshape(-1)
+    stream = ((c[:, None] >> np.arange(bits, dtype=np.uint8)) & 1).astype(np.uint8).reshape(-1)
+    stream = np.concatenate([stream, np.zeros((-stream.size) % 8, np.uint8)]).reshape(-1, 8)
+    return (stream << np.arange(7, -1, -1, dtype=np.uint8)).sum(axis=1, dtype=np.uint32).astype(np.uint8)
+
+
+def unpack_key_codes(packed: np.ndarray, n_values: int, bits: int) -> np.ndarray:
+    """The inverse of :func:`pack_key_codes` (turboquant_pro/per_channel_kv.py:94-100)."""
+    b = np.asarray(packed, np.uint8).reshape(-1)
+    stream = ((b[:, None] >> np.arange(7, -1, -1, dtype=np.uint8)) & 1).reshape(-1)[: n_values * bits]
+    return (stream.reshape(n_values, bits).astype(np.uint16) << np.arange(bits, dtype=np.uint16)).sum(
+        axis=1).astype(np.uint8)
+
+
+def key_rows_from_codes(codes: np.ndarray, bits: int) -> np.ndarray:
+    """Codes ``(n, D)`` -> stored key rows ``(n, D * bits / 8)``: 4-bit keys in
+    the reference's pack; 3- and 2-bit keys as four 32-channel chunks of
+    little-endian pair fields (field i of chunk c = code(32c + 2i) |
+    code(32c + 2i + 1) << bits at bit 2 * bits * i)."""
+    codes = np.asarray(codes, np.uint8)
+    n, D = codes.shape
+    if bits == 4:
+        return pack_key_codes(codes, 4).reshape(n, D // 2)
+    # inside a chunk, channel k's code starts at bit bits * k (fields are
+    # consecutive pairs), its bits least significant first
+    bitv = ((codes[:, :, None] >> np.arange(bits, dtype=np.uint8)) & 1).astype(np.uint8)
+    return np.packbits(bitv.reshape(n, D // 32, 32 * bits), axis=-1, bitorder="little").reshape(n, D * bits // 8)
+
+
+def codes_from_key_rows(rows: np.ndarray, bits: int, D: int = 128) -> np.ndarray:
+    """The inverse of :func:`key_rows_from_codes`: stored rows -> codes ``(n, D)``."""
+    rows = np.asarray(rows, np.uint8)
+    n = rows.shape[0]
+    if bits == 4:
+        return unpack_keys(rows.reshape(-1), n * D).reshape(n, D)
+    bitv = np.unpackbits(rows.reshape(n, D // 32, D * bits // 32), axis=-1, bitorder="little")
+    bitv = bitv.reshape(n, D, bits).astype(np.uint8)
+    return (bitv << np.arange(bits, dtype=np.uint8)).sum(axis=-1, dtype=np.uint32).astype(np.uint8)
 
 
 def restore_outlier_codes(kp: np.ndarray, idx: np.ndarray, val: np.ndarray,

@@ -38,7 +38,7 @@ from typing import Any, Protocol, runtime_checkable
 import numpy as np
 
 from .codebooks import outliers_per_channel, random_rotation
-from .formats import NF4, pack_values, unpack_keys, unpack_values
+from .formats import NF4, pack_values, unpack_key_codes, unpack_values
 
 logger = logging.getLogger(__name__)
 
@@ -286,14 +286,14 @@ _ZERO_POINTS = {"calibrated": 0, "sparse": 1, "bias": 2}
 
 class PerChannelKVQuantizer:
     """``"per_channel"`` keys on the gfx950 library: asym-NF4 4-bit (zero
-    point "calibrated", "sparse" or "bias") or uniform 4-bit (the reference's
-    default mode), with the fp16 outlier side-list; every (b, h) pair of a
-    block is one group.
+    point "calibrated", "sparse" or "bias") or uniform 2-, 3- or 4-bit (the
+    reference's default mode), with the fp16 outlier side-list; every (b, h)
+    pair of a block is one group.
 
     The constructor validates like ``PerChannelKV.__init__``
     (turboquant_pro/per_channel_kv.py:182-213) and raises
     ``NotImplementedError`` for the modes the library does not encode
-    (2/3-bit uniform, symmetric NF4, data-fit quantiles, head_dim != 128)."""
+    (symmetric NF4, data-fit quantiles, head_dim != 128)."""
 
     _ZP_MODES = ("calibrated", "sparse", "bias")
 
@@ -318,10 +318,10 @@ class PerChannelKVQuantizer:
                 raise ValueError(f"zero_point={zero_point!r} requires rope_theta")
         if zero_point == "bias" and k_bias is None:
             raise ValueError('zero_point="bias" requires k_bias')
-        uniform = bits == 4 and not nf4 and not nuq
+        uniform = not nf4 and not nuq
         if not (nf4_asym or uniform) or head_dim != 128:
-            raise NotImplementedError("the gfx950 key encode is per-channel 4-bit, asym-NF4 (any zero "
-                                      "point) or uniform, at head_dim 128")
+            raise NotImplementedError("the gfx950 key encode is per-channel asym-NF4 (any zero point) "
+                                      "or uniform 2/3/4-bit, at head_dim 128")
         self.head_dim, self.n_heads, self.bits = head_dim, n_heads, bits
         self.uniform = uniform
         self.key_grid = "uniform" if uniform else "nf4_asym"
@@ -355,7 +355,7 @@ class PerChannelKVQuantizer:
             zp = torch.from_numpy(rope_averaged_bias(self.k_bias, self.rope_theta, D, position_start, S)
                                   ).to(xt.device)
         u8, f32t, i32 = torch.uint8, torch.float32, torch.int32
-        kp = torch.empty(B * H * S * D // 2, dtype=u8, device=xt.device)
+        kp = torch.empty(B * H * S * D * self.bits // 8, dtype=u8, device=xt.device)
         scale = torch.empty((B, H, D), dtype=f32t, device=xt.device)
         zero = torch.empty_like(scale)
         count = torch.zeros(B * H, dtype=i32, device=xt.device)
@@ -363,7 +363,7 @@ class PerChannelKVQuantizer:
         while True:
             pos = torch.empty((B * H, max(cap, 1)), dtype=torch.int32, device=xt.device)
             val = torch.empty((B * H, max(cap, 1)), dtype=torch.float16, device=xt.device)
-            d = _block_desc(xt.shape, 4, int(self.uniform), _ZERO_POINTS[zp_mode], k, cap, f32, dc)
+            d = _block_desc(xt.shape, self.bits, int(self.uniform), _ZERO_POINTS[zp_mode], k, cap, f32, dc)
             N.check(N.lib().tqk_encode_key_block(
                 ctypes.byref(d), xt.data_ptr(), zp.data_ptr() if zp is not None else None,
                 kp.data_ptr(), scale.data_ptr(), zero.data_ptr(), pos.data_ptr(), val.data_ptr(),
@@ -380,7 +380,7 @@ class PerChannelKVQuantizer:
             oidx = np.concatenate([pos_np[i, :cnt[i]].astype(np.int64) + i * S * D
                                    for i in range(B * H)]).astype(np.int32)
             oval = np.concatenate([val_np[i, :cnt[i]] for i in range(B * H)]).astype(np.float16)
-        indices = kp_np if packed else unpack_keys(kp_np, B * H * S * D).reshape(B, H, S, D)
+        indices = kp_np if packed else unpack_key_codes(kp_np, B * H * S * D, self.bits).reshape(B, H, S, D)
         sc, zr = scale.cpu().numpy(), zero.cpu().numpy()
         if self.uniform:
             # per_channel_kv.py:303-317: (B, H, 1, D) scale and zero, no NF4 fields
@@ -406,8 +406,9 @@ class PerChannelKVQuantizer:
         uniform = c.nf4_scale is None and c.levels is None and c.scale is not None and c.zero is not None
         if c.levels is not None or (not uniform and c.nf4_scale is None):
             raise NotImplementedError("data-fit (quantile) key grids have no gfx950 dequant")
-        if c.bits != 4 or D != 128:
-            raise NotImplementedError("the gfx950 dequant reads 4-bit keys at head_dim 128")
+        if c.bits not in (2, 3, 4) or (c.bits != 4 and not uniform) or D != 128:
+            raise NotImplementedError("the gfx950 dequant reads asym-NF4 4-bit or uniform 2/3/4-bit "
+                                      "keys at head_dim 128")
         if uniform:
             scale = np.asarray(c.scale, np.float32)[:, :, 0, :]
             zero = np.asarray(c.zero, np.float32)[:, :, 0, :]
@@ -426,7 +427,8 @@ class PerChannelKVQuantizer:
                 zero = np.asarray(c.nf4_mean, np.float32)
             else:  # symmetric NF4 container: no zero point
                 zero = np.zeros((B, H, D), np.float32)
-        kp = np.asarray(c.indices if c.packed else _pack_keys(np.asarray(c.indices)), np.uint8).reshape(-1)
+        kp = np.asarray(c.indices if c.packed else _pack_keys(np.asarray(c.indices), c.bits),
+                        np.uint8).reshape(-1)
         has_out = c.outlier_idx is not None and c.outlier_val is not None
         _check_key_container(kp, scale, zero, c, B * H * S * D, (B, H, D), has_out)
         dev = torch.device(self.device if self.device is not None else "cuda")
@@ -436,7 +438,7 @@ class PerChannelKVQuantizer:
         idx_d = t(np.asarray(c.outlier_idx, np.int32).reshape(-1), np.int32) if n_out else None
         val_d = t(np.asarray(c.outlier_val, np.float16).reshape(-1).view(np.int16), np.int16) if n_out else None
         out = torch.empty((B, H, S, D), dtype=torch.float32, device=dev)
-        d = _block_desc(c.shape, 4, int(uniform))
+        d = _block_desc(c.shape, c.bits, int(uniform))
         N.check(N.lib().tqk_dequant_key_block(
             ctypes.byref(d), kp_d.data_ptr(), sc_d.data_ptr(), zr_d.data_ptr(), n_out,
             idx_d.data_ptr() if n_out else None, val_d.data_ptr() if n_out else None, out.data_ptr(),
@@ -453,7 +455,7 @@ class PerChannelKVQuantizer:
         if c.nf4_scale is None and c.levels is None and c.scale is not None:
             # uniform: dequant = zero + scale * code
             return (np.asarray(c.zero)[0, :, 0, :].astype(np.float32),
-                    np.asarray(c.scale)[0, :, 0, :].astype(np.float32), np.arange(16, dtype=np.float32))
+                    np.asarray(c.scale)[0, :, 0, :].astype(np.float32), np.arange(1 << c.bits, dtype=np.float32))
         if c.nf4_scale is None:
             raise NotImplementedError("only NF4-family and uniform containers carry the affine grid here")
         mu = (np.asarray(c.nf4_mean)[0] if c.nf4_mean is not None
@@ -464,7 +466,7 @@ class PerChannelKVQuantizer:
         """Unpacked codes ``(B, H, S, D)`` uint8."""
         B, H, S, D = c.shape
         if c.packed:
-            return unpack_keys(c.indices, B * H * S * D).reshape(B, H, S, D)
+            return unpack_key_codes(c.indices, B * H * S * D, c.bits).reshape(B, H, S, D)
         return np.asarray(c.indices)
 
     def outlier_csr(self, c: CompressedPerChannelKV):
@@ -494,13 +496,11 @@ class PerChannelKVQuantizer:
         return None
 
 
-def _pack_keys(codes: np.ndarray) -> np.ndarray:
-    """Flat 4-bit codes -> reference key bytes (code 2n bit-reversed in the
-    high nibble, 2n + 1 in the low one)."""
-    from .formats import _rev4
+def _pack_keys(codes: np.ndarray, bits: int = 4) -> np.ndarray:
+    """Flat key codes -> reference key bytes (turboquant_pro/per_channel_kv.py:87-93)."""
+    from .formats import pack_key_codes
 
-    v = np.asarray(codes, np.uint8).reshape(-1, 2)
-    return ((_rev4(v[:, 0]) << 4) | _rev4(v[:, 1])).astype(np.uint8)
+    return pack_key_codes(codes, bits)
 
 
 class PolarQuantizer:
@@ -603,8 +603,8 @@ class PolarQuantizer:
 def _check_key_container(kp, scale, zero, c, n, bhd, has_out) -> None:
     """Sizes and side-list indices of a key container before its arrays go to
     the GPU (a container read from a store may be damaged or foreign)."""
-    if kp.size != n // 2:
-        raise ValueError(f"key container holds {kp.size} code bytes, shape {c.shape} needs {n // 2}")
+    if kp.size != n * c.bits // 8:
+        raise ValueError(f"key container holds {kp.size} code bytes, shape {c.shape} needs {n * c.bits // 8}")
     if scale.shape != bhd or zero.shape != bhd:
         raise ValueError(f"key container scale {scale.shape} / zero point {zero.shape}, expected {bhd}")
     if has_out:

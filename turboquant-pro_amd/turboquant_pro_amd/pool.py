@@ -23,7 +23,8 @@ import math
 import numpy as np
 
 from . import _native as N
-from .formats import (mark_outlier_codes, pack_values, restore_outlier_codes, tile_value_rows,
+from .formats import (NF4_ZERO_CODE, codes_from_key_rows, key_rows_from_codes, nf4_codes,
+                      pack_key_codes, pack_values, tile_value_rows, uniform_codes, unpack_key_codes,
                       unpack_values, untile_value_rows)
 from .codebooks import (dc_channel_mask, dc_mask_words, group_tokens_for, n_groups_for,
                         outliers_per_channel, random_rotation, rope_averaged_bias, value_codebook)
@@ -356,7 +357,7 @@ class TQKVPool:
         ``(1, H, G, D)``), ``vpacked`` (CompressedKV.indices), ``vnorms`` ``(H, G)``."""
         phys, off = self._rows(b, g)
         H, G, D = self.n_kv_heads, self.group_tokens, self.head_dim
-        kp = self.kcodes[:, phys, off].contiguous().cpu().numpy()  # (H, G, 64)
+        kp = self.kcodes[:, phys, off].contiguous().cpu().numpy()  # (H, G, D * key_bits / 8)
         vp = self.vcodes[:, phys, off].contiguous().cpu().numpy()  # (H, G, vrow)
         if self.tiled:
             vp = np.stack([pack_values(untile_value_rows(vp[h], self.value_bits, D), self.value_bits)
@@ -373,7 +374,16 @@ class TQKVPool:
         oidx = np.concatenate(idx) if idx else np.zeros(0, np.int64)
         oval = np.concatenate(val).view(np.float16) if val else np.zeros(0, np.float16)
         scale, mean = self.gscale[slot].cpu().numpy(), self.gmean[slot].cpu().numpy()
-        kp = restore_outlier_codes(kp, oidx, oval, scale, mean, grid=self.key_grid)
+        # the reference's codes: the stored rows, with the code of the stored
+        # fp16 value put back at every outlier position, in the reference's pack
+        kb = self.key_bits
+        codes = codes_from_key_rows(kp.reshape(H * G, -1), kb, D).reshape(H, G, D)
+        if oidx.size:
+            h, t, j = oidx // (G * D), (oidx // D) % G, oidx % D
+            v32 = oval.astype(np.float32)
+            codes[h, t, j] = (uniform_codes(v32, scale[h, j], mean[h, j], kb) if self.key_grid == "uniform"
+                              else nf4_codes(v32, scale[h, j], mean[h, j]))
+        kp = pack_key_codes(codes, kb)
         # the reference's stored zero point: every channel's ("calibrated"),
         # the DC channels' ("sparse") or none ("bias": recomputed from the bias)
         stored_mean = (mean[:, self.dc_mask] if self.zero_point == "sparse"
@@ -404,7 +414,11 @@ class TQKVPool:
         phys, off = self._rows(b, g)
         slot = int(self.group_table[b, g])
         if keys is not None:
-            kp = np.asarray(keys["kpacked"], np.uint8).reshape(H, G, D // 2)
+            kb = self.key_bits
+            kp = np.asarray(keys["kpacked"], np.uint8).reshape(-1)
+            if kp.size != H * G * D * kb // 8:
+                raise ValueError(f"kpacked holds {kp.size} bytes; a group of {kb}-bit keys takes "
+                                 f"{H * G * D * kb // 8}")
             oidx = keys.get("outlier_idx")
             oval = keys.get("outlier_val")
             oidx = np.zeros(0, np.int64) if oidx is None else np.asarray(oidx, np.int64).reshape(-1)
@@ -413,8 +427,14 @@ class TQKVPool:
                 raise ValueError("outlier_idx and outlier_val differ in length")
             if oidx.size and (oidx.min() < 0 or oidx.max() >= H * G * D):
                 raise ValueError("outlier_idx outside the (H, G, D) block")
-            kp = mark_outlier_codes(kp, oidx, grid=self.key_grid)
-            self.kcodes[:, phys, off] = torch.from_numpy(kp).to(self.device)
+            # stored form: the zero-level code at every outlier position, in the
+            # pool's row layout
+            codes = unpack_key_codes(kp, H * G * D, kb).reshape(H, G, D)
+            if oidx.size:
+                zc = 0 if self.key_grid == "uniform" else NF4_ZERO_CODE
+                codes[oidx // (G * D), (oidx // D) % G, oidx % D] = zc
+            kp = key_rows_from_codes(codes.reshape(H * G, D), kb).reshape(H, G, -1)
+            self.kcodes[:, phys, off] = torch.from_numpy(np.ascontiguousarray(kp)).to(self.device)
             self.gscale[slot] = torch.from_numpy(np.asarray(keys["nf4_scale"], np.float32).reshape(H, D)).to(self.device)
             if self.zero_point == "bias":
                 self.gmean[slot] = self.zp_mean[g]
