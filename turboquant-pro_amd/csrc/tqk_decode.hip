@@ -30,6 +30,10 @@ struct DecodeArgs {
   int n_cold_splits;
   int n_hot_splits;
   int groups_per_split;
+  // MFMA kernel, splits of fewer groups than waves: each wave takes this many
+  // consecutive blocks of the split (0: each wave takes whole groups, every
+  // eighth group of the split)
+  int wave_blocks;
   int hot_per_split;
   int split_base;  // added to blockIdx.x (hot-only launches start after the coded splits)
   int batch;
@@ -831,13 +835,29 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     // outlier entries are read at clamped indices (never past the group's list)
     const uint32_t* __restrict__ oent_all = cap > 0 ? a.p.oent : reinterpret_cast<const uint32_t*>(a.p.ocount);
     const int capm1 = cap > 0 ? cap - 1 : 0;
-    // this wave streams the split's groups wu, wu + 8, ... (meta_s rows), block after block
+    // This wave streams T blocks, block after block: the split's groups wu,
+    // wu + 8, ... whole (meta_s rows g0 + gstep * j), or, for splits of fewer
+    // groups than waves, wave_blocks consecutive blocks of the split starting
+    // at block kb0 of its first group.
     const int wu = __builtin_amdgcn_readfirstlane(w);
     const int gbeg = split * a.groups_per_split;
     const int gcnt = max(0, min(ng, gbeg + a.groups_per_split) - gbeg);
-    const int nw = wu < gcnt ? (gcnt - wu + kMWaves - 1) / kMWaves : 0;
     const int nblk = G / 32;
-    const int T = nw * nblk;
+    int g0, gstep, kb0, nw, T;
+    if (a.wave_blocks > 0) {
+      const int b0 = wu * a.wave_blocks;
+      T = max(0, min(a.wave_blocks, gcnt * nblk - b0));
+      g0 = b0 / nblk;
+      kb0 = b0 % nblk;
+      gstep = 1;
+      nw = T > 0 ? (kb0 + T + nblk - 1) / nblk : 0;
+    } else {
+      g0 = wu;
+      kb0 = 0;
+      gstep = kMWaves;
+      nw = wu < gcnt ? (gcnt - wu + kMWaves - 1) / kMWaves : 0;
+      T = nw * nblk;
+    }
     // per-lane parts of the block addresses (the row parts are wave-uniform)
     // (the lane's token row c, its 32-channel chunk lg)
     const uint32_t koffL = (uint32_t)c * KROW + (uint32_t)(KROW / 4) * (uint32_t)lg;
@@ -847,12 +867,12 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     // entries of lane group lg in 16-entry chunk k then sit in lanes 2k and
     // 2k + 1 of the lane group's own row (DPP row broadcast reaches them)
     const int eidx = 16 * (c >> 1) + 4 * lg + 2 * (c & 1);
-    auto meta = [&](int j, int f) { return __builtin_amdgcn_readfirstlane(meta_s[wu + kMWaves * j][f]); };
+    auto meta = [&](int j, int f) { return __builtin_amdgcn_readfirstlane(meta_s[g0 + gstep * j][f]); };
     // the metadata of the wave group being loaded (jl below), field f in lane
     // f: the block loads read it with v_readlane, with no LDS round trip per block
     int mv = 0;
     auto load_meta = [&](int j) {
-      mv = (lane < kMetaInts && nw > 0) ? meta_s[wu + kMWaves * min(j, nw - 1)][lane] : 0;
+      mv = (lane < kMetaInts && nw > 0) ? meta_s[g0 + gstep * min(j, nw - 1)][lane] : 0;
     };
     auto meta_l = [&](int f) { return __builtin_amdgcn_readlane(mv, f); };
     // buffer resources of this head's page regions (32-bit offsets:
@@ -864,7 +884,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
 
     // Every step issues the same loads (past the end: the last block again,
     // already in L2), so the waits on the oldest buffer stay exact.
-    int jl = 0, kbl = 0, nl = 0;  // next block to load: wave group jl, block kbl, stream index nl
+    int jl = 0, kbl = kb0, nl = 0;  // next block to load: wave group jl, block kbl, stream index nl
     load_meta(0);
     auto load_next = [&](ColdBlock<VB>& cb) {
       // rows of the two tiles in this head's region (wave-uniform: SGPR offsets)
@@ -1224,7 +1244,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
 
     // A ring of kColdBuf buffers, kColdBuf - 1 blocks in flight: step i
     // issues the loads of block i + kColdBuf - 1 and computes block i.
-    int jp = 0, kbp = 0;  // computed block: wave group jp, block kbp
+    int jp = 0, kbp = kb0;  // computed block: wave group jp, block kbp
     auto step = [&](const ColdBlock<VB>& cur, ColdBlock<VB>& nxt, const ColdBlock<VB>& nx1) {
       store_group_stats();
       load_group_stats(meta_l(16 + TQK_NOB), jl);  // group of the block load_next fetches now
@@ -1240,7 +1260,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     };
     if (T > 0) {
       // groups of the first two blocks, synchronously
-      const int j1 = min(1, T - 1) / nblk;
+      const int j1 = (kb0 + min(1, T - 1)) / nblk;
       load_group_stats(meta(0, 16 + TQK_NOB), 0);
       store_group_stats();
       load_group_stats(meta(j1, 16 + TQK_NOB), j1);
@@ -1250,7 +1270,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       for (int s = 0; s < kColdBuf - 1; ++s) load_next(ring[s]);
       wave_sync();
       begin_group(0);
-      pend = stage_entries(ring[0].ent, min(128, ring[0].ne), 0, 0);
+      pend = stage_entries(ring[0].ent, min(128, ring[0].ne), kb0, 0);
       {
         H8 x[8];
         key_tile(ring[0].kA, x);
@@ -1259,7 +1279,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         qk_tile(x, CBn);
       }
       wave_sync();
-      apply_block(ring[0], 0, 0, CAn, CBn);
+      apply_block(ring[0], kb0, 0, CAn, CBn);
       for (int i = 0; i < T; i += kColdBuf) {
 #pragma unroll
         for (int s = 0; s < kColdBuf; ++s) {
@@ -1654,6 +1674,7 @@ inline int counter_seqs(const tqk_cache_desc& d) { return d.n_pages; }
 
 struct Plan {
   int n_cold_splits, n_hot_splits, groups_per_split, hot_per_split;
+  int wave_blocks;  // MFMA kernel: blocks per wave of a split smaller than 8 groups, else 0
   size_t counter_bytes;  // arrival counters at the workspace's start, then the partials
   size_t partial_bytes;  // the split partials (m, l, acc)
   size_t ws_bytes;
@@ -1712,6 +1733,21 @@ Plan make_plan(const tqk_cache_desc* d, int batch, int max_len) {
       }
     }
     gps = kMWaves * gpw_best;
+    // Short contexts: splits of 1, 2 or 4 groups whose blocks the eight waves
+    // share (wave_blocks each) put more workgroups on the CUs when there are
+    // few (seq, kv head) pairs (same cost model, in groups per wave)
+    const int nblk = d->group_tokens / 32;
+    for (int g = 1; g < kMWaves; g *= 2) {
+      if ((g * nblk) % kMWaves) continue;
+      const long items = (long)batch * d->n_kv_heads * ((ngmax + g - 1) / g);
+      const long rounds = (items + ncu - 1) / ncu;
+      const double cost = (double)rounds * ((double)g / kMWaves + 0.35);
+      if (cost < best - 1e-9) {
+        best = cost;
+        gps = g;
+        pl.wave_blocks = g * nblk / kMWaves;
+      }
+    }
   } else {
     gps = (int)((units + 4095) / 4096);
     if (gps < 1) gps = 1;
@@ -1785,6 +1821,7 @@ DecodeArgs make_args(const tqk_cache_desc* d, const tqk_cache_ptrs* p, const Pla
   a.n_cold_splits = pl.n_cold_splits;
   a.n_hot_splits = pl.n_hot_splits;
   a.groups_per_split = pl.groups_per_split;
+  a.wave_blocks = pl.wave_blocks;
   a.hot_per_split = pl.hot_per_split;
   a.split_base = 0;
   a.batch = batch;
