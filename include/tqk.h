@@ -85,7 +85,10 @@ typedef struct tqk_cache_desc {
   float sm_scale;               /* softmax scale, 1/sqrt(D) */
   int32_t key_grid;             /* 0: asym-NF4 (gmean = the zero point, gscale = abs-max of the
                                    channel centred on it, levels NF4); 1: uniform (gmean = channel min,
-                                   gscale = max(max - min, 1e-8) / 15, levels 0..15) */
+                                   gscale = max(max - min, 1e-8) / (2^key_bits - 1), levels 0..2^key_bits-1);
+                                   2: PolarQuant keys (TurboQuantKV with kind="key": the value
+                                   encode on the keys, key_bits == value_bits, levels vcent, per-token
+                                   norms in knorm; gscale 1, gmean 0, no side-list) */
   int32_t zero_point;           /* asym-NF4 zero point (turboquant_pro/per_channel_kv.py:327-345):
                                    0 "calibrated", the channel mean over the group;
                                    1 "sparse", the channel mean on the dc_mask channels, 0 elsewhere;
@@ -111,9 +114,10 @@ typedef struct tqk_cache_ptrs {
   const float* vbnd;    /* 2^vb - 1 fp32 value boundaries */
   const float* zp_mean; /* zero_point 2: [max_groups_per_seq][n_kv_heads][head_dim] zero points of
                            the groups starting at token g * group_tokens; unused otherwise */
+  float* knorm;         /* key_grid 2: [n_kv_heads][n_pages][page_tokens] f32 key norms; unused otherwise */
 } tqk_cache_ptrs;
 
-/* Library ABI version (bumped on any signature or layout change); this header is version 7. */
+/* Library ABI version (bumped on any signature or layout change); this header is version 8. */
 int tqk_version(void);
 
 /* Validate a descriptor; TQK_OK when the GPU path supports it. */

@@ -405,7 +405,10 @@ class SequenceCache:
     value_bits: int
     outlier_frac: float
     seed: int | None = 0
-    key_grid: str = "nf4_asym"       # or "uniform" (per_channel_kv.py:303-317)
+    # or "uniform" (per_channel_kv.py:303-317), or "polar": PolarQuant keys
+    # (per_channel_keys=False, turboquant_pro/core.py:1028-1029 -- the value
+    # encode with kind="key", whose codebook is key_bits' = value_bits' here)
+    key_grid: str = "nf4_asym"
     key_bits: int = 4                # uniform keys: 2, 3 or 4
     zero_point: str = "calibrated"   # asym-NF4: or "sparse" / "bias" (per_channel_kv.py:327-345)
     rope_theta: float | None = None
@@ -424,7 +427,11 @@ class SequenceCache:
         self.keys, self.values = [], []
         for i in range(ng):
             sl = slice(G * i, G * (i + 1))
-            if self.key_grid == "uniform":
+            if self.key_grid == "polar":
+                if self.key_bits != self.value_bits:
+                    raise ValueError("polar keys here take key_bits == value_bits")
+                self.keys.append(encode_values(k[:, sl].astype(np.float32), pi_t, bnd, self.value_bits))
+            elif self.key_grid == "uniform":
                 self.keys.append(encode_keys_uniform(k[:, sl].astype(np.float32), self.outlier_frac,
                                                      self.key_bits))
             else:
@@ -439,7 +446,8 @@ class SequenceCache:
 
     def get_keys(self) -> np.ndarray:
         """(H, L, D) fp32, ``get_keys(0, L)[0]`` (turboquant_pro/core.py:1040-1117)."""
-        parts = [decode_keys(g) for g in self.keys] + [self.hot_k.astype(np.float32)]
+        parts = [decode_values(g, self._cent, self._pi) if isinstance(g, ValueGroup) else decode_keys(g)
+                 for g in self.keys] + [self.hot_k.astype(np.float32)]
         return np.concatenate(parts, axis=1)
 
     def get_values(self) -> np.ndarray:

@@ -124,7 +124,8 @@ def test_stats_clear_and_errors():
     with pytest.raises(ValueError):
         cache.append(np.zeros((3, 128), np.float16), np.zeros((3, 128), np.float16))
     with pytest.raises(NotImplementedError):
-        TurboQuantKVCache(head_dim=128, n_heads=2, bits=3, per_channel_keys=False)   # PolarQuant keys
+        # PolarQuant keys share the value codebook: unequal widths have no GPU form
+        TurboQuantKVCache(head_dim=128, n_heads=2, key_bits=4, value_bits=3, per_channel_keys=False)
 
 
 def test_uniform_key_cache():

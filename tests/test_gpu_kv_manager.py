@@ -74,7 +74,7 @@ def test_backend_blocks():
     assert be.load_block(0)[0].shape == (1, 2, 0, 128)
 
 
-def test_polar_keys_have_no_gpu_form():
+def test_polar_keys_with_unequal_widths_have_no_gpu_form():
     from turboquant_pro_amd import TurboQuantKVManager
     with pytest.raises(NotImplementedError):
-        TurboQuantKVManager(n_layers=1, n_kv_heads=2, bits=3, per_channel_keys=False)
+        TurboQuantKVManager(n_layers=1, n_kv_heads=2, key_bits=4, value_bits=3, per_channel_keys=False)

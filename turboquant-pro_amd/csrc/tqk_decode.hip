@@ -126,6 +126,7 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
   const float sm = d.sm_scale;
 
   __shared__ float q_s[GQ][D];
+  __shared__ float qr_s[GQ][D];  // q @ pi_t (PolarQuant keys' weights)
   __shared__ float w_s[GQ][D];
   __shared__ float sc_s[GQ][kThreads];
   __shared__ float kl_s[256][2];
@@ -141,12 +142,28 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
     q_s[i / D][i % D] = (i / D < gq) ? h2f(a.q[((size_t)b * Hq + h * gq + i / D) * D + i % D]) : 0.f;
   // key pair table: index of a channel pair (the code byte, or the 3-/2-bit
   // pair field) -> its two levels
-  kl_s[tid][0] = key_level(a.d.key_grid, k_code_even((uint32_t)tid & 0xFFu, a.d.key_bits) & 15u);
-  kl_s[tid][1] = key_level(a.d.key_grid, k_code_odd((uint32_t)tid & 0xFFu, a.d.key_bits) & 15u);
+  // pair field) -> its two levels (PolarQuant keys: value centroids)
+  const bool polar = a.d.key_grid == 2;
+  {
+    const uint32_t c0 = k_code_even((uint32_t)tid & 0xFFu, a.d.key_bits) & 15u;
+    const uint32_t c1 = k_code_odd((uint32_t)tid & 0xFFu, a.d.key_bits) & 15u;
+    const uint32_t cm = (1u << a.d.key_bits) - 1u;
+    kl_s[tid][0] = polar ? a.p.vcent[c0 & cm] : key_level(a.d.key_grid, c0);
+    kl_s[tid][1] = polar ? a.p.vcent[c1 & cm] : key_level(a.d.key_grid, c1);
+  }
   // value pair table: field f of two channels' codes -> their two centroids
   if (tid < (1 << (2 * VB))) {
     vl_s[tid][0] = a.p.vcent[tid & ((1 << VB) - 1)];
     vl_s[tid][1] = a.p.vcent[tid >> VB];
+  }
+
+  if (polar) {
+    __syncthreads();
+    for (int i = tid; i < GQ * D; i += kThreads) {
+      float x = 0.f;
+      for (int dd = 0; dd < D; ++dd) x += q_s[i / D][dd] * a.p.pi_t[dd * D + i % D];
+      qr_s[i / D][i % D] = x;
+    }
   }
 
   float m_run[GQ], l_run[GQ], acc0[GQ], acc1[GQ];
@@ -176,7 +193,7 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
         float bias_part[GQ];
 #pragma unroll
         for (int i = 0; i < GQ; ++i) {
-          w_s[i][tid] = q_s[i][tid] * av;
+          w_s[i][tid] = (polar ? qr_s[i][tid] : q_s[i][tid]) * av;
           bias_part[i] = wave_sum(q_s[i][tid] * mv);
         }
         if ((tid & 63) == 0) {
@@ -208,8 +225,9 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
 #pragma unroll
           for (int i = 0; i < GQ; ++i) s[i] += w_s[i][j] * k0 + w_s[i][j + 1] * k1;
         }
+        const float kn = polar ? a.p.knorm[row] * sm : sm;  // score = |k| * (q_rot . centroids)
 #pragma unroll
-        for (int i = 0; i < GQ; ++i) sc_s[i][tid] = (s[i] + bias[i]) * sm;
+        for (int i = 0; i < GQ; ++i) sc_s[i][tid] = (s[i] + bias[i]) * kn;
         norm_t = a.p.vnorm[row];
       }
       __syncthreads();
@@ -479,6 +497,7 @@ struct ColdBlock {
   // to LDS by the compiler, which then waits on every prefetch right away.
   uint4 uA, uB;
   float nv;        // value norm of token 16 * ((c >> 2) & 1) + 4lg + (c & 3)
+  float kn;        // ... and its key norm (PolarQuant keys only)
   uint2 ent;       // outlier entries 2*lane, 2*lane + 1 of the block
   int e0, ne;      // the block's outliers are entries [e0, e0 + ne) of its group
   uint32_t obase;  // slot * Hkv + h of the block's group
@@ -670,7 +689,10 @@ __device__ __forceinline__ H8 dup_quad(float x0, float x1, float x2, float x3, f
   return r;
 }
 
-template <int GQ, int VB, int KB>
+// PK: PolarQuant keys (key_grid 2, KB == VB): the key table holds centroids,
+// the QK^T weights are the rotated query, and every score is scaled by its
+// token's key norm
+template <int GQ, int VB, int KB, bool PK>
 __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs a) {
   constexpr int D = TQK_D;
   constexpr int VROW = D * VB / 8;
@@ -752,7 +774,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   __shared__ __align__(16) uint32_t od_s[kMWaves][128];
   // NF4 levels [0, 16) and value centroids [16, 16 + 2^vb), for the table fill
   __shared__ float lvl_s[32];
-  if (tid < 16) lvl_s[tid] = key_level(a.d.key_grid, tid);
+  if (tid < 16) lvl_s[tid] = PK ? (tid < (1 << KB) ? a.p.vcent[tid] : 0.f) : key_level(a.d.key_grid, tid);
   else if (tid < 16 + (1 << VB)) lvl_s[tid] = a.p.vcent[tid - 16];
   // Metadata of the split's groups, read once here so the block stream issues
   // nothing but block loads: [0, 16) first row of each 16-token tile,
@@ -790,6 +812,25 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     q_h_s[i / D][i % D] = h2f((uint16_t)qr) * qscale;
   }
   __syncthreads();
+  if constexpr (PK) {
+    // the coded keys' weights: the rotated query q @ pi_t (scaled), from the raw q
+    float qrot[(GQ * D + kMThreads - 1) / kMThreads];
+#pragma unroll
+    for (int r = 0; r < (GQ * D + kMThreads - 1) / kMThreads; ++r) {
+      const int i = tid + r * kMThreads;
+      float x = 0.f;
+      if (i < GQ * D)
+        for (int dd = 0; dd < D; ++dd) x += h2f(qf_s[i / D][dd]) * a.p.pi_t[dd * D + i % D];
+      qrot[r] = x * qscale;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < (GQ * D + kMThreads - 1) / kMThreads; ++r) {
+      const int i = tid + r * kMThreads;
+      if (i < GQ * D) q_h_s[i / D][i % D] = qrot[r];
+    }
+    __syncthreads();
+  }
   {
     // unit u (8 bytes): key part first (entry u / copies, copy u % copies), then values;
     // consecutive lanes write consecutive units; levels come from LDS, so the
@@ -881,6 +922,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     const __amdgpu_buffer_rsrc_t rk = buf_rsrc(a.p.kcodes + (size_t)h * hrows * KROW, hrows * KROW);
     const __amdgpu_buffer_rsrc_t rv = buf_rsrc(a.p.vcodes + (size_t)h * hrows * VROW, hrows * VROW);
     const __amdgpu_buffer_rsrc_t rn = buf_rsrc(a.p.vnorm + (size_t)h * hrows, hrows * 4u);
+    const __amdgpu_buffer_rsrc_t rkn = buf_rsrc(PK ? a.p.knorm + (size_t)h * hrows : a.p.vnorm, PK ? hrows * 4u : 0u);
 
     // Every step issues the same loads (past the end: the last block again,
     // already in L2), so the waits on the oldest buffer stay exact.
@@ -929,6 +971,9 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       // below tile A's, so the row is picked per lane, not offset from rowA)
       cb.nv = bitsf(__builtin_amdgcn_raw_buffer_load_b32(
           rn, (int)(4u * (((c & 4) ? rowB : rowA) + (uint32_t)ntl)), 0, 0));
+      if constexpr (PK)
+        cb.kn = bitsf(__builtin_amdgcn_raw_buffer_load_b32(
+            rkn, (int)(4u * (((c & 4) ? rowB : rowA) + (uint32_t)ntl)), 0, 0));
       // the group's side-list as its own buffer: reads past its end return 0,
       // reads past e1 are masked where they are used (the outlier pass)
       const __amdgpu_buffer_rsrc_t ro = buf_rsrc(oent_all + (size_t)obase * cap, 4u * (uint32_t)cap);
@@ -1220,6 +1265,17 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         for (int i = 0; i < 4; ++i) {
           sc[i] = pair_sum(CA[i]);
           sc[4 + i] = pair_sum(CB[i]);
+        }
+        if constexpr (PK) {
+          // score = |k| * (q_rot . centroids)
+          sc[0] *= row_bcast<0>(cur.kn);
+          sc[1] *= row_bcast<1>(cur.kn);
+          sc[2] *= row_bcast<2>(cur.kn);
+          sc[3] *= row_bcast<3>(cur.kn);
+          sc[4] *= row_bcast<4>(cur.kn);
+          sc[5] *= row_bcast<5>(cur.kn);
+          sc[6] *= row_bcast<6>(cur.kn);
+          sc[7] *= row_bcast<7>(cur.kn);
         }
         float p[8];
         softmax_block<GQ>(st, sc, p, lg);
@@ -1775,12 +1831,14 @@ Plan make_plan(const tqk_cache_desc* d, int batch, int max_len) {
 
 template <int GQ, int KB>
 void launch_mfma_kb(const DecodeArgs& a, dim3 g1, hipStream_t st) {
-  if (a.d.value_bits == 2)
-    hipLaunchKernelGGL((tqk_decode_split_mfma<GQ, 2, KB>), g1, dim3(kMThreads), 0, st, a);
+  if (a.d.key_grid == 2)  // PolarQuant keys: value_bits == key_bits
+    hipLaunchKernelGGL((tqk_decode_split_mfma<GQ, KB, KB, true>), g1, dim3(kMThreads), 0, st, a);
+  else if (a.d.value_bits == 2)
+    hipLaunchKernelGGL((tqk_decode_split_mfma<GQ, 2, KB, false>), g1, dim3(kMThreads), 0, st, a);
   else if (a.d.value_bits == 3)
-    hipLaunchKernelGGL((tqk_decode_split_mfma<GQ, 3, KB>), g1, dim3(kMThreads), 0, st, a);
+    hipLaunchKernelGGL((tqk_decode_split_mfma<GQ, 3, KB, false>), g1, dim3(kMThreads), 0, st, a);
   else
-    hipLaunchKernelGGL((tqk_decode_split_mfma<GQ, 4, KB>), g1, dim3(kMThreads), 0, st, a);
+    hipLaunchKernelGGL((tqk_decode_split_mfma<GQ, 4, KB, false>), g1, dim3(kMThreads), 0, st, a);
 }
 
 template <int GQ>
@@ -1839,6 +1897,7 @@ int check_decode_args(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int batc
   int rc = tqk_check_desc(d);
   if (rc != TQK_OK) return rc;
   if (!p || batch <= 0 || max_len <= 0) return TQK_EINVAL;
+  if (d->key_grid == 2 && !p->knorm) return TQK_EINVAL;
   if (batch > counter_seqs(*d)) return TQK_EINVAL;
   return TQK_OK;
 }
@@ -1957,15 +2016,17 @@ int noalloc_scratch(hipStream_t stream, void** out) {
 
 extern "C" {
 
-int tqk_version(void) { return 7; }
+int tqk_version(void) { return 8; }
 
 int tqk_check_desc(const tqk_cache_desc* d) {
   if (!d) return TQK_EINVAL;
   if (d->head_dim != TQK_D) return TQK_EUNSUPPORTED;
   if (d->key_bits < 2 || d->key_bits > 4) return TQK_EUNSUPPORTED;
-  if (d->key_grid != 0 && d->key_grid != 1) return TQK_EINVAL;
-  // NF4 is a 4-bit grid; 3- and 2-bit keys are uniform
-  if (d->key_bits != 4 && d->key_grid != 1) return TQK_EUNSUPPORTED;
+  if (d->key_grid < 0 || d->key_grid > 2) return TQK_EINVAL;
+  // NF4 is a 4-bit grid; 3- and 2-bit keys are uniform or PolarQuant
+  if (d->key_bits != 4 && d->key_grid == 0) return TQK_EUNSUPPORTED;
+  // PolarQuant keys share the value codebook and carry no side-list
+  if (d->key_grid == 2 && (d->key_bits != d->value_bits || d->outliers_per_channel != 0)) return TQK_EUNSUPPORTED;
   if (d->value_bits < 2 || d->value_bits > 4) return TQK_EUNSUPPORTED;
   if (d->zero_point < 0 || d->zero_point > 2 || (d->zero_point != 0 && d->key_grid != 0))
     return TQK_EINVAL;

@@ -67,181 +67,183 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
   // the NF4 zero level (code 7) at every stored outlier position
   __shared__ __align__(16) uint8_t kc_s[TQK_MAX_G][D / 2];
 
-  // ---- stage the key tile ----------------------------------------------
-  for (int idx = tid; idx < G * 16; idx += kEncThreads) {
-    const int t = idx >> 4, c = idx & 15;
-    const uint4* src =
-        reinterpret_cast<const uint4*>(token_src(a, a.p.hot_k, a.chunk_k, b, h, g * G + t));
-    reinterpret_cast<uint4*>(&kt_s[t][0])[c] = src[c];
-  }
-  __syncthreads();
-
-  // ---- per-channel statistics (threads 0..127) and outlier thresholds (128..255)
-  const size_t mbase = ((size_t)slot * Hkv + h) * D;
-  if (tid < D && d.key_grid == 1) {
-    // uniform keys (turboquant_pro/per_channel_kv.py:303-306): channel min and
-    // max over the tokens, scale = max(max - min, 1e-8) / (2^bits - 1) (NaN propagates)
-    const int j = tid;
-    float mn = h2f(kt_s[0][j]), mx = mn;
-    bool nan = (mn != mn);
-    for (int s = 1; s < G; ++s) {
-      const float xv = h2f(kt_s[s][j]);
-      nan |= (xv != xv);
-      mn = fminf(mn, xv);
-      mx = fmaxf(mx, xv);
+  if (d.key_grid != 2) {
+    // ---- stage the key tile ----------------------------------------------
+    for (int idx = tid; idx < G * 16; idx += kEncThreads) {
+      const int t = idx >> 4, c = idx & 15;
+      const uint4* src =
+          reinterpret_cast<const uint4*>(token_src(a, a.p.hot_k, a.chunk_k, b, h, g * G + t));
+      reinterpret_cast<uint4*>(&kt_s[t][0])[c] = src[c];
     }
-    const float rng = __fsub_rn(mx, mn);
-    const float sc = nan ? __builtin_nanf("") : __fdiv_rn(fmaxf(rng, 1e-8f), (float)((1 << d.key_bits) - 1));
-    if (nan) mn = __builtin_nanf("");
-    cent_s[j][0] = mn;
-    cent_s[j][1] = sc;
-    a.p.gscale[mbase + j] = sc;
-    a.p.gmean[mbase + j] = mn;
-  } else if (tid < D) {
-    const int j = tid;
-    // the zero point (turboquant_pro/per_channel_kv.py:327-345)
-    float mu;
-    if (d.zero_point == 2) {
-      // "bias": the RoPE-averaged k_proj bias of the group's positions
-      mu = a.p.zp_mean[((size_t)g * Hkv + h) * D + j];
-    } else {
-      float acc = 0.0f;
-      for (int s = 0; s < G; ++s) acc = __fadd_rn(acc, h2f(kt_s[s][j]));
-      // np.mean divides the fp32 sum by an intp count: a float64 division, then fp32
-      mu = (float)((double)acc / (double)G);
-      // "sparse": the mean times the DC-channel mask (a float product, so a
-      // non-DC channel gets a signed zero, or NaN from a NaN mean)
-      if (d.zero_point == 1) mu = __fmul_rn(mu, ((d.dc_mask[j >> 5] >> (j & 31)) & 1u) ? 1.0f : 0.0f);
-    }
-    float amax = 0.0f;
-    bool nan = (mu != mu);
-    for (int s = 0; s < G; ++s) {
-      const float dv = fabsf(__fsub_rn(h2f(kt_s[s][j]), mu));
-      nan |= (dv != dv);
-      amax = fmaxf(amax, dv);
-    }
-    amax = nan ? __builtin_nanf("") : fmaxf(amax, 1e-8f);
-#pragma unroll
-    for (int l = 0; l < 16; ++l) cent_s[j][l] = __fadd_rn(mu, __fmul_rn(amax, kNF4[l]));
-    a.p.gscale[mbase + j] = amax;
-    a.p.gmean[mbase + j] = mu;
-  } else if (tid < 2 * D && kout > 0 && kout < G) {
-    // k-th largest |x| as the largest fp16 magnitude pattern T with
-    // #{ |x_s| >= T } >= k (NaN patterns order above inf, as np.partition does).
-    const int j = tid - D;
-    uint32_t T = 0;
-    for (int bit = 14; bit >= 0; --bit) {
-      const uint32_t cand = T | (1u << bit);
-      int cnt = 0;
-      for (int s = 0; s < G; ++s) cnt += (abs_h(kt_s[s][j]) >= cand);
-      if (cnt >= kout) T = cand;
-    }
-    thr_s[j] = T;
-  }
-  __syncthreads();
-
-  // ---- codes: thread = (channel pair, token slice); one byte per (token, pair)
-  if (d.key_grid == 1) {
-    // uniform: clip(round_half_even((x - min) / scale), 0, 2^bits - 1)
-    const int jp = tid & 63, sq = tid >> 6, kb = d.key_bits;
-    const float qmax = (float)((1 << kb) - 1);
-    const float mn0 = cent_s[2 * jp][0], sc0 = cent_s[2 * jp][1];
-    const float mn1 = cent_s[2 * jp + 1][0], sc1 = cent_s[2 * jp + 1][1];
-    const int per_q = (G + kEncWaves - 1) / kEncWaves;
-    const int s0 = sq * per_q, s1 = min(G, s0 + per_q);
-    for (int s = s0; s < s1; ++s) {
-      const float r0 = __builtin_rintf(__fdiv_rn(__fsub_rn(h2f(kt_s[s][2 * jp]), mn0), sc0));
-      const float r1 = __builtin_rintf(__fdiv_rn(__fsub_rn(h2f(kt_s[s][2 * jp + 1]), mn1), sc1));
-      const uint32_t b0 = (uint32_t)fminf(fmaxf(r0, 0.0f), qmax);
-      const uint32_t b1 = (uint32_t)fminf(fmaxf(r1, 0.0f), qmax);
-      // one table index per channel pair (the key row layout of tqk_common.h)
-      kc_s[s][jp] = (uint8_t)(kb == 4 ? ((rev4(b0) << 4) | rev4(b1)) : (b0 | (b1 << kb)));
-    }
-  } else {
-    const int jp = tid & 63, sq = tid >> 6;
-    float c0[16], c1[16];
-#pragma unroll
-    for (int l = 0; l < 16; ++l) {
-      c0[l] = cent_s[2 * jp][l];
-      c1[l] = cent_s[2 * jp + 1][l];
-    }
-    const int per_q = (G + kEncWaves - 1) / kEncWaves;
-    const int s0 = sq * per_q, s1 = min(G, s0 + per_q);
-    for (int s = s0; s < s1; ++s) {
-      const float x0 = h2f(kt_s[s][2 * jp]), x1 = h2f(kt_s[s][2 * jp + 1]);
-      int b0 = 0, b1 = 0;
-      float d0 = fabsf(__fsub_rn(x0, c0[0])), d1 = fabsf(__fsub_rn(x1, c1[0]));
-#pragma unroll
-      for (int l = 1; l < 16; ++l) {
-        const float e0 = fabsf(__fsub_rn(x0, c0[l])), e1 = fabsf(__fsub_rn(x1, c1[l]));
-        // np.argmin: strictly smaller wins; the first NaN wins over any number
-        if (e0 < d0 || (e0 != e0 && d0 == d0)) { d0 = e0; b0 = l; }
-        if (e1 < d1 || (e1 != e1 && d1 == d1)) { d1 = e1; b1 = l; }
-      }
-      kc_s[s][jp] = (uint8_t)((rev4(b0) << 4) | rev4(b1));
-    }
-  }
-
-  // ---- outlier side-list in flat (token, channel) order ---------------------
-  // ocount holds cumulative counts at every TQK_OBLK-token boundary of the
-  // group (entry TQK_NOB-1 = total), so a decode block finds its entries
-  // without searching.
-  const size_t obase = (size_t)slot * Hkv + h;
-  if (kout > 0) {
-    const bool all = kout >= G;
-    int cnt = 0;
-    if (tid < G) {
-      for (int j = 0; j < D; ++j) {
-        const float mag = fabsf(h2f(kt_s[tid][j]));
-        cnt += all ? 1 : (mag >= fabsf(h2f((uint16_t)thr_s[j])));
-      }
-    }
-    // block exclusive scan of cnt
-    int incl = cnt;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int v = __shfl_up(incl, o, 64);
-      if ((tid & 63) >= o) incl += v;
-    }
-    if ((tid & 63) == 63) wsum_s[tid >> 6] = incl;
     __syncthreads();
-    int wofs = 0;
-    for (int w = 0; w < (tid >> 6); ++w) wofs += wsum_s[w];
-    int total = 0;
-    for (int w = 0; w < kEncWaves; ++w) total += wsum_s[w];
-    int off = wofs + incl - cnt;
-    // token s = TQK_OBLK*k - 1 closes block k-1: its inclusive offset is the bound
-    if (tid < G && ((tid + 1) % TQK_OBLK) == 0 && (tid + 1) / TQK_OBLK <= TQK_NOB)
-      a.p.ocount[obase * TQK_NOB + (tid + 1) / TQK_OBLK - 1] = off + cnt;
-    if (tid < TQK_NOB && TQK_OBLK * (tid + 1) > G) a.p.ocount[obase * TQK_NOB + tid] = total;
-    if (tid < G && cnt > 0) {
-      for (int j = 0; j < D; ++j) {
-        const uint16_t xv = kt_s[tid][j];
-        const bool sel = all || (fabsf(h2f(xv)) >= fabsf(h2f((uint16_t)thr_s[j])));
-        if (sel) {
-          if (off < d.outlier_cap) {
-            a.p.oent[obase * d.outlier_cap + off] = (uint32_t)(tid * D + j) | ((uint32_t)xv << 16);
-            // the stored code becomes the level whose value is gmean -- NF4's
-            // zero level (rev4(7) = 14), or code 0 of a uniform grid -- so the
-            // dense part of a decode contributes only gmean here and the
-            // side-list adds val - gmean; export restores the reference's code
-            uint8_t& kp = kc_s[tid][j >> 1];
-            if (d.key_bits == 4) {
-              const uint32_t zc = d.key_grid == 1 ? 0u : 14u;
-              kp = (j & 1) ? (uint8_t)((kp & 0xF0u) | zc) : (uint8_t)((kp & 0x0Fu) | (zc << 4));
-            } else {
-              // 3- and 2-bit keys are uniform: the pair field's code of channel j to 0
-              const uint32_t m = (1u << d.key_bits) - 1u;
-              kp = (uint8_t)(kp & ~((j & 1) ? (m << d.key_bits) : m));
-            }
-          }
-          ++off;
+
+    // ---- per-channel statistics (threads 0..127) and outlier thresholds (128..255)
+    const size_t mbase = ((size_t)slot * Hkv + h) * D;
+    if (tid < D && d.key_grid == 1) {
+      // uniform keys (turboquant_pro/per_channel_kv.py:303-306): channel min and
+      // max over the tokens, scale = max(max - min, 1e-8) / (2^bits - 1) (NaN propagates)
+      const int j = tid;
+      float mn = h2f(kt_s[0][j]), mx = mn;
+      bool nan = (mn != mn);
+      for (int s = 1; s < G; ++s) {
+        const float xv = h2f(kt_s[s][j]);
+        nan |= (xv != xv);
+        mn = fminf(mn, xv);
+        mx = fmaxf(mx, xv);
+      }
+      const float rng = __fsub_rn(mx, mn);
+      const float sc = nan ? __builtin_nanf("") : __fdiv_rn(fmaxf(rng, 1e-8f), (float)((1 << d.key_bits) - 1));
+      if (nan) mn = __builtin_nanf("");
+      cent_s[j][0] = mn;
+      cent_s[j][1] = sc;
+      a.p.gscale[mbase + j] = sc;
+      a.p.gmean[mbase + j] = mn;
+    } else if (tid < D) {
+      const int j = tid;
+      // the zero point (turboquant_pro/per_channel_kv.py:327-345)
+      float mu;
+      if (d.zero_point == 2) {
+        // "bias": the RoPE-averaged k_proj bias of the group's positions
+        mu = a.p.zp_mean[((size_t)g * Hkv + h) * D + j];
+      } else {
+        float acc = 0.0f;
+        for (int s = 0; s < G; ++s) acc = __fadd_rn(acc, h2f(kt_s[s][j]));
+        // np.mean divides the fp32 sum by an intp count: a float64 division, then fp32
+        mu = (float)((double)acc / (double)G);
+        // "sparse": the mean times the DC-channel mask (a float product, so a
+        // non-DC channel gets a signed zero, or NaN from a NaN mean)
+        if (d.zero_point == 1) mu = __fmul_rn(mu, ((d.dc_mask[j >> 5] >> (j & 31)) & 1u) ? 1.0f : 0.0f);
+      }
+      float amax = 0.0f;
+      bool nan = (mu != mu);
+      for (int s = 0; s < G; ++s) {
+        const float dv = fabsf(__fsub_rn(h2f(kt_s[s][j]), mu));
+        nan |= (dv != dv);
+        amax = fmaxf(amax, dv);
+      }
+      amax = nan ? __builtin_nanf("") : fmaxf(amax, 1e-8f);
+#pragma unroll
+      for (int l = 0; l < 16; ++l) cent_s[j][l] = __fadd_rn(mu, __fmul_rn(amax, kNF4[l]));
+      a.p.gscale[mbase + j] = amax;
+      a.p.gmean[mbase + j] = mu;
+    } else if (tid < 2 * D && kout > 0 && kout < G) {
+      // k-th largest |x| as the largest fp16 magnitude pattern T with
+      // #{ |x_s| >= T } >= k (NaN patterns order above inf, as np.partition does).
+      const int j = tid - D;
+      uint32_t T = 0;
+      for (int bit = 14; bit >= 0; --bit) {
+        const uint32_t cand = T | (1u << bit);
+        int cnt = 0;
+        for (int s = 0; s < G; ++s) cnt += (abs_h(kt_s[s][j]) >= cand);
+        if (cnt >= kout) T = cand;
+      }
+      thr_s[j] = T;
+    }
+    __syncthreads();
+
+    // ---- codes: thread = (channel pair, token slice); one byte per (token, pair)
+    if (d.key_grid == 1) {
+      // uniform: clip(round_half_even((x - min) / scale), 0, 2^bits - 1)
+      const int jp = tid & 63, sq = tid >> 6, kb = d.key_bits;
+      const float qmax = (float)((1 << kb) - 1);
+      const float mn0 = cent_s[2 * jp][0], sc0 = cent_s[2 * jp][1];
+      const float mn1 = cent_s[2 * jp + 1][0], sc1 = cent_s[2 * jp + 1][1];
+      const int per_q = (G + kEncWaves - 1) / kEncWaves;
+      const int s0 = sq * per_q, s1 = min(G, s0 + per_q);
+      for (int s = s0; s < s1; ++s) {
+        const float r0 = __builtin_rintf(__fdiv_rn(__fsub_rn(h2f(kt_s[s][2 * jp]), mn0), sc0));
+        const float r1 = __builtin_rintf(__fdiv_rn(__fsub_rn(h2f(kt_s[s][2 * jp + 1]), mn1), sc1));
+        const uint32_t b0 = (uint32_t)fminf(fmaxf(r0, 0.0f), qmax);
+        const uint32_t b1 = (uint32_t)fminf(fmaxf(r1, 0.0f), qmax);
+        // one table index per channel pair (the key row layout of tqk_common.h)
+        kc_s[s][jp] = (uint8_t)(kb == 4 ? ((rev4(b0) << 4) | rev4(b1)) : (b0 | (b1 << kb)));
+      }
+    } else {
+      const int jp = tid & 63, sq = tid >> 6;
+      float c0[16], c1[16];
+#pragma unroll
+      for (int l = 0; l < 16; ++l) {
+        c0[l] = cent_s[2 * jp][l];
+        c1[l] = cent_s[2 * jp + 1][l];
+      }
+      const int per_q = (G + kEncWaves - 1) / kEncWaves;
+      const int s0 = sq * per_q, s1 = min(G, s0 + per_q);
+      for (int s = s0; s < s1; ++s) {
+        const float x0 = h2f(kt_s[s][2 * jp]), x1 = h2f(kt_s[s][2 * jp + 1]);
+        int b0 = 0, b1 = 0;
+        float d0 = fabsf(__fsub_rn(x0, c0[0])), d1 = fabsf(__fsub_rn(x1, c1[0]));
+#pragma unroll
+        for (int l = 1; l < 16; ++l) {
+          const float e0 = fabsf(__fsub_rn(x0, c0[l])), e1 = fabsf(__fsub_rn(x1, c1[l]));
+          // np.argmin: strictly smaller wins; the first NaN wins over any number
+          if (e0 < d0 || (e0 != e0 && d0 == d0)) { d0 = e0; b0 = l; }
+          if (e1 < d1 || (e1 != e1 && d1 == d1)) { d1 = e1; b1 = l; }
+        }
+        kc_s[s][jp] = (uint8_t)((rev4(b0) << 4) | rev4(b1));
+      }
+    }
+
+    // ---- outlier side-list in flat (token, channel) order ---------------------
+    // ocount holds cumulative counts at every TQK_OBLK-token boundary of the
+    // group (entry TQK_NOB-1 = total), so a decode block finds its entries
+    // without searching.
+    const size_t obase = (size_t)slot * Hkv + h;
+    if (kout > 0) {
+      const bool all = kout >= G;
+      int cnt = 0;
+      if (tid < G) {
+        for (int j = 0; j < D; ++j) {
+          const float mag = fabsf(h2f(kt_s[tid][j]));
+          cnt += all ? 1 : (mag >= fabsf(h2f((uint16_t)thr_s[j])));
         }
       }
+      // block exclusive scan of cnt
+      int incl = cnt;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int v = __shfl_up(incl, o, 64);
+        if ((tid & 63) >= o) incl += v;
+      }
+      if ((tid & 63) == 63) wsum_s[tid >> 6] = incl;
+      __syncthreads();
+      int wofs = 0;
+      for (int w = 0; w < (tid >> 6); ++w) wofs += wsum_s[w];
+      int total = 0;
+      for (int w = 0; w < kEncWaves; ++w) total += wsum_s[w];
+      int off = wofs + incl - cnt;
+      // token s = TQK_OBLK*k - 1 closes block k-1: its inclusive offset is the bound
+      if (tid < G && ((tid + 1) % TQK_OBLK) == 0 && (tid + 1) / TQK_OBLK <= TQK_NOB)
+        a.p.ocount[obase * TQK_NOB + (tid + 1) / TQK_OBLK - 1] = off + cnt;
+      if (tid < TQK_NOB && TQK_OBLK * (tid + 1) > G) a.p.ocount[obase * TQK_NOB + tid] = total;
+      if (tid < G && cnt > 0) {
+        for (int j = 0; j < D; ++j) {
+          const uint16_t xv = kt_s[tid][j];
+          const bool sel = all || (fabsf(h2f(xv)) >= fabsf(h2f((uint16_t)thr_s[j])));
+          if (sel) {
+            if (off < d.outlier_cap) {
+              a.p.oent[obase * d.outlier_cap + off] = (uint32_t)(tid * D + j) | ((uint32_t)xv << 16);
+              // the stored code becomes the level whose value is gmean -- NF4's
+              // zero level (rev4(7) = 14), or code 0 of a uniform grid -- so the
+              // dense part of a decode contributes only gmean here and the
+              // side-list adds val - gmean; export restores the reference's code
+              uint8_t& kp = kc_s[tid][j >> 1];
+              if (d.key_bits == 4) {
+                const uint32_t zc = d.key_grid == 1 ? 0u : 14u;
+                kp = (j & 1) ? (uint8_t)((kp & 0xF0u) | zc) : (uint8_t)((kp & 0x0Fu) | (zc << 4));
+              } else {
+                // 3- and 2-bit keys are uniform: the pair field's code of channel j to 0
+                const uint32_t m = (1u << d.key_bits) - 1u;
+                kp = (uint8_t)(kp & ~((j & 1) ? (m << d.key_bits) : m));
+              }
+            }
+            ++off;
+          }
+        }
+      }
+      if (tid == 0 && total > d.outlier_cap && a.overflow) atomicOr(a.overflow, TQK_OVF_OUTLIERS);
+    } else if (tid < TQK_NOB) {
+      a.p.ocount[obase * TQK_NOB + tid] = 0;
     }
-    if (tid == 0 && total > d.outlier_cap && a.overflow) atomicOr(a.overflow, TQK_OVF_OUTLIERS);
-  } else if (tid < TQK_NOB) {
-    a.p.ocount[obase * TQK_NOB + tid] = 0;
   }
 
   // ---- values: one token per thread ---------------------------------------
@@ -250,6 +252,124 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
   // tiled layout: codes are staged in the (no longer needed) key tile and
   // re-assembled into 4-token x 8-channel units below
   uint8_t (*vc_s)[D] = reinterpret_cast<uint8_t (*)[D]>(&kt_s[0][0]);
+  __syncthreads();
+  // PolarQuant codes of the group's tokens (the value encode; PolarQuant keys
+  // run it on the keys): norms to nout, codes staged in vc_s[token][channel]
+  auto polar_phase = [&](const uint16_t* ring, const uint16_t* chunk, float* nout, bool vcheck) {
+    // Rotation operands: lane e of wave w owns rotated channel
+    // 64 * (w & 1) + lane and keeps column e of Pi_T (pi[e][0..D)) in
+    // registers; waves w and w ^ 1 split the channels, w >> 1 the tokens
+    // (two waves per SIMD).
+    // Normalised rows u of kVBatch tokens at a time sit in LDS after the code
+    // staging area, read as wave-uniform broadcasts.  Every y_e is still the
+    // sequential, separately rounded sum over d.
+    const int lane = tid & 63, wv = tid >> 6;
+    const int ecol = 64 * (wv & 1) + lane;
+    float pcol[D];
+#pragma unroll
+    for (int k = 0; k < D / 4; ++k) {
+      const float4 p4 = reinterpret_cast<const float4*>(a.p.pi + (size_t)ecol * D)[k];
+      pcol[4 * k] = p4.x;
+      pcol[4 * k + 1] = p4.y;
+      pcol[4 * k + 2] = p4.z;
+      pcol[4 * k + 3] = p4.w;
+    }
+    float bnd[15];
+#pragma unroll
+    for (int k = 0; k < (1 << VB) - 1; ++k) bnd[k] = a.p.vbnd[k];
+    constexpr int kVBatch = 64;
+    float (*u_s)[D] = reinterpret_cast<float (*)[D]>(&kt_s[0][0] + TQK_MAX_G * D / 2);
+    static_assert(TQK_MAX_G * D + kVBatch * D * 4 <= TQK_MAX_G * (D + 8) * 2, "value staging overflows the key tile");
+    for (int t0 = 0; t0 < G; t0 += kVBatch) {
+      const int nb = min(kVBatch, G - t0);
+      // (1) norms and normalised rows, four threads per token: thread q holds
+      // the pairwise partial sums r[2q], r[2q + 1] (channels 8m + 2q, 8m + 2q + 1)
+      {
+        const int tt = tid >> 2, q = tid & 3;
+        if (tt < nb) {
+          const int t = g * G + t0 + tt;
+          const uint32_t* src = reinterpret_cast<const uint32_t*>(token_src(a, ring, chunk, b, h, t));
+          float x0[16], x1[16];
+#pragma unroll
+          for (int m = 0; m < 16; ++m) {
+            const uint32_t w2 = src[4 * m + q];  // channels 8m + 2q, 8m + 2q + 1
+            x0[m] = h2f((uint16_t)(w2 & 0xFFFFu));
+            x1[m] = h2f((uint16_t)(w2 >> 16));
+          }
+          float r0 = __fmul_rn(x0[0], x0[0]), r1 = __fmul_rn(x1[0], x1[0]);
+#pragma unroll
+          for (int m = 1; m < 16; ++m) {
+            r0 = __fadd_rn(r0, __fmul_rn(x0[m], x0[m]));
+            r1 = __fadd_rn(r1, __fmul_rn(x1[m], x1[m]));
+          }
+          // pairwise tree ((r0 + r1) + (r2 + r3)) + ((r4 + r5) + (r6 + r7))
+          const float pa = __fadd_rn(r0, r1);
+          const float po = __shfl_xor(pa, 1, 4);
+          const float pb = (q & 1) ? __fadd_rn(po, pa) : __fadd_rn(pa, po);
+          const float pbo = __shfl_xor(pb, 2, 4);
+          const float ss = (q & 2) ? __fadd_rn(pbo, pb) : __fadd_rn(pb, pbo);
+          const float nrm = __builtin_sqrtf(ss);  // correctly rounded (-fhip-fp32-correctly-rounded-divide-sqrt)
+          const float safe = fmaxf(nrm, 1e-30f);
+#pragma unroll
+          for (int m = 0; m < 16; ++m) {
+            u_s[tt][8 * m + 2 * q] = __fdiv_rn(x0[m], safe);
+            u_s[tt][8 * m + 2 * q + 1] = __fdiv_rn(x1[m], safe);
+          }
+          if (q == 0) {
+            nout[page_row(a.p.block_table, d.max_pages_per_seq, b, t, P, d.n_pages, h)] = nrm;
+            if (vcheck && nrm > TQK_MAX_VNORM && a.overflow) atomicOr(a.overflow, TQK_OVF_VNORM);
+          }
+        }
+      }
+      __syncthreads();
+      // (2) rotation and codes: tokens j, j + 1 of the batch per step (two chains)
+      for (int j = 2 * (wv >> 1); j < nb; j += kEncWaves) {
+        const int j1 = min(j + 1, nb - 1);
+        float y0 = 0.f, y1 = 0.f;
+#pragma unroll
+        for (int d4 = 0; d4 < D / 4; ++d4) {
+          const float4 ua = *reinterpret_cast<const float4*>(&u_s[j][4 * d4]);
+          const float4 ub = *reinterpret_cast<const float4*>(&u_s[j1][4 * d4]);
+          y0 = __fadd_rn(y0, __fmul_rn(ua.x, pcol[4 * d4]));
+          y1 = __fadd_rn(y1, __fmul_rn(ub.x, pcol[4 * d4]));
+          y0 = __fadd_rn(y0, __fmul_rn(ua.y, pcol[4 * d4 + 1]));
+          y1 = __fadd_rn(y1, __fmul_rn(ub.y, pcol[4 * d4 + 1]));
+          y0 = __fadd_rn(y0, __fmul_rn(ua.z, pcol[4 * d4 + 2]));
+          y1 = __fadd_rn(y1, __fmul_rn(ub.z, pcol[4 * d4 + 2]));
+          y0 = __fadd_rn(y0, __fmul_rn(ua.w, pcol[4 * d4 + 3]));
+          y1 = __fadd_rn(y1, __fmul_rn(ub.w, pcol[4 * d4 + 3]));
+        }
+        uint32_t c0 = 0, c1 = 0;
+#pragma unroll
+        for (int k = 0; k < (1 << VB) - 1; ++k) {
+          c0 += (bnd[k] < y0) ? 1u : 0u;
+          c1 += (bnd[k] < y1) ? 1u : 0u;
+        }
+        vc_s[t0 + j][ecol] = (uint8_t)c0;
+        if (j + 1 < nb) vc_s[t0 + j + 1][ecol] = (uint8_t)c1;
+      }
+      __syncthreads();
+    }
+  };
+  if (d.key_grid == 2) {
+    // PolarQuant keys (turboquant_pro/core.py:542-617 with kind="key"): the
+    // value encode on the key tokens, norms to knorm, one table index per
+    // channel pair into kc_s; the per-channel stats are the identity
+    // (scale 1, mean 0) and there is no side-list
+    polar_phase(a.p.hot_k, a.chunk_k, a.p.knorm, false);
+    __syncthreads();
+    for (int idx = tid; idx < G * (D / 2); idx += kEncThreads) {
+      const int t = idx / (D / 2), jp = idx % (D / 2);
+      const uint32_t c0 = vc_s[t][2 * jp], c1 = vc_s[t][2 * jp + 1];
+      kc_s[t][jp] = (uint8_t)(d.key_bits == 4 ? ((rev4(c0) << 4) | rev4(c1)) : (c0 | (c1 << d.key_bits)));
+    }
+    const size_t mb = ((size_t)slot * Hkv + h) * D;
+    if (tid < D) {
+      a.p.gscale[mb + tid] = 1.0f;
+      a.p.gmean[mb + tid] = 0.0f;
+    }
+    if (tid < TQK_NOB) a.p.ocount[((size_t)slot * Hkv + h) * TQK_NOB + tid] = 0;
+  }
   __syncthreads();
   // key code rows, one 32-channel chunk (16 pair indices) per thread
   const int KROW = k_row_bytes(d.key_bits);
@@ -274,100 +394,7 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
       for (int w = 0; w < kb; ++w) dst[w] = o[w];
     }
   }
-  // Rotation operands: lane e of wave w owns rotated channel
-  // 64 * (w & 1) + lane and keeps column e of Pi_T (pi[e][0..D)) in
-  // registers; waves w and w ^ 1 split the channels, w >> 1 the tokens
-  // (two waves per SIMD).
-  // Normalised rows u of kVBatch tokens at a time sit in LDS after the code
-  // staging area, read as wave-uniform broadcasts.  Every y_e is still the
-  // sequential, separately rounded sum over d.
-  const int lane = tid & 63, wv = tid >> 6;
-  const int ecol = 64 * (wv & 1) + lane;
-  float pcol[D];
-#pragma unroll
-  for (int k = 0; k < D / 4; ++k) {
-    const float4 p4 = reinterpret_cast<const float4*>(a.p.pi + (size_t)ecol * D)[k];
-    pcol[4 * k] = p4.x;
-    pcol[4 * k + 1] = p4.y;
-    pcol[4 * k + 2] = p4.z;
-    pcol[4 * k + 3] = p4.w;
-  }
-  float bnd[15];
-#pragma unroll
-  for (int k = 0; k < (1 << VB) - 1; ++k) bnd[k] = a.p.vbnd[k];
-  constexpr int kVBatch = 64;
-  float (*u_s)[D] = reinterpret_cast<float (*)[D]>(&kt_s[0][0] + TQK_MAX_G * D / 2);
-  static_assert(TQK_MAX_G * D + kVBatch * D * 4 <= TQK_MAX_G * (D + 8) * 2, "value staging overflows the key tile");
-  for (int t0 = 0; t0 < G; t0 += kVBatch) {
-    const int nb = min(kVBatch, G - t0);
-    // (1) norms and normalised rows, four threads per token: thread q holds
-    // the pairwise partial sums r[2q], r[2q + 1] (channels 8m + 2q, 8m + 2q + 1)
-    {
-      const int tt = tid >> 2, q = tid & 3;
-      if (tt < nb) {
-        const int t = g * G + t0 + tt;
-        const uint32_t* src = reinterpret_cast<const uint32_t*>(token_src(a, a.p.hot_v, a.chunk_v, b, h, t));
-        float x0[16], x1[16];
-#pragma unroll
-        for (int m = 0; m < 16; ++m) {
-          const uint32_t w2 = src[4 * m + q];  // channels 8m + 2q, 8m + 2q + 1
-          x0[m] = h2f((uint16_t)(w2 & 0xFFFFu));
-          x1[m] = h2f((uint16_t)(w2 >> 16));
-        }
-        float r0 = __fmul_rn(x0[0], x0[0]), r1 = __fmul_rn(x1[0], x1[0]);
-#pragma unroll
-        for (int m = 1; m < 16; ++m) {
-          r0 = __fadd_rn(r0, __fmul_rn(x0[m], x0[m]));
-          r1 = __fadd_rn(r1, __fmul_rn(x1[m], x1[m]));
-        }
-        // pairwise tree ((r0 + r1) + (r2 + r3)) + ((r4 + r5) + (r6 + r7))
-        const float pa = __fadd_rn(r0, r1);
-        const float po = __shfl_xor(pa, 1, 4);
-        const float pb = (q & 1) ? __fadd_rn(po, pa) : __fadd_rn(pa, po);
-        const float pbo = __shfl_xor(pb, 2, 4);
-        const float ss = (q & 2) ? __fadd_rn(pbo, pb) : __fadd_rn(pb, pbo);
-        const float nrm = __builtin_sqrtf(ss);  // correctly rounded (-fhip-fp32-correctly-rounded-divide-sqrt)
-        const float safe = fmaxf(nrm, 1e-30f);
-#pragma unroll
-        for (int m = 0; m < 16; ++m) {
-          u_s[tt][8 * m + 2 * q] = __fdiv_rn(x0[m], safe);
-          u_s[tt][8 * m + 2 * q + 1] = __fdiv_rn(x1[m], safe);
-        }
-        if (q == 0) {
-          a.p.vnorm[page_row(a.p.block_table, d.max_pages_per_seq, b, t, P, d.n_pages, h)] = nrm;
-          if (nrm > TQK_MAX_VNORM && a.overflow) atomicOr(a.overflow, TQK_OVF_VNORM);
-        }
-      }
-    }
-    __syncthreads();
-    // (2) rotation and codes: tokens j, j + 1 of the batch per step (two chains)
-    for (int j = 2 * (wv >> 1); j < nb; j += kEncWaves) {
-      const int j1 = min(j + 1, nb - 1);
-      float y0 = 0.f, y1 = 0.f;
-#pragma unroll
-      for (int d4 = 0; d4 < D / 4; ++d4) {
-        const float4 ua = *reinterpret_cast<const float4*>(&u_s[j][4 * d4]);
-        const float4 ub = *reinterpret_cast<const float4*>(&u_s[j1][4 * d4]);
-        y0 = __fadd_rn(y0, __fmul_rn(ua.x, pcol[4 * d4]));
-        y1 = __fadd_rn(y1, __fmul_rn(ub.x, pcol[4 * d4]));
-        y0 = __fadd_rn(y0, __fmul_rn(ua.y, pcol[4 * d4 + 1]));
-        y1 = __fadd_rn(y1, __fmul_rn(ub.y, pcol[4 * d4 + 1]));
-        y0 = __fadd_rn(y0, __fmul_rn(ua.z, pcol[4 * d4 + 2]));
-        y1 = __fadd_rn(y1, __fmul_rn(ub.z, pcol[4 * d4 + 2]));
-        y0 = __fadd_rn(y0, __fmul_rn(ua.w, pcol[4 * d4 + 3]));
-        y1 = __fadd_rn(y1, __fmul_rn(ub.w, pcol[4 * d4 + 3]));
-      }
-      uint32_t c0 = 0, c1 = 0;
-#pragma unroll
-      for (int k = 0; k < (1 << VB) - 1; ++k) {
-        c0 += (bnd[k] < y0) ? 1u : 0u;
-        c1 += (bnd[k] < y1) ? 1u : 0u;
-      }
-      vc_s[t0 + j][ecol] = (uint8_t)c0;
-      if (j + 1 < nb) vc_s[t0 + j + 1][ecol] = (uint8_t)c1;
-    }
-    __syncthreads();
-  }
+  polar_phase(a.p.hot_v, a.chunk_v, a.p.vnorm, true);
   // (3) the code rows: 4-token x 8-channel units of 16-token tiles, or the
   // reference's little-endian bit stream per token
   if (tiled) {
@@ -469,13 +496,30 @@ __global__ __launch_bounds__(kThreads) void tqk_dequant_group(DequantArgs a) {
     uint32_t rw[TQK_D / 8];
     const uint32_t* kr = reinterpret_cast<const uint32_t*>(a.p.kcodes + row * KROW);
     for (int w = 0; w < KROW / 4; ++w) rw[w] = kr[w];
-    for (int jj = 0; jj < D / 2; ++jj) {
-      const uint32_t f = k_pair_index(rw, kb, jj);
-      const int j0 = 2 * jj, j1 = 2 * jj + 1;
-      ko[(size_t)tid * D + j0] =
-          __fadd_rn(__fmul_rn(a.p.gscale[mbase + j0], key_level(d.key_grid, k_code_even(f, kb))), a.p.gmean[mbase + j0]);
-      ko[(size_t)tid * D + j1] =
-          __fadd_rn(__fmul_rn(a.p.gscale[mbase + j1], key_level(d.key_grid, k_code_odd(f, kb))), a.p.gmean[mbase + j1]);
+    if (d.key_grid == 2) {
+      // PolarQuant keys: (cent[code] @ Pi) * norm, as the values below
+      float yk[D];
+      for (int jj = 0; jj < D / 2; ++jj) {
+        const uint32_t f = k_pair_index(rw, kb, jj);
+        yk[2 * jj] = a.p.vcent[k_code_even(f, kb)];
+        yk[2 * jj + 1] = a.p.vcent[k_code_odd(f, kb)];
+      }
+      const float kn = a.p.knorm[row];
+      for (int e = 0; e < D; ++e) {
+        float x = 0.f;
+#pragma unroll
+        for (int j = 0; j < D; ++j) x = __fadd_rn(x, __fmul_rn(yk[j], a.p.pi[j * D + e]));
+        ko[(size_t)tid * D + e] = __fmul_rn(x, kn);
+      }
+    } else {
+      for (int jj = 0; jj < D / 2; ++jj) {
+        const uint32_t f = k_pair_index(rw, kb, jj);
+        const int j0 = 2 * jj, j1 = 2 * jj + 1;
+        ko[(size_t)tid * D + j0] =
+            __fadd_rn(__fmul_rn(a.p.gscale[mbase + j0], key_level(d.key_grid, k_code_even(f, kb))), a.p.gmean[mbase + j0]);
+        ko[(size_t)tid * D + j1] =
+            __fadd_rn(__fmul_rn(a.p.gscale[mbase + j1], key_level(d.key_grid, k_code_odd(f, kb))), a.p.gmean[mbase + j1]);
+      }
     }
     float y[D];
     if (v_tiled(G, P)) {
@@ -540,6 +584,7 @@ int tqk_encode_groups(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t 
   a.overflow = overflow;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (d->key_grid == 0 && d->zero_point == 2 && !p->zp_mean) return TQK_EINVAL;
+  if (d->key_grid == 2 && !p->knorm) return TQK_EINVAL;
   const dim3 grid(n_items, d->n_kv_heads);
   if (d->value_bits == 2)
     hipLaunchKernelGGL(tqk_encode_group<2>, grid, dim3(kEncThreads), 0, st, a);
@@ -580,6 +625,7 @@ int tqk_dequant_groups(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t
   if (rc != TQK_OK) return rc;
   if (!p || n_items < 0 || (n_items > 0 && (!items || !kout || !vout))) return TQK_EINVAL;
   if (n_items == 0) return TQK_OK;
+  if (d->key_grid == 2 && !p->knorm) return TQK_EINVAL;
   DequantArgs a;
   a.d = *d;
   a.p = *p;

@@ -19,7 +19,7 @@ TQK_EUNSUPPORTED = 2
 TQK_EHIP = 3
 TQK_EWORKSPACE = 4
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 # Every symbol include/tqk.h declares (checked by the CPU test suite).
 EXPORTS = (
@@ -42,7 +42,7 @@ class CacheDesc(ctypes.Structure):
 class CachePtrs(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in (
         "kcodes", "vcodes", "vnorm", "gscale", "gmean", "ocount", "oent", "hot_k", "hot_v",
-        "block_table", "group_table", "pi", "pi_t", "vcent", "vbnd", "zp_mean")]
+        "block_table", "group_table", "pi", "pi_t", "vcent", "vbnd", "zp_mean", "knorm")]
 
 
 class BlockDesc(ctypes.Structure):

@@ -5,8 +5,8 @@ Same constructor, methods and return conventions as the reference's
 hot window of ``hot_window`` tokens, and flushed groups of
 ``(hot_window + 1) // 2`` tokens coded as per-channel keys (4-bit asym-NF4
 with a calibrated, sparse or bias zero point, or uniform 2/3/4-bit -- the
-reference's default) with an fp16 outlier side-list plus 2/3/4-bit PolarQuant
-values.  Storage and compute live on the GPU:
+reference's default) with an fp16 outlier side-list, or as PolarQuant
+(``per_channel_keys=False``), plus 2/3/4-bit PolarQuant values.  Storage and compute live on the GPU:
 ``append`` runs the quantize-on-flush kernel when a group completes,
 ``fused_decode`` runs the fused split-K kernel, ``get_keys``/``get_values``
 reconstruct on the GPU.
@@ -17,8 +17,10 @@ Differences from the reference, all deliberate:
     AutoConfig default and the point of this build);
   * keys/values/queries are converted to fp16 on entry (the serving dtype the
     kernels consume); codes are bit-exact with the reference for fp16 inputs;
-  * configurations without a gfx950 form (PolarQuant, symmetric-NF4 and
-    quantile keys; head_dim != 128) raise
+  * ``per_channel_keys=False`` (PolarQuant keys, turboquant_pro/core.py:1028-1029)
+    requires ``key_bits == value_bits``, as the reference's fused decode does;
+  * configurations without a gfx950 form (symmetric-NF4 and quantile keys;
+    head_dim != 128) raise
     NotImplementedError at construction instead of silently running on the CPU;
   * an optional ``n_q_heads`` (a multiple of ``n_heads``) serves GQA queries.
 """
@@ -80,6 +82,16 @@ class TurboQuantKVCache:
             raise ValueError("zero_point must be one of ('calibrated', 'sparse', 'bias')")
         if key_nf4_asym:
             key_nf4 = True
+        if not per_channel_keys:
+            # PolarQuant keys (turboquant_pro/core.py:1028-1029): the per-channel
+            # flags configure a quantizer the reference then never builds
+            key_nf4 = key_nf4_asym = key_nuq = False
+            key_zero_point, key_rope_theta, key_k_bias = "calibrated", None, None
+            self.key_zero_point = key_zero_point
+            if self.key_bits != self.value_bits:
+                raise NotImplementedError(
+                    "PolarQuant keys on the gfx950 cache share the value codebook: key_bits must "
+                    "equal value_bits (the reference's fused decode has the same requirement)")
         if key_nf4 and self.key_bits != 4:
             raise ValueError("nf4=True requires bits=4")
         # zero-point checks of PerChannelKV.__init__ (turboquant_pro/per_channel_kv.py:199-213)
@@ -95,14 +107,14 @@ class TurboQuantKVCache:
         self.key_rope_theta, self.key_k_bias = key_rope_theta, key_k_bias
         # per-channel keys: asym-NF4 (robust / build_cache) or, without any NF4
         # or quantile flag, the reference's uniform mode (its default, at 2, 3 or
-        # 4 bits)
+        # 4 bits); per_channel_keys=False: PolarQuant keys
         uniform = per_channel_keys and not key_nuq and not key_nf4
-        if not per_channel_keys or key_nuq or not (key_nf4_asym or uniform):
+        if per_channel_keys and (key_nuq or not (key_nf4_asym or uniform)):
             raise NotImplementedError(
-                "the gfx950 cache codes keys per channel, as asym-NF4 (TurboQuantKVCache.robust / "
-                "AutoConfig.build_cache) or uniform 2/3/4-bit; PolarQuant, symmetric-NF4 and "
-                "quantile keys have no GPU form here")
-        self.key_grid = "uniform" if uniform else "nf4_asym"
+                "the gfx950 cache codes keys per channel as asym-NF4 (TurboQuantKVCache.robust / "
+                "AutoConfig.build_cache) or uniform 2/3/4-bit, or as PolarQuant "
+                "(per_channel_keys=False); symmetric-NF4 and quantile keys have no GPU form here")
+        self.key_grid = "polar" if not per_channel_keys else "uniform" if uniform else "nf4_asym"
         if head_dim != 128:
             raise NotImplementedError("the gfx950 kernels are built for head_dim=128")
         if group_tokens_for(hot_window) > 256 or hot_window < 1:
@@ -116,7 +128,8 @@ class TurboQuantKVCache:
         return TQKVPool(n_kv_heads=self.n_heads, n_q_heads=self.n_q_heads, head_dim=self.head_dim,
                         max_batch=1, max_seq_len=capacity, hot_window=self.hot_window,
                         key_bits=self.key_bits, value_bits=self.value_bits,
-                        outlier_frac=self.key_outlier_frac, seed=self.seed, rotation=rotation,
+                        outlier_frac=self.key_outlier_frac if self.key_grid != "polar" else 0.0,
+                        seed=self.seed, rotation=rotation,
                         device=self._device, key_grid=self.key_grid,
                         zero_point=self.key_zero_point, rope_theta=self.key_rope_theta,
                         k_bias=self.key_k_bias)
@@ -234,7 +247,11 @@ class TurboQuantKVCache:
         zp_ch = {"calibrated": D, "bias": 0}.get(self.key_zero_point, None)
         if zp_ch is None:
             zp_ch = int(self._pool.dc_mask.sum())
-        key_bytes = ng * (H * G * D * self.key_bits // 8 + H * D * 4 + H * zp_ch * 4) + n_out * 6
+        if self.key_grid == "polar":
+            # CompressedKV: packed codes + one f32 norm per token and head
+            key_bytes = ng * (-(-H * G * D * self.key_bits // 8) + H * G * 4)
+        else:
+            key_bytes = ng * (H * G * D * self.key_bits // 8 + H * D * 4 + H * zp_ch * 4) + n_out * 6
         val_bytes = ng * (H * G * D * self.value_bits // 8 + H * G * 4)
         cold = float(key_bytes + val_bytes)
         hot = float(self.hot_length * H * D * 2 * 2)

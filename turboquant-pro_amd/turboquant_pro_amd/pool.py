@@ -30,6 +30,9 @@ from .codebooks import (dc_channel_mask, dc_mask_words, group_tokens_for, n_grou
                         outliers_per_channel, random_rotation, rope_averaged_bias, value_codebook)
 
 ZERO_POINTS = {"calibrated": 0, "sparse": 1, "bias": 2}
+# key forms: per-channel asym-NF4, per-channel uniform, PolarQuant (the value
+# encode on the keys: per-token norms, rotated codes on the value codebook)
+KEY_GRIDS = {"nf4_asym": 0, "uniform": 1, "polar": 2}
 
 
 def _torch():
@@ -55,6 +58,13 @@ class TQKVPool:
         self._custom_table = block_table is not None
         if zero_point not in ZERO_POINTS:
             raise ValueError(f"zero_point must be one of {tuple(ZERO_POINTS)}")
+        if key_grid not in KEY_GRIDS:
+            raise ValueError(f"key_grid must be one of {tuple(KEY_GRIDS)}")
+        if key_grid == "polar":
+            if key_bits != value_bits:
+                raise NotImplementedError("PolarQuant keys share the value codebook: key_bits must "
+                                          "equal value_bits")
+            outlier_frac = 0.0  # PolarQuant keys have no side-list
         if zero_point != "calibrated":
             if key_grid != "nf4_asym":
                 raise ValueError(f"zero_point={zero_point!r} requires asym-NF4 keys")
@@ -90,7 +100,7 @@ class TQKVPool:
             outliers_per_channel=k_out, outlier_cap=outlier_cap,
             max_pages_per_seq=max_pages, max_groups_per_seq=max_groups,
             hot_ring=hot_window, n_pages=max_batch * max_pages, sm_scale=1.0 / math.sqrt(head_dim),
-            key_grid={"nf4_asym": 0, "uniform": 1}[key_grid], zero_point=ZERO_POINTS[zero_point])
+            key_grid=KEY_GRIDS[key_grid], zero_point=ZERO_POINTS[zero_point])
         self.key_grid = key_grid
         self.zero_point, self.rope_theta = zero_point, rope_theta
         # "sparse": the channels whose rotary wavelength exceeds a group
@@ -108,6 +118,9 @@ class TQKVPool:
         self.kcodes = torch.zeros((n_kv_heads, n_pages, P, head_dim * key_bits // 8), dtype=u8, device=dev)
         self.vcodes = torch.zeros((n_kv_heads, n_pages, P, head_dim * value_bits // 8), dtype=u8, device=dev)
         self.vnorm = torch.zeros((n_kv_heads, n_pages, P), dtype=f32, device=dev)
+        # PolarQuant keys: per-token key norms, laid out as vnorm
+        self.knorm = (torch.zeros((n_kv_heads, n_pages, P), dtype=f32, device=dev)
+                      if key_grid == "polar" else None)
         self.gscale = torch.zeros((n_slots, n_kv_heads, head_dim), dtype=f32, device=dev)
         self.gmean = torch.zeros((n_slots, n_kv_heads, head_dim), dtype=f32, device=dev)
         # cumulative outlier counts at every 32-token boundary of a group (last = total)
@@ -147,7 +160,8 @@ class TQKVPool:
             block_table=self.block_table.data_ptr(), group_table=self.group_table.data_ptr(),
             pi=self.pi.data_ptr(), pi_t=self.pi_t.data_ptr(), vcent=self.vcent.data_ptr(),
             vbnd=self.vbnd.data_ptr(),
-            zp_mean=self.zp_mean.data_ptr() if self.zp_mean is not None else None)
+            zp_mean=self.zp_mean.data_ptr() if self.zp_mean is not None else None,
+            knorm=self.knorm.data_ptr() if self.knorm is not None else None)
         self.lengths = [0] * max_batch
         self.seq_lens = torch.zeros(max_batch, dtype=i32, device=dev)
         self._overflow = torch.zeros(1, dtype=i32, device=dev)
@@ -203,7 +217,7 @@ class TQKVPool:
         old_bt = self.block_table.long()[:, :mp_old]
         new_bt = new.block_table.long()[:, :mp_old]
         src, dst = old_bt.reshape(-1), new_bt.reshape(-1)
-        for name in ("kcodes", "vcodes", "vnorm"):
+        for name in ("kcodes", "vcodes", "vnorm") + (("knorm",) if self.knorm is not None else ()):
             getattr(new, name)[:, dst] = getattr(self, name)[:, src]
         so = self.group_table.long()[:, :mg_old].reshape(-1)
         sn = new.group_table.long()[:, :mg_old].reshape(-1)
@@ -354,7 +368,10 @@ class TQKVPool:
         """Group ``g`` of sequence ``b`` in the reference container layout:
         ``kpacked`` (CompressedPerChannelKV.indices), ``nf4_scale``/``nf4_mean``
         ``(H, D)``, ``outlier_idx`` int32 / ``outlier_val`` fp16 (flat over
-        ``(1, H, G, D)``), ``vpacked`` (CompressedKV.indices), ``vnorms`` ``(H, G)``."""
+        ``(1, H, G, D)``), ``vpacked`` (CompressedKV.indices), ``vnorms`` ``(H, G)``.
+        PolarQuant keys: ``kpacked`` is the keys' CompressedKV.indices (the value
+        pack) and ``knorms`` ``(H, G)`` their norms, with no scale, mean or
+        side-list."""
         phys, off = self._rows(b, g)
         H, G, D = self.n_kv_heads, self.group_tokens, self.head_dim
         kp = self.kcodes[:, phys, off].contiguous().cpu().numpy()  # (H, G, D * key_bits / 8)
@@ -363,6 +380,15 @@ class TQKVPool:
             vp = np.stack([pack_values(untile_value_rows(vp[h], self.value_bits, D), self.value_bits)
                            for h in range(H)])
         vn = self.vnorm[:, phys, off].contiguous()
+        if self.key_grid == "polar":
+            codes = codes_from_key_rows(kp.reshape(H * G, -1), self.key_bits, D)
+            return {
+                "kpacked": pack_values(codes, self.key_bits).reshape(-1),
+                "knorms": self.knorm[:, phys, off].contiguous().cpu().numpy(),
+                "position_start": g * G,
+                "vpacked": np.ascontiguousarray(vp).reshape(-1),
+                "vnorms": vn.cpu().numpy(),
+            }
         slot = int(self.group_table[b, g])
         cnt = self.ocount[slot, :, -1].cpu().numpy()
         ent = self.oent[slot].cpu().numpy().view(np.uint32)
@@ -406,14 +432,30 @@ class TQKVPool:
         layout (the inverse of :meth:`export_group`).  ``keys``: ``kpacked``
         (H*G*D/2 bytes), ``nf4_scale``/``nf4_mean`` (H, D), ``outlier_idx``
         (flat over (H, G, D), token-major within a head as the reference emits
-        them) and ``outlier_val`` fp16, or ``None`` outliers; ``values``:
+        them) and ``outlier_val`` fp16, or ``None`` outliers (PolarQuant keys:
+        ``kpacked``, the value pack of H*G*D codes, and ``knorms`` (H, G)); ``values``:
         ``vpacked`` (reference pack of H*G*D codes) and ``vnorms`` (H, G); a
         tiled pool stores them in its MFMA-tiled order."""
         torch = _torch()
         H, G, D = self.n_kv_heads, self.group_tokens, self.head_dim
         phys, off = self._rows(b, g)
         slot = int(self.group_table[b, g])
-        if keys is not None:
+        if keys is not None and self.key_grid == "polar":
+            kb = self.key_bits
+            kp = np.asarray(keys["kpacked"], np.uint8).reshape(-1)
+            need = -(-H * G * D * kb // 8)
+            if kp.size < need:
+                raise ValueError(f"kpacked holds {kp.size} bytes; a group of {kb}-bit keys takes {need}")
+            codes = unpack_values(kp, H * G * D, kb).reshape(H * G, D)
+            rows = key_rows_from_codes(codes, kb).reshape(H, G, -1)
+            self.kcodes[:, phys, off] = torch.from_numpy(np.ascontiguousarray(rows)).to(self.device)
+            self.knorm[:, phys, off] = torch.from_numpy(
+                np.asarray(keys["knorms"], np.float32).reshape(H, G)).to(self.device)
+            # the identity per-channel stats and an empty side-list, as the encode writes them
+            self.gscale[slot] = 1.0
+            self.gmean[slot] = 0.0
+            self.ocount[slot] = 0
+        elif keys is not None:
             kb = self.key_bits
             kp = np.asarray(keys["kpacked"], np.uint8).reshape(-1)
             if kp.size != H * G * D * kb // 8:

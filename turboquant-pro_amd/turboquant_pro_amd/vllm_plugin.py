@@ -10,9 +10,10 @@ layer, ``load`` reconstructs a token range, ``memory_stats`` /
 known.  Each layer's cache is the GPU cache built with the constructor's
 arguments, so a layer's coded groups are bit-exact to the reference's for the
 same configuration and fp16-valued input (the reference's default, 3-bit
-uniform keys and values, included); configurations the GPU cache has no form
-for (PolarQuant or quantile keys) raise ``NotImplementedError`` at
-construction.  ``fused_decode`` runs one layer's
+uniform keys and values, and PolarQuant keys with ``per_channel_keys=False``
+included); configurations the GPU cache has no form for (quantile keys,
+PolarQuant keys of another width than the values) raise
+``NotImplementedError`` at construction.  ``fused_decode`` runs one layer's
 decode step on codes.
 """
 
