@@ -49,6 +49,31 @@ __device__ __forceinline__ const uint16_t* token_src(const EncodeArgs& a, const 
 
 __device__ __forceinline__ uint32_t abs_h(uint16_t x) { return x & 0x7FFFu; }
 
+// Lane I of each 16-lane row, broadcast to the row (DPP row_newbcast).
+template <int I>
+__device__ __forceinline__ float row_bcast(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x150 + I, 0xF, 0xF, true));
+}
+
+// y0 += u_a[d] * pcol[d], y1 += u_b[d] * pcol[d] for d = 8K .. 8K + 7 and on
+// to d = 127, each product and sum separately rounded (this unit is built
+// with -ffp-contract=off), in d order; u_a[d] lives in register d % 8 of
+// lane d / 8 of the 16-lane row.  Plain operators, so that the broadcast
+// folds into the multiply as its DPP source operand.
+template <int K>
+__device__ __forceinline__ void rotate_row(float& y0, float& y1, const float (&ua)[8],
+                                           const float (&ub)[8], const float (&pcol)[TQK_D]) {
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const float p0 = row_bcast<K>(ua[r]) * pcol[8 * K + r];
+    const float p1 = row_bcast<K>(ub[r]) * pcol[8 * K + r];
+    y0 = y0 + p0;
+    y1 = y1 + p1;
+  }
+  if constexpr (K + 1 < TQK_D / 8) rotate_row<K + 1>(y0, y1, ua, ub, pcol);
+}
+
 template <int VB>
 __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
   constexpr int D = TQK_D;
@@ -256,15 +281,17 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
   // PolarQuant codes of the group's tokens (the value encode; PolarQuant keys
   // run it on the keys): norms to nout, codes staged in vc_s[token][channel]
   auto polar_phase = [&](const uint16_t* ring, const uint16_t* chunk, float* nout, bool vcheck) {
-    // Rotation operands: lane e of wave w owns rotated channel
-    // 64 * (w & 1) + lane and keeps column e of Pi_T (pi[e][0..D)) in
-    // registers; waves w and w ^ 1 split the channels, w >> 1 the tokens
-    // (two waves per SIMD).
-    // Normalised rows u of kVBatch tokens at a time sit in LDS after the code
-    // staging area, read as wave-uniform broadcasts.  Every y_e is still the
-    // sequential, separately rounded sum over d.
-    const int lane = tid & 63, wv = tid >> 6;
-    const int ecol = 64 * (wv & 1) + lane;
+    // Rotation operands: wave w owns the 16 rotated channels [16w, 16w + 16);
+    // lane l holds column e = 16w + (l & 15) of Pi_T (pi[e][0..D)) in
+    // registers, and its 16-lane row (l >> 4) works on one token of a 4-token
+    // pass.  The token's normalised row u sits in LDS (kVBatch tokens at a
+    // time, after the code staging area); each lane of the row loads channels
+    // [8(l & 15), 8(l & 15) + 8) of it, and u_d reaches the row's 16 lanes by
+    // a DPP row broadcast from lane d / 8 folded into the multiply -- no LDS
+    // broadcast reads, which would cost the LDS a full wave's bandwidth each.
+    // Every y_e is still the sequential, separately rounded sum over d.
+    const int lane = tid & 63, wv = tid >> 6, rt = lane >> 4, li = lane & 15;
+    const int ecol = 16 * wv + li;
     float pcol[D];
 #pragma unroll
     for (int k = 0; k < D / 4; ++k) {
@@ -322,31 +349,33 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
         }
       }
       __syncthreads();
-      // (2) rotation and codes: tokens j, j + 1 of the batch per step (two chains)
-      for (int j = 2 * (wv >> 1); j < nb; j += kEncWaves) {
-        const int j1 = min(j + 1, nb - 1);
-        float y0 = 0.f, y1 = 0.f;
-#pragma unroll
-        for (int d4 = 0; d4 < D / 4; ++d4) {
-          const float4 ua = *reinterpret_cast<const float4*>(&u_s[j][4 * d4]);
-          const float4 ub = *reinterpret_cast<const float4*>(&u_s[j1][4 * d4]);
-          y0 = __fadd_rn(y0, __fmul_rn(ua.x, pcol[4 * d4]));
-          y1 = __fadd_rn(y1, __fmul_rn(ub.x, pcol[4 * d4]));
-          y0 = __fadd_rn(y0, __fmul_rn(ua.y, pcol[4 * d4 + 1]));
-          y1 = __fadd_rn(y1, __fmul_rn(ub.y, pcol[4 * d4 + 1]));
-          y0 = __fadd_rn(y0, __fmul_rn(ua.z, pcol[4 * d4 + 2]));
-          y1 = __fadd_rn(y1, __fmul_rn(ub.z, pcol[4 * d4 + 2]));
-          y0 = __fadd_rn(y0, __fmul_rn(ua.w, pcol[4 * d4 + 3]));
-          y1 = __fadd_rn(y1, __fmul_rn(ub.w, pcol[4 * d4 + 3]));
+      // (2) rotation and codes: tokens ja = 8p + rt and jb = ja + 4 of the
+      // batch per pass (two chains per lane)
+      for (int j0 = 0; j0 < nb; j0 += 8) {
+        const int ja = j0 + rt, jb = j0 + 4 + rt;
+        float ua[8], ub[8];
+        {
+          const float4* ra = reinterpret_cast<const float4*>(&u_s[min(ja, nb - 1)][8 * li]);
+          const float4* rb = reinterpret_cast<const float4*>(&u_s[min(jb, nb - 1)][8 * li]);
+          const float4 a0 = ra[0], a1 = ra[1], b0 = rb[0], b1 = rb[1];
+          ua[0] = a0.x; ua[1] = a0.y; ua[2] = a0.z; ua[3] = a0.w;
+          ua[4] = a1.x; ua[5] = a1.y; ua[6] = a1.z; ua[7] = a1.w;
+          ub[0] = b0.x; ub[1] = b0.y; ub[2] = b0.z; ub[3] = b0.w;
+          ub[4] = b1.x; ub[5] = b1.y; ub[6] = b1.z; ub[7] = b1.w;
         }
+        float y0 = 0.f, y1 = 0.f;
+        rotate_row<0>(y0, y1, ua, ub, pcol);
+        // keeps the sums out of the conditional stores below: sunk into them,
+        // the multiplies would leave their broadcasts behind as separate moves
+        asm volatile("" : "+v"(y0), "+v"(y1));
         uint32_t c0 = 0, c1 = 0;
 #pragma unroll
         for (int k = 0; k < (1 << VB) - 1; ++k) {
           c0 += (bnd[k] < y0) ? 1u : 0u;
           c1 += (bnd[k] < y1) ? 1u : 0u;
         }
-        vc_s[t0 + j][ecol] = (uint8_t)c0;
-        if (j + 1 < nb) vc_s[t0 + j + 1][ecol] = (uint8_t)c1;
+        if (ja < nb) vc_s[t0 + ja][ecol] = (uint8_t)c0;
+        if (jb < nb) vc_s[t0 + jb][ecol] = (uint8_t)c1;
       }
       __syncthreads();
     }
