@@ -49,6 +49,16 @@ __device__ __forceinline__ const uint16_t* token_src(const EncodeArgs& a, const 
 
 __device__ __forceinline__ uint32_t abs_h(uint16_t x) { return x & 0x7FFFu; }
 
+typedef uint16_t u16x2_t __attribute__((ext_vector_type(2)));
+
+// Sum over lanes l, l ^ 16, l ^ 32, l ^ 48 (the four 16-lane rows).
+__device__ __forceinline__ int sum_quarters(int x) {
+  auto a = __builtin_amdgcn_permlane32_swap((uint32_t)x, (uint32_t)x, false, false);
+  x = (int)(a[0] + a[1]);
+  auto b = __builtin_amdgcn_permlane16_swap((uint32_t)x, (uint32_t)x, false, false);
+  return (int)(b[0] + b[1]);
+}
+
 // Lane I of each 16-lane row, broadcast to the row (DPP row_newbcast).
 template <int I>
 __device__ __forceinline__ float row_bcast(float x) {
@@ -102,7 +112,7 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
     }
     __syncthreads();
 
-    // ---- per-channel statistics (threads 0..127) and outlier thresholds (128..255)
+    // ---- per-channel statistics (threads 0..127)
     const size_t mbase = ((size_t)slot * Hkv + h) * D;
     if (tid < D && d.key_grid == 1) {
       // uniform keys (turboquant_pro/per_channel_kv.py:303-306): channel min and
@@ -151,18 +161,37 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
       for (int l = 0; l < 16; ++l) cent_s[j][l] = __fadd_rn(mu, __fmul_rn(amax, kNF4[l]));
       a.p.gscale[mbase + j] = amax;
       a.p.gmean[mbase + j] = mu;
-    } else if (tid < 2 * D && kout > 0 && kout < G) {
-      // k-th largest |x| as the largest fp16 magnitude pattern T with
-      // #{ |x_s| >= T } >= k (NaN patterns order above inf, as np.partition does).
-      const int j = tid - D;
+    }
+    // ---- outlier thresholds: the k-th largest |x| of each channel as the
+    // largest fp16 magnitude pattern T with #{ |x_s| >= T } >= k (NaN patterns
+    // order above inf, as np.partition does).  Every thread: wave w takes
+    // channels [16w, 16w + 16), lanes l, l ^ 16, l ^ 32, l ^ 48 a quarter of
+    // the tokens each, two magnitudes per register; a candidate's count is the
+    // carry bit of a packed 16-bit add, summed over the four lanes.
+    if (kout > 0 && kout < G) {
+      const int lane = tid & 63, wv = tid >> 6;
+      const int j = 16 * wv + (lane & 15), part = lane >> 4;
+      u16x2_t m2[TQK_MAX_G / 8];
+#pragma unroll
+      for (int i = 0; i < TQK_MAX_G / 8; ++i) {
+        const int s = (TQK_MAX_G / 4) * part + 2 * i;  // tokens past G count as magnitude 0
+        m2[i] = u16x2_t{(uint16_t)(s < G ? abs_h(kt_s[s][j]) : 0u),
+                        (uint16_t)(s + 1 < G ? abs_h(kt_s[s + 1][j]) : 0u)};
+      }
       uint32_t T = 0;
       for (int bit = 14; bit >= 0; --bit) {
         const uint32_t cand = T | (1u << bit);
-        int cnt = 0;
-        for (int s = 0; s < G; ++s) cnt += (abs_h(kt_s[s][j]) >= cand);
+        // m + (0x8000 - cand) has bit 15 set exactly when m >= cand (m, cand < 2^15)
+        const uint16_t bias = (uint16_t)(0x8000u - cand);
+        const u16x2_t bv = {bias, bias};
+        uint32_t acc = 0;  // two 16-bit counts
+#pragma unroll
+        for (int i = 0; i < TQK_MAX_G / 8; ++i)
+          acc += (__builtin_bit_cast(uint32_t, (u16x2_t)(m2[i] + bv)) >> 15) & 0x00010001u;
+        const int cnt = sum_quarters((int)((acc & 0xFFFFu) + (acc >> 16)));
         if (cnt >= kout) T = cand;
       }
-      thr_s[j] = T;
+      if (part == 0) thr_s[j] = T;
     }
     __syncthreads();
 
