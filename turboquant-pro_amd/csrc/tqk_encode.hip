@@ -21,8 +21,9 @@
 namespace {
 
 constexpr int kThreads = 256;
-// the group encode: eight waves, two per SIMD (its LDS allows one workgroup per CU)
-constexpr int kEncThreads = 512;
+// the group encode: four waves; its LDS (under 80 KiB) lets two workgroups share
+// a CU, so one's latency-bound key phase runs beside the other's value rotation
+constexpr int kEncThreads = 256;
 constexpr int kEncWaves = kEncThreads / 64;
 
 struct EncodeArgs {
@@ -88,19 +89,27 @@ template <int VB>
 __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
   constexpr int D = TQK_D;
   const int item = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+  const int lane = tid & 63, wv = tid >> 6;
   const tqk_cache_desc& d = a.d;
   const int b = a.items[2 * item], g = a.items[2 * item + 1];
   const int G = d.group_tokens, P = d.page_tokens, Hkv = d.n_kv_heads;
   const int slot = a.p.group_table[(size_t)b * d.max_groups_per_seq + g];
   const int kout = d.outliers_per_channel;
+  const size_t mbase = ((size_t)slot * Hkv + h) * D;
+  const size_t obase = (size_t)slot * Hkv + h;
 
-  __shared__ __align__(16) uint16_t kt_s[TQK_MAX_G][D + 8];  // key tile, fp16 bits (row padded vs bank conflicts)
-  __shared__ float cent_s[D][17];            // per-channel grids (padded)
+  // Key tile (fp16 bits, rows padded against bank conflicts).  Its rows also
+  // take the key codes: the codes of token t overwrite the first D / 2 bytes of
+  // row t once the wave that owns the row has read it (kc_row).  Then the area
+  // holds the value phase's codes (vc_s) and normalised rows (u_s).
+  __shared__ __align__(16) uint16_t kt_s[TQK_MAX_G][D + 8];
+  __shared__ float stat_s[D][2];             // per channel: (mean, amax) or (min, scale)
   __shared__ uint32_t thr_s[D];              // fp16 magnitude threshold per channel
+  __shared__ uint32_t omask_s[TQK_MAX_G][D / 32];  // channels of each token stored in the side-list
   __shared__ int32_t wsum_s[kEncWaves];
-  // packed key codes of the group, written out after the outlier pass has put
-  // the NF4 zero level (code 7) at every stored outlier position
-  __shared__ __align__(16) uint8_t kc_s[TQK_MAX_G][D / 2];
+  auto kc_row = [&](int t) { return reinterpret_cast<uint8_t*>(&kt_s[t][0]); };
+  uint8_t (*vc_s)[D] = reinterpret_cast<uint8_t (*)[D]>(&kt_s[0][0]);
+  static_assert(TQK_MAX_G * (D + 8) * 2 >= TQK_MAX_G * D + 64 * D * 4, "value staging overflows the key tile");
 
   if (d.key_grid != 2) {
     // ---- stage the key tile ----------------------------------------------
@@ -112,8 +121,7 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
     }
     __syncthreads();
 
-    // ---- per-channel statistics (threads 0..127)
-    const size_t mbase = ((size_t)slot * Hkv + h) * D;
+    // ---- per-channel statistics (threads 0..127) ---------------------------
     if (tid < D && d.key_grid == 1) {
       // uniform keys (turboquant_pro/per_channel_kv.py:303-306): channel min and
       // max over the tokens, scale = max(max - min, 1e-8) / (2^bits - 1) (NaN propagates)
@@ -129,8 +137,8 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
       const float rng = __fsub_rn(mx, mn);
       const float sc = nan ? __builtin_nanf("") : __fdiv_rn(fmaxf(rng, 1e-8f), (float)((1 << d.key_bits) - 1));
       if (nan) mn = __builtin_nanf("");
-      cent_s[j][0] = mn;
-      cent_s[j][1] = sc;
+      stat_s[j][0] = mn;
+      stat_s[j][1] = sc;
       a.p.gscale[mbase + j] = sc;
       a.p.gmean[mbase + j] = mn;
     } else if (tid < D) {
@@ -157,91 +165,50 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
         amax = fmaxf(amax, dv);
       }
       amax = nan ? __builtin_nanf("") : fmaxf(amax, 1e-8f);
-#pragma unroll
-      for (int l = 0; l < 16; ++l) cent_s[j][l] = __fadd_rn(mu, __fmul_rn(amax, kNF4[l]));
+      stat_s[j][0] = mu;
+      stat_s[j][1] = amax;
       a.p.gscale[mbase + j] = amax;
       a.p.gmean[mbase + j] = mu;
     }
     // ---- outlier thresholds: the k-th largest |x| of each channel as the
     // largest fp16 magnitude pattern T with #{ |x_s| >= T } >= k (NaN patterns
-    // order above inf, as np.partition does).  Every thread: wave w takes
-    // channels [16w, 16w + 16), lanes l, l ^ 16, l ^ 32, l ^ 48 a quarter of
-    // the tokens each, two magnitudes per register; a candidate's count is the
+    // order above inf, as np.partition does).  Every thread, 16 channels per
+    // wave and pass: lanes l, l ^ 16, l ^ 32, l ^ 48 take a quarter of the
+    // tokens each, two magnitudes per register; a candidate's count is the
     // carry bit of a packed 16-bit add, summed over the four lanes.
     if (kout > 0 && kout < G) {
-      const int lane = tid & 63, wv = tid >> 6;
-      const int j = 16 * wv + (lane & 15), part = lane >> 4;
-      u16x2_t m2[TQK_MAX_G / 8];
+      const int part = lane >> 4;
+      for (int j = 16 * wv + (lane & 15); j < D; j += 16 * kEncWaves) {
+        u16x2_t m2[TQK_MAX_G / 8];
 #pragma unroll
-      for (int i = 0; i < TQK_MAX_G / 8; ++i) {
-        const int s = (TQK_MAX_G / 4) * part + 2 * i;  // tokens past G count as magnitude 0
-        m2[i] = u16x2_t{(uint16_t)(s < G ? abs_h(kt_s[s][j]) : 0u),
-                        (uint16_t)(s + 1 < G ? abs_h(kt_s[s + 1][j]) : 0u)};
-      }
-      uint32_t T = 0;
-      for (int bit = 14; bit >= 0; --bit) {
-        const uint32_t cand = T | (1u << bit);
-        // m + (0x8000 - cand) has bit 15 set exactly when m >= cand (m, cand < 2^15)
-        const uint16_t bias = (uint16_t)(0x8000u - cand);
-        const u16x2_t bv = {bias, bias};
-        uint32_t acc = 0;  // two 16-bit counts
+        for (int i = 0; i < TQK_MAX_G / 8; ++i) {
+          const int s = (TQK_MAX_G / 4) * part + 2 * i;  // tokens past G count as magnitude 0
+          m2[i] = u16x2_t{(uint16_t)(s < G ? abs_h(kt_s[s][j]) : 0u),
+                          (uint16_t)(s + 1 < G ? abs_h(kt_s[s + 1][j]) : 0u)};
+        }
+        uint32_t T = 0;
+        for (int bit = 14; bit >= 0; --bit) {
+          const uint32_t cand = T | (1u << bit);
+          // m + (0x8000 - cand) has bit 15 set exactly when m >= cand (m, cand < 2^15)
+          const uint16_t bias = (uint16_t)(0x8000u - cand);
+          const u16x2_t bv = {bias, bias};
+          uint32_t acc = 0;  // two 16-bit counts
 #pragma unroll
-        for (int i = 0; i < TQK_MAX_G / 8; ++i)
-          acc += (__builtin_bit_cast(uint32_t, (u16x2_t)(m2[i] + bv)) >> 15) & 0x00010001u;
-        const int cnt = sum_quarters((int)((acc & 0xFFFFu) + (acc >> 16)));
-        if (cnt >= kout) T = cand;
+          for (int i = 0; i < TQK_MAX_G / 8; ++i)
+            acc += (__builtin_bit_cast(uint32_t, (u16x2_t)(m2[i] + bv)) >> 15) & 0x00010001u;
+          const int cnt = sum_quarters((int)((acc & 0xFFFFu) + (acc >> 16)));
+          if (cnt >= kout) T = cand;
+        }
+        if (part == 0) thr_s[j] = T;
       }
-      if (part == 0) thr_s[j] = T;
     }
     __syncthreads();
 
-    // ---- codes: thread = (channel pair, token slice); one byte per (token, pair)
-    if (d.key_grid == 1) {
-      // uniform: clip(round_half_even((x - min) / scale), 0, 2^bits - 1)
-      const int jp = tid & 63, sq = tid >> 6, kb = d.key_bits;
-      const float qmax = (float)((1 << kb) - 1);
-      const float mn0 = cent_s[2 * jp][0], sc0 = cent_s[2 * jp][1];
-      const float mn1 = cent_s[2 * jp + 1][0], sc1 = cent_s[2 * jp + 1][1];
-      const int per_q = (G + kEncWaves - 1) / kEncWaves;
-      const int s0 = sq * per_q, s1 = min(G, s0 + per_q);
-      for (int s = s0; s < s1; ++s) {
-        const float r0 = __builtin_rintf(__fdiv_rn(__fsub_rn(h2f(kt_s[s][2 * jp]), mn0), sc0));
-        const float r1 = __builtin_rintf(__fdiv_rn(__fsub_rn(h2f(kt_s[s][2 * jp + 1]), mn1), sc1));
-        const uint32_t b0 = (uint32_t)fminf(fmaxf(r0, 0.0f), qmax);
-        const uint32_t b1 = (uint32_t)fminf(fmaxf(r1, 0.0f), qmax);
-        // one table index per channel pair (the key row layout of tqk_common.h)
-        kc_s[s][jp] = (uint8_t)(kb == 4 ? ((rev4(b0) << 4) | rev4(b1)) : (b0 | (b1 << kb)));
-      }
-    } else {
-      const int jp = tid & 63, sq = tid >> 6;
-      float c0[16], c1[16];
-#pragma unroll
-      for (int l = 0; l < 16; ++l) {
-        c0[l] = cent_s[2 * jp][l];
-        c1[l] = cent_s[2 * jp + 1][l];
-      }
-      const int per_q = (G + kEncWaves - 1) / kEncWaves;
-      const int s0 = sq * per_q, s1 = min(G, s0 + per_q);
-      for (int s = s0; s < s1; ++s) {
-        const float x0 = h2f(kt_s[s][2 * jp]), x1 = h2f(kt_s[s][2 * jp + 1]);
-        int b0 = 0, b1 = 0;
-        float d0 = fabsf(__fsub_rn(x0, c0[0])), d1 = fabsf(__fsub_rn(x1, c1[0]));
-#pragma unroll
-        for (int l = 1; l < 16; ++l) {
-          const float e0 = fabsf(__fsub_rn(x0, c0[l])), e1 = fabsf(__fsub_rn(x1, c1[l]));
-          // np.argmin: strictly smaller wins; the first NaN wins over any number
-          if (e0 < d0 || (e0 != e0 && d0 == d0)) { d0 = e0; b0 = l; }
-          if (e1 < d1 || (e1 != e1 && d1 == d1)) { d1 = e1; b1 = l; }
-        }
-        kc_s[s][jp] = (uint8_t)((rev4(b0) << 4) | rev4(b1));
-      }
-    }
-
-    // ---- outlier side-list in flat (token, channel) order ---------------------
-    // ocount holds cumulative counts at every TQK_OBLK-token boundary of the
-    // group (entry TQK_NOB-1 = total), so a decode block finds its entries
-    // without searching.
-    const size_t obase = (size_t)slot * Hkv + h;
+    // ---- outlier side-list in flat (token, channel) order, one token per
+    // thread.  ocount holds cumulative counts at every TQK_OBLK-token boundary
+    // of the group (entry TQK_NOB-1 = total), so a decode block finds its
+    // entries without searching; omask_s records the stored (token, channel)
+    // positions, whose codes become the grid's zero level below.
     if (kout > 0) {
       const bool all = kout >= G;
       int cnt = 0;
@@ -256,12 +223,12 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) {
         const int v = __shfl_up(incl, o, 64);
-        if ((tid & 63) >= o) incl += v;
+        if (lane >= o) incl += v;
       }
-      if ((tid & 63) == 63) wsum_s[tid >> 6] = incl;
+      if (lane == 63) wsum_s[wv] = incl;
       __syncthreads();
       int wofs = 0;
-      for (int w = 0; w < (tid >> 6); ++w) wofs += wsum_s[w];
+      for (int w = 0; w < wv; ++w) wofs += wsum_s[w];
       int total = 0;
       for (int w = 0; w < kEncWaves; ++w) total += wsum_s[w];
       int off = wofs + incl - cnt;
@@ -269,73 +236,115 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
       if (tid < G && ((tid + 1) % TQK_OBLK) == 0 && (tid + 1) / TQK_OBLK <= TQK_NOB)
         a.p.ocount[obase * TQK_NOB + (tid + 1) / TQK_OBLK - 1] = off + cnt;
       if (tid < TQK_NOB && TQK_OBLK * (tid + 1) > G) a.p.ocount[obase * TQK_NOB + tid] = total;
-      if (tid < G && cnt > 0) {
-        for (int j = 0; j < D; ++j) {
-          const uint16_t xv = kt_s[tid][j];
-          const bool sel = all || (fabsf(h2f(xv)) >= fabsf(h2f((uint16_t)thr_s[j])));
-          if (sel) {
-            if (off < d.outlier_cap) {
-              a.p.oent[obase * d.outlier_cap + off] = (uint32_t)(tid * D + j) | ((uint32_t)xv << 16);
-              // the stored code becomes the level whose value is gmean -- NF4's
-              // zero level (rev4(7) = 14), or code 0 of a uniform grid -- so the
-              // dense part of a decode contributes only gmean here and the
-              // side-list adds val - gmean; export restores the reference's code
-              uint8_t& kp = kc_s[tid][j >> 1];
-              if (d.key_bits == 4) {
-                const uint32_t zc = d.key_grid == 1 ? 0u : 14u;
-                kp = (j & 1) ? (uint8_t)((kp & 0xF0u) | zc) : (uint8_t)((kp & 0x0Fu) | (zc << 4));
-              } else {
-                // 3- and 2-bit keys are uniform: the pair field's code of channel j to 0
-                const uint32_t m = (1u << d.key_bits) - 1u;
-                kp = (uint8_t)(kp & ~((j & 1) ? (m << d.key_bits) : m));
+      if (tid < G) {
+        uint32_t om[D / 32] = {0u, 0u, 0u, 0u};
+        if (cnt > 0) {
+          for (int j = 0; j < D; ++j) {
+            const uint16_t xv = kt_s[tid][j];
+            const bool sel = all || (fabsf(h2f(xv)) >= fabsf(h2f((uint16_t)thr_s[j])));
+            if (sel) {
+              if (off < d.outlier_cap) {
+                a.p.oent[obase * d.outlier_cap + off] = (uint32_t)(tid * D + j) | ((uint32_t)xv << 16);
+                om[j >> 5] |= 1u << (j & 31);
               }
+              ++off;
             }
-            ++off;
           }
         }
+#pragma unroll
+        for (int k = 0; k < D / 32; ++k) omask_s[tid][k] = om[k];
       }
       if (tid == 0 && total > d.outlier_cap && a.overflow) atomicOr(a.overflow, TQK_OVF_OUTLIERS);
     } else if (tid < TQK_NOB) {
       a.p.ocount[obase * TQK_NOB + tid] = 0;
     }
+    __syncthreads();
+
+    // ---- codes: thread = (channel pair jp, token slice = wave); the slice's
+    // rows belong to this wave alone, so a row's code bytes replace its first
+    // D / 2 bytes right after the wave has read it.  A stored outlier takes the
+    // grid level whose value is gmean -- NF4's zero level (code 7), or code 0
+    // of a uniform grid -- so the dense part of a decode contributes gmean
+    // there and the side-list adds val - gmean; export restores the
+    // reference's code.
+    {
+      const int jp = lane, kb = d.key_bits;
+      const int per_q = (G + kEncWaves - 1) / kEncWaves;
+      const int s0 = wv * per_q, s1 = min(G, s0 + per_q);
+      const uint32_t zc = d.key_grid == 1 ? 0u : 7u;
+      const float st00 = stat_s[2 * jp][0], st01 = stat_s[2 * jp][1];
+      const float st10 = stat_s[2 * jp + 1][0], st11 = stat_s[2 * jp + 1][1];
+      if (d.key_grid == 1) {
+        // uniform: clip(round_half_even((x - min) / scale), 0, 2^bits - 1)
+        const float qmax = (float)((1 << kb) - 1);
+        for (int s = s0; s < s1; ++s) {
+          const uint32_t xx = *reinterpret_cast<const uint32_t*>(&kt_s[s][2 * jp]);
+          const float r0 = __builtin_rintf(__fdiv_rn(__fsub_rn(h2f((uint16_t)xx), st00), st01));
+          const float r1 = __builtin_rintf(__fdiv_rn(__fsub_rn(h2f((uint16_t)(xx >> 16)), st10), st11));
+          uint32_t b0 = (uint32_t)fminf(fmaxf(r0, 0.0f), qmax);
+          uint32_t b1 = (uint32_t)fminf(fmaxf(r1, 0.0f), qmax);
+          if (kout > 0) {
+            const uint32_t om = omask_s[s][jp >> 4] >> (2 * (jp & 15));
+            if (om & 1u) b0 = zc;
+            if (om & 2u) b1 = zc;
+          }
+          // one table index per channel pair (the key row layout of tqk_common.h)
+          kc_row(s)[jp] = (uint8_t)(kb == 4 ? ((rev4(b0) << 4) | rev4(b1)) : (b0 | (b1 << kb)));
+        }
+      } else {
+        // asym-NF4 levels cent_l = mean + amax * NF4[l]
+        float c0[16], c1[16];
+#pragma unroll
+        for (int l = 0; l < 16; ++l) {
+          c0[l] = __fadd_rn(st00, __fmul_rn(st01, kNF4[l]));
+          c1[l] = __fadd_rn(st10, __fmul_rn(st11, kNF4[l]));
+        }
+        for (int s = s0; s < s1; ++s) {
+          const uint32_t xx = *reinterpret_cast<const uint32_t*>(&kt_s[s][2 * jp]);
+          const float x0 = h2f((uint16_t)xx), x1 = h2f((uint16_t)(xx >> 16));
+          uint32_t b0 = 0, b1 = 0;
+          float d0 = fabsf(__fsub_rn(x0, c0[0])), d1 = fabsf(__fsub_rn(x1, c1[0]));
+#pragma unroll
+          for (int l = 1; l < 16; ++l) {
+            const float e0 = fabsf(__fsub_rn(x0, c0[l])), e1 = fabsf(__fsub_rn(x1, c1[l]));
+            // np.argmin: strictly smaller wins; the first NaN wins over any number
+            if (e0 < d0 || (e0 != e0 && d0 == d0)) { d0 = e0; b0 = l; }
+            if (e1 < d1 || (e1 != e1 && d1 == d1)) { d1 = e1; b1 = l; }
+          }
+          if (kout > 0) {
+            const uint32_t om = omask_s[s][jp >> 4] >> (2 * (jp & 15));
+            if (om & 1u) b0 = zc;
+            if (om & 2u) b1 = zc;
+          }
+          kc_row(s)[jp] = (uint8_t)((rev4(b0) << 4) | rev4(b1));
+        }
+      }
+    }
   }
 
-  // ---- values: one token per thread ---------------------------------------
+  // ---- values -------------------------------------------------------------
   constexpr int VROW = D * VB / 8;
   const bool tiled = v_tiled(G, P);
-  // tiled layout: codes are staged in the (no longer needed) key tile and
-  // re-assembled into 4-token x 8-channel units below
-  uint8_t (*vc_s)[D] = reinterpret_cast<uint8_t (*)[D]>(&kt_s[0][0]);
-  __syncthreads();
   // PolarQuant codes of the group's tokens (the value encode; PolarQuant keys
   // run it on the keys): norms to nout, codes staged in vc_s[token][channel]
+  // (the first TQK_MAX_G * D bytes of the key tile area)
   auto polar_phase = [&](const uint16_t* ring, const uint16_t* chunk, float* nout, bool vcheck) {
-    // Rotation operands: wave w owns the 16 rotated channels [16w, 16w + 16);
-    // lane l holds column e = 16w + (l & 15) of Pi_T (pi[e][0..D)) in
-    // registers, and its 16-lane row (l >> 4) works on one token of a 4-token
-    // pass.  The token's normalised row u sits in LDS (kVBatch tokens at a
-    // time, after the code staging area); each lane of the row loads channels
-    // [8(l & 15), 8(l & 15) + 8) of it, and u_d reaches the row's 16 lanes by
-    // a DPP row broadcast from lane d / 8 folded into the multiply -- no LDS
-    // broadcast reads, which would cost the LDS a full wave's bandwidth each.
-    // Every y_e is still the sequential, separately rounded sum over d.
-    const int lane = tid & 63, wv = tid >> 6, rt = lane >> 4, li = lane & 15;
-    const int ecol = 16 * wv + li;
-    float pcol[D];
-#pragma unroll
-    for (int k = 0; k < D / 4; ++k) {
-      const float4 p4 = reinterpret_cast<const float4*>(a.p.pi + (size_t)ecol * D)[k];
-      pcol[4 * k] = p4.x;
-      pcol[4 * k + 1] = p4.y;
-      pcol[4 * k + 2] = p4.z;
-      pcol[4 * k + 3] = p4.w;
-    }
+    // Rotation operands: in pass p, wave w owns the 16 rotated channels
+    // [64p + 16w, +16); lane l holds column e = 64p + 16w + (l & 15) of Pi_T
+    // (pi[e][0..D)) in registers, and its 16-lane row (l >> 4) works on one
+    // token of a 4-token step.  The token's normalised row u sits in LDS
+    // (kVBatch tokens at a time, after the code staging area); each lane of
+    // the row loads channels [8(l & 15), 8(l & 15) + 8) of it, and u_d reaches
+    // the row's 16 lanes by a DPP row broadcast from lane d / 8 folded into
+    // the multiply -- no LDS broadcast reads, which would cost the LDS a full
+    // wave's bandwidth each.  Every y_e is still the sequential, separately
+    // rounded sum over d.
+    const int rt = lane >> 4, li = lane & 15;
     float bnd[15];
 #pragma unroll
     for (int k = 0; k < (1 << VB) - 1; ++k) bnd[k] = a.p.vbnd[k];
     constexpr int kVBatch = 64;
     float (*u_s)[D] = reinterpret_cast<float (*)[D]>(&kt_s[0][0] + TQK_MAX_G * D / 2);
-    static_assert(TQK_MAX_G * D + kVBatch * D * 4 <= TQK_MAX_G * (D + 8) * 2, "value staging overflows the key tile");
     for (int t0 = 0; t0 < G; t0 += kVBatch) {
       const int nb = min(kVBatch, G - t0);
       // (1) norms and normalised rows, four threads per token: thread q holds
@@ -378,55 +387,71 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
         }
       }
       __syncthreads();
-      // (2) rotation and codes: tokens ja = 8p + rt and jb = ja + 4 of the
-      // batch per pass (two chains per lane)
-      for (int j0 = 0; j0 < nb; j0 += 8) {
-        const int ja = j0 + rt, jb = j0 + 4 + rt;
-        float ua[8], ub[8];
-        {
-          const float4* ra = reinterpret_cast<const float4*>(&u_s[min(ja, nb - 1)][8 * li]);
-          const float4* rb = reinterpret_cast<const float4*>(&u_s[min(jb, nb - 1)][8 * li]);
-          const float4 a0 = ra[0], a1 = ra[1], b0 = rb[0], b1 = rb[1];
-          ua[0] = a0.x; ua[1] = a0.y; ua[2] = a0.z; ua[3] = a0.w;
-          ua[4] = a1.x; ua[5] = a1.y; ua[6] = a1.z; ua[7] = a1.w;
-          ub[0] = b0.x; ub[1] = b0.y; ub[2] = b0.z; ub[3] = b0.w;
-          ub[4] = b1.x; ub[5] = b1.y; ub[6] = b1.z; ub[7] = b1.w;
-        }
-        float y0 = 0.f, y1 = 0.f;
-        rotate_row<0>(y0, y1, ua, ub, pcol);
-        // keeps the sums out of the conditional stores below: sunk into them,
-        // the multiplies would leave their broadcasts behind as separate moves
-        asm volatile("" : "+v"(y0), "+v"(y1));
-        uint32_t c0 = 0, c1 = 0;
+      // (2) rotation and codes, D / (16 * kEncWaves) passes over the channels:
+      // tokens ja = j0 + rt and jb = ja + 4 of the batch per step (two chains per lane)
+      for (int pass = 0; pass < D / (16 * kEncWaves); ++pass) {
+        const int ecol = 16 * kEncWaves * pass + 16 * wv + li;
+        float pcol[D];
 #pragma unroll
-        for (int k = 0; k < (1 << VB) - 1; ++k) {
-          c0 += (bnd[k] < y0) ? 1u : 0u;
-          c1 += (bnd[k] < y1) ? 1u : 0u;
+        for (int k = 0; k < D / 4; ++k) {
+          const float4 p4 = reinterpret_cast<const float4*>(a.p.pi + (size_t)ecol * D)[k];
+          pcol[4 * k] = p4.x;
+          pcol[4 * k + 1] = p4.y;
+          pcol[4 * k + 2] = p4.z;
+          pcol[4 * k + 3] = p4.w;
         }
-        if (ja < nb) vc_s[t0 + ja][ecol] = (uint8_t)c0;
-        if (jb < nb) vc_s[t0 + jb][ecol] = (uint8_t)c1;
+        for (int j0 = 0; j0 < nb; j0 += 8) {
+          const int ja = j0 + rt, jb = j0 + 4 + rt;
+          float ua[8], ub[8];
+          {
+            const float4* ra = reinterpret_cast<const float4*>(&u_s[min(ja, nb - 1)][8 * li]);
+            const float4* rb = reinterpret_cast<const float4*>(&u_s[min(jb, nb - 1)][8 * li]);
+            const float4 a0 = ra[0], a1 = ra[1], b0 = rb[0], b1 = rb[1];
+            ua[0] = a0.x; ua[1] = a0.y; ua[2] = a0.z; ua[3] = a0.w;
+            ua[4] = a1.x; ua[5] = a1.y; ua[6] = a1.z; ua[7] = a1.w;
+            ub[0] = b0.x; ub[1] = b0.y; ub[2] = b0.z; ub[3] = b0.w;
+            ub[4] = b1.x; ub[5] = b1.y; ub[6] = b1.z; ub[7] = b1.w;
+          }
+          float y0 = 0.f, y1 = 0.f;
+          rotate_row<0>(y0, y1, ua, ub, pcol);
+          // keeps the sums out of the conditional stores below: sunk into them,
+          // the multiplies would leave their broadcasts behind as separate moves
+          asm volatile("" : "+v"(y0), "+v"(y1));
+          uint32_t c0 = 0, c1 = 0;
+#pragma unroll
+          for (int k = 0; k < (1 << VB) - 1; ++k) {
+            c0 += (bnd[k] < y0) ? 1u : 0u;
+            c1 += (bnd[k] < y1) ? 1u : 0u;
+          }
+          if (ja < nb) vc_s[t0 + ja][ecol] = (uint8_t)c0;
+          if (jb < nb) vc_s[t0 + jb][ecol] = (uint8_t)c1;
+        }
       }
       __syncthreads();
     }
   };
+  // code row of token t for the key write-out
+  const uint8_t* kc_base = kc_row(0);
+  int kc_stride = (D + 8) * 2;
   if (d.key_grid == 2) {
     // PolarQuant keys (turboquant_pro/core.py:542-617 with kind="key"): the
-    // value encode on the key tokens, norms to knorm, one table index per
-    // channel pair into kc_s; the per-channel stats are the identity
-    // (scale 1, mean 0) and there is no side-list
+    // value encode on the key tokens, norms to knorm, then each row's codes
+    // turned in place (one wave per row) into one table index per channel
+    // pair; the per-channel stats are the identity (scale 1, mean 0) and
+    // there is no side-list
     polar_phase(a.p.hot_k, a.chunk_k, a.p.knorm, false);
-    __syncthreads();
-    for (int idx = tid; idx < G * (D / 2); idx += kEncThreads) {
-      const int t = idx / (D / 2), jp = idx % (D / 2);
-      const uint32_t c0 = vc_s[t][2 * jp], c1 = vc_s[t][2 * jp + 1];
-      kc_s[t][jp] = (uint8_t)(d.key_bits == 4 ? ((rev4(c0) << 4) | rev4(c1)) : (c0 | (c1 << d.key_bits)));
+    for (int t = wv; t < G; t += kEncWaves) {
+      const uint32_t cc = *reinterpret_cast<const uint16_t*>(&vc_s[t][2 * lane]);
+      const uint32_t c0 = cc & 0xFFu, c1 = cc >> 8;
+      vc_s[t][lane] = (uint8_t)(d.key_bits == 4 ? ((rev4(c0) << 4) | rev4(c1)) : (c0 | (c1 << d.key_bits)));
     }
-    const size_t mb = ((size_t)slot * Hkv + h) * D;
+    kc_base = &vc_s[0][0];
+    kc_stride = D;
     if (tid < D) {
-      a.p.gscale[mb + tid] = 1.0f;
-      a.p.gmean[mb + tid] = 0.0f;
+      a.p.gscale[mbase + tid] = 1.0f;
+      a.p.gmean[mbase + tid] = 0.0f;
     }
-    if (tid < TQK_NOB) a.p.ocount[((size_t)slot * Hkv + h) * TQK_NOB + tid] = 0;
+    if (tid < TQK_NOB) a.p.ocount[obase * TQK_NOB + tid] = 0;
   }
   __syncthreads();
   // key code rows, one 32-channel chunk (16 pair indices) per thread
@@ -434,7 +459,7 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
   for (int idx = tid; idx < G * (D / 32); idx += kEncThreads) {
     const int t = idx / (D / 32), ch = idx % (D / 32);
     const size_t row = page_row(a.p.block_table, d.max_pages_per_seq, b, g * G + t, P, d.n_pages, h);
-    const uint4 f16 = *reinterpret_cast<const uint4*>(&kc_s[t][16 * ch]);
+    const uint4 f16 = *reinterpret_cast<const uint4*>(kc_base + (size_t)t * kc_stride + 16 * ch);
     if (d.key_bits == 4) {
       *reinterpret_cast<uint4*>(a.p.kcodes + row * KROW + 16 * ch) = f16;
     } else {
@@ -452,6 +477,7 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
       for (int w = 0; w < kb; ++w) dst[w] = o[w];
     }
   }
+  __syncthreads();
   polar_phase(a.p.hot_v, a.chunk_v, a.p.vnorm, true);
   // (3) the code rows: 4-token x 8-channel units of 16-token tiles, or the
   // reference's little-endian bit stream per token
