@@ -299,17 +299,32 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
           c0[l] = __fadd_rn(st00, __fmul_rn(st01, kNF4[l]));
           c1[l] = __fadd_rn(st10, __fmul_rn(st11, kNF4[l]));
         }
+        // with finite levels and a finite x no distance is NaN, and the
+        // argmin needs only the strict comparison
+        bool lv_finite = true;
+#pragma unroll
+        for (int l = 0; l < 16; ++l) lv_finite &= __builtin_isfinite(c0[l]) && __builtin_isfinite(c1[l]);
         for (int s = s0; s < s1; ++s) {
           const uint32_t xx = *reinterpret_cast<const uint32_t*>(&kt_s[s][2 * jp]);
           const float x0 = h2f((uint16_t)xx), x1 = h2f((uint16_t)(xx >> 16));
           uint32_t b0 = 0, b1 = 0;
           float d0 = fabsf(__fsub_rn(x0, c0[0])), d1 = fabsf(__fsub_rn(x1, c1[0]));
+          const bool fin = lv_finite && (xx & 0x7C00u) != 0x7C00u && (xx & 0x7C000000u) != 0x7C000000u;
+          if (__all(fin)) {
 #pragma unroll
-          for (int l = 1; l < 16; ++l) {
-            const float e0 = fabsf(__fsub_rn(x0, c0[l])), e1 = fabsf(__fsub_rn(x1, c1[l]));
-            // np.argmin: strictly smaller wins; the first NaN wins over any number
-            if (e0 < d0 || (e0 != e0 && d0 == d0)) { d0 = e0; b0 = l; }
-            if (e1 < d1 || (e1 != e1 && d1 == d1)) { d1 = e1; b1 = l; }
+            for (int l = 1; l < 16; ++l) {
+              const float e0 = fabsf(__fsub_rn(x0, c0[l])), e1 = fabsf(__fsub_rn(x1, c1[l]));
+              if (e0 < d0) { d0 = e0; b0 = l; }
+              if (e1 < d1) { d1 = e1; b1 = l; }
+            }
+          } else {
+#pragma unroll
+            for (int l = 1; l < 16; ++l) {
+              const float e0 = fabsf(__fsub_rn(x0, c0[l])), e1 = fabsf(__fsub_rn(x1, c1[l]));
+              // np.argmin: strictly smaller wins; the first NaN wins over any number
+              if (e0 < d0 || (e0 != e0 && d0 == d0)) { d0 = e0; b0 = l; }
+              if (e1 < d1 || (e1 != e1 && d1 == d1)) { d1 = e1; b1 = l; }
+            }
           }
           if (kout > 0) {
             const uint32_t om = omask_s[s][jp >> 4] >> (2 * (jp & 15));
