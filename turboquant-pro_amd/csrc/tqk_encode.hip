@@ -104,7 +104,10 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
   // holds the value phase's codes (vc_s) and normalised rows (u_s).
   __shared__ __align__(16) uint16_t kt_s[TQK_MAX_G][D + 8];
   __shared__ float stat_s[D][2];             // per channel: (mean, amax) or (min, scale)
-  __shared__ uint32_t thr_s[D];              // fp16 magnitude threshold per channel
+  // per channel: 0x8000 - the fp16 magnitude threshold T (so m + it has bit 15
+  // set exactly when m >= T; 0 for a NaN T), read eight channels at a time by
+  // the side-list scan
+  __shared__ __align__(16) uint16_t tbias_s[D];
   __shared__ uint32_t omask_s[TQK_MAX_G][D / 32];  // channels of each token stored in the side-list
   __shared__ int32_t wsum_s[kEncWaves];
   auto kc_row = [&](int t) { return reinterpret_cast<uint8_t*>(&kt_s[t][0]); };
@@ -199,7 +202,9 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
           const int cnt = sum_quarters((int)((acc & 0xFFFFu) + (acc >> 16)));
           if (cnt >= kout) T = cand;
         }
-        if (part == 0) thr_s[j] = T;
+        // the scan compares magnitudes as floats, as the reference's mask
+        // |x| >= t does: a NaN threshold selects nothing (bias 0)
+        if (part == 0) tbias_s[j] = (uint16_t)(T > 0x7C00u ? 0u : 0x8000u - T);
       }
     }
     __syncthreads();
@@ -211,13 +216,32 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
     // positions, whose codes become the grid's zero level below.
     if (kout > 0) {
       const bool all = kout >= G;
-      int cnt = 0;
+      // the token's outlier channels, eight at a time: magnitudes and biases
+      // as packed 16-bit pairs, bit 15 of each half of m + bias is the test
+      // m >= T; NaN magnitudes (m > 0x7C00, where m + 0x03FF reaches bit 15)
+      // are never selected, as |x| >= t is false for them
+      uint32_t om[D / 32] = {0u, 0u, 0u, 0u};
       if (tid < G) {
-        for (int j = 0; j < D; ++j) {
-          const float mag = fabsf(h2f(kt_s[tid][j]));
-          cnt += all ? 1 : (mag >= fabsf(h2f((uint16_t)thr_s[j])));
+#pragma unroll
+        for (int c8 = 0; c8 < D / 8; ++c8) {
+          const uint4 xw = *reinterpret_cast<const uint4*>(&kt_s[tid][8 * c8]);
+          const uint4 bw = *reinterpret_cast<const uint4*>(&tbias_s[8 * c8]);
+          const uint32_t xs[4] = {xw.x, xw.y, xw.z, xw.w}, bs[4] = {bw.x, bw.y, bw.z, bw.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const u16x2_t m = __builtin_bit_cast(u16x2_t, xs[i] & 0x7FFF7FFFu);
+            const uint32_t t = __builtin_bit_cast(uint32_t, (u16x2_t)(m + __builtin_bit_cast(u16x2_t, bs[i])));
+            const uint32_t tn = __builtin_bit_cast(uint32_t, (u16x2_t)(m + u16x2_t{0x03FF, 0x03FF}));
+            const uint32_t sel = t & ~tn;
+            const uint32_t two = ((sel >> 15) & 1u) | ((sel >> 30) & 2u);  // channels 8c8 + 2i, + 1
+            om[c8 >> 2] |= two << (8 * (c8 & 3) + 2 * i);
+          }
         }
+        if (all) om[0] = om[1] = om[2] = om[3] = 0xFFFFFFFFu;
       }
+      const int cnt = tid < G ? __builtin_popcount(om[0]) + __builtin_popcount(om[1]) +
+                                    __builtin_popcount(om[2]) + __builtin_popcount(om[3])
+                              : 0;
       // block exclusive scan of cnt
       int incl = cnt;
 #pragma unroll
@@ -237,18 +261,19 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
         a.p.ocount[obase * TQK_NOB + (tid + 1) / TQK_OBLK - 1] = off + cnt;
       if (tid < TQK_NOB && TQK_OBLK * (tid + 1) > G) a.p.ocount[obase * TQK_NOB + tid] = total;
       if (tid < G) {
-        uint32_t om[D / 32] = {0u, 0u, 0u, 0u};
-        if (cnt > 0) {
-          for (int j = 0; j < D; ++j) {
-            const uint16_t xv = kt_s[tid][j];
-            const bool sel = all || (fabsf(h2f(xv)) >= fabsf(h2f((uint16_t)thr_s[j])));
-            if (sel) {
-              if (off < d.outlier_cap) {
-                a.p.oent[obase * d.outlier_cap + off] = (uint32_t)(tid * D + j) | ((uint32_t)xv << 16);
-                om[j >> 5] |= 1u << (j & 31);
-              }
-              ++off;
-            }
+        // entries in channel order; those past the side-list's capacity are
+        // dropped (and leave their codes alone)
+#pragma unroll
+        for (int k = 0; k < D / 32; ++k) {
+          uint32_t w = om[k];
+          while (w) {
+            const int j = 32 * k + __builtin_ctz(w);
+            w &= w - 1u;
+            if (off < d.outlier_cap)
+              a.p.oent[obase * d.outlier_cap + off] = (uint32_t)(tid * D + j) | ((uint32_t)kt_s[tid][j] << 16);
+            else
+              om[k] &= ~(1u << (j & 31));
+            ++off;
           }
         }
 #pragma unroll
