@@ -321,6 +321,9 @@ __global__ __launch_bounds__(kVbThreads) void tqk_value_block(ValueBlockArgs a) 
       c0 += (bnd[k] < y0) ? 1u : 0u;
       c1 += (bnd[k] < y1) ? 1u : 0u;
     }
+    // searchsorted places NaN after every boundary
+    if (y0 != y0) c0 = (1u << VB) - 1u;
+    if (y1 != y1) c1 = (1u << VB) - 1u;
     vc_s[j][ecol] = (uint8_t)c0;
     if (j + 1 < nb) vc_s[j + 1][ecol] = (uint8_t)c1;
   }

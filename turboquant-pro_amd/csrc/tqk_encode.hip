@@ -15,7 +15,8 @@
 //     norm  = sqrt(pairwise-8 sum of squares)            (numpy pairwise_sum, n = 128)
 //     u     = v / max(norm, 1e-30)
 //     y_e   = sequential over d of (u_d * PiT[d][e]), separately rounded
-//     code  = #{ boundaries < y_e }                      (searchsorted, side="left")
+//     code  = #{ boundaries < y_e }                      (searchsorted, side="left";
+//                                                         a NaN y_e takes the last code)
 #include "tqk_common.h"
 
 namespace {
@@ -463,6 +464,9 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
             c0 += (bnd[k] < y0) ? 1u : 0u;
             c1 += (bnd[k] < y1) ? 1u : 0u;
           }
+          // searchsorted places NaN after every boundary
+          if (y0 != y0) c0 = (1u << VB) - 1u;
+          if (y1 != y1) c1 = (1u << VB) - 1u;
           if (ja < nb) vc_s[t0 + ja][ecol] = (uint8_t)c0;
           if (jb < nb) vc_s[t0 + jb][ecol] = (uint8_t)c1;
         }
