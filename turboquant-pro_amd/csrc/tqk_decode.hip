@@ -1180,16 +1180,19 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
             qv[i].v = *reinterpret_cast<const uint4*>(&oq_s[w][hq][16 * (k0 + i) + 4 * lg]);
           }
         };
+        // chunk k holds entries [16k, 16k + 16): it touches tile A while
+        // k < endA, tile B from k = beginB on, and exists while k < end
+        const int endA = (nA + 15) >> 4, beginB = nA >> 4, end = (cnt + 15) >> 4;
         auto chunk = [&](auto kc) {
           constexpr int k = decltype(kc)::value;
-          if (16 * k >= cnt) return;
+          if (k >= end) return;
           const uint32_t tw = k < 4 ? u4_word<k & 3>(tw03) : u4_word<k & 3>(tw47);
-          if (16 * k < nA) {
+          if (k < endA) {
             H8 o;
             onehot_operand(tw, (uint32_t)c, dq[k & 3], o.u);
             CA = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.h, qv[k & 3].h, CA, 0, 0, 0);
           }
-          if (16 * k + 16 > nA) {
+          if (k >= beginB) {
             H8 o;
             onehot_operand(tw, (uint32_t)(16 + c), dq[k & 3], o.u);
             CB = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.h, qv[k & 3].h, CB, 0, 0, 0);
