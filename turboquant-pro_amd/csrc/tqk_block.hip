@@ -238,9 +238,8 @@ struct ValueBlockArgs {
 
 // 64 tokens of one (b, h) per workgroup.  Four threads per token compute the
 // norm in the reference's pairwise order and stage the normalised row in LDS;
-// then lane e of wave w owns rotated channel 64 * (w & 1) + e with its column
-// of Pi_T (row e of Pi) in registers, waves w >> 1 split the tokens, and each
-// y_e is the sequential, separately rounded sum over d.
+// then the rotation as in the group encode (DPP row broadcasts of register-
+// held row slices, a column of Pi_T per lane).
 template <int VB>
 __global__ __launch_bounds__(kVbThreads) void tqk_value_block(ValueBlockArgs a) {
   constexpr int D = TQK_D;
@@ -284,8 +283,14 @@ __global__ __launch_bounds__(kVbThreads) void tqk_value_block(ValueBlockArgs a) 
       if (q == 0) a.norms[tok0 + tt] = nrm;
     }
   }
-  const int lane = tid & 63, wv = tid >> 6;
-  const int ecol = 64 * (wv & 1) + lane;
+  // rotation: wave w owns the 16 rotated channels [16w, 16w + 16), lane l
+  // column e = 16w + (l & 15) of Pi_T (row e of Pi) in registers; each 16-lane
+  // row takes one token of a 4-token step, holds eight channels of its
+  // normalised row and broadcasts them to the row by DPP (no LDS broadcast
+  // reads); every y_e is the sequential, separately rounded sum over d
+  const int lane = tid & 63, wv = tid >> 6, rt = lane >> 4, li = lane & 15;
+  const int ecol = 16 * wv + li;
+  static_assert(kVbThreads / 64 * 16 == D, "eight waves of 16 rotated channels");
   float pcol[D];
 #pragma unroll
   for (int k = 0; k < D / 4; ++k) {
@@ -299,22 +304,23 @@ __global__ __launch_bounds__(kVbThreads) void tqk_value_block(ValueBlockArgs a) 
 #pragma unroll
   for (int k = 0; k < (1 << VB) - 1; ++k) bnd[k] = a.vbnd[k];
   __syncthreads();
-  for (int j = 2 * (wv >> 1); j < nb; j += kVbThreads / 64) {
-    const int j1 = min(j + 1, nb - 1);
-    float y0 = 0.f, y1 = 0.f;
-#pragma unroll
-    for (int d4 = 0; d4 < D / 4; ++d4) {
-      const float4 ua = *reinterpret_cast<const float4*>(&u_s[j][4 * d4]);
-      const float4 ub = *reinterpret_cast<const float4*>(&u_s[j1][4 * d4]);
-      y0 = __fadd_rn(y0, __fmul_rn(ua.x, pcol[4 * d4]));
-      y1 = __fadd_rn(y1, __fmul_rn(ub.x, pcol[4 * d4]));
-      y0 = __fadd_rn(y0, __fmul_rn(ua.y, pcol[4 * d4 + 1]));
-      y1 = __fadd_rn(y1, __fmul_rn(ub.y, pcol[4 * d4 + 1]));
-      y0 = __fadd_rn(y0, __fmul_rn(ua.z, pcol[4 * d4 + 2]));
-      y1 = __fadd_rn(y1, __fmul_rn(ub.z, pcol[4 * d4 + 2]));
-      y0 = __fadd_rn(y0, __fmul_rn(ua.w, pcol[4 * d4 + 3]));
-      y1 = __fadd_rn(y1, __fmul_rn(ub.w, pcol[4 * d4 + 3]));
+  for (int j0 = 0; j0 < nb; j0 += 8) {
+    const int ja = j0 + rt, jb = j0 + 4 + rt;
+    float ua[8], ub[8];
+    {
+      const float4* ra = reinterpret_cast<const float4*>(&u_s[min(ja, nb - 1)][8 * li]);
+      const float4* rb = reinterpret_cast<const float4*>(&u_s[min(jb, nb - 1)][8 * li]);
+      const float4 a0 = ra[0], a1 = ra[1], b0 = rb[0], b1 = rb[1];
+      ua[0] = a0.x; ua[1] = a0.y; ua[2] = a0.z; ua[3] = a0.w;
+      ua[4] = a1.x; ua[5] = a1.y; ua[6] = a1.z; ua[7] = a1.w;
+      ub[0] = b0.x; ub[1] = b0.y; ub[2] = b0.z; ub[3] = b0.w;
+      ub[4] = b1.x; ub[5] = b1.y; ub[6] = b1.z; ub[7] = b1.w;
     }
+    float y0 = 0.f, y1 = 0.f;
+    rotate_row_dpp<0>(y0, y1, ua, ub, pcol);
+    // keeps the sums out of the conditional stores below: sunk into them, the
+    // multiplies would leave their broadcasts behind as separate moves
+    asm volatile("" : "+v"(y0), "+v"(y1));
     uint32_t c0 = 0, c1 = 0;
 #pragma unroll
     for (int k = 0; k < (1 << VB) - 1; ++k) {
@@ -324,8 +330,8 @@ __global__ __launch_bounds__(kVbThreads) void tqk_value_block(ValueBlockArgs a) 
     // searchsorted places NaN after every boundary
     if (y0 != y0) c0 = (1u << VB) - 1u;
     if (y1 != y1) c1 = (1u << VB) - 1u;
-    vc_s[j][ecol] = (uint8_t)c0;
-    if (j + 1 < nb) vc_s[j + 1][ecol] = (uint8_t)c1;
+    if (ja < nb) vc_s[ja][ecol] = (uint8_t)c0;
+    if (jb < nb) vc_s[jb][ecol] = (uint8_t)c1;
   }
   __syncthreads();
   // the reference's little-endian bit stream, one token per thread

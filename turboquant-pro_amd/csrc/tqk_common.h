@@ -103,6 +103,32 @@ __device__ __forceinline__ size_t page_row(const int32_t* __restrict__ block_tab
   return ((size_t)h * n_pages + phys) * P + (t % P);
 }
 
+// Lane I of each 16-lane row, broadcast to the row (DPP row_newbcast).
+template <int I>
+__device__ __forceinline__ float dpp_row_bcast(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x150 + I, 0xF, 0xF, true));
+}
+
+// y0 += u_a[d] * pcol[d], y1 += u_b[d] * pcol[d] for d = 8K .. 8K + 7 and on
+// to d = 127, each product and sum separately rounded, in d order; u_a[d]
+// lives in register d % 8 of lane d / 8 of the 16-lane row.  Plain
+// operators, so that the broadcast folds into the multiply as its DPP source
+// operand: only for units built with -ffp-contract=off (the encode and the
+// block quantizers), where a product and a sum are never fused.
+template <int K>
+__device__ __forceinline__ void rotate_row_dpp(float& y0, float& y1, const float (&ua)[8],
+                                               const float (&ub)[8], const float (&pcol)[TQK_D]) {
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const float p0 = dpp_row_bcast<K>(ua[r]) * pcol[8 * K + r];
+    const float p1 = dpp_row_bcast<K>(ub[r]) * pcol[8 * K + r];
+    y0 = y0 + p0;
+    y1 = y1 + p1;
+  }
+  if constexpr (K + 1 < TQK_D / 8) rotate_row_dpp<K + 1>(y0, y1, ua, ub, pcol);
+}
+
 template <typename T>
 __device__ __forceinline__ T wave_max(T v) {
 #pragma unroll

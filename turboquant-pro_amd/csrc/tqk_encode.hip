@@ -61,30 +61,6 @@ __device__ __forceinline__ int sum_quarters(int x) {
   return (int)(b[0] + b[1]);
 }
 
-// Lane I of each 16-lane row, broadcast to the row (DPP row_newbcast).
-template <int I>
-__device__ __forceinline__ float row_bcast(float x) {
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x150 + I, 0xF, 0xF, true));
-}
-
-// y0 += u_a[d] * pcol[d], y1 += u_b[d] * pcol[d] for d = 8K .. 8K + 7 and on
-// to d = 127, each product and sum separately rounded (this unit is built
-// with -ffp-contract=off), in d order; u_a[d] lives in register d % 8 of
-// lane d / 8 of the 16-lane row.  Plain operators, so that the broadcast
-// folds into the multiply as its DPP source operand.
-template <int K>
-__device__ __forceinline__ void rotate_row(float& y0, float& y1, const float (&ua)[8],
-                                           const float (&ub)[8], const float (&pcol)[TQK_D]) {
-#pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    const float p0 = row_bcast<K>(ua[r]) * pcol[8 * K + r];
-    const float p1 = row_bcast<K>(ub[r]) * pcol[8 * K + r];
-    y0 = y0 + p0;
-    y1 = y1 + p1;
-  }
-  if constexpr (K + 1 < TQK_D / 8) rotate_row<K + 1>(y0, y1, ua, ub, pcol);
-}
 
 template <int VB>
 __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
@@ -454,7 +430,7 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
             ub[4] = b1.x; ub[5] = b1.y; ub[6] = b1.z; ub[7] = b1.w;
           }
           float y0 = 0.f, y1 = 0.f;
-          rotate_row<0>(y0, y1, ua, ub, pcol);
+          rotate_row_dpp<0>(y0, y1, ua, ub, pcol);
           // keeps the sums out of the conditional stores below: sunk into them,
           // the multiplies would leave their broadcasts behind as separate moves
           asm volatile("" : "+v"(y0), "+v"(y1));
