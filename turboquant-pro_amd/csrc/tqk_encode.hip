@@ -301,18 +301,41 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
           c0[l] = __fadd_rn(st00, __fmul_rn(st01, kNF4[l]));
           c1[l] = __fadd_rn(st10, __fmul_rn(st11, kNF4[l]));
         }
-        // with finite levels and a finite x no distance is NaN, and the
-        // argmin needs only the strict comparison
-        bool lv_finite = true;
+        // With finite levels and a finite x no distance is NaN, and the
+        // argmin needs only the strict comparison.  Sorted levels far enough
+        // apart make it a count: for x >= c_l the distances x - c_l fall
+        // strictly with l (their real gaps exceed the rounding, see below)
+        // and for c_l > x they never fall, so the first argmin is the number
+        // of strict decreases d_l < d_(l-1).  Every token of the group has
+        // |x - mean| <= amax, so a distance is below R = 2 (|mean| + amax);
+        // gaps of at least R * 2^-19 (16 ulps of R) cannot round away.
+        bool lv_finite = true, spread = true;
 #pragma unroll
         for (int l = 0; l < 16; ++l) lv_finite &= __builtin_isfinite(c0[l]) && __builtin_isfinite(c1[l]);
+        {
+          const float r0 = __fmul_rn(__fadd_rn(fabsf(st00), st01), 0x1p-18f);
+          const float r1 = __fmul_rn(__fadd_rn(fabsf(st10), st11), 0x1p-18f);
+#pragma unroll
+          for (int l = 1; l < 16; ++l)
+            spread &= __fsub_rn(c0[l], c0[l - 1]) >= r0 && __fsub_rn(c1[l], c1[l - 1]) >= r1;
+          spread &= lv_finite;
+        }
         for (int s = s0; s < s1; ++s) {
           const uint32_t xx = *reinterpret_cast<const uint32_t*>(&kt_s[s][2 * jp]);
           const float x0 = h2f((uint16_t)xx), x1 = h2f((uint16_t)(xx >> 16));
           uint32_t b0 = 0, b1 = 0;
           float d0 = fabsf(__fsub_rn(x0, c0[0])), d1 = fabsf(__fsub_rn(x1, c1[0]));
           const bool fin = lv_finite && (xx & 0x7C00u) != 0x7C00u && (xx & 0x7C000000u) != 0x7C000000u;
-          if (__all(fin)) {
+          if (__all(fin && spread)) {
+#pragma unroll
+            for (int l = 1; l < 16; ++l) {
+              const float e0 = fabsf(__fsub_rn(x0, c0[l])), e1 = fabsf(__fsub_rn(x1, c1[l]));
+              b0 += (e0 < d0) ? 1u : 0u;
+              b1 += (e1 < d1) ? 1u : 0u;
+              d0 = e0;
+              d1 = e1;
+            }
+          } else if (__all(fin)) {
 #pragma unroll
             for (int l = 1; l < 16; ++l) {
               const float e0 = fabsf(__fsub_rn(x0, c0[l])), e1 = fabsf(__fsub_rn(x1, c1[l]));
