@@ -47,6 +47,11 @@ CONFIGS = {
     # config 3: 64 sequences of seeded lengths U[1024, 32768], 16-token pages,
     # block table a seeded permutation of the physical pages
     "c3_paged_ragged": dict(B=64, Hkv=8, Hq=32, L=32768, vbits=3, ragged=True, page=16),
+    # other key forms at the headline shape (not BASELINE configs): the
+    # reference's default cache (bits=3: uniform 3-bit per-channel keys, no
+    # outliers) and PolarQuant keys (per_channel_keys=False), both with V3
+    "k3v3_default": dict(B=16, Hkv=8, Hq=32, L=32768, vbits=3, kbits=3, key_grid="uniform", ofrac=0.0),
+    "k3v3_polar": dict(B=16, Hkv=8, Hq=32, L=32768, vbits=3, kbits=3, key_grid="polar", ofrac=0.0),
 }
 
 
@@ -63,18 +68,38 @@ def n_groups(L, W=512):
     return 0 if L <= W else (L - (W + 1)) // G + 1
 
 
-def step_bytes(lens, Hkv, Hq, D=128, kbits=4, vbits=3, W=512, n_out=640, out_bytes=2):
+def step_bytes(lens, Hkv, Hq, D=128, kbits=4, vbits=3, W=512, n_out=640, out_bytes=2, polar_keys=False):
     """Canonical compressed bytes of one decode step (storage-of-record sizes):
     per (sequence, kv head) n_cold*(D*kb/8 + D*vb/8 + 4) + n_grp*(2*D*4 + n_out*6)
-    + n_hot*2*D*2, plus q in and output per query head."""
+    + n_hot*2*D*2, plus q in and output per query head.  PolarQuant keys carry
+    a 4-byte norm per token instead of the per-group scale and mean."""
     G = (W + 1) // 2
     tot = 0
     for L in lens:
         ng = n_groups(L, W)
         n_cold, n_hot = ng * G, L - ng * G
-        tot += Hkv * (n_cold * (D * kbits // 8 + D * vbits // 8 + 4) + ng * (2 * D * 4 + n_out * 6)
-                      + n_hot * 2 * D * 2 + (Hq // Hkv) * D * (2 + out_bytes))
+        per_tok = D * kbits // 8 + D * vbits // 8 + 4 + (4 if polar_keys else 0)
+        per_grp = (0 if polar_keys else 2 * D * 4) + n_out * 6
+        tot += Hkv * (n_cold * per_tok + ng * per_grp + n_hot * 2 * D * 2 + (Hq // Hkv) * D * (2 + out_bytes))
     return tot
+
+
+def key_form(cfg):
+    """The key form of a config, in words."""
+    grid = cfg.get("key_grid", "nf4_asym")
+    kb = cfg.get("kbits", 4)
+    if grid == "polar":
+        return f"K{kb} PolarQuant keys"
+    outl = " + 2% fp16 outliers" if cfg.get("ofrac", 0.02) > 0 else ""
+    return f"K{kb} {'uniform per-channel' if grid == 'uniform' else 'asym-NF4'}{outl}"
+
+
+def config_step_bytes(cfg):
+    """step_bytes of a config: its key form, widths and outlier count (2 % of
+    a 256-token group per channel: 5 x 128)."""
+    n_out = 640 if cfg.get("ofrac", 0.02) > 0 else 0
+    return step_bytes(config_lengths(cfg), cfg["Hkv"], cfg["Hq"], kbits=cfg.get("kbits", 4),
+                      vbits=cfg["vbits"], n_out=n_out, polar_keys=cfg.get("key_grid") == "polar")
 
 
 def synth_chunk(torch, gen, scale, t0, n, B, Hkv, D=128, theta=10000.0):
@@ -103,6 +128,8 @@ def build_pool(torch, cfg, seed, chunk=4096):
         P = cfg["page"]
         max_pages = n_groups(L) * 256 // P
         extra = dict(page_tokens=P, block_table=np.random.default_rng(4).permutation(B * max_pages).astype(np.int32))
+    if "key_grid" in cfg:
+        extra.update(key_grid=cfg["key_grid"], key_bits=cfg["kbits"], outlier_frac=cfg["ofrac"])
     pool = TQKVPool(n_kv_heads=Hkv, n_q_heads=Hq, max_batch=B, max_seq_len=L,
                     value_bits=cfg["vbits"], seed=seed, **extra)
     gen = torch.Generator(device="cuda")
@@ -231,7 +258,9 @@ def encode_bench(torch, cfg, fills, chunk=4096):
     gen.manual_seed(11)
     scale = torch.exp(torch.randn((B, Hkv, 1, 128), generator=gen, device="cuda"))
     chunks = [synth_chunk(torch, gen, scale, t, min(chunk, L - t), B, Hkv) for t in range(0, L, chunk)]
-    pool = TQKVPool(n_kv_heads=Hkv, n_q_heads=Hq, max_batch=B, max_seq_len=L, value_bits=vb, seed=0)
+    kf = (dict(key_grid=cfg["key_grid"], key_bits=cfg["kbits"], outlier_frac=cfg["ofrac"])
+          if "key_grid" in cfg else {})
+    pool = TQKVPool(n_kv_heads=Hkv, n_q_heads=Hq, max_batch=B, max_seq_len=L, value_bits=vb, seed=0, **kf)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     times = []
     for it in range(fills + 1):
@@ -246,9 +275,14 @@ def encode_bench(torch, cfg, fills, chunk=4096):
             times.append(e0.elapsed_time(e1))
     ms = sorted(times)[len(times) // 2]
     n_cold = n_groups(L) * ((512 + 1) // 2)
-    nbytes = B * Hkv * (L * 2 * 128 * 2 + n_cold * (128 * 4 // 8 + 128 * vb // 8 + 4)) \
-        + B * Hkv * n_groups(L) * (2 * 128 * 4 + 640 * 6)
-    rot_ops = B * Hkv * n_cold * 2 * 128 * 128
+    kb = cfg.get("kbits", 4)
+    polar = cfg.get("key_grid") == "polar"
+    n_out = 640 if cfg.get("ofrac", 0.02) > 0 else 0
+    per_token = 128 * kb // 8 + 128 * vb // 8 + 4 + (4 if polar else 0)
+    per_group = 0 if polar else 2 * 128 * 4 + n_out * 6
+    nbytes = B * Hkv * (L * 2 * 128 * 2 + n_cold * per_token) + B * Hkv * n_groups(L) * per_group
+    # PolarQuant keys go through the same rotation as the values
+    rot_ops = B * Hkv * n_cold * 2 * 128 * 128 * (2 if polar else 1)
     return {"metric": "prefill encode GB/s (fp16 K+V in + coded groups out)",
             "value": round(nbytes / (ms * 1e-3) / 1e9, 1), "unit": "GB/s",
             "ms_per_fill": round(ms, 3), "tokens_per_s": round(B * L / (ms * 1e-3)),
@@ -256,7 +290,7 @@ def encode_bench(torch, cfg, fills, chunk=4096):
             "rotation_ops_per_s": round(rot_ops / (ms * 1e-3) / 1e12, 2),
             "valu_frac": round(rot_ops / (ms * 1e-3) / VALU_OPS_PEAK, 3),
             "config": {"name": cfg.get("name", ""), "batch": B, "context": L, "n_kv_heads": Hkv,
-                       "chunk": chunk, "value_bits": vb}}
+                       "chunk": chunk, "value_bits": vb, "keys": key_form(cfg)}}
 
 
 def preroll(fn, min_ms):
@@ -305,7 +339,7 @@ def main():
 
     cfg = CONFIGS[args.config]
     cpu = None
-    if not args.encode and not args.no_cpu_baseline:
+    if not args.encode and not args.no_cpu_baseline and "key_grid" not in cfg:
         # single-threaded BLAS in each worker process; set before NumPy loads
         for var in ("OPENBLAS_NUM_THREADS", "MKL_NUM_THREADS"):
             os.environ[var] = "1"
@@ -367,7 +401,7 @@ def main():
     torch.cuda.synchronize()
     launch_ms = sorted(a.elapsed_time(b) for a, b in ev)
     kernel_ms = launch_ms[len(launch_ms) // 2]
-    nbytes = step_bytes(config_lengths(cfg), Hkv, Hq, vbits=cfg["vbits"])
+    nbytes = config_step_bytes(cfg)
     achieved = nbytes / (kernel_ms * 1e-3) / 1e9
     step_gbs = nbytes / (ms_per_step * 1e-3) / 1e9
 
@@ -407,7 +441,7 @@ def main():
                                   f"{cfg['page']}-token pages, permuted block table"
                                   if cfg.get("ragged") else f"{L}")
                                + f", {Hq} q-heads / {Hkv} kv-heads, "
-                               f"head_dim 128, K4 asym-NF4 + 2% fp16 outliers, V{cfg['vbits']} "
+                               f"head_dim 128, {key_form(cfg)}, V{cfg['vbits']} "
                                f"PolarQuant, fp16 hot window 512",
                    "name": args.config, "batch": B, "context": L, "n_q_heads": Hq,
                    "n_kv_heads": Hkv, "replicas": args.replicas},
