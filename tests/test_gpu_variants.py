@@ -205,16 +205,47 @@ def test_v2_pool_decode_gqa(W, P):
 
 def test_value_norm_beyond_the_decode_range_is_refused():
     """A value vector whose norm exceeds 16376 (weight <= 4 times the norm
-    must stay below fp16's 65504 in the decode) is flagged by the encode and
-    refused at append."""
+    must stay below fp16's 65504 in the decode) is flagged by the encode;
+    the pool refuses it at its next check (the append does not wait for the
+    flag), and a decode checks before it runs."""
     from turboquant_pro_amd import TQKVPool
     print("[variants] value norm overflow", flush=True)
     k, v, _ = O.synthetic_kv(5, 1, 1, 1, 600)
     v = v.astype(np.float32)
     v[0, 0, 10] = 2000.0          # norm ~ 22600 > 16376
     pool = TQKVPool(n_kv_heads=1, max_batch=1, max_seq_len=600, seed=0)
+    pool.append(torch.from_numpy(k).cuda(), torch.from_numpy(v.astype(np.float16)).cuda())
     with pytest.raises(ValueError, match="16376"):
-        pool.append(torch.from_numpy(k).cuda(), torch.from_numpy(v.astype(np.float16)).cuda())
+        pool.check()
+    # the same through the decode of a second pool
+    other = TQKVPool(n_kv_heads=1, max_batch=1, max_seq_len=600, seed=0)
+    other.append(torch.from_numpy(k).cuda(), torch.from_numpy(v.astype(np.float16)).cuda())
+    with pytest.raises(ValueError, match="16376"):
+        other.decode(torch.zeros((1, 1, 128), dtype=torch.float16, device="cuda"))
+    # a pool with in-range norms has nothing pending after its checks
+    _, v0, _ = O.synthetic_kv(5, 1, 1, 1, 600)
+    ok = TQKVPool(n_kv_heads=1, max_batch=1, max_seq_len=600, seed=0)
+    ok.append(torch.from_numpy(k).cuda(), torch.from_numpy(v0).cuda())
+    ok.check()
+    assert ok._pending == []
+
+
+def test_side_list_beyond_its_cap_is_refused():
+    """A group whose side-list needs more entries than ``outlier_cap`` sets
+    the encode's flag; the pool's next check raises, and so does a decode."""
+    from turboquant_pro_amd import TQKVPool
+    print("[variants] side-list beyond outlier_cap", flush=True)
+    k, v, _ = O.synthetic_kv(6, 1, 1, 1, 600)
+    mk = lambda: TQKVPool(n_kv_heads=1, max_batch=1, max_seq_len=600, seed=0,  # noqa: E731
+                          outlier_frac=0.1, outlier_cap=64)
+    pool = mk()
+    pool.append(torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda())
+    with pytest.raises(RuntimeError, match="outlier_cap"):
+        pool.check()
+    other = mk()
+    other.append(torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda())
+    with pytest.raises(RuntimeError, match="outlier_cap"):
+        other.decode(torch.zeros((1, 1, 128), dtype=torch.float16, device="cuda"))
 
 
 def test_pool_grows_with_its_codes():

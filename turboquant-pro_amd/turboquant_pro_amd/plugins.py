@@ -432,7 +432,8 @@ class PerChannelKVQuantizer:
         has_out = c.outlier_idx is not None and c.outlier_val is not None
         _check_key_container(kp, scale, zero, c, B * H * S * D, (B, H, D), has_out)
         dev = torch.device(self.device if self.device is not None else "cuda")
-        t = lambda a, dt: torch.from_numpy(np.ascontiguousarray(a, dt)).to(dev)  # noqa: E731
+        # a writable host copy: containers may hold read-only arrays (np.load)
+        t = lambda a, dt: torch.from_numpy(np.array(a, dt, order="C")).to(dev)  # noqa: E731
         kp_d, sc_d, zr_d = t(kp, np.uint8), t(scale, np.float32), t(zero, np.float32)
         n_out = int(np.asarray(c.outlier_idx).size) if has_out else 0
         idx_d = t(np.asarray(c.outlier_idx, np.int32).reshape(-1), np.int32) if n_out else None

@@ -165,6 +165,8 @@ class TQKVPool:
         self.lengths = [0] * max_batch
         self.seq_lens = torch.zeros(max_batch, dtype=i32, device=dev)
         self._overflow = torch.zeros(1, dtype=i32, device=dev)
+        # (event, pinned flag word) of appends whose encode flags are not read yet
+        self._pending = []
         self._ws = None
 
     # ------------------------------------------------------------------ #
@@ -194,8 +196,33 @@ class TQKVPool:
         return self.lengths[b] - self.n_groups(b) * self.group_tokens
 
     def reset(self) -> None:
+        self.check()
         self.lengths = [0] * self.max_batch
         self.seq_lens.zero_()
+
+    def check(self, wait: bool = True) -> None:
+        """Raise the first error an earlier append's encode flagged (a value
+        norm beyond the decode's range, a side-list beyond ``outlier_cap``).
+        ``append`` copies the flags to pinned host memory without waiting, so
+        that consecutive appends keep the GPU busy; they are read here: by the
+        next append (flags already arrived), and with ``wait`` by every call
+        that reads the cache (decode, export, dequant, growth)."""
+        keep = []
+        for ev, flag in self._pending:
+            if not wait and not ev.query():
+                keep.append((ev, flag))
+                continue
+            ev.synchronize()
+            ovf = int(flag[0])
+            if ovf & 2:
+                self._pending = []
+                raise ValueError("a value vector's norm exceeds 16376, the largest the gfx950 decode "
+                                 "carries (softmax weight <= 4 times the norm in fp16)")
+            if ovf & 1:
+                self._pending = []
+                raise RuntimeError("outlier side-list exceeded outlier_cap for a group; "
+                                   "rebuild the pool with a larger outlier_cap")
+        self._pending = keep
 
     def grown(self, max_seq_len: int) -> "TQKVPool":
         """A pool of the same format holding up to ``max_seq_len`` tokens per
@@ -204,6 +231,7 @@ class TQKVPool:
         codes are moved, never re-encoded).  Pools with a caller's block
         table cannot grow."""
         torch = _torch()
+        self.check()
         if self._custom_table:
             raise ValueError("a pool with a caller's block table cannot grow")
         if max_seq_len <= self.max_seq_len:
@@ -239,6 +267,7 @@ class TQKVPool:
         default).  Equivalent to T one-token ``TurboQuantKVCache.append`` calls
         per sequence (turboquant_pro/core.py:986-1038)."""
         torch = _torch()
+        self.check(wait=False)
         B, T = self.max_batch, int(k.shape[2])
         if tuple(k.shape) != (B, self.n_kv_heads, T, self.head_dim) or k.shape != v.shape:
             raise ValueError(f"append expects ({B}, {self.n_kv_heads}, T, {self.head_dim}) K and V")
@@ -258,32 +287,32 @@ class TQKVPool:
             for g in range(n_groups_for(prev[b], self.hot_window), n_groups_for(new[b], self.hot_window)):
                 items += [b, g]
         hot_start = [n_groups_for(L, self.hot_window) * self.group_tokens for L in new]
-        host = torch.tensor(prev + n_new + hot_start + items, dtype=torch.int32)
-        dev = host.to(self.device, non_blocking=False)
+        # pinned and asynchronous: the caching host allocator keeps the block
+        # until the copy, queued behind earlier work on the stream, has run
+        host = torch.tensor(prev + n_new + hot_start + items, dtype=torch.int32).pin_memory()
+        dev = host.to(self.device, non_blocking=True)
         prev_d, nnew_d, hs_d = dev[:B], dev[B:2 * B], dev[2 * B:3 * B]
         items_d = dev[3 * B:]
         L = N.lib()
         st = self._stream()
         if items:
-            if check_overflow:
-                self._overflow.zero_()
+            self._overflow.zero_()
             N.check(L.tqk_encode_groups(ctypes.byref(self.desc), ctypes.byref(self.ptrs), B,
                                         len(items) // 2, items_d.data_ptr(), prev_d.data_ptr(),
                                         k.data_ptr(), v.data_ptr(), T,
                                         self._overflow.data_ptr(), st), "tqk_encode_groups")
+            if check_overflow:
+                flag = torch.empty(1, dtype=torch.int32, pin_memory=True)
+                flag.copy_(self._overflow, non_blocking=True)
+                ev = torch.cuda.Event()
+                ev.record(torch.cuda.current_stream(self.device))
+                self._pending.append((ev, flag))
         if T > 0:
             N.check(L.tqk_append_hot(ctypes.byref(self.desc), ctypes.byref(self.ptrs), B,
                                      prev_d.data_ptr(), nnew_d.data_ptr(), hs_d.data_ptr(),
                                      k.data_ptr(), v.data_ptr(), T, st), "tqk_append_hot")
         self.lengths = new
-        self.seq_lens.copy_(torch.tensor(new, dtype=torch.int32), non_blocking=False)
-        ovf = int(self._overflow.item()) if items and check_overflow else 0
-        if ovf & 2:
-            raise ValueError("a value vector's norm exceeds 16376, the largest the gfx950 decode "
-                             "carries (softmax weight <= 4 times the norm in fp16)")
-        if ovf & 1:
-            raise RuntimeError("outlier side-list exceeded outlier_cap for a group; "
-                               "rebuild the pool with a larger outlier_cap")
+        torch.add(prev_d, nnew_d, out=self.seq_lens)
 
     # ------------------------------------------------------------------ #
     def workspace(self, batch: int, max_len: int):
@@ -309,6 +338,7 @@ class TQKVPool:
         fp32 ``(B, Hq, D)`` attention output over each sequence's whole cache."""
         torch = _torch()
         q = self._check_q(q)
+        self.check()
         B, max_len = self.max_batch, max(self.lengths)
         if out is None:
             out = torch.empty((B, self.n_q_heads, self.head_dim), dtype=torch.float32, device=self.device)
@@ -323,6 +353,7 @@ class TQKVPool:
         ``(B, Hq)``, ``(B, Hq)``, ``(B, Hq, D)`` fp32 with ``out = acc / l``."""
         torch = _torch()
         q = self._check_q(q)
+        self.check()
         B, max_len = self.max_batch, max(self.lengths)
         m = torch.empty((B, self.n_q_heads), dtype=torch.float32, device=self.device)
         l_ = torch.empty_like(m)
@@ -340,6 +371,7 @@ class TQKVPool:
         """fp32 reconstructions of groups ``[(b, g), ...]``: keys and values,
         each ``(n, Hkv, G, D)`` (PerChannelKV.decompress / TurboQuantKV.decompress)."""
         torch = _torch()
+        self.check()
         n = len(items)
         G, H, D = self.group_tokens, self.n_kv_heads, self.head_dim
         kout = torch.empty((n, H, G, D), dtype=torch.float32, device=self.device)
@@ -372,6 +404,7 @@ class TQKVPool:
         PolarQuant keys: ``kpacked`` is the keys' CompressedKV.indices (the value
         pack) and ``knorms`` ``(H, G)`` their norms, with no scale, mean or
         side-list."""
+        self.check()
         phys, off = self._rows(b, g)
         H, G, D = self.n_kv_heads, self.group_tokens, self.head_dim
         kp = self.kcodes[:, phys, off].contiguous().cpu().numpy()  # (H, G, D * key_bits / 8)
