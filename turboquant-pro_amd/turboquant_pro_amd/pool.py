@@ -196,7 +196,8 @@ class TQKVPool:
         return self.lengths[b] - self.n_groups(b) * self.group_tokens
 
     def reset(self) -> None:
-        self.check()
+        # the cache's contents go, and with them any flags still unread
+        self._pending = []
         self.lengths = [0] * self.max_batch
         self.seq_lens.zero_()
 
@@ -206,7 +207,8 @@ class TQKVPool:
         ``append`` copies the flags to pinned host memory without waiting, so
         that consecutive appends keep the GPU busy; they are read here: by the
         next append (flags already arrived), and with ``wait`` by every call
-        that reads the cache (decode, export, dequant, growth)."""
+        that reads the cache (decode, export, dequant, growth).  ``reset``
+        drops unread flags with the contents they describe."""
         keep = []
         for ev, flag in self._pending:
             if not wait and not ev.query():
