@@ -577,7 +577,12 @@ struct HotArgs {
   int chunk_tokens;
 };
 
-// grid (batch, Hkv); copies the surviving new tokens into the ring.
+constexpr int kHotSlice = 64;  // tokens per workgroup of the ring copy
+
+// grid (batch, Hkv, slices): copies the surviving new tokens into the ring,
+// kHotSlice tokens per workgroup and round (slices stride by gridDim.z), so a
+// chunk's copy spreads over the whole chip instead of one workgroup per
+// (sequence, kv head).
 __global__ __launch_bounds__(kThreads) void tqk_append_hot_kernel(HotArgs a) {
   const int b = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
   const tqk_cache_desc& d = a.d;
@@ -586,12 +591,15 @@ __global__ __launch_bounds__(kThreads) void tqk_append_hot_kernel(HotArgs a) {
   const int R = d.hot_ring;
   const size_t rb = ((size_t)b * d.n_kv_heads + h) * R;
   const size_t cb = ((size_t)b * d.n_kv_heads + h) * a.chunk_tokens;
-  for (int idx = tid; idx < (t1 - t0) * 16; idx += kThreads) {
-    const int t = t0 + (idx >> 4), c = idx & 15;
-    const size_t src = (cb + (t - prev)) * TQK_D;
-    const size_t dst = (rb + (t % R)) * TQK_D;
-    reinterpret_cast<uint4*>(a.hot_k + dst)[c] = reinterpret_cast<const uint4*>(a.chunk_k + src)[c];
-    reinterpret_cast<uint4*>(a.hot_v + dst)[c] = reinterpret_cast<const uint4*>(a.chunk_v + src)[c];
+  for (int s0 = t0 + (int)blockIdx.z * kHotSlice; s0 < t1; s0 += (int)gridDim.z * kHotSlice) {
+    const int n = min(kHotSlice, t1 - s0);
+    for (int idx = tid; idx < n * 16; idx += kThreads) {
+      const int t = s0 + (idx >> 4), c = idx & 15;
+      const size_t src = (cb + (t - prev)) * TQK_D;
+      const size_t dst = (rb + (t % R)) * TQK_D;
+      reinterpret_cast<uint4*>(a.hot_k + dst)[c] = reinterpret_cast<const uint4*>(a.chunk_k + src)[c];
+      reinterpret_cast<uint4*>(a.hot_v + dst)[c] = reinterpret_cast<const uint4*>(a.chunk_v + src)[c];
+    }
   }
 }
 
@@ -741,7 +749,10 @@ int tqk_append_hot(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t bat
   a.chunk_k = chunk_k;
   a.chunk_v = chunk_v;
   a.chunk_tokens = chunk_tokens;
-  hipLaunchKernelGGL(tqk_append_hot_kernel, dim3(batch, d->n_kv_heads), dim3(kThreads), 0,
+  // the surviving tokens of a sequence number at most min(chunk, ring)
+  const int span = min(chunk_tokens, d->hot_ring);
+  const int slices = max(1, (span + kHotSlice - 1) / kHotSlice);
+  hipLaunchKernelGGL(tqk_append_hot_kernel, dim3(batch, d->n_kv_heads, slices), dim3(kThreads), 0,
                      reinterpret_cast<hipStream_t>(stream), a);
   return hipGetLastError() == hipSuccess ? TQK_OK : TQK_EHIP;
 }
