@@ -132,6 +132,13 @@ DECODE_CASES = [
     (1, 2, 8, 200, 3, 64, None),       # groups of 32 (one block), hot ring of 64
     (2, 2, 4, 777, 3, 512, 32),        # 32-token pages, partial hot block
     (1, 8, 8, 1500, 3, 512, None),     # MHA with V3
+    # query heads per kv head that are not powers of two (padded heads in the
+    # kernel): 3, 5, and 7 (Qwen2.5-7B's 28 / 4), on both decode kernels
+    (1, 2, 6, 900, 3, 512, None),
+    (2, 2, 10, 1100, 3, 512, 32),
+    (1, 4, 28, 1300, 3, 512, None),
+    (1, 2, 14, 90, 3, 16, None),
+    (1, 2, 6, 200, 4, 64, None),
 ]
 
 
