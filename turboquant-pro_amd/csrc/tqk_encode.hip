@@ -53,6 +53,61 @@ __device__ __forceinline__ uint32_t abs_h(uint16_t x) { return x & 0x7FFFu; }
 
 typedef uint16_t u16x2_t __attribute__((ext_vector_type(2)));
 
+// v into the K-long descending lists held in the two halves of t (one
+// packed 16-bit max and min per list entry)
+template <int K>
+__device__ __forceinline__ void topk_insert(u16x2_t (&t)[K], u16x2_t v) {
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    const u16x2_t hi = __builtin_elementwise_max(t[i], v);
+    v = __builtin_elementwise_min(t[i], v);
+    t[i] = hi;
+  }
+}
+
+// The k-th largest (1 <= k <= K) of a channel's magnitude patterns, held two
+// per register in m by the four lanes l, l ^ 16, l ^ 32, l ^ 48: each lane
+// keeps the K largest of each half of its registers, the halves' lists are
+// merged, then the lanes' lists over the two permlane swaps.  The largest T
+// with #{m >= T} >= k is exactly this k-th largest value (with multiplicity),
+// so it equals the bitwise threshold search's result.
+template <int K>
+__device__ __forceinline__ uint32_t kth_largest(const u16x2_t (&m)[TQK_MAX_G / 8], int k) {
+  u16x2_t t[K];
+#pragma unroll
+  for (int i = 0; i < K; ++i) t[i] = u16x2_t{0, 0};
+#pragma unroll
+  for (int i = 0; i < TQK_MAX_G / 8; ++i) topk_insert<K>(t, m[i]);
+  {
+    u16x2_t sw[K];
+#pragma unroll
+    for (int i = 0; i < K; ++i) sw[i] = t[i].yx;
+#pragma unroll
+    for (int i = 0; i < K; ++i) topk_insert<K>(t, sw[i]);
+  }
+  // a permlane swap returns this lane's list and its partner's, in an order
+  // that depends on the lane; the merge is symmetric in the two
+#pragma unroll
+  for (int step = 0; step < 2; ++step) {
+    u16x2_t other[K];
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      const uint32_t x = __builtin_bit_cast(uint32_t, t[i]);
+      const auto r = step == 0 ? __builtin_amdgcn_permlane32_swap(x, x, false, false)
+                               : __builtin_amdgcn_permlane16_swap(x, x, false, false);
+      t[i] = __builtin_bit_cast(u16x2_t, (uint32_t)r[0]);
+      other[i] = __builtin_bit_cast(u16x2_t, (uint32_t)r[1]);
+    }
+#pragma unroll
+    for (int i = 0; i < K; ++i) topk_insert<K>(t, other[i]);
+  }
+  uint32_t T = t[0].x;
+#pragma unroll
+  for (int i = 1; i < K; ++i)
+    if (i == k - 1) T = t[i].x;
+  return T;
+}
+
 // Sum over lanes l, l ^ 16, l ^ 32, l ^ 48 (the four 16-lane rows).
 __device__ __forceinline__ int sum_quarters(int x) {
   auto a = __builtin_amdgcn_permlane32_swap((uint32_t)x, (uint32_t)x, false, false);
@@ -154,8 +209,10 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
     // largest fp16 magnitude pattern T with #{ |x_s| >= T } >= k (NaN patterns
     // order above inf, as np.partition does).  Every thread, 16 channels per
     // wave and pass: lanes l, l ^ 16, l ^ 32, l ^ 48 take a quarter of the
-    // tokens each, two magnitudes per register; a candidate's count is the
-    // carry bit of a packed 16-bit add, summed over the four lanes.
+    // tokens each, two magnitudes per register.  For k <= 8 the k largest are
+    // kept directly (packed 16-bit max/min insertion); otherwise a bitwise
+    // search, a candidate's count the carry bit of a packed 16-bit add,
+    // summed over the four lanes.
     if (kout > 0 && kout < G) {
       const int part = lane >> 4;
       for (int j = 16 * wv + (lane & 15); j < D; j += 16 * kEncWaves) {
@@ -167,17 +224,23 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
                           (uint16_t)(s + 1 < G ? abs_h(kt_s[s + 1][j]) : 0u)};
         }
         uint32_t T = 0;
-        for (int bit = 14; bit >= 0; --bit) {
-          const uint32_t cand = T | (1u << bit);
-          // m + (0x8000 - cand) has bit 15 set exactly when m >= cand (m, cand < 2^15)
-          const uint16_t bias = (uint16_t)(0x8000u - cand);
-          const u16x2_t bv = {bias, bias};
-          uint32_t acc = 0;  // two 16-bit counts
+        if (kout <= 5) {
+          T = kth_largest<5>(m2, kout);
+        } else if (kout <= 8) {
+          T = kth_largest<8>(m2, kout);
+        } else {
+          for (int bit = 14; bit >= 0; --bit) {
+            const uint32_t cand = T | (1u << bit);
+            // m + (0x8000 - cand) has bit 15 set exactly when m >= cand (m, cand < 2^15)
+            const uint16_t bias = (uint16_t)(0x8000u - cand);
+            const u16x2_t bv = {bias, bias};
+            uint32_t acc = 0;  // two 16-bit counts
 #pragma unroll
-          for (int i = 0; i < TQK_MAX_G / 8; ++i)
-            acc += (__builtin_bit_cast(uint32_t, (u16x2_t)(m2[i] + bv)) >> 15) & 0x00010001u;
-          const int cnt = sum_quarters((int)((acc & 0xFFFFu) + (acc >> 16)));
-          if (cnt >= kout) T = cand;
+            for (int i = 0; i < TQK_MAX_G / 8; ++i)
+              acc += (__builtin_bit_cast(uint32_t, (u16x2_t)(m2[i] + bv)) >> 15) & 0x00010001u;
+            const int cnt = sum_quarters((int)((acc & 0xFFFFu) + (acc >> 16)));
+            if (cnt >= kout) T = cand;
+          }
         }
         // the scan compares magnitudes as floats, as the reference's mask
         // |x| >= t does: a NaN threshold selects nothing (bias 0)
