@@ -219,7 +219,10 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
         u16x2_t m2[TQK_MAX_G / 8];
 #pragma unroll
         for (int i = 0; i < TQK_MAX_G / 8; ++i) {
-          const int s = (TQK_MAX_G / 4) * part + 2 * i;  // tokens past G count as magnitude 0
+          // lane quarter `part` takes token pairs 8i + 2 part (rows 4 apart
+          // fall on LDS banks 8 apart, so the four quarters never conflict);
+          // tokens past G count as magnitude 0
+          const int s = 8 * i + 2 * part;
           m2[i] = u16x2_t{(uint16_t)(s < G ? abs_h(kt_s[s][j]) : 0u),
                           (uint16_t)(s + 1 < G ? abs_h(kt_s[s + 1][j]) : 0u)};
         }
