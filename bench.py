@@ -246,9 +246,10 @@ VALU_OPS_PEAK = 256 * 4 * 16 * 2.4e9  # separately rounded fp32 ops/s: 256 CUs x
 def encode_bench(torch, cfg, fills, chunk=4096):
     """Prefill encode: the config's batch appended in ``chunk``-token chunks up
     to its context (group flushes through the encode kernel, hot-ring copies),
-    ``fills`` times after one untimed fill; median fill.  Bytes per the
-    survey's encode formula: fp16 K+V in (512 B per token-head) + the coded
-    groups out (135 B per cold token-head at K4/V3).  The encode is bound by
+    ``fills`` times after one untimed fill; median fill.  Bytes: fp16 K+V in
+    (512 B per token-head) + the coded groups out in the reference's container
+    sizes (116 B per cold token-head at K4/V3 plus 4864 B of stats and
+    side-list per group-head).  The encode is bound by
     the value rotation's 2 * 128^2 separately rounded fp32 operations per
     token-head (no FMA, no packed math: the bit-exactness contract), reported
     against the chip's unpacked VALU issue rate."""
