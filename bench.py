@@ -52,6 +52,10 @@ CONFIGS = {
     # outliers) and PolarQuant keys (per_channel_keys=False), both with V3
     "k3v3_default": dict(B=16, Hkv=8, Hq=32, L=32768, vbits=3, kbits=3, key_grid="uniform", ofrac=0.0),
     "k3v3_polar": dict(B=16, Hkv=8, Hq=32, L=32768, vbits=3, kbits=3, key_grid="polar", ofrac=0.0),
+    # 4-bit keys without the side-list: asym-NF4 (the headline's keys minus
+    # its outliers) and uniform (PerChannelKV's default grid)
+    "k4v3_nf4_noout": dict(B=16, Hkv=8, Hq=32, L=32768, vbits=3, kbits=4, key_grid="nf4_asym", ofrac=0.0),
+    "k4v3_uniform": dict(B=16, Hkv=8, Hq=32, L=32768, vbits=3, kbits=4, key_grid="uniform", ofrac=0.0),
 }
 
 
