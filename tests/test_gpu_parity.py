@@ -172,6 +172,26 @@ def test_decode_ragged_batch():
         assert_attn_close(got[b], sc.attend(q[b]), what=f"ragged seq {b} L={L}")
 
 
+def test_decode_edge_lengths():
+    """One batch with sequences of 1, 2, 31, 32, 33, 511, 512, 513, 768, 769,
+    1024 and 1025 tokens: hot-only windows of one token, whole and partial
+    32-token hot blocks, exactly at the first flush and one past it, and
+    one token either side of the next group boundaries; GQA 4 on the MFMA
+    kernel, whose item order is reranked for batches (longest first)."""
+    lens = [1, 2, 31, 32, 33, 511, 512, 513, 768, 769, 1024, 1025]
+    B, Hkv, Hq, T = len(lens), 2, 8, max(lens)
+    print(f"[decode edge lengths] lens={lens}", flush=True)
+    k, v, q = O.synthetic_kv(73, B, Hkv, Hq, T)
+    pi, pi_t = O.rotation(9, 128)
+    pool = _pool(n_kv_heads=Hkv, n_q_heads=Hq, max_batch=B, max_seq_len=T, rotation=(pi, pi_t))
+    _fill(pool, k, v, n_new=lens)
+    got = pool.decode(_dev(q)).cpu().numpy()
+    for b, L in enumerate(lens):
+        sc = O.SequenceCache(hot_window=512, value_bits=3, outlier_frac=0.02).build(
+            k[b, :, :L], v[b, :, :L], pi, pi_t)
+        assert_attn_close(got[b], sc.attend(q[b]), what=f"seq {b} L={L}")
+
+
 def test_decode_partials_merge():
     B, Hkv, Hq, L = 1, 2, 8, 1200
     k, v, q = O.synthetic_kv(81, B, Hkv, Hq, L)
