@@ -139,6 +139,11 @@ DECODE_CASES = [
     (1, 4, 28, 1300, 3, 512, None),
     (1, 2, 14, 90, 3, 16, None),
     (1, 2, 6, 200, 4, 64, None),
+    # other page sizes: 64- and 256-token pages (a page per group), and
+    # 8-token pages (not a whole MFMA tile: the VALU kernel)
+    (2, 2, 8, 1300, 3, 512, 64),
+    (1, 2, 8, 1300, 3, 512, 256),
+    (1, 2, 8, 900, 3, 512, 8),
 ]
 
 
@@ -151,6 +156,9 @@ def test_decode_matches_dequant_then_attend(case):
     pool = _pool(n_kv_heads=Hkv, n_q_heads=Hq, max_batch=B, max_seq_len=L, hot_window=W,
                  value_bits=vbits, rotation=rot, page_tokens=P)
     _fill(pool, k, v)
+    if P not in (None, 16, 32):
+        # page sizes the encode tests do not cover: its codes too, bit for bit
+        _check_codes(pool, seqs, B)
     got = pool.decode(_dev(q)).cpu().numpy()
     for b in range(B):
         assert_attn_close(got[b], seqs[b].attend(q[b]), what=f"case {case} seq {b}")
