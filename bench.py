@@ -13,10 +13,10 @@ cannot serve repeat steps.
 Prints one JSON line.  `value` is microseconds per decode step (lower is
 better), averaged over `--steps` back-to-back steps after a time-based
 pre-roll (GPU clock ramp) and `--warmup` steps.  `roofline.achieved` is the
-canonical compressed-KV bytes of one step divided by the median duration of
+canonical compressed-KV bytes of one step divided by the average duration of
 one decode-kernel launch (split-K over the coded groups and the hot window,
-merged by its last workgroups: the whole step is this one launch), from a HIP
-event pair around each launch on the stream it runs on.  `encode` holds the
+merged by its last workgroups: the whole step is this one launch), from one
+HIP event pair on the launch stream around `--steps` back-to-back launches.  `encode` holds the
 prefill encode of the same workload and `cpu_baseline` the reference's CPU
 decode path (oracle restatement) on this host's cores.
 """
@@ -158,18 +158,24 @@ COPY_PROBE_BYTES = 256 << 20
 
 
 def measured_traffic(config):
-    """HBM bytes per launch of the split kernel on this workload, as measured by
-    the FETCH_SIZE / WRITE_SIZE counter passes summarised in
-    profiles/tqk_decode_split_mfma_<config>_traffic.md (each counter scaled by
-    its reading on a plain copy of known size); None when not measured."""
+    """HBM bytes per launch of the split kernel on this workload, read from the
+    committed counter profile profiles/tqk_decode_split_mfma_<config>_traffic.md
+    (FETCH_SIZE / WRITE_SIZE passes, each scaled by its reading on a plain copy
+    of known size).  It is not counted in this run: the profile names the build
+    it was measured on.  Returns (bytes or None, source text)."""
     import re
-    path = os.path.join(ROOT, "profiles", f"tqk_decode_split_mfma_{config}_traffic.md")
+    name = f"tqk_decode_split_mfma_{config}_traffic.md"
+    path = os.path.join(ROOT, "profiles", name)
     try:
         with open(path) as f:
-            m = re.search(r"traffic_bytes_per_launch\s*=\s*(\d+)", f.read())
+            text = f.read()
     except OSError:
-        return None
-    return int(m.group(1)) if m else None
+        return None, "not measured for this config"
+    m = re.search(r"traffic_bytes_per_launch\s*=\s*(\d+)", text)
+    b = re.search(r"build_commit\s*=\s*(\w+)", text)
+    src = f"committed counter profile profiles/{name}" + (f" (build {b.group(1)})" if b else "") + \
+        ", not counted in this run"
+    return (int(m.group(1)) if m else None), src
 
 
 _CPU_STATE = {}
@@ -386,26 +392,25 @@ def main():
     torch.cuda.synchronize()
     ms_per_step = e0.elapsed_time(e1) / args.steps
 
-    # the kernel alone: a HIP event pair on its stream around each of `steps`
+    # the kernel alone: one HIP event pair on its stream around `steps`
     # back-to-back tqk_decode calls straight through the C ABI (one launch
-    # each); kernel_us is the median launch
+    # each, no host work between them); kernel_us is the pair's time / steps,
+    # the average launch duration that the kernel trace's mean reproduces
     lib = N.lib()
     st = ctypes.c_void_p(stream.cuda_stream)
     wss = [p.workspace(B, max(p.lengths)) for p in pools]
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(args.steps)]
+    args_c = [(ctypes.byref(p.desc), ctypes.byref(p.ptrs), p.seq_lens.data_ptr(), max(p.lengths))
+              for p in pools]
     torch.cuda.synchronize()
+    e0.record(stream)
     for i in range(args.steps):
-        p = pools[i % len(pools)]
+        desc, ptrs, sl, ml = args_c[i % len(pools)]
         ws, need = wss[i % len(pools)]
-        ev[i][0].record(stream)
-        N.check(lib.tqk_decode(ctypes.byref(p.desc), ctypes.byref(p.ptrs), B, q.data_ptr(),
-                               p.seq_lens.data_ptr(), max(p.lengths), outs[i % len(pools)].data_ptr(),
+        N.check(lib.tqk_decode(desc, ptrs, B, q.data_ptr(), sl, ml, outs[i % len(pools)].data_ptr(),
                                ws.data_ptr(), need, st), "tqk_decode")
-        ev[i][1].record(stream)
+    e1.record(stream)
     torch.cuda.synchronize()
-    launch_ms = sorted(a.elapsed_time(b) for a, b in ev)
-    kernel_ms = launch_ms[len(launch_ms) // 2]
+    kernel_ms = e0.elapsed_time(e1) / args.steps
     nbytes = config_step_bytes(cfg)
     achieved = nbytes / (kernel_ms * 1e-3) / 1e9
     step_gbs = nbytes / (ms_per_step * 1e-3) / 1e9
@@ -418,6 +423,8 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes": COPY_PROBE_BYTES, "copies": 3}), file=sys.stderr, flush=True)
+
+    traffic, traffic_src = measured_traffic(args.config)
 
     enc = None
     if not args.no_encode:
@@ -454,10 +461,12 @@ def main():
         "step_gbs": round(step_gbs, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(args.config),
+                     "traffic": traffic,
+                     "traffic_source": traffic_src,
                      "kernel": "tqk_decode_split_mfma", "kernel_us": round(kernel_ms * 1e3, 2),
-                     "kernel_us_p10_p90": [round(launch_ms[len(launch_ms) // 10] * 1e3, 2),
-                                           round(launch_ms[(9 * len(launch_ms)) // 10] * 1e3, 2)]},
+                     "kernel_us_method": f"one HIP event pair around {args.steps} back-to-back "
+                                         "tqk_decode launches on their stream, divided by "
+                                         f"{args.steps}"},
         "encode": enc,
         "cpu_baseline": cpu,
     }

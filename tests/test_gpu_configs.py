@@ -138,3 +138,30 @@ def test_config4_70b_append_chunks_and_decode():
     q = torch.randn((B, Hq, 128), generator=torch.Generator(device="cuda").manual_seed(14),
                     device="cuda").half()
     _decode_vs_reference(pool, q, [L] * B, "config4", every=3)
+
+
+def test_headline_timed_shape_b16_32k():
+    """The shape bench.py times (its "headline" config): B16 x 32768 tokens,
+    32 q-heads / 8 kv-heads, the default pool (32-token pages in the clustered
+    block table, K4 asym-NF4 + 2 % outliers, V3, hot window 512), filled in
+    4096-token chunks as bench.build_pool fills it, with the measurement
+    spec's synthetic data.  Sampled groups bit-exact against the oracle and
+    every sequence's decode against the fp32 dequantize-then-attend, on the
+    kernel plan the benchmark's number comes from."""
+    import bench
+    print("[headline] B16 Hkv8 Hq32 L32768, bench pool", flush=True)
+    cfg = bench.CONFIGS["headline"]
+    B, Hkv, Hq, L = cfg["B"], cfg["Hkv"], cfg["Hq"], cfg["L"]
+    k, v = synth_gpu(torch, 5, B, Hkv, L)
+    pool = _pool(n_kv_heads=Hkv, n_q_heads=Hq, max_batch=B, max_seq_len=L, value_bits=cfg["vbits"],
+                 seed=1000)
+    assert pool.page_tokens == 32 and pool.tiled
+    _append_chunks(pool, k, v, chunk=4096)
+    ng = pool.n_groups(0)
+    assert ng == 126
+    pi_t = pool.pi_t.cpu().numpy()
+    for b in (0, 7, 15):
+        check_groups_vs_oracle(pool, k, v, b, (0, 63, ng - 1), pi_t, 3, what="headline")
+    q = torch.randn((B, Hq, 128), generator=torch.Generator(device="cuda").manual_seed(7),
+                    device="cuda").half()
+    _decode_vs_reference(pool, q, [L] * B, "headline")

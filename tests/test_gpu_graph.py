@@ -69,3 +69,34 @@ def test_decode_replays_in_a_graph_equal_the_eager_decode(W):
     for b in range(B):
         sc = O.SequenceCache(hot_window=W, value_bits=3, outlier_frac=0.02).build(k[b], v[b], pi, pi_t)
         assert_attn_close(out[b].cpu().numpy(), sc.attend(q2[b]), what=f"graph W={W} seq {b}")
+
+
+def test_capture_with_unread_encode_flags_is_refused():
+    """An append leaves its encode flags unread (it does not wait for them); a
+    decode captured right after it would need a host wait, which capture
+    forbids, so the pool raises before launching anything.  After
+    ``pool.check()`` the same capture works."""
+    from turboquant_pro_amd import TQKVPool
+    print("[graph] capture after an unchecked append", flush=True)
+    B, Hkv, Hq = 1, 2, 8
+    k, v, q = O.synthetic_kv(32, B, Hkv, Hq, 1700)
+    pool = TQKVPool(n_kv_heads=Hkv, n_q_heads=Hq, max_batch=B, max_seq_len=1700, seed=0)
+    kd, vd, qd = (torch.from_numpy(x).cuda() for x in (k, v, q))
+    pool.append(kd[:, :, :1400], vd[:, :, :1400])
+    eager = pool.decode(qd).clone()      # workspace allocated, flags read
+    pool.append(kd[:, :, 1400:], vd[:, :, 1400:])   # flushes a group: flags pending
+    assert pool._pending
+    g = torch.cuda.CUDAGraph()
+    with pytest.raises(RuntimeError, match="pool.check"):
+        with torch.cuda.graph(g):
+            pool.decode(qd)
+    torch.cuda.synchronize()
+    pool.check()
+    g2 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g2):
+        out = pool.decode(qd)
+    g2.replay()
+    torch.cuda.synchronize()
+    want = pool.decode(qd)
+    torch.cuda.synchronize()
+    assert torch.equal(out, want) and not torch.equal(out, eager)

@@ -222,6 +222,14 @@ def test_value_norm_beyond_the_decode_range_is_refused():
     other.append(torch.from_numpy(k).cuda(), torch.from_numpy(v.astype(np.float16)).cuda())
     with pytest.raises(ValueError, match="16376"):
         other.decode(torch.zeros((1, 1, 128), dtype=torch.float16, device="cuda"))
+    # the error is sticky: the offending codes stay, so a second decode (and
+    # an export) raise too, until reset() drops the contents
+    with pytest.raises(ValueError, match="16376"):
+        other.decode(torch.zeros((1, 1, 128), dtype=torch.float16, device="cuda"))
+    with pytest.raises(ValueError, match="16376"):
+        other.export_group(0, 0)
+    other.reset()
+    other.check()
     # a pool with in-range norms has nothing pending after its checks
     _, v0, _ = O.synthetic_kv(5, 1, 1, 1, 600)
     ok = TQKVPool(n_kv_heads=1, max_batch=1, max_seq_len=600, seed=0)
@@ -244,6 +252,8 @@ def test_side_list_beyond_its_cap_is_refused():
         pool.check()
     other = mk()
     other.append(torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda())
+    with pytest.raises(RuntimeError, match="outlier_cap"):
+        other.decode(torch.zeros((1, 1, 128), dtype=torch.float16, device="cuda"))
     with pytest.raises(RuntimeError, match="outlier_cap"):
         other.decode(torch.zeros((1, 1, 128), dtype=torch.float16, device="cuda"))
 

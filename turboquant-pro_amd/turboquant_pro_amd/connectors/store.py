@@ -130,15 +130,19 @@ class TurboQuantBlockStore:
         return x.reshape((-1,) + x.shape[-3:])
 
     # ---------------------------------------------------------------- API
-    def make_record(self, keys: Any, values: Any, packed: bool = False) -> BlockRecord:
-        """Quantize one layer block into a record (the body of ``save``)."""
+    def make_record(self, keys: Any, values: Any, packed: bool = False,
+                    position_start: int = 0) -> BlockRecord:
+        """Quantize one layer block into a record (the body of ``save``);
+        ``position_start`` is the block's first token position (the RoPE
+        zero point of ``bias`` keys depends on it)."""
         k, v = self._host_f32(keys), self._host_f32(values)
         if k.shape != v.shape:
             raise ValueError(f"keys {k.shape} and values {v.shape} differ in shape")
         k4, v4 = self._as_bhsd(k), self._as_bhsd(v)
         d, h = int(k4.shape[-1]), int(k4.shape[1])
         kw = {"packed": True} if packed else {}
-        return BlockRecord(key_payload=self._quantizer("key", d, h).compress(k4, **kw),
+        kkw = dict(kw, position_start=int(position_start)) if position_start else kw
+        return BlockRecord(key_payload=self._quantizer("key", d, h).compress(k4, **kkw),
                            value_payload=self._quantizer("value", d, h).compress(v4, **kw),
                            shape=tuple(int(s) for s in k.shape), dtype="float32",
                            num_tokens=int(k4.shape[-2]), head_dim=d, n_heads=h)
@@ -164,7 +168,8 @@ class TurboQuantBlockStore:
         L, G = int(k4.shape[2]), int(group_tokens)
         ng = n_groups_for(L, int(hot_window))
         recs = {self._group_name(layer_name, g): self.make_record(
-                    k4[:, :, g * G:(g + 1) * G], v4[:, :, g * G:(g + 1) * G], packed=True)
+                    k4[:, :, g * G:(g + 1) * G], v4[:, :, g * G:(g + 1) * G], packed=True,
+                    position_start=g * G)
                 for g in range(ng)}
         if L > ng * G:
             hk = np.ascontiguousarray(k4[:, :, ng * G:], dtype=np.float16)
@@ -185,7 +190,8 @@ class TurboQuantBlockStore:
         dequantize / re-encode), the hot window as the fp16 tokens it held.
         Returns the tokens restored, 0 when nothing is stored (a miss).
         Raises ``ValueError`` when the records are not in the pool's format
-        (key grid, zero point, value width, rotation, group size)."""
+        (key grid, zero point and, for sparse/bias zero points, rope_theta and
+        group positions, value width, rotation, group size)."""
         import torch
 
         groups = []
@@ -216,6 +222,18 @@ class TurboQuantBlockStore:
             zp = "calibrated" if uniform else getattr(kp, "zp_mode", "calibrated")
             if zp != pool.zero_point:
                 raise ValueError(f"stored key zero point {zp!r}, the pool's {pool.zero_point!r}")
+            if zp != "calibrated":
+                # the zero point of a sparse/bias group is a function of its
+                # rope_theta and first position (per_channel_kv.py:234-267):
+                # the pool rebuilds it from its own, so both must match
+                theta = getattr(kp, "rope_theta", None)
+                if theta is None or float(theta) != float(pool.rope_theta):
+                    raise ValueError(f"stored keys use rope_theta={theta}, the pool's "
+                                     f"{pool.rope_theta}")
+                start = int(getattr(kp, "position_start", 0))
+                if start != len(items) * G:
+                    raise ValueError(f"stored group {len(items)} starts at position {start}, "
+                                     f"not {len(items) * G}")
             if uniform:
                 scale, mean = np.asarray(kp.scale)[0, :, 0, :], np.asarray(kp.zero)[0, :, 0, :]
             else:

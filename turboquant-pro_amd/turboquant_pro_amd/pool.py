@@ -167,6 +167,9 @@ class TQKVPool:
         self._overflow = torch.zeros(1, dtype=i32, device=dev)
         # (event, pinned flag word) of appends whose encode flags are not read yet
         self._pending = []
+        # the first flagged encode error: sticky until reset(), so every later
+        # call that reads the cache raises it, not only the first
+        self._error = None
         self._ws = None
 
     # ------------------------------------------------------------------ #
@@ -196,8 +199,10 @@ class TQKVPool:
         return self.lengths[b] - self.n_groups(b) * self.group_tokens
 
     def reset(self) -> None:
-        # the cache's contents go, and with them any flags still unread
+        # the cache's contents go, and with them any flags still unread and
+        # any error they raised
         self._pending = []
+        self._error = None
         self.lengths = [0] * self.max_batch
         self.seq_lens.zero_()
 
@@ -207,8 +212,17 @@ class TQKVPool:
         ``append`` copies the flags to pinned host memory without waiting, so
         that consecutive appends keep the GPU busy; they are read here: by the
         next append (flags already arrived), and with ``wait`` by every call
-        that reads the cache (decode, export, dequant, growth).  ``reset``
-        drops unread flags with the contents they describe."""
+        that reads the cache (decode, export, dequant, growth).  An error is
+        sticky: once flagged, every later check raises it again, because the
+        codes that caused it stay in the pool; ``reset`` clears the contents
+        and the error.  Under HIP graph capture a host wait is impossible, so
+        a capture with flags still unread raises instead of waiting (call
+        ``check()`` before capturing)."""
+        if self._error is not None:
+            raise self._error[0](self._error[1])
+        if self._pending and wait and _torch().cuda.is_current_stream_capturing():
+            raise RuntimeError("TQKVPool: encode flags of earlier appends are unread; call "
+                               "pool.check() before capturing a decode in a HIP graph")
         keep = []
         for ev, flag in self._pending:
             if not wait and not ev.query():
@@ -218,12 +232,14 @@ class TQKVPool:
             ovf = int(flag[0])
             if ovf & 2:
                 self._pending = []
-                raise ValueError("a value vector's norm exceeds 16376, the largest the gfx950 decode "
-                                 "carries (softmax weight <= 4 times the norm in fp16)")
-            if ovf & 1:
+                self._error = (ValueError, "a value vector's norm exceeds 16376, the largest the "
+                               "gfx950 decode carries (softmax weight <= 4 times the norm in fp16)")
+            elif ovf & 1:
                 self._pending = []
-                raise RuntimeError("outlier side-list exceeded outlier_cap for a group; "
-                                   "rebuild the pool with a larger outlier_cap")
+                self._error = (RuntimeError, "outlier side-list exceeded outlier_cap for a group; "
+                               "rebuild the pool with a larger outlier_cap")
+            if self._error is not None:
+                raise self._error[0](self._error[1])
         self._pending = keep
 
     def grown(self, max_seq_len: int) -> "TQKVPool":
