@@ -360,15 +360,17 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
 //         A = NF4 level of the key code as fp16 hi + lo (two MFMAs),
 //         B = q * nf4_scale as fp16 hi (cols 0..GQ-1) and lo (cols GQ..2GQ-1);
 //         col h + col h+GQ is the full-precision score of query head h.
-//   PV    O[row][ch] += P[row][token] * V[token][ch]
-//         P = softmax weight * value norm, hi rows 0..GQ-1, lo rows GQ..2GQ-1,
-//         V = value centroid as fp16 hi + lo (two MFMAs).
+//   PV    O[row][ch] += P[row][token] * V[token][ch]   (one MFMA per 32 tokens)
+//         P = softmax weight * value norm as fp16 hi (rows 0..7) or the fp16
+//         residual (rows 8..15) of head row & (GQ - 1),
+//         V = value centroid in fp16 (its rounding, <= 2^-12 relative, is
+//         far inside the output tolerance; the weights need both halves).
 // The QK^T accumulator layout (lane 16*lg + col holds tokens 4lg..4lg+3 of a
 // tile) is the PV A-operand layout, so scores stay in registers; only blocks
 // that hold outliers round-trip through a per-wave LDS block for the sparse
-// q_j * (val - dense) corrections.  Key bytes and value fields become fp16
-// hi/lo operand pairs through a bank-replicated LDS table (one copy per lane
-// of a 16-lane LDS pass).  The next block's loads are issued before the
+// q_j * (val - dense) corrections.  Key bytes become fp16 hi/lo operand pairs
+// through a bank-replicated LDS table, value codes become fp16 centroids four
+// tokens per lookup (LutGeom).  The next blocks' loads are issued before the
 // current block is computed.
 // ---------------------------------------------------------------------------
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
@@ -398,31 +400,41 @@ constexpr int kMaxGPS = 64;      // groups per cold split of the MFMA kernel (me
 constexpr int kMetaInts = 32;    // per group: 16 tile rows, 8 outlier bounds, slot*Hkv+h
 constexpr int kLutEntry = 256;   // bytes per table entry
 
-// Code tables in LDS.  Every entry holds one 8-byte {hi pair, lo pair} copy
-// per lane of an LDS pass so that random lookups never share a bank:
-//   2-bit values: value table [16 entries x 32 copies] at 0, key table
-//                 [256 entries x 32 copies] after it (68 KiB);
-//   3-bit values: value table [64 entries x 32 copies] at 0, key table
-//                 [256 entries x 32 copies] at kKeyBase3 (80 KiB);
-//   4-bit values: 256 entries x (16 key copies | 16 value copies) (64 KiB).
-// LDS code tables: entry e holds {fp16 hi pair, fp16 lo pair} (8 bytes) of
-// its two levels in kCopies bank-spread copies (copy c at byte 8c of the
-// entry's 256-byte row).  Key entries: 256 bytes of 4-bit codes, or the
-// 2^(2kb) pair fields of 3-/2-bit codes; value entries: the 2^(2vb) fields.
-// With 4-bit keys and 4-bit values (256 entries each) both share the rows,
-// 16 copies each; otherwise the value rows come first, then the key rows.
-template <int KB, int VB>
+// Code tables in LDS.
+// Key table: entry e (a code byte of 4-bit keys, the 2^(2kb) pair fields of
+// 3-/2-bit keys, value-code pairs for PolarQuant keys) holds {fp16 hi pair,
+// fp16 lo pair} (8 bytes) of its two levels in kKeyCopies bank-spread copies:
+// copy c at byte 8c of the entry's 256-byte row, so the bank of a lookup
+// depends only on the lane's copy and random entries never share a bank.
+// Value table: single fp16 centroids (the PV weights carry the fp16 hi/lo
+// split instead), four tokens of one channel per lookup where possible:
+//   3-bit values: the 12-bit field of four codes -> their four centroids
+//     (8 bytes), 4096 entries, one copy (32 KiB) at offset 0; with 8 query
+//     heads per kv head (whose outlier staging needs the LDS) the 6-bit
+//     field of two codes -> two centroids (4 bytes) in 64 rows of 256 bytes;
+//   2-bit values: a code byte (four codes) -> four centroids (8 bytes);
+//   4-bit values: a code byte (two codes) -> two centroids (4 bytes);
+//   byte tables take 256-byte rows like the key table.  With 4-bit keys the
+//   key and value entries of byte e share row e (keys in its first 128
+//   bytes, 16 copies; values in the second 128); otherwise a 2-/4-bit value
+//   table fills its own 64 KiB of rows at offset 0.  The key rows follow
+//   the value table.
+template <int KB, int VB, int GQ>
 struct LutGeom {
   static constexpr int kKeyEntries = KB == 4 ? 256 : 1 << (2 * KB);
-  static constexpr int kValEntries = 1 << (2 * VB);
-  static constexpr bool kShared = KB == 4 && VB == 4;
-  static constexpr int kCopies = kShared ? 16 : 32;
+  static constexpr bool kQuad12 = VB == 3 && GQ <= 4;
+  static constexpr bool kPair6 = VB == 3 && GQ > 4;
+  static constexpr bool kShared = KB == 4 && VB != 3;
+  static constexpr int kKeyCopies = kShared ? 16 : 32;
+  static constexpr int kValEntryBytes = VB == 4 || kPair6 ? 4 : 8;
+  static constexpr int kValCopies = (kShared ? 128 : 256) / kValEntryBytes;
+  static constexpr int kValBytes = kQuad12 ? 4096 * 8 : kPair6 ? 64 * 256 : (kShared ? 0 : 256 * 256);
+  static constexpr uint32_t kKeyBase = kShared ? 0u : (uint32_t)kValBytes;
+  static constexpr uint32_t kValOff = kShared ? 128u : 0u;  // value copy base inside a byte row
+  static constexpr int kTableBytes = (int)kKeyBase + (kShared ? 256 : kKeyEntries) * kLutEntry;
   // at least 64 KiB: after the stream the area holds the waves' coded states
   // (8 x GQ x (D + 2) floats) and then Pi (D x D floats) for the merge
-  static constexpr int kTableBytes = kShared ? 256 * 256 : (kKeyEntries + kValEntries) * 256;
   static constexpr int kBytes = kTableBytes > 65536 ? kTableBytes : 65536;
-  static constexpr uint32_t kKeyBase = kShared ? 0u : (uint32_t)kValEntries * 256u;
-  static constexpr uint32_t kValOff = kShared ? 128u : 0u;  // value copy base inside a row
 };
 
 __device__ __forceinline__ uint2 split_pair(float x0, float x1) {
@@ -689,6 +701,22 @@ __device__ __forceinline__ H8 dup_quad(float x0, float x1, float x2, float x3, f
   return r;
 }
 
+// Eight floats as fp16 (lo_sel = 0) or as the fp16 residual x - fp16(x)
+// (lo_sel = 1), in pairs: the PV weight operand.
+__device__ __forceinline__ H8 split8(float x0, float x1, float x2, float x3, float x4, float x5,
+                                     float x6, float x7, float lo_sel) {
+  auto pair = [&](float a, float b) {
+    const uint32_t h = pk_f16(a, b);
+    return pk_f16(fmaf(-lo_sel, lo_f16(h), a), fmaf(-lo_sel, hi_f16(h), b));
+  };
+  H8 r;
+  r.u[0] = pair(x0, x1);
+  r.u[1] = pair(x2, x3);
+  r.u[2] = pair(x4, x5);
+  r.u[3] = pair(x6, x7);
+  return r;
+}
+
 // PK: PolarQuant keys (key_grid 2, KB == VB): the key table holds centroids,
 // the QK^T weights are the rotated query, and every score is scaled by its
 // token's key norm
@@ -753,10 +781,10 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   // scores in the log2 domain: q * sm_scale * log2(e), softmax with exp2
   const float qscale = d.sm_scale * 1.4426950408889634f;
 
-  __shared__ __align__(16) uint8_t lut[LutGeom<KB, VB>::kBytes];
+  __shared__ __align__(16) uint8_t lut[LutGeom<KB, VB, GQ>::kBytes];
   // the area's later uses: the coded wave states of the fold, Pi in the merge
-  static_assert(LutGeom<KB, VB>::kBytes >= (int)sizeof(float) * kMWaves * GQ * (D + 2), "fold area");
-  static_assert(LutGeom<KB, VB>::kBytes >= (int)sizeof(float) * D * D, "Pi area");
+  static_assert(LutGeom<KB, VB, GQ>::kBytes >= (int)sizeof(float) * kMWaves * GQ * (D + 2), "fold area");
+  static_assert(LutGeom<KB, VB, GQ>::kBytes >= (int)sizeof(float) * D * D, "Pi area");
   __shared__ __align__(16) uint32_t qq_s[D][GQ];        // raw fp16 q twice {q, q}: [channel][head]
   __shared__ __align__(16) uint16_t qf_s[GQ][D];        // raw fp16 q, head-major (hot-window operand)
   // scaled q, head-major; rows padded by 4 banks so that the head rows read by
@@ -832,26 +860,37 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     __syncthreads();
   }
   {
-    // unit u (8 bytes): key part first (entry u / copies, copy u % copies), then values;
-    // consecutive lanes write consecutive units; levels come from LDS, so the
-    // fill issues no memory loads
-    using LG = LutGeom<KB, VB>;
-    constexpr int NC = LG::kCopies;
+    // key unit u (8 bytes): entry u / copies, copy u % copies; consecutive
+    // lanes write consecutive units; levels come from LDS, so the fill issues
+    // no memory loads
+    using LG = LutGeom<KB, VB, GQ>;
+    constexpr int NC = LG::kKeyCopies;
     constexpr int NK = LG::kKeyEntries;
-    constexpr int NV = LG::kValEntries;
-    for (int u = tid; u < NK * NC + NV * NC; u += kMThreads) {
-      uint2 val;
-      uint32_t off;
-      if (u < NK * NC) {
-        const uint32_t e = (uint32_t)(u / NC);
-        val = split_pair(lvl_s[k_code_even(e, KB)], lvl_s[k_code_odd(e, KB)]);
-        off = LG::kKeyBase + (uint32_t)e * kLutEntry + (uint32_t)(u % NC) * 8u;
-      } else {
-        const int v = u - NK * NC, e = v / NC, m = (1 << VB) - 1;
-        val = split_pair(lvl_s[16 + (e & m)], lvl_s[16 + (e >> VB)]);
-        off = (uint32_t)e * kLutEntry + LG::kValOff + (uint32_t)(v % NC) * 8u;
+    for (int u = tid; u < NK * NC; u += kMThreads) {
+      const uint32_t e = (uint32_t)(u / NC);
+      *reinterpret_cast<uint2*>(lut + LG::kKeyBase + e * kLutEntry + (uint32_t)(u % NC) * 8u) =
+          split_pair(lvl_s[k_code_even(e, KB)], lvl_s[k_code_odd(e, KB)]);
+    }
+    const float* cv = &lvl_s[16];  // value centroids
+    if constexpr (LG::kQuad12) {
+      // entry e: centroids of codes e & 7, e >> 3 & 7, e >> 6 & 7, e >> 9
+      for (uint32_t e = tid; e < 4096u; e += kMThreads)
+        *reinterpret_cast<uint2*>(lut + 8u * e) =
+            make_uint2(pk_f16(cv[e & 7u], cv[(e >> 3) & 7u]), pk_f16(cv[(e >> 6) & 7u], cv[e >> 9]));
+    } else {
+      constexpr int NVC = LG::kValCopies, EB = LG::kValEntryBytes;
+      constexpr int NE = LG::kPair6 ? 64 : 256;
+      for (int u = tid; u < NE * NVC; u += kMThreads) {
+        const uint32_t e = (uint32_t)(u / NVC), off = e * kLutEntry + LG::kValOff + (uint32_t)(u % NVC) * EB;
+        if constexpr (LG::kPair6) {
+          *reinterpret_cast<uint32_t*>(lut + off) = pk_f16(cv[e & 7u], cv[e >> 3]);
+        } else if constexpr (VB == 4) {
+          *reinterpret_cast<uint32_t*>(lut + off) = pk_f16(cv[e & 15u], cv[e >> 4]);
+        } else {
+          *reinterpret_cast<uint2*>(lut + off) =
+              make_uint2(pk_f16(cv[e & 3u], cv[(e >> 2) & 3u]), pk_f16(cv[(e >> 4) & 3u], cv[e >> 6]));
+        }
       }
-      *reinterpret_cast<uint2*>(lut + off) = val;
     }
   }
   __syncthreads();
@@ -868,10 +907,12 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   reset_state(st);
 
   {
-    constexpr int NC = LutGeom<KB, VB>::kCopies;
+    constexpr int NC = LutGeom<KB, VB, GQ>::kKeyCopies;
     const uint32_t koff = (uint32_t)(lane % NC) * 8u;
-    const uint32_t voff = LutGeom<KB, VB>::kValOff + (uint32_t)(lane % NC) * 8u;
-    const uint8_t* __restrict__ klut = lut + LutGeom<KB, VB>::kKeyBase;
+    // (byte value tables) this lane's value copy inside a row
+    const uint32_t voff = LutGeom<KB, VB, GQ>::kValOff +
+                          (uint32_t)(lane % LutGeom<KB, VB, GQ>::kValCopies) * LutGeom<KB, VB, GQ>::kValEntryBytes;
+    const uint8_t* __restrict__ klut = lut + LutGeom<KB, VB, GQ>::kKeyBase;
     const int cap = d.outlier_cap;
     // outlier entries are read at clamped indices (never past the group's list)
     const uint32_t* __restrict__ oent_all = cap > 0 ? a.p.oent : reinterpret_cast<const uint32_t*>(a.p.ocount);
@@ -1078,35 +1119,61 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         r.u[3] = t1.y;
         return r;
       };
-      // B operand of PV MFMA (nt, tile) from value unit un: fields 2nt (tokens
-      // 0, 1 of the unit, channel 8c + nt) and 2nt + 1 (tokens 2, 3), each a
-      // table row {fp16 hi pair, fp16 lo pair}: k-slots [hi t0, hi t1, lo t0,
-      // lo t1, hi t2, hi t3, lo t2, lo t3], matching the weight quad.
-      auto val_quad = [&](const uint4& un, int nt) {
-        uint32_t f0, f1;
-        if constexpr (VB == 2) {
-          // 4-bit fields 2nt, 2nt + 1 at bits 8nt, 8nt + 4 of the 64-bit unit
-          const uint32_t word = nt < 4 ? un.x : un.y;
-          f0 = (word >> (8 * (nt & 3))) & 15u;
-          f1 = (word >> (8 * (nt & 3) + 4)) & 15u;
-        } else if constexpr (VB == 3) {
-          switch (nt) {
-#define TQK_V3(NT) case NT: f0 = v3_field<2 * NT>(un); f1 = v3_field<2 * NT + 1>(un); break;
-            TQK_V3(0) TQK_V3(1) TQK_V3(2) TQK_V3(3) TQK_V3(4) TQK_V3(5) TQK_V3(6) TQK_V3(7)
-#undef TQK_V3
-          }
-        } else {
-          const uint32_t word = (nt >> 1) == 0 ? un.x : (nt >> 1) == 1 ? un.y : (nt >> 1) == 2 ? un.z : un.w;
-          f0 = (word >> (16 * (nt & 1))) & 0xFFu;
-          f1 = (word >> (16 * (nt & 1) + 8)) & 0xFFu;
-        }
-        const uint2 r0 = *reinterpret_cast<const uint2*>(lut + ((f0 << 8) | voff));
-        const uint2 r1 = *reinterpret_cast<const uint2*>(lut + ((f1 << 8) | voff));
+      // B operand of PV MFMA nt: single fp16 centroids of tokens 0..3 of the
+      // lane's value unit in tile A (channel 8n + nt), then of tile B:
+      // k-slots [A t0 t1 t2 t3, B t0 t1 t2 t3], matching the weight operand.
+      auto val_op = [&](const uint4& uA, const uint4& uB, auto ntc) {
+        constexpr int nt = decltype(ntc)::value;
         H8 r;
-        r.u[0] = r0.x;
-        r.u[1] = r0.y;
-        r.u[2] = r1.x;
-        r.u[3] = r1.y;
+        if constexpr (LutGeom<KB, VB, GQ>::kPair6) {
+          // 6-bit fields 2nt (tokens 0, 1) and 2nt + 1 (tokens 2, 3)
+          auto lk = [&](uint32_t f) { return *reinterpret_cast<const uint32_t*>(lut + ((f << 8) | voff)); };
+          r.u[0] = lk(v3_field<2 * nt>(uA));
+          r.u[1] = lk(v3_field<2 * nt + 1>(uA));
+          r.u[2] = lk(v3_field<2 * nt>(uB));
+          r.u[3] = lk(v3_field<2 * nt + 1>(uB));
+        } else if constexpr (VB == 3) {
+          // the 12-bit field nt (bits 12nt..12nt+11 of the 96-bit unit) is its
+          // own table index: the address is the field times 8, taken with one
+          // funnel shift that leaves it at bit 3 and one mask (the table sits
+          // at LDS offset 0)
+          constexpr int o = 12 * nt, w = o / 32, sh = o % 32;
+          auto addr = [&](const uint4& u) -> uint32_t {
+            if constexpr (sh == 0) {
+              return (u4_word<w>(u) << 3) & 0x7FF8u;
+            } else if constexpr (sh + 12 <= 32) {
+              return (u4_word<w>(u) >> (sh - 3)) & 0x7FF8u;
+            } else {
+              return __builtin_amdgcn_alignbit(u4_word<w + 1>(u), u4_word<w>(u), sh - 3) & 0x7FF8u;
+            }
+          };
+          const uint2 x = *reinterpret_cast<const uint2*>(lut + addr(uA));
+          const uint2 y = *reinterpret_cast<const uint2*>(lut + addr(uB));
+          r.u[0] = x.x;
+          r.u[1] = x.y;
+          r.u[2] = y.x;
+          r.u[3] = y.y;
+        } else if constexpr (VB == 2) {
+          // code byte nt (four 2-bit codes) of the 8-byte unit
+          const uint32_t sel = 0x0C0C0000u | ((4u + (uint32_t)(nt & 3)) << 8);
+          const uint32_t ax = __builtin_amdgcn_perm(nt < 4 ? uA.x : uA.y, voff, sel);
+          const uint32_t ay = __builtin_amdgcn_perm(nt < 4 ? uB.x : uB.y, voff, sel);
+          const uint2 x = *reinterpret_cast<const uint2*>(lut + ax);
+          const uint2 y = *reinterpret_cast<const uint2*>(lut + ay);
+          r.u[0] = x.x;
+          r.u[1] = x.y;
+          r.u[2] = y.x;
+          r.u[3] = y.y;
+        } else {
+          // code bytes 2nt (tokens 0, 1) and 2nt + 1 (tokens 2, 3) of the 16-byte unit
+          const uint32_t s0 = 0x0C0C0000u | ((4u + 2u * (uint32_t)(nt & 1)) << 8);
+          const uint32_t s1 = 0x0C0C0000u | ((5u + 2u * (uint32_t)(nt & 1)) << 8);
+          const uint32_t wa = u4_word<nt / 2>(uA), wb = u4_word<nt / 2>(uB);
+          r.u[0] = *reinterpret_cast<const uint32_t*>(lut + __builtin_amdgcn_perm(wa, voff, s0));
+          r.u[1] = *reinterpret_cast<const uint32_t*>(lut + __builtin_amdgcn_perm(wa, voff, s1));
+          r.u[2] = *reinterpret_cast<const uint32_t*>(lut + __builtin_amdgcn_perm(wb, voff, s0));
+          r.u[3] = *reinterpret_cast<const uint32_t*>(lut + __builtin_amdgcn_perm(wb, voff, s1));
+        }
         return r;
       };
       // ---- sparse outliers, folded into the QK^T accumulators:
@@ -1229,11 +1296,18 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
 #pragma unroll
         for (int m = 0; m < 8; ++m) C = __builtin_amdgcn_mfma_f32_16x16x32_f16(x[m].h, Bw[m].h, C, 0, 0, 0);
       };
-      auto val_tile = [&](const uint4& u, H8 (&v)[8]) {
-#pragma unroll
-        for (int nt = 0; nt < 8; ++nt) v[nt] = val_quad(u, nt);
+      auto val_block = [&](const uint4& uA, const uint4& uB, H8 (&v)[8]) {
+        v[0] = val_op(uA, uB, IntC<0>{});
+        v[1] = val_op(uA, uB, IntC<1>{});
+        v[2] = val_op(uA, uB, IntC<2>{});
+        v[3] = val_op(uA, uB, IntC<3>{});
+        v[4] = val_op(uA, uB, IntC<4>{});
+        v[5] = val_op(uA, uB, IntC<5>{});
+        v[6] = val_op(uA, uB, IntC<6>{});
+        v[7] = val_op(uA, uB, IntC<7>{});
       };
-      auto pv_tile = [&](const H8& pw, const H8 (&v)[8]) {
+      // PV over the whole 32-token block: k = the lane group's 8 tokens
+      auto pv_block = [&](const H8& pw, const H8 (&v)[8]) {
 #pragma unroll
         for (int nt = 0; nt < 8; ++nt) st.O[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pw.h, v[nt].h, st.O[nt], 0, 0, 0);
       };
@@ -1282,20 +1356,21 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         }
         float p[8];
         softmax_block<GQ>(st, sc, p, lg);
-        const H8 pa = dup_quad(p[0] * row_bcast<0>(cur.nv), p[1] * row_bcast<1>(cur.nv),
-                               p[2] * row_bcast<2>(cur.nv), p[3] * row_bcast<3>(cur.nv), lo_sel);
-        const H8 pb = dup_quad(p[4] * row_bcast<4>(cur.nv), p[5] * row_bcast<5>(cur.nv),
-                               p[6] * row_bcast<6>(cur.nv), p[7] * row_bcast<7>(cur.nv), lo_sel);
-        H8 va[8], xa[8], vb[8], xb[8];
+        // A operand of PV: weight times value norm of the lane's 8 tokens
+        // (tile A 4lg..4lg+3, tile B 4lg..4lg+3) for head hq, fp16 hi in rows
+        // c < 8, the fp16 residual in rows c >= 8
+        const H8 pw = split8(p[0] * row_bcast<0>(cur.nv), p[1] * row_bcast<1>(cur.nv),
+                             p[2] * row_bcast<2>(cur.nv), p[3] * row_bcast<3>(cur.nv),
+                             p[4] * row_bcast<4>(cur.nv), p[5] * row_bcast<5>(cur.nv),
+                             p[6] * row_bcast<6>(cur.nv), p[7] * row_bcast<7>(cur.nv), lo_sel);
+        H8 vv[8], xa[8], xb[8];
         // (no scheduling fences between the phases: the compiler's own
         // interleaving measured faster and needs fewer registers)
-        val_tile(cur.uA, va);
+        val_block(cur.uA, cur.uB, vv);
         key_tile(nx1.kA, xa);
-        pv_tile(pa, va);
-        val_tile(cur.uB, vb);
+        pv_block(pw, vv);
         qk_tile(xa, CAn);
         key_tile(nx1.kB, xb);
-        pv_tile(pb, vb);
         qk_tile(xb, CBn);
         wave_sync();
         apply_block(nx1, blk1, gslot1, CAn, CBn);
