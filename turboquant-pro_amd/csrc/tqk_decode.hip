@@ -510,9 +510,6 @@ struct ColdBlock {
   uint4 uA, uB;
   float nv;        // value norm of token 16 * ((c >> 2) & 1) + 4lg + (c & 3)
   float kn;        // ... and its key norm (PolarQuant keys only)
-  uint2 ent;       // outlier entries 2*lane, 2*lane + 1 of the block
-  int e0, ne;      // the block's outliers are entries [e0, e0 + ne) of its group
-  uint32_t obase;  // slot * Hkv + h of the block's group
 };
 
 // Per-wave online-softmax state for query head (c & (GQ - 1)) and the PV accumulators.
@@ -643,35 +640,9 @@ __device__ __forceinline__ float row_bcast(float x) {
   return bitsf((uint32_t)__builtin_amdgcn_update_dpp(0, (int)fbits(x), 0x150 + I, 0xF, 0xF, false));
 }
 
-// Outlier A operand of one tile row: dword i = dq[i] when byte i of tw
-// (the token of slot i) equals row, else 0.  Four byte compares into four
-// SGPR pairs, then four selects, each four instructions after its compare:
-// independent operations with no dependency chain through VCC and no DPP.
-__device__ __forceinline__ void onehot_operand(uint32_t tw, uint32_t row, const uint4& dq,
-                                               uint32_t (&o)[4]) {
-  uint64_t m0, m1, m2, m3;
-  asm("v_cmp_eq_u32_sdwa %4, %8, %9 src0_sel:BYTE_0 src1_sel:DWORD\n\t"
-      "v_cmp_eq_u32_sdwa %5, %8, %9 src0_sel:BYTE_1 src1_sel:DWORD\n\t"
-      "v_cmp_eq_u32_sdwa %6, %8, %9 src0_sel:BYTE_2 src1_sel:DWORD\n\t"
-      "v_cmp_eq_u32_sdwa %7, %8, %9 src0_sel:BYTE_3 src1_sel:DWORD\n\t"
-      "v_cndmask_b32_e64 %0, 0, %10, %4\n\t"
-      "v_cndmask_b32_e64 %1, 0, %11, %5\n\t"
-      "v_cndmask_b32_e64 %2, 0, %12, %6\n\t"
-      "v_cndmask_b32_e64 %3, 0, %13, %7"
-      : "=&v"(o[0]), "=&v"(o[1]), "=&v"(o[2]), "=&v"(o[3]), "=&s"(m0), "=&s"(m1), "=&s"(m2),
-        "=&s"(m3)
-      : "v"(tw), "v"(row), "v"(dq.x), "v"(dq.y), "v"(dq.z), "v"(dq.w));
-}
 template <int K>
 struct IntC {
   static constexpr int value = K;
-};
-
-// Outlier entries of one block as staged for the apply: the block's entry
-// count (<= 128 per pass) and how many fall in tile A (the tokens, operand
-// values and q pairs are in LDS).
-struct OutEntries {
-  int cnt, nA;
 };
 
 // fp16 pair (RNE) of two floats in one dword, and the fp32 value of a half
@@ -716,6 +687,12 @@ __device__ __forceinline__ H8 split8(float x0, float x1, float x2, float x3, flo
   r.u[3] = pair(x6, x7);
   return r;
 }
+
+// Tokens per outlier-correction segment: a whole 256-token group, or half of
+// one with 8 query heads per kv head (so that the per-wave buffers of
+// GQ x kSegTokens floats fit the LDS beside the code tables).
+template <int GQ>
+constexpr int kSegTokens = GQ > 4 ? 128 : 256;
 
 // PK: PolarQuant keys (key_grid 2, KB == VB): the key table holds centroids,
 // the QK^T weights are the rotated query, and every score is scaled by its
@@ -785,21 +762,23 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   // the area's later uses: the coded wave states of the fold, Pi in the merge
   static_assert(LutGeom<KB, VB, GQ>::kBytes >= (int)sizeof(float) * kMWaves * GQ * (D + 2), "fold area");
   static_assert(LutGeom<KB, VB, GQ>::kBytes >= (int)sizeof(float) * D * D, "Pi area");
-  __shared__ __align__(16) uint32_t qq_s[D][GQ];        // raw fp16 q twice {q, q}: [channel][head]
+  // raw fp16 q, channel-major: the outlier corrections' gathers
+  __shared__ __align__(16) uint16_t qc_s[D][GQ];
   __shared__ __align__(16) uint16_t qf_s[GQ][D];        // raw fp16 q, head-major (hot-window operand)
   // scaled q, head-major; rows padded by 4 banks so that the head rows read by
   // one lane group fall in different banks
   __shared__ __align__(16) float q_h_s[GQ][D + 4];
-  // (nf4_scale[128], nf4_mean[128]) of a wave's current and next group
-  __shared__ __align__(16) float gsm_s[kMWaves][2][2 * D];
-  // outlier correction B operand of the block computed next: per head, each
-  // entry's raw fp16 q twice (rows 4 banks apart)
-  __shared__ __align__(16) uint32_t oq_s[kMWaves][GQ][132];
-  // ... each entry's token in the block (255 = none): byte 4k + i of row
-  // lg is slot i of lane group lg in 16-entry chunk k
-  __shared__ __align__(16) uint8_t otb_s[kMWaves][4][32];
-  // ... and each entry's A-operand value, fp16 {hi, lo} of (val - mean) * s / 2
-  __shared__ __align__(16) uint32_t od_s[kMWaves][128];
+  // (nf4_scale[128], nf4_mean[128]) of the group a wave starts next
+  __shared__ __align__(16) float gsm_s[kMWaves][2 * D];
+  // per wave: the QK^T initial value of every token of its current group
+  // segment (kSegTokens tokens) and head, mean bias plus outlier corrections
+  // ([head][token]); each row ends in 64 per-lane slots that take the
+  // corrections' unused stores (the pass stores every step, no branch)
+  constexpr int kCT = kSegTokens<GQ>;
+  constexpr int kRow = kCT + 64;
+  __shared__ __align__(16) float corr_s[kMWaves][GQ][kRow];
+  __shared__ __align__(16) float zero4_s[4];             // the lo columns' initial value
+  if (tid < 4) zero4_s[tid] = 0.f;
   // NF4 levels [0, 16) and value centroids [16, 16 + 2^vb), for the table fill
   __shared__ float lvl_s[32];
   if (tid < 16) lvl_s[tid] = PK ? (tid < (1 << KB) ? a.p.vcent[tid] : 0.f) : key_level(a.d.key_grid, tid);
@@ -811,6 +790,10 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   {
     const int gbeg = split * a.groups_per_split;
     const int gcnt = max(0, min(ng, gbeg + a.groups_per_split) - gbeg);
+    // rows past the split's groups are zero (slot 0 of head 0: a valid
+    // address, although nothing reads them)
+    for (int x = gcnt * kMetaInts + tid; x < kMaxGPS * kMetaInts; x += kMThreads)
+      meta_s[x / kMetaInts][x % kMetaInts] = 0;
     for (int x = tid; x < gcnt * kMetaInts; x += kMThreads) {
       const int jg = x / kMetaInts, f = x % kMetaInts, g = gbeg + jg;
       const int slot = a.p.group_table[(size_t)b * d.max_groups_per_seq + g];
@@ -835,7 +818,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   const int gq = Hq / Hkv;
   for (int i = tid; i < GQ * D; i += kMThreads) {
     const uint32_t qr = (i / D < gq) ? a.q[((size_t)b * Hq + h * gq + i / D) * D + i % D] : 0u;
-    qq_s[i % D][i / D] = qr | (qr << 16);
+    qc_s[i % D][i / D] = (uint16_t)qr;
     qf_s[i / D][i % D] = (uint16_t)qr;
     q_h_s[i / D][i % D] = h2f((uint16_t)qr) * qscale;
   }
@@ -914,9 +897,8 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
                           (uint32_t)(lane % LutGeom<KB, VB, GQ>::kValCopies) * LutGeom<KB, VB, GQ>::kValEntryBytes;
     const uint8_t* __restrict__ klut = lut + LutGeom<KB, VB, GQ>::kKeyBase;
     const int cap = d.outlier_cap;
-    // outlier entries are read at clamped indices (never past the group's list)
+    // the side-list base (a valid pointer even without a side-list)
     const uint32_t* __restrict__ oent_all = cap > 0 ? a.p.oent : reinterpret_cast<const uint32_t*>(a.p.ocount);
-    const int capm1 = cap > 0 ? cap - 1 : 0;
     // This wave streams T blocks, block after block: the split's groups wu,
     // wu + 8, ... whole (meta_s rows g0 + gstep * j), or, for splits of fewer
     // groups than waves, wave_blocks consecutive blocks of the split starting
@@ -945,10 +927,6 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     const uint32_t koffL = (uint32_t)c * KROW + (uint32_t)(KROW / 4) * (uint32_t)lg;
     const uint32_t uoffL = (uint32_t)(16 * lg + c) * UNIT;
     const int ntl = 4 * lg + (c & 3);  // token (of tile A if c & 4 == 0, else B) whose norm this lane reads
-    // outlier entries eidx, eidx + 1 of a block are this lane's: the four
-    // entries of lane group lg in 16-entry chunk k then sit in lanes 2k and
-    // 2k + 1 of the lane group's own row (DPP row broadcast reaches them)
-    const int eidx = 16 * (c >> 1) + 4 * lg + 2 * (c & 1);
     auto meta = [&](int j, int f) { return __builtin_amdgcn_readfirstlane(meta_s[g0 + gstep * j][f]); };
     // the metadata of the wave group being loaded (jl below), field f in lane
     // f: the block loads read it with v_readlane, with no LDS round trip per block
@@ -965,17 +943,14 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     const __amdgpu_buffer_rsrc_t rn = buf_rsrc(a.p.vnorm + (size_t)h * hrows, hrows * 4u);
     const __amdgpu_buffer_rsrc_t rkn = buf_rsrc(PK ? a.p.knorm + (size_t)h * hrows : a.p.vnorm, PK ? hrows * 4u : 0u);
 
-    // Every step issues the same loads (past the end: the last block again,
-    // already in L2), so the waits on the oldest buffer stay exact.
+    // Every step issues the same block loads (past the end: the last block
+    // again, already in L2), so the waits on the oldest buffer stay exact.
     int jl = 0, kbl = kb0, nl = 0;  // next block to load: wave group jl, block kbl, stream index nl
     load_meta(0);
     auto load_next = [&](ColdBlock<VB>& cb) {
       // rows of the two tiles in this head's region (wave-uniform: SGPR offsets)
       const uint32_t rowA = (uint32_t)meta_l(2 * kbl);
       const uint32_t rowB = (uint32_t)meta_l(2 * kbl + 1);
-      const uint32_t obase = (uint32_t)meta_l(16 + TQK_NOB);
-      const int e0 = kbl == 0 ? 0 : meta_l(16 + kbl - 1);
-      const int e1 = meta_l(16 + kbl);
       if constexpr (KB == 4) {
         const u32x4_t x = __builtin_amdgcn_raw_buffer_load_b128(rk, (int)koffL, (int)(rowA * KROW), 0);
         const u32x4_t y = __builtin_amdgcn_raw_buffer_load_b128(rk, (int)koffL, (int)(rowB * KROW), 0);
@@ -1015,16 +990,6 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       if constexpr (PK)
         cb.kn = bitsf(__builtin_amdgcn_raw_buffer_load_b32(
             rkn, (int)(4u * (((c & 4) ? rowB : rowA) + (uint32_t)ntl)), 0, 0));
-      // the group's side-list as its own buffer: reads past its end return 0,
-      // reads past e1 are masked where they are used (the outlier pass)
-      const __amdgpu_buffer_rsrc_t ro = buf_rsrc(oent_all + (size_t)obase * cap, 4u * (uint32_t)cap);
-      {
-        const u32x2_t x = __builtin_amdgcn_raw_buffer_load_b64(ro, 4 * eidx, 4 * e0, 0);
-        cb.ent = make_uint2(x.x, x.y);
-      }
-      cb.e0 = e0;
-      cb.ne = e1 - e0;
-      cb.obase = obase;
       if (nl + 1 < T) {
         ++nl;
         if (++kbl == nblk) {
@@ -1036,24 +1001,24 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     };
 
     // (nf4_scale, nf4_mean) of channels 2*lane, 2*lane + 1 of a wave group,
-    // staged through registers into LDS slot (group & 1): every step loads
-    // the stats of the group of the block it prefetches (before the block
-    // loads, unconditionally, so the loads are never sunk to their use) and
-    // the next step writes them, a step before that group can start.
+    // staged through registers into the wave's LDS slot: every step loads the
+    // stats of the group of the block it prefetches (before the block loads,
+    // unconditionally, so the loads are never sunk to their use) and the next
+    // step writes them, before that group can start.  One slot suffices: a
+    // group's stats are read only at its start (weights, bias, corrections),
+    // and a group's first block is computed a step after its stats arrive.
     float2 pend_s, pend_m;  // stats loaded by the previous step
-    int pend_slot = 0;
-    // (obase: slot * Hkv + h of wave group j)
-    auto load_group_stats = [&](int obase, int j) {
+    // (obase: slot * Hkv + h of the group)
+    auto load_group_stats = [&](int obase) {
       const size_t mb = (size_t)D * (uint32_t)obase;
       const u32x2_t x = __builtin_amdgcn_raw_buffer_load_b64(buf_rsrc(a.p.gscale + mb, 4u * D), 8 * lane, 0, 0);
       const u32x2_t y = __builtin_amdgcn_raw_buffer_load_b64(buf_rsrc(a.p.gmean + mb, 4u * D), 8 * lane, 0, 0);
       pend_s = make_float2(bitsf(x.x), bitsf(x.y));
       pend_m = make_float2(bitsf(y.x), bitsf(y.y));
-      pend_slot = j & 1;
     };
     auto store_group_stats = [&]() {
-      *reinterpret_cast<float2*>(&gsm_s[w][pend_slot][2 * lane]) = pend_s;
-      *reinterpret_cast<float2*>(&gsm_s[w][pend_slot][D + 2 * lane]) = pend_m;
+      *reinterpret_cast<float2*>(&gsm_s[w][2 * lane]) = pend_s;
+      *reinterpret_cast<float2*>(&gsm_s[w][D + 2 * lane]) = pend_m;
     };
     // QK^T: C[token][col] = sum_k A[token][k] * B[k][col] over k-slots that
     // pair each channel's fp16 hi and lo NF4 level with the same weight.
@@ -1062,13 +1027,14 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     // hi ch3, lo ch2, lo ch3] are two table rows read straight into the
     // operand, B = [w0 w1 w0 w1 w2 w3 w2 w3] with w = q * nf4_scale of the
     // column's head as fp16 hi (c < 8) or lo (c >= 8).  Column c plus column
-    // c ^ 8 is the fp32 score; the mean bias enters as the initial
-    // accumulator of the hi columns.
+    // c ^ 8 is the fp32 score.  The hi columns start from the group's per-token
+    // initial values (mean bias plus the token's outlier corrections, built
+    // once per group in corr_s); the lo columns start from zero.
     H8 Bw[8];
-    floatx4_t binit;
-    // Start of wave group j: weights and mean bias from slot j & 1.
-    auto begin_group = [&](int j) {
-      const float* gs = &gsm_s[w][j & 1][0];
+    float bias_h;  // q . mean of head hq (the hi columns' constant term)
+    // Start of wave group j: weights and mean bias from the wave's stats slot.
+    auto begin_group = [&]() {
+      const float* gs = &gsm_s[w][0];
       float biasp = 0.f;
 #pragma unroll
       for (int m = 0; m < 8; ++m) {
@@ -1079,8 +1045,186 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         biasp += q4.x * m4.x + q4.y * m4.y + q4.z * m4.z + q4.w * m4.w;
         Bw[m] = dup_quad(q4.x * s4.x, q4.y * s4.y, q4.z * s4.z, q4.w * s4.w, lo_sel);
       }
-      const float bv = is_hi ? colgroup_sum(biasp) : 0.f;
-      binit = floatx4_t{bv, bv, bv, bv};
+      bias_h = colgroup_sum(biasp);
+    };
+
+    // ---- sparse outliers, once per segment of kCT tokens of a group: the
+    // score of token t for head h gains q_h[j] * (val - mean_j) for every
+    // side-list entry (t, j, val) (the stored code of an outlier is the NF4
+    // zero level, so the dense pass gave exactly mean_j there, inside the
+    // bias).  The wave turns the segment's stretch of the token-sorted
+    // side-list into corr_s[w][h][t] = bias_h + the sum of token t's
+    // corrections (fp32), and each block's QK^T accumulators of the hi
+    // columns start from it.  Lane L takes E consecutive entries, E =
+    // ceil(n / 64): runs of one token inside a lane are summed in registers;
+    // a run that closes inside the lane and is not its first belongs to the
+    // lane alone (the list is sorted) and is written; the lane's first and
+    // last runs may continue in the neighbouring lanes and are added with LDS
+    // float atomics after the bias fill.  The first kPre entries of every
+    // lane arrive in registers a segment ahead.
+    constexpr int SB = kCT / 32;  // blocks per segment
+    constexpr int kPre = 12;
+    uint32_t gent[kPre];
+#pragma unroll
+    for (int k = 0; k < kPre; ++k) gent[k] = 0u;
+    int gent_lo = 0, gent_n = 0;  // the segment whose entries gent holds: first entry, count
+    float* const corr = &corr_s[w][0][0];
+    // entries [lo, hi) of wave group j's side-list cover segment sg
+    auto seg_range = [&](int j, int sg, int& lo, int& n) {
+      lo = sg == 0 ? 0 : meta(j, 16 + sg * SB - 1);
+      n = meta(j, 16 + min((sg + 1) * SB, nblk) - 1) - lo;
+    };
+    // the first kPre entries of every lane of [lo, lo + n) of the side-list
+    // of group obase; a false `real` makes it a zero-size buffer (the loads
+    // return zeros and touch no memory), so that every block load issues the
+    // same loads and the waits on them stay exact
+    auto load_entries = [&](int obase, int lo, int n, bool real) {
+      const int E = (n + 63) >> 6;
+      gent_lo = lo;
+      gent_n = real ? n : 0;
+      // the group's side-list as its own buffer: reads past its end return 0
+      const __amdgpu_buffer_rsrc_t ro = buf_rsrc(oent_all + (size_t)(uint32_t)obase * cap,
+                                                 real ? 4u * (uint32_t)cap : 0u);
+      const int off = 4 * (lo + lane * E);
+      const u32x4_t x0 = __builtin_amdgcn_raw_buffer_load_b128(ro, off, 0, 0);
+      const u32x4_t x1 = __builtin_amdgcn_raw_buffer_load_b128(ro, off, 16, 0);
+      const u32x4_t x2 = __builtin_amdgcn_raw_buffer_load_b128(ro, off, 32, 0);
+      gent[0] = x0.x; gent[1] = x0.y; gent[2] = x0.z; gent[3] = x0.w;
+      gent[4] = x1.x; gent[5] = x1.y; gent[6] = x1.z; gent[7] = x1.w;
+      gent[8] = x2.x; gent[9] = x2.y; gent[10] = x2.z; gent[11] = x2.w;
+    };
+    auto load_seg_entries = [&](int j, int sg) {
+      int lo, n;
+      seg_range(j, sg, lo, n);
+      load_entries(meta(j, 16 + TQK_NOB), lo, n, n > 0);
+    };
+    // with the loads of the block load_next fetches next (wave group jl,
+    // block kbl): its segment's entries when it starts one
+    auto load_block_entries = [&]() {
+      const int sg = kbl / SB;
+      const bool seg = kbl % SB == 0;
+      const int lo = sg == 0 ? 0 : meta_l(16 + sg * SB - 1);
+      const int n = meta_l(16 + min((sg + 1) * SB, nblk) - 1) - lo;
+      load_entries(meta_l(16 + TQK_NOB), lo, n, seg && n > 0);
+    };
+    auto seg_pass = [&](int j, int sg) {
+      // bias fill: lane L writes head hq (= L mod GQ) for the tokens
+      // [NT (L / GQ), NT (L / GQ) + NT), NT = kCT GQ / 64
+      {
+        constexpr int NT = kCT * GQ / 64;
+        const float4 bv = make_float4(bias_h, bias_h, bias_h, bias_h);
+        float4* row = reinterpret_cast<float4*>(corr + hq * kRow + NT * (lane / GQ));
+#pragma unroll
+        for (int i = 0; i < NT / 4; ++i) row[i] = bv;
+      }
+      const int n = gent_n, lo = gent_lo;
+      if (n == 0) return;
+      // every head's bias, for the runs written whole
+      float bh[GQ];
+#pragma unroll
+      for (int i = 0; i < GQ; ++i) bh[i] = bitsf((uint32_t)__builtin_amdgcn_readlane((int)fbits(bias_h), i));
+      const int E = (n + 63) >> 6;
+      const int nl = n - lane * E;  // entries k < nl of this lane are in the list
+      const __amdgpu_buffer_rsrc_t ro =
+          buf_rsrc(oent_all + (size_t)(uint32_t)meta(j, 16 + TQK_NOB) * cap, 4u * (uint32_t)cap);
+      const int t0 = kCT * sg;
+      float acc[GQ], facc[GQ];
+#pragma unroll
+      for (int i = 0; i < GQ; ++i) acc[i] = facc[i] = 0.f;
+      int tcur = -1, tfirst = -1;  // open run's token, first closed run's token (segment-relative)
+      // One entry, without branches: a run closing inside the lane that is
+      // not its first is stored at its token, every other step stores into
+      // the lane's own slot past the row's tokens.
+      auto entry = [&](int k, uint32_t x) {
+        // (an entry outside the segment's tokens is dropped, whatever the
+        // list holds: every LDS index below stays in corr_s)
+        const int tx = (int)((x >> 7) & 0xFFu) - t0;
+        const bool valid = k < nl && (unsigned)tx < (unsigned)kCT;
+        const int t = valid ? tx : -1;
+        const bool close = t != tcur && tcur >= 0;
+        const bool first = close && tfirst < 0;
+        const int st_tok = close && tfirst >= 0 ? tcur : kCT + lane;
+#pragma unroll
+        for (int i = 0; i < GQ; ++i) corr[i * kRow + st_tok] = bh[i] + acc[i];
+#pragma unroll
+        for (int i = 0; i < GQ; ++i) facc[i] = first ? acc[i] : facc[i];
+        tfirst = first ? tcur : tfirst;
+        const bool same = t == tcur;
+        tcur = t;
+        const int jc = (int)(x & (uint32_t)(D - 1));
+        const float dv = valid ? (h2f((uint16_t)(x >> 16)) - gsm_s[w][D + jc]) * qscale : 0.f;
+        // q of every head at channel jc, fp16 (exact), into fp32 FMAs
+        _Float16 qv[GQ];
+        if constexpr (GQ >= 4) {
+#pragma unroll
+          for (int i = 0; i < GQ; i += 4) {
+            const uint2 q4 = *reinterpret_cast<const uint2*>(&qc_s[jc][i]);
+            qv[i] = __builtin_bit_cast(_Float16, (uint16_t)(q4.x & 0xFFFFu));
+            qv[i + 1] = __builtin_bit_cast(_Float16, (uint16_t)(q4.x >> 16));
+            qv[i + 2] = __builtin_bit_cast(_Float16, (uint16_t)(q4.y & 0xFFFFu));
+            qv[i + 3] = __builtin_bit_cast(_Float16, (uint16_t)(q4.y >> 16));
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < GQ; ++i) qv[i] = __builtin_bit_cast(_Float16, qc_s[jc][i]);
+        }
+#pragma unroll
+        for (int i = 0; i < GQ; ++i) acc[i] = fmaf((float)qv[i], dv, same ? acc[i] : 0.f);
+      };
+#pragma unroll
+      for (int k = 0; k < kPre; ++k)
+        if (k < E) entry(k, gent[k]);
+      for (int k = kPre; k < E; ++k)  // long lists only; reads past the list return 0
+        entry(k, __builtin_amdgcn_raw_buffer_load_b32(ro, 4 * (lo + lane * E + k), 0, 0));
+      // The lane's first and last runs may continue in its neighbours (the
+      // list is sorted, so the lanes that share a token are consecutive, all
+      // but the two ends holding that token only).  An inclusive scan of the
+      // last-run sums over the lanes, segmented by the last-run token, gives
+      // each lane the sum of its token's runs so far; the first run of a lane
+      // takes its left neighbour's scan, and the last lane of a token's chain
+      // stores it.  (LDS float atomics here serialise per lane.)
+      float sv[GQ];
+#pragma unroll
+      for (int i = 0; i < GQ; ++i) sv[i] = acc[i];
+      const int tl = tcur;                         // last run's token (-1: none)
+      const int tf = tfirst >= 0 ? tfirst : tcur;  // first run's token
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int kd = __shfl_up(tl, d);
+        const bool add = lane >= d && kd == tl && tl >= 0;
+#pragma unroll
+        for (int i = 0; i < GQ; ++i) {
+          const float v = __shfl_up(sv[i], d);
+          sv[i] += add ? v : 0.f;
+        }
+      }
+      // (every lane takes part in each shuffle: a lane outside the exec mask
+      // has nothing to hand over; the edges are resolved after the shuffle)
+      const int tl_up = __shfl_up(tl, 1), tf_dn = __shfl_down(tf, 1);
+      const int tl_prev = lane > 0 ? tl_up : -1;
+      const int tf_next = lane < 63 ? tf_dn : -1;
+      float sprev[GQ];
+#pragma unroll
+      for (int i = 0; i < GQ; ++i) sprev[i] = __shfl_up(sv[i], 1);
+      if (tfirst >= 0) {
+        // the first run ends inside this lane: complete with the carry-in
+        const bool cin = tl_prev == tfirst;
+#pragma unroll
+        for (int i = 0; i < GQ; ++i) corr[i * kRow + tfirst] = bh[i] + facc[i] + (cin ? sprev[i] : 0.f);
+      }
+      if (tl >= 0 && tf_next != tl) {
+#pragma unroll
+        for (int i = 0; i < GQ; ++i) corr[i * kRow + tl] = bh[i] + sv[i];
+      }
+    };
+    // QK^T accumulator start of block kb of the current group: hi columns
+    // from corr_s (tokens 4lg..4lg+3 of tile A, then of tile B), lo columns 0
+    const float* const init_base = is_hi ? corr + hq * kRow + 4 * lg : zero4_s;
+    const int init_step = is_hi ? 32 : 0;
+    auto block_init = [&](int kb, floatx4_t& CA, floatx4_t& CB) {
+      const float* p = init_base + init_step * (kb % SB);
+      CA = *reinterpret_cast<const floatx4_t*>(p);
+      CB = *reinterpret_cast<const floatx4_t*>(p + (is_hi ? 16 : 0));
     };
 
       // A operand of QK^T MFMA m from the lane's key bytes (a table row of a code
@@ -1119,6 +1263,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         r.u[3] = t1.y;
         return r;
       };
+
       // B operand of PV MFMA nt: single fp16 centroids of tokens 0..3 of the
       // lane's value unit in tile A (channel 8n + nt), then of tile B:
       // k-slots [A t0 t1 t2 t3, B t0 t1 t2 t3], matching the weight operand.
@@ -1176,123 +1321,19 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         }
         return r;
       };
-      // ---- sparse outliers, folded into the QK^T accumulators:
-      //   C[t][col] += sum_e [t_e == t] * d_e * q_h[j_e],   d = (val - mean_j) * s / 2
-      // with s = sm_scale * log2(e); the stored code of an outlier is the NF4
-      // zero level, so the dense pass contributed exactly mean_j there (inside
-      // the bias).  16 entries per MFMA: A k-slots {hi, lo} fp16 of d_e in row
-      // t_e (zero in other rows), B k-slots {q, q} (q is exact in fp16); the hi
-      // and the lo column of a head each take half, which pair_sum adds up.
-      // Stage a pass of <= 128 (token-sorted) entries: this lane's two in
-      // registers, their q pairs per head into oq_s set buf.
-      const float dscale = 0.5f * qscale;
-      auto stage_entries = [&](const uint2 ent, int cnt, int blk, int gslot) {
-        uint32_t tv[2], dv[2];
-        int jv[2];
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const uint32_t en = u ? ent.y : ent.x;
-          const int pos = en & 0xFFFFu;
-          const int j = pos & (D - 1);
-          const float dl = (h2f((uint16_t)(en >> 16)) - gsm_s[w][gslot][D + j]) * dscale;
-          const _Float16 dh = (_Float16)dl;
-          dv[u] = pk_f16(dl, dl - (float)dh);
-          tv[u] = eidx + u < cnt ? (uint32_t)((pos >> 7) - 32 * blk) : 255u;
-          jv[u] = j;
-        }
-        uint32_t qv[2][GQ];
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          if constexpr (GQ >= 4) {
-#pragma unroll
-            for (int hh = 0; hh < GQ; hh += 4) {
-              const uint4 q4 = *reinterpret_cast<const uint4*>(&qq_s[jv[u]][hh]);
-              qv[u][hh] = q4.x; qv[u][hh + 1] = q4.y; qv[u][hh + 2] = q4.z; qv[u][hh + 3] = q4.w;
-            }
-          } else {
-#pragma unroll
-            for (int k2 = 0; k2 < GQ; ++k2) qv[u][k2] = qq_s[jv[u]][k2];
-          }
-        }
-#pragma unroll
-        for (int hh = 0; hh < GQ; ++hh)
-          *reinterpret_cast<uint2*>(&oq_s[w][hh][eidx]) = make_uint2(qv[0][hh], qv[1][hh]);
-        *reinterpret_cast<uint16_t*>(&otb_s[w][lg][4 * (c >> 1) + 2 * (c & 1)]) = (uint16_t)(tv[0] | (tv[1] << 8));
-        *reinterpret_cast<uint2*>(&od_s[w][eidx]) = make_uint2(dv[0], dv[1]);
-        OutEntries oe;
-        oe.cnt = cnt;
-        // token-sorted: the entries of tile A (tokens 0..15) come first
-        oe.nA = (int)__popcll(__ballot(tv[0] < 16u)) + (int)__popcll(__ballot(tv[1] < 16u));
-        return oe;
-      };
-      // Apply a staged pass: one MFMA per touched tile and 16-entry chunk k
-      // (lane group lg: entries 16k + 4lg + i, i < 4).  The operands of every
-      // chunk the pass holds are read up front.
-      auto apply_entries = [&](const OutEntries& oe, floatx4_t& CA, floatx4_t& CB) {
-        // wave-uniform counts, so the chunk tests below are plain scalar branches
-        const int cnt = __builtin_amdgcn_readfirstlane(oe.cnt);
-        const int nA = __builtin_amdgcn_readfirstlane(oe.nA);
-        // tokens of every chunk's four slots of this lane group (dword k = chunk k)
-        const uint4 tw03 = *reinterpret_cast<const uint4*>(&otb_s[w][lg][0]);
-        const uint4 tw47 = *reinterpret_cast<const uint4*>(&otb_s[w][lg][16]);
-        // chunk operands four at a time, read before the first of them is used
-        // (one LDS round trip per four chunks; the staged arrays hold 128
-        // entries, so the reads stay inside them whatever cnt is)
-        uint4 dq[4];
-        H8 qv[4];
-        auto read4 = [&](int k0) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            dq[i] = *reinterpret_cast<const uint4*>(&od_s[w][16 * (k0 + i) + 4 * lg]);
-            qv[i].v = *reinterpret_cast<const uint4*>(&oq_s[w][hq][16 * (k0 + i) + 4 * lg]);
-          }
-        };
-        // chunk k holds entries [16k, 16k + 16): it touches tile A while
-        // k < endA, tile B from k = beginB on, and exists while k < end
-        const int endA = (nA + 15) >> 4, beginB = nA >> 4, end = (cnt + 15) >> 4;
-        auto chunk = [&](auto kc) {
-          constexpr int k = decltype(kc)::value;
-          if (k >= end) return;
-          const uint32_t tw = k < 4 ? u4_word<k & 3>(tw03) : u4_word<k & 3>(tw47);
-          if (k < endA) {
-            H8 o;
-            onehot_operand(tw, (uint32_t)c, dq[k & 3], o.u);
-            CA = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.h, qv[k & 3].h, CA, 0, 0, 0);
-          }
-          if (k >= beginB) {
-            H8 o;
-            onehot_operand(tw, (uint32_t)(16 + c), dq[k & 3], o.u);
-            CB = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.h, qv[k & 3].h, CB, 0, 0, 0);
-          }
-        };
-        read4(0);
-        chunk(IntC<0>{});
-        chunk(IntC<1>{});
-        chunk(IntC<2>{});
-        chunk(IntC<3>{});
-        if (cnt > 64) {
-          read4(4);
-          chunk(IntC<4>{});
-          chunk(IntC<5>{});
-          chunk(IntC<6>{});
-          chunk(IntC<7>{});
-        }
-      };
 
       // Software pipeline over a wave's blocks.  Step i starts with the QK^T
-      // accumulators of block i, outliers included (computed at the end of
-      // step i - 1): it stages block i + 1's outlier entries, runs block i's
-      // softmax, interleaves block i's PV with block i + 1's QK^T so that the
-      // table reads of one overlap the MFMAs of the other, and adds block
-      // i + 1's outlier corrections.
-      OutEntries pend;          // staged outlier entries of the block computed next
-      floatx4_t CAn, CBn;       // QK^T (with the bias) of the block computed next
+      // accumulators of block i (computed in step i - 1 from the initial
+      // values of its group's corr_s): it runs block i's softmax, and
+      // interleaves block i's PV with block i + 1's QK^T so that the table
+      // reads of one overlap the MFMAs of the other.  When block i + 1 starts
+      // a group, its weights and corr_s are built in between.
+      floatx4_t CAn, CBn;       // QK^T of the block computed next
       auto key_tile = [&](const uint4& k, H8 (&x)[8]) {
 #pragma unroll
         for (int m = 0; m < 8; ++m) x[m] = key_quad(k, m);
       };
       auto qk_tile = [&](const H8 (&x)[8], floatx4_t& C) {
-        C = binit;
 #pragma unroll
         for (int m = 0; m < 8; ++m) C = __builtin_amdgcn_mfma_f32_16x16x32_f16(x[m].h, Bw[m].h, C, 0, 0, 0);
       };
@@ -1311,32 +1352,10 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
 #pragma unroll
         for (int nt = 0; nt < 8; ++nt) st.O[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pw.h, v[nt].h, st.O[nt], 0, 0, 0);
       };
-      // Outlier corrections of block blk (its first pass staged in pend) into
-      // that block's QK^T accumulators; passes beyond the first 128 entries
-      // (rare) read the side-list here and drain, so the common path keeps
-      // exact wait counts.  Applied right after the block's QK^T, a step
-      // before its scores are read, so the MFMA chain's latency is hidden.
-      auto apply_block = [&](const ColdBlock<VB>& cb, int blk, int gslot, floatx4_t& CA, floatx4_t& CB) {
-        apply_entries(pend, CA, CB);
-        if (cb.ne > 128) {
-          const uint32_t* __restrict__ oent = oent_all + (size_t)cb.obase * cap;
-          for (int base = 128; base < cb.ne; base += 128) {
-            const int cnt = min(128, cb.ne - base);
-            const int i0 = cb.e0 + base + eidx;
-            const uint32_t x0 = oent[min(i0, capm1)], x1 = oent[min(i0 + 1, capm1)];
-            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-            wave_sync();
-            const OutEntries ex = stage_entries(make_uint2(x0, x1), cnt, blk, gslot);
-            wave_sync();
-            apply_entries(ex, CA, CB);
-          }
-        }
-      };
-      auto process = [&](const ColdBlock<VB>& cur, const ColdBlock<VB>& nx1, int blk1, int gslot1) {
+      // blk1: block index of block i + 1 inside its group (whose weights and
+      // corrections are built before the step when it starts a segment)
+      auto process = [&](const ColdBlock<VB>& cur, const ColdBlock<VB>& nx1, int blk1) {
         const floatx4_t CA = CAn, CB = CBn;
-        // next block's entries (this block's were applied in the previous step)
-        wave_sync();
-        pend = stage_entries(nx1.ent, min(128, nx1.ne), blk1, gslot1);
         float sc[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -1369,51 +1388,69 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         val_block(cur.uA, cur.uB, vv);
         key_tile(nx1.kA, xa);
         pv_block(pw, vv);
+        block_init(blk1, CAn, CBn);
         qk_tile(xa, CAn);
         key_tile(nx1.kB, xb);
         qk_tile(xb, CBn);
-        wave_sync();
-        apply_block(nx1, blk1, gslot1, CAn, CBn);
       };
 
     // A ring of kColdBuf buffers, kColdBuf - 1 blocks in flight: step i
     // issues the loads of block i + kColdBuf - 1 and computes block i.
     int jp = 0, kbp = kb0;  // computed block: wave group jp, block kbp
+    int si = 0;             // stream index of the computed block
     auto step = [&](const ColdBlock<VB>& cur, ColdBlock<VB>& nxt, const ColdBlock<VB>& nx1) {
-      store_group_stats();
-      load_group_stats(meta_l(16 + TQK_NOB), jl);  // group of the block load_next fetches now
+      store_group_stats();  // block i + 1's group
+      const bool starts = kbp + 1 == nblk;  // block i + 1 starts wave group jp + 1
+      const int kb1 = starts ? 0 : kbp + 1, j1 = starts ? jp + 1 : jp;
+      // (after the wave's last block there is no block i + 1: nothing to
+      // build, and process's QK^T of it runs on a stale buffer, unused)
+      if (__builtin_expect(si + 1 < T && kb1 % SB == 0, 0)) {
+        // block i + 1 starts a segment (and maybe its group): weights and
+        // bias, then the segment's corrections from the entries loaded with
+        // the block in the previous step
+        wave_sync();
+        if (starts) begin_group();
+        seg_pass(j1, kb1 / SB);
+      }
+      load_group_stats(meta_l(16 + TQK_NOB));  // group of the block load_next fetches now
       wave_sync();
-      const bool last = kbp + 1 == nblk;  // block i + 1 starts wave group jp + 1
-      if (last) begin_group(jp + 1);     // weights for the QK^T of block i + 1
+      load_block_entries();
       load_next(nxt);
-      process(cur, nx1, last ? 0 : kbp + 1, last ? (jp + 1) & 1 : jp & 1);
+      process(cur, nx1, kb1);
       if (++kbp == nblk) {
         kbp = 0;
         ++jp;
       }
+      ++si;
     };
     if (T > 0) {
-      // groups of the first two blocks, synchronously
+      // the first group: stats and the side-list of the first block's segment
+      // synchronously; the group of the second block's stats into the pending
+      // registers
       const int j1 = (kb0 + min(1, T - 1)) / nblk;
-      load_group_stats(meta(0, 16 + TQK_NOB), 0);
+      const int sg0 = kb0 / SB;
+      load_group_stats(meta(0, 16 + TQK_NOB));
+      load_seg_entries(0, sg0);
       store_group_stats();
-      load_group_stats(meta(j1, 16 + TQK_NOB), j1);
-      store_group_stats();
+      wave_sync();
+      begin_group();
+      seg_pass(0, sg0);
+      load_group_stats(meta(j1, 16 + TQK_NOB));
       ColdBlock<VB> ring[kColdBuf];
 #pragma unroll
-      for (int s = 0; s < kColdBuf - 1; ++s) load_next(ring[s]);
+      for (int s = 0; s < kColdBuf - 1; ++s) {
+        load_block_entries();
+        load_next(ring[s]);
+      }
       wave_sync();
-      begin_group(0);
-      pend = stage_entries(ring[0].ent, min(128, ring[0].ne), kb0, 0);
       {
         H8 x[8];
+        block_init(kb0, CAn, CBn);
         key_tile(ring[0].kA, x);
         qk_tile(x, CAn);
         key_tile(ring[0].kB, x);
         qk_tile(x, CBn);
       }
-      wave_sync();
-      apply_block(ring[0], kb0, 0, CAn, CBn);
       for (int i = 0; i < T; i += kColdBuf) {
 #pragma unroll
         for (int s = 0; s < kColdBuf; ++s) {
@@ -1527,10 +1564,11 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       }
     }
   };
-  // hot state: this wave's own slices of the outlier staging (no longer read)
-  float* const hm = &gsm_s[0][0][0];                        // wave ww: hm[ww * 4D + i]
-  float* const hco = reinterpret_cast<float*>(&oq_s[0][0][0]);  // wave ww: hco[ww * GQ * 132 + i * D + j]
-  constexpr int kHmStride = 4 * D, kHcoStride = GQ * 132;
+  // hot state: this wave's own stats slot and corrections (no longer read)
+  float* const hm = &gsm_s[0][0];                 // wave ww: hm[ww * 2D + i]
+  float* const hco = &corr_s[0][0][0];            // wave ww: hco[ww * GQ * kRow + i * D + j]
+  constexpr int kHmStride = 2 * D, kHcoStride = GQ * kRow;
+  static_assert(kCT >= D, "hot-state area");
   put_state(st, hm + w * kHmStride, hm + w * kHmStride + D, hco + w * kHcoStride);
   // coded state: the code table's area, once every wave is past its groups
   __syncthreads();
