@@ -777,8 +777,9 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   constexpr int kCT = kSegTokens<GQ>;
   constexpr int kRow = kCT + 64;
   __shared__ __align__(16) float corr_s[kMWaves][GQ][kRow];
-  __shared__ __align__(16) float zero4_s[4];             // the lo columns' initial value
-  if (tid < 4) zero4_s[tid] = 0.f;
+  // per wave and head: the lo columns' initial value, the group's mean bias
+  // q . mean (four copies: one tile's accumulator)
+  __shared__ __align__(16) float bias_s[kMWaves][GQ][4];
   // NF4 levels [0, 16) and value centroids [16, 16 + 2^vb), for the table fill
   __shared__ float lvl_s[32];
   if (tid < 16) lvl_s[tid] = PK ? (tid < (1 << KB) ? a.p.vcent[tid] : 0.f) : key_level(a.d.key_grid, tid);
@@ -1031,7 +1032,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     // initial values (mean bias plus the token's outlier corrections, built
     // once per group in corr_s); the lo columns start from zero.
     H8 Bw[8];
-    float bias_h;  // q . mean of head hq (the hi columns' constant term)
+    float bias_h;  // q . mean of head hq (the lo columns' initial value)
     // Start of wave group j: weights and mean bias from the wave's stats slot.
     auto begin_group = [&]() {
       const float* gs = &gsm_s[w][0];
@@ -1046,6 +1047,8 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         Bw[m] = dup_quad(q4.x * s4.x, q4.y * s4.y, q4.z * s4.z, q4.w * s4.w, lo_sel);
       }
       bias_h = colgroup_sum(biasp);
+      // lanes c < GQ of lane group 0: the bias of head c, four copies
+      if (lane < GQ) *reinterpret_cast<float4*>(&bias_s[w][lane][0]) = make_float4(bias_h, bias_h, bias_h, bias_h);
     };
 
     // ---- sparse outliers, once per segment of kCT tokens of a group: the
@@ -1053,9 +1056,9 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     // side-list entry (t, j, val) (the stored code of an outlier is the NF4
     // zero level, so the dense pass gave exactly mean_j there, inside the
     // bias).  The wave turns the segment's stretch of the token-sorted
-    // side-list into corr_s[w][h][t] = bias_h + the sum of token t's
-    // corrections (fp32), and each block's QK^T accumulators of the hi
-    // columns start from it.  Lane L takes E consecutive entries, E =
+    // side-list into corr_s[w][h][t] = the sum of token t's corrections
+    // (fp32), and each block's QK^T accumulators of the hi columns start from
+    // it (the lo columns start from the mean bias).  Lane L takes E consecutive entries, E =
     // ceil(n / 64): runs of one token inside a lane are summed in registers;
     // a run that closes inside the lane and is not its first belongs to the
     // lane alone (the list is sorted) and is written; the lane's first and
@@ -1108,21 +1111,17 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       load_entries(meta_l(16 + TQK_NOB), lo, n, seg && n > 0);
     };
     auto seg_pass = [&](int j, int sg) {
-      // bias fill: lane L writes head hq (= L mod GQ) for the tokens
-      // [NT (L / GQ), NT (L / GQ) + NT), NT = kCT GQ / 64
+      // zero fill (tokens without outliers): lane L writes head hq
+      // (= L mod GQ) for the tokens [NT (L / GQ), NT (L / GQ) + NT),
+      // NT = kCT GQ / 64
       {
         constexpr int NT = kCT * GQ / 64;
-        const float4 bv = make_float4(bias_h, bias_h, bias_h, bias_h);
         float4* row = reinterpret_cast<float4*>(corr + hq * kRow + NT * (lane / GQ));
 #pragma unroll
-        for (int i = 0; i < NT / 4; ++i) row[i] = bv;
+        for (int i = 0; i < NT / 4; ++i) row[i] = make_float4(0.f, 0.f, 0.f, 0.f);
       }
       const int n = gent_n, lo = gent_lo;
       if (n == 0) return;
-      // every head's bias, for the runs written whole
-      float bh[GQ];
-#pragma unroll
-      for (int i = 0; i < GQ; ++i) bh[i] = bitsf((uint32_t)__builtin_amdgcn_readlane((int)fbits(bias_h), i));
       const int E = (n + 63) >> 6;
       const int nl = n - lane * E;  // entries k < nl of this lane are in the list
       const __amdgpu_buffer_rsrc_t ro =
@@ -1145,14 +1144,16 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         const bool first = close && tfirst < 0;
         const int st_tok = close && tfirst >= 0 ? tcur : kCT + lane;
 #pragma unroll
-        for (int i = 0; i < GQ; ++i) corr[i * kRow + st_tok] = bh[i] + acc[i];
+        for (int i = 0; i < GQ; ++i) corr[i * kRow + st_tok] = acc[i];
 #pragma unroll
         for (int i = 0; i < GQ; ++i) facc[i] = first ? acc[i] : facc[i];
         tfirst = first ? tcur : tfirst;
         const bool same = t == tcur;
         tcur = t;
         const int jc = (int)(x & (uint32_t)(D - 1));
-        const float dv = valid ? (h2f((uint16_t)(x >> 16)) - gsm_s[w][D + jc]) * qscale : 0.f;
+        // (read for every lane: an invalid entry's channel is still in range)
+        const float dv0 = (h2f((uint16_t)(x >> 16)) - gsm_s[w][D + jc]) * qscale;
+        const float dv = valid ? dv0 : 0.f;
         // q of every head at channel jc, fp16 (exact), into fp32 FMAs
         _Float16 qv[GQ];
         if constexpr (GQ >= 4) {
@@ -1210,16 +1211,17 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         // the first run ends inside this lane: complete with the carry-in
         const bool cin = tl_prev == tfirst;
 #pragma unroll
-        for (int i = 0; i < GQ; ++i) corr[i * kRow + tfirst] = bh[i] + facc[i] + (cin ? sprev[i] : 0.f);
+        for (int i = 0; i < GQ; ++i) corr[i * kRow + tfirst] = facc[i] + (cin ? sprev[i] : 0.f);
       }
       if (tl >= 0 && tf_next != tl) {
 #pragma unroll
-        for (int i = 0; i < GQ; ++i) corr[i * kRow + tl] = bh[i] + sv[i];
+        for (int i = 0; i < GQ; ++i) corr[i * kRow + tl] = sv[i];
       }
     };
     // QK^T accumulator start of block kb of the current group: hi columns
-    // from corr_s (tokens 4lg..4lg+3 of tile A, then of tile B), lo columns 0
-    const float* const init_base = is_hi ? corr + hq * kRow + 4 * lg : zero4_s;
+    // from corr_s (tokens 4lg..4lg+3 of tile A, then of tile B), lo columns
+    // the group's mean bias
+    const float* const init_base = is_hi ? corr + hq * kRow + 4 * lg : &bias_s[w][hq][0];
     const int init_step = is_hi ? 32 : 0;
     auto block_init = [&](int kb, floatx4_t& CA, floatx4_t& CB) {
       const float* p = init_base + init_step * (kb % SB);
