@@ -232,16 +232,132 @@ def test_connector_protocol_host_side():
     over a store holding the reference's records; without vLLM, ``register``
     reports False instead of failing."""
     from turboquant_pro_amd.connectors import TurboQuantKVConnector
-    from turboquant_pro_amd.connectors.vllm import register
+    from turboquant_pro_amd.connectors.vllm import TurboQuantConnectorMetadata, register
     st, _ = _loaded_store()
     conn = TurboQuantKVConnector(store=st)
     req = type("Req", (), {"request_id": "req1"})()
     assert conn.get_num_new_matched_tokens(req, 0) == (200, False)
     assert conn.get_num_new_matched_tokens(req, 150) == (50, False)
     assert conn.get_num_new_matched_tokens(req, 500) == (0, False)
-    assert conn.build_connector_meta() == {"version": 1}
+    meta = conn.build_connector_meta()
+    assert isinstance(meta, TurboQuantConnectorMetadata) and meta.loads == []
     assert conn.request_finished(req) == (False, None)
-    assert conn.start_load_kv(requests={"req1": 0}) == 0      # no pool bound: nothing to restore into
+    conn.bind_connector_metadata(TurboQuantConnectorMetadata(loads=[("req1", 0, 200)]))
+    assert conn.start_load_kv(None) == 0      # no pool bound: nothing to restore into
     conn.get_finished({"req1"})
     assert st.matched_tokens("req1") == 0 and st.stats()["records"] == 0
+    m = conn.get_metrics()
+    assert m["evictions"] == st.metrics.to_dict()["evictions"] > 0
     assert register() is False
+
+
+class _RecordingStore:
+    """A store stand-in for the connector's metadata flow: what the worker
+    was asked to restore, where."""
+
+    def __init__(self, tokens):
+        from turboquant_pro_amd.connectors.metrics import ConnectorMetrics
+        self.tokens, self.calls, self.metrics = dict(tokens), [], ConnectorMetrics()
+
+    def matched_tokens(self, rid):
+        return self.tokens.get(rid, 0)
+
+    def load_into_pool(self, rid, layer, pool, slot):
+        self.calls.append((rid, layer, pool, slot))
+        return self.tokens.get(rid, 0)
+
+    def evict(self, rid):
+        return int(self.tokens.pop(rid, None) is not None)
+
+
+def _metadata_round(mod):
+    """Scheduler -> metadata -> worker, as vLLM V1 drives a connector: the
+    scheduler instance answers the match, takes the allocation of requests
+    that load, and builds the step's metadata; the worker instance is bound
+    to it and restores each request into its slot of every bound pool."""
+    store = _RecordingStore({"a": 600, "b": 1300, "c": 40})
+    sched = mod.TurboQuantKVConnector(role=mod.KVConnectorRole.SCHEDULER, store=store)
+    work = mod.TurboQuantKVConnector(role=mod.KVConnectorRole.WORKER, store=store)
+    pools = {"layers.0.attn": object(), "layers.1.attn": object()}
+    for name, p in pools.items():
+        work.bind_pool(name, p)
+    reqs = {r: type("Req", (), {"request_id": r})() for r in "abcd"}
+    for r, computed in (("a", 0), ("b", 256), ("c", 40), ("d", 0)):
+        n, pending = sched.get_num_new_matched_tokens(reqs[r], computed)
+        assert not pending
+        sched.update_state_after_alloc(reqs[r], [], n)
+    meta = sched.build_connector_meta()
+    assert isinstance(meta, mod.TurboQuantConnectorMetadata)
+    # only the requests with tokens to take from the store load, in order,
+    # each in its own slot
+    assert meta.loads == [("a", 0, 600), ("b", 1, 1044)]
+    assert sched.build_connector_meta().loads == []      # handed over once
+    work.bind_connector_metadata(meta)
+    assert work.start_load_kv(None) == 2 * (600 + 1300)
+    assert sorted((c[0], c[1], c[3]) for c in store.calls) == sorted(
+        (r, layer, s) for r, s in (("a", 0), ("b", 1)) for layer in pools)
+    assert all(c[2] is pools[c[1]] for c in store.calls)
+    work.clear_connector_metadata()
+    assert work.start_load_kv(None) == 0
+    # a finished request frees its slot for the next one
+    assert sched.request_finished(reqs["a"], []) == (False, None)
+    sched.update_state_after_alloc(reqs["c"], [], 40)
+    assert sched.build_connector_meta().loads == [("c", 0, 40)]
+    assert sched.slot_of(reqs["b"]) == 1 and sched.slot_of(reqs["a"]) is None
+    return sched, work
+
+
+def test_connector_metadata_flow_without_vllm():
+    from turboquant_pro_amd.connectors import vllm as mod
+    _metadata_round(mod)
+
+
+def test_connector_metadata_flow_with_stubbed_vllm(monkeypatch):
+    """With vLLM importable (stub modules, as the reference's own connector
+    test does, tests/test_vllm_connector.py:89-119), the connector is a
+    subclass of vLLM's KVConnectorBase_V1, its metadata of
+    KVConnectorMetadata, and the base's bind/clear hooks carry the flow."""
+    import importlib
+    import sys
+    import types
+
+    class KVConnectorRole:
+        SCHEDULER = "scheduler"
+        WORKER = "worker"
+
+    class KVConnectorMetadata:
+        pass
+
+    class KVConnectorBase_V1:  # noqa: N801
+        def __init__(self, vllm_config, role):
+            self._vllm_config, self._role = vllm_config, role
+            self._connector_metadata = None
+
+        def bind_connector_metadata(self, m):
+            self._connector_metadata = m
+
+        def clear_connector_metadata(self):
+            self._connector_metadata = None
+
+        def _get_connector_metadata(self):
+            return self._connector_metadata
+
+    names = ["vllm", "vllm.distributed", "vllm.distributed.kv_transfer",
+             "vllm.distributed.kv_transfer.kv_connector", "vllm.distributed.kv_transfer.kv_connector.v1"]
+    for n in names:
+        monkeypatch.setitem(sys.modules, n, types.ModuleType(n))
+    base = types.ModuleType("vllm.distributed.kv_transfer.kv_connector.v1.base")
+    base.KVConnectorBase_V1, base.KVConnectorMetadata, base.KVConnectorRole = (
+        KVConnectorBase_V1, KVConnectorMetadata, KVConnectorRole)
+    monkeypatch.setitem(sys.modules, base.__name__, base)
+    from turboquant_pro_amd.connectors import vllm as mod
+    try:
+        mod = importlib.reload(mod)
+        assert issubclass(mod.TurboQuantKVConnector, KVConnectorBase_V1)
+        assert mod.KVConnectorRole is KVConnectorRole
+        sched, work = _metadata_round(mod)
+        assert isinstance(sched.build_connector_meta(), KVConnectorMetadata)
+        assert work._role == KVConnectorRole.WORKER
+    finally:
+        monkeypatch.undo()
+        importlib.reload(mod)

@@ -83,7 +83,21 @@ def test_start_load_kv_restores_codes():
     assert conn.get_num_new_matched_tokens(type("R", (), {"request_id": "reqB"})(), 300) == (400, False)
     dst = _pool()
     conn.bind_pool("layers.0.attn", dst)
-    assert conn.start_load_kv(requests={"reqA": 0, "reqB": 1, "missing": 0}) == 1800
+    # vLLM's flow: the scheduler-side instance takes the allocations of the
+    # requests that load and hands them over as connector metadata; the
+    # worker is bound to it and restores each request into its slot
+    from turboquant_pro_amd.connectors.vllm import KVConnectorRole
+    sched = TurboQuantKVConnector(role=KVConnectorRole.SCHEDULER, store=conn.store)
+    for rid in ("reqA", "reqB", "missing"):
+        req = type("R", (), {"request_id": rid})()
+        n, _ = sched.get_num_new_matched_tokens(req, 0)
+        sched.update_state_after_alloc(req, [], n)
+    meta = sched.build_connector_meta()
+    assert meta.loads == [("reqA", 0, 1100), ("reqB", 1, 700)]
+    conn.bind_connector_metadata(meta)
+    assert conn.start_load_kv(None) == 1800
+    conn.clear_connector_metadata()
+    assert conn.get_metrics()["hits"] >= 2
     assert dst.lengths == lens
     for b in range(2):
         assert dst.n_groups(b) == src.n_groups(b)
@@ -115,3 +129,40 @@ def test_start_load_kv_restores_codes():
         conn.store.load_into_pool("reqA", "layers.0.attn", uni, 0)
     conn.get_finished({"reqA"})
     assert conn.store.matched_tokens("reqA") == 0 and conn.store.matched_tokens("reqB") == 700
+
+
+def test_bias_zero_point_groups_restore_with_their_positions():
+    """Keys with the RoPE-averaged ``bias`` zero point (per_channel_kv.py:
+    245-267): each group's zero point depends on its first position, so the
+    live-path save records group g at position g * G; restored into a pool of
+    the same rope_theta and k_bias, every group is bit-identical to the pool
+    that encoded the tokens itself.  A pool with another rope_theta refuses
+    the records (its zero points would be another function)."""
+    from turboquant_pro_amd import TQKVPool
+    from turboquant_pro_amd.connectors import TurboQuantBlockStore
+    print("[restore] bias zero point", flush=True)
+    k, v, q = O.synthetic_kv(57, 1, 2, 8, 1100)
+    kbias = np.random.default_rng(3).standard_normal((2, 128)).astype(np.float32)
+    kw = dict(n_kv_heads=2, n_q_heads=8, max_batch=1, max_seq_len=2048, value_bits=3, seed=0,
+              zero_point="bias", rope_theta=10000.0, k_bias=kbias)
+    kd, vd = torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda()
+    src = TQKVPool(**kw)
+    src.append(kd, vd)
+    store = TurboQuantBlockStore(
+        key_config={"nf4_asym": True, "outlier_frac": 0.02, "zero_point": "bias",
+                    "rope_theta": 10000.0, "k_bias": kbias},
+        value_config={"bits": 3, "seed": 0})
+    ng = store.save_sequence("r", "l0", kd[0], vd[0], src.group_tokens, src.hot_window)
+    assert ng == src.n_groups(0) == 3
+    dst = TQKVPool(**kw)
+    assert store.load_into_pool("r", "l0", dst, 0) == 1100
+    for g in range(ng):
+        a, c = src.export_group(0, g), dst.export_group(0, g)
+        for key in a:
+            assert np.array_equal(np.asarray(a[key]), np.asarray(c[key])), f"group {g} {key}"
+    qd = torch.from_numpy(q).cuda()
+    assert torch.equal(dst.decode(qd), src.decode(qd))
+    other = TQKVPool(**dict(kw, rope_theta=500000.0))
+    with pytest.raises(ValueError, match="rope_theta"):
+        store.load_into_pool("r", "l0", other, 0)
+    assert store.metrics.to_dict()["misses_incompatible"] == 1

@@ -19,9 +19,10 @@ a complete, matching :class:`KVIdentityProfile`:
   file names other than 24 hex digits + ``.rec`` are refused.
 
 A ``load`` that cannot decode a record is a miss: the record is dropped and
-``None`` returned.  Saves are synchronous (the reference's async queue,
-backpressure and metrics are serving-side glue that this build leaves to the
-caller).
+``None`` returned.  Every save, load, miss (by cause), eviction and restore is
+counted in ``metrics`` (:class:`ConnectorMetrics`, the reference's counter
+names).  Saves are synchronous (the reference's async queue and backpressure
+are serving-side glue that this build leaves to the caller).
 """
 
 from __future__ import annotations
@@ -38,6 +39,7 @@ from typing import Any
 import numpy as np
 
 from .identity import IncompatibleProfile, KVIdentityProfile
+from .metrics import ConnectorMetrics
 from .records import BlockRecord, RawTokens, payload_nbytes, rec_from_blob, rec_to_blob
 
 logger = logging.getLogger(__name__)
@@ -86,6 +88,7 @@ class TurboQuantBlockStore:
         self._tokens: dict[str, int] = {}
         self._quantizers: dict[tuple, Any] = {}
         self._lock = threading.Lock()
+        self.metrics = ConnectorMetrics()
 
     # ------------------------------------------------------------ plugins
     def quant_descriptor(self) -> dict:
@@ -182,6 +185,8 @@ class TurboQuantBlockStore:
             for name, rec in recs.items():
                 self._records[(request_id, name)] = rec
             self._tokens[request_id] = L
+        for rec in recs.values():
+            self._count_save(rec)
         return ng
 
     def load_into_pool(self, request_id: str, layer_name: str, pool, b: int) -> int:
@@ -192,15 +197,29 @@ class TurboQuantBlockStore:
         Raises ``ValueError`` when the records are not in the pool's format
         (key grid, zero point and, for sparse/bias zero points, rope_theta and
         group positions, value width, rotation, group size)."""
-        import torch
-
         groups = []
         with self._lock:
             while (request_id, self._group_name(layer_name, len(groups))) in self._records:
                 groups.append(self._records[(request_id, self._group_name(layer_name, len(groups)))])
             hot = self._records.get((request_id, f"{layer_name}#hot0"))
         if not groups and hot is None:
+            self.metrics.miss("empty")
             return 0
+        with self.metrics.timed("load"):
+            try:
+                n = self._restore(groups, hot, pool, b)
+            except ValueError:
+                self.metrics.miss("incompatible")
+                raise
+        self.metrics.inc("loads")
+        self.metrics.inc("hits")
+        self.metrics.inc("records_restored", len(groups) + (hot is not None))
+        return n
+
+    def _restore(self, groups: list, hot, pool, b: int) -> int:
+        """The body of :meth:`load_into_pool`: format checks, then the import."""
+        import torch
+
         H, D, G = pool.n_kv_heads, pool.head_dim, pool.group_tokens
         vq = self._quantizer("value", D, H)
         if getattr(vq, "value_bits", None) != pool.value_bits:
@@ -250,12 +269,22 @@ class TurboQuantBlockStore:
         pool.load_sequence(b, items, hk, hv)
         return len(items) * G + int(hk.shape[1])
 
+    def _count_save(self, rec: BlockRecord) -> None:
+        self.metrics.inc("saves")
+        n = 1
+        for dim in rec.shape:
+            n *= int(dim)
+        self.metrics.bytes_saved(logical=2 * 4 * n,  # fp32 keys and values
+                                 physical=payload_nbytes(rec.key_payload) + payload_nbytes(rec.value_payload))
+
     def save(self, request_id: str, layer_name: str, keys: Any, values: Any) -> None:
         """Quantize and store one layer's KV for ``request_id``."""
-        rec = self.make_record(keys, values)
-        with self._lock:
-            self._records[(request_id, layer_name)] = rec
-            self._tokens[request_id] = rec.num_tokens
+        with self.metrics.timed("save"):
+            rec = self.make_record(keys, values)
+            with self._lock:
+                self._records[(request_id, layer_name)] = rec
+                self._tokens[request_id] = rec.num_tokens
+        self._count_save(rec)
 
     def record(self, request_id: str, layer_name: str) -> BlockRecord | None:
         with self._lock:
@@ -266,19 +295,28 @@ class TurboQuantBlockStore:
         stored, or a record that does not decode -- then it is dropped)."""
         rec = self.record(request_id, layer_name)
         if rec is None:
+            self.metrics.miss("empty")
             return None
         if hasattr(rec.key_payload, "data") and not hasattr(rec.key_payload, "indices"):
             # a live-path hot window, stored as it is
+            self.metrics.inc("loads")
+            self.metrics.inc("hits")
             return (np.asarray(rec.key_payload.data, np.float32).reshape(rec.shape),
                     np.asarray(rec.value_payload.data, np.float32).reshape(rec.shape))
         try:
-            k = self._quantizer("key", rec.head_dim, rec.n_heads).decompress(rec.key_payload)
-            v = self._quantizer("value", rec.head_dim, rec.n_heads).decompress(rec.value_payload)
-            return (np.asarray(k, dtype=np.float32).reshape(rec.shape),
-                    np.asarray(v, dtype=np.float32).reshape(rec.shape))
+            with self.metrics.timed("load"):
+                k = self._quantizer("key", rec.head_dim, rec.n_heads).decompress(rec.key_payload)
+                v = self._quantizer("value", rec.head_dim, rec.n_heads).decompress(rec.value_payload)
+                out = (np.asarray(k, dtype=np.float32).reshape(rec.shape),
+                       np.asarray(v, dtype=np.float32).reshape(rec.shape))
+            self.metrics.inc("loads")
+            self.metrics.inc("hits")
+            return out
         except Exception:
             logger.warning("undecodable KV record (%s, %s): treated as a miss", request_id,
                            layer_name, exc_info=True)
+            self.metrics.miss("corrupt")
+            self.metrics.inc("integrity_failures")
             with self._lock:
                 self._records.pop((request_id, layer_name), None)
             return None
@@ -293,6 +331,8 @@ class TurboQuantBlockStore:
             for key in gone:
                 del self._records[key]
             self._tokens.pop(request_id, None)
+        if gone:
+            self.metrics.inc("evictions", len(gone))
         return len(gone)
 
     def stats(self) -> dict:
@@ -333,17 +373,20 @@ class TurboQuantBlockStore:
             blob = item["blob"]
             if _sha256(blob) != item.get("sha256"):
                 logger.warning("integrity failure on %r: skipped", key)
+                self.metrics.inc("integrity_failures")
                 continue
             try:
                 rec = rec_from_blob(blob)
             except Exception:
                 logger.warning("undecodable record %r: skipped", key, exc_info=True)
+                self.metrics.inc("integrity_failures")
                 continue
             rid, layer = key.split("\x00", 1)
             with self._lock:
                 self._records[(rid, layer)] = rec
                 self._tokens[rid] = rec.num_tokens
             accepted += 1
+        self.metrics.inc("records_restored", accepted)
         return accepted
 
     def save_to_dir(self, path: str) -> int:
@@ -381,6 +424,7 @@ class TurboQuantBlockStore:
         sync_dir()
         write_synced(state["profile_digest"], "COMMIT")
         sync_dir()
+        self.metrics.inc("records_persisted", len(manifest["records"]))
         return len(manifest["records"])
 
     def load_from_dir(self, path: str) -> int:
