@@ -249,8 +249,9 @@ def encode_keys(x: np.ndarray, outlier_frac: float, zero_point: str = "calibrate
 
     Restates turboquant_pro/per_channel_kv.py:269-283 (outliers) and
     :285-401 (nf4_asym) with the zero point of :327-345: the channel mean
-    ("calibrated"), the mean on the DC channels only ("sparse"), or the
-    RoPE-averaged k_proj bias of positions ``[position_start, +S)`` ("bias").
+    ("calibrated"), the mean on the DC channels only ("sparse"), the
+    RoPE-averaged k_proj bias of positions ``[position_start, +S)`` ("bias"),
+    or none ("symmetric": symmetric NF4, :354-357).
     ``nf4_mean`` holds the zero point of every channel (the reference stores
     only the DC channels for "sparse" and nothing for "bias").  The reference
     works on a ``(1, H, S, D)`` array; the same shape is used here so NumPy's
@@ -262,6 +263,11 @@ def encode_keys(x: np.ndarray, outlier_frac: float, zero_point: str = "calibrate
     if zero_point == "bias":
         mean = np.broadcast_to(rope_averaged_bias(k_bias, rope_theta, D, position_start, S)[None],
                                (1, H, D))
+    elif zero_point == "symmetric":
+        # PerChannelKV(nf4=True) without nf4_asym (per_channel_kv.py:354-357):
+        # the raw channel's abs-max scales the grid, no mean (zero here, and
+        # 0 + fl(amax * NF4[l]) is fl(amax * NF4[l]) exactly)
+        mean = np.zeros((1, H, D), np.float32)
     elif zero_point == "sparse":
         mean = x4.mean(axis=2) * dc_channel_mask(rope_theta, D, S)[None, None, :]
     else:

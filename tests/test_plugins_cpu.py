@@ -68,9 +68,11 @@ def test_per_channel_constructor_validation():
     # valid reference configurations without a gfx950 encode
     uni = PL.create("per_channel", bits=4, outlier_frac=0.02)      # the reference's default mode
     assert uni.uniform and uni.key_grid == "uniform"
-    for cfg in (dict(nf4=True), dict(nuq=True), dict(nf4_asym=True, head_dim=64)):
+    for cfg in (dict(nuq=True), dict(nf4_asym=True, head_dim=64)):
         with pytest.raises(NotImplementedError):
             PL.create("per_channel", **cfg)
+    sym = PL.create("per_channel", nf4=True)                         # symmetric NF4
+    assert sym.symmetric and sym.key_grid == "nf4_asym" and not sym.uniform
     for b in (2, 3):                                                  # uniform 3- and 2-bit keys
         low = PL.create("per_channel", bits=b, outlier_frac=0.02)
         assert low.uniform and low.bits == b

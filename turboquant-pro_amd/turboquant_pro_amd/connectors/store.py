@@ -239,6 +239,8 @@ class TurboQuantBlockStore:
                 raise ValueError(f"stored keys are {'uniform' if uniform else 'asym-NF4'}, the pool's "
                                  f"{pool.key_grid}")
             zp = "calibrated" if uniform else getattr(kp, "zp_mode", "calibrated")
+            if zp == "calibrated" and not uniform and getattr(kp, "nf4_mean", None) is None:
+                zp = "symmetric"  # symmetric NF4: no mean stored (per_channel_kv.py:354-357)
             if zp != pool.zero_point:
                 raise ValueError(f"stored key zero point {zp!r}, the pool's {pool.zero_point!r}")
             if zp != "calibrated":

@@ -109,12 +109,16 @@ class TurboQuantKVCache:
         # or quantile flag, the reference's uniform mode (its default, at 2, 3 or
         # 4 bits); per_channel_keys=False: PolarQuant keys
         uniform = per_channel_keys and not key_nuq and not key_nf4
-        if per_channel_keys and (key_nuq or not (key_nf4_asym or uniform)):
+        if per_channel_keys and key_nuq:
             raise NotImplementedError(
                 "the gfx950 cache codes keys per channel as asym-NF4 (TurboQuantKVCache.robust / "
-                "AutoConfig.build_cache) or uniform 2/3/4-bit, or as PolarQuant "
-                "(per_channel_keys=False); symmetric-NF4 and quantile keys have no GPU form here")
+                "AutoConfig.build_cache), symmetric NF4 or uniform 2/3/4-bit, or as PolarQuant "
+                "(per_channel_keys=False); data-fit quantile keys have no GPU form here")
         self.key_grid = "polar" if not per_channel_keys else "uniform" if uniform else "nf4_asym"
+        # symmetric NF4 (key_nf4 without key_nf4_asym, per_channel_kv.py:354-357):
+        # the asym-NF4 encode with no mean
+        self._pool_zero_point = ("symmetric" if per_channel_keys and key_nf4 and not key_nf4_asym
+                                 else key_zero_point)
         if head_dim != 128:
             raise NotImplementedError("the gfx950 kernels are built for head_dim=128")
         if group_tokens_for(hot_window) > 256 or hot_window < 1:
@@ -131,7 +135,7 @@ class TurboQuantKVCache:
                         outlier_frac=self.key_outlier_frac if self.key_grid != "polar" else 0.0,
                         seed=self.seed, rotation=rotation,
                         device=self._device, key_grid=self.key_grid,
-                        zero_point=self.key_zero_point, rope_theta=self.key_rope_theta,
+                        zero_point=self._pool_zero_point, rope_theta=self.key_rope_theta,
                         k_bias=self.key_k_bias)
 
     def _grow(self, need: int) -> None:

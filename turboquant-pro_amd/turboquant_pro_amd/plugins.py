@@ -281,19 +281,22 @@ def _stream():
     return ctypes.c_void_p(_torch().cuda.current_stream().cuda_stream)
 
 
-_ZERO_POINTS = {"calibrated": 0, "sparse": 1, "bias": 2}
+# the block descriptor's zero points; symmetric NF4 is its "sparse" mode with
+# no DC channel (every mean 0)
+_ZERO_POINTS = {"calibrated": 0, "sparse": 1, "bias": 2, "symmetric": 1}
 
 
 class PerChannelKVQuantizer:
     """``"per_channel"`` keys on the gfx950 library: asym-NF4 4-bit (zero
-    point "calibrated", "sparse" or "bias") or uniform 2-, 3- or 4-bit (the
-    reference's default mode), with the fp16 outlier side-list; every (b, h)
-    pair of a block is one group.
+    point "calibrated", "sparse" or "bias"), symmetric NF4 (``nf4=True``
+    without ``nf4_asym``) or uniform 2-, 3- or 4-bit (the reference's default
+    mode), with the fp16 outlier side-list; every (b, h) pair of a block is
+    one group.
 
     The constructor validates like ``PerChannelKV.__init__``
     (turboquant_pro/per_channel_kv.py:182-213) and raises
     ``NotImplementedError`` for the modes the library does not encode
-    (symmetric NF4, data-fit quantiles, head_dim != 128)."""
+    (data-fit quantiles, head_dim != 128)."""
 
     _ZP_MODES = ("calibrated", "sparse", "bias")
 
@@ -319,11 +322,14 @@ class PerChannelKVQuantizer:
         if zero_point == "bias" and k_bias is None:
             raise ValueError('zero_point="bias" requires k_bias')
         uniform = not nf4 and not nuq
-        if not (nf4_asym or uniform) or head_dim != 128:
-            raise NotImplementedError("the gfx950 key encode is per-channel asym-NF4 (any zero point) "
+        if nuq or head_dim != 128:
+            raise NotImplementedError("the gfx950 key encode is per-channel asym-NF4 (any zero point), "
+                                      "symmetric NF4 "
                                       "or uniform 2/3/4-bit, at head_dim 128")
         self.head_dim, self.n_heads, self.bits = head_dim, n_heads, bits
         self.uniform = uniform
+        # symmetric NF4 (nf4 without nf4_asym): the asym-NF4 encode with no mean
+        self.symmetric = nf4 and not nf4_asym
         self.key_grid = "uniform" if uniform else "nf4_asym"
         self.nuq, self.nf4, self.nf4_asym = nuq, nf4, nf4_asym
         self.outlier_frac, self.zero_point = outlier_frac, zero_point
@@ -345,8 +351,9 @@ class PerChannelKVQuantizer:
         if D != self.head_dim:
             raise ValueError(f"head_dim {D} != {self.head_dim}")
         k = outliers_per_channel(S, self.outlier_frac)
-        zp_mode = "calibrated" if self.uniform else self.zero_point
-        dc = dc_channel_mask(self.rope_theta, D, S) if zp_mode == "sparse" else None
+        zp_mode = "calibrated" if self.uniform else "symmetric" if self.symmetric else self.zero_point
+        dc = (dc_channel_mask(self.rope_theta, D, S) if zp_mode == "sparse"
+              else np.zeros(D, bool) if zp_mode == "symmetric" else None)
         zp = None
         if zp_mode == "bias":
             if H != self.n_heads:
@@ -387,11 +394,15 @@ class PerChannelKVQuantizer:
             return CompressedPerChannelKV(indices, sc[:, :, None, :], zr[:, :, None, :], self.bits,
                                           (B, H, S, D), packed, outlier_idx=oidx, outlier_val=oval)
         # the stored zero point: every channel's, the DC channels', or none
-        mean = {"calibrated": zr, "sparse": zr[:, :, dc] if dc is not None else None, "bias": None}[zp_mode]
+        # (bias: recomputed; symmetric NF4: there is none, and its container
+        # says "calibrated", per_channel_kv.py:354-357)
+        mean = {"calibrated": zr, "sparse": zr[:, :, dc] if dc is not None else None, "bias": None,
+                "symmetric": None}[zp_mode]
+        stored_mode = "calibrated" if zp_mode == "symmetric" else zp_mode
         return CompressedPerChannelKV(
             indices, None, None, self.bits, (B, H, S, D), packed, nf4_scale=sc, nf4_mean=mean,
-            outlier_idx=oidx, outlier_val=oval, zp_mode=zp_mode,
-            rope_theta=self.rope_theta if zp_mode != "calibrated" else None,
+            outlier_idx=oidx, outlier_val=oval, zp_mode=stored_mode,
+            rope_theta=self.rope_theta if stored_mode != "calibrated" else None,
             position_start=position_start)
 
     def decompress(self, c: CompressedPerChannelKV) -> np.ndarray:

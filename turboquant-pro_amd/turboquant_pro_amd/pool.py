@@ -29,7 +29,9 @@ from .formats import (NF4_ZERO_CODE, codes_from_key_rows, key_rows_from_codes, n
 from .codebooks import (dc_channel_mask, dc_mask_words, group_tokens_for, n_groups_for,
                         outliers_per_channel, random_rotation, rope_averaged_bias, value_codebook)
 
-ZERO_POINTS = {"calibrated": 0, "sparse": 1, "bias": 2}
+# key zero points; "symmetric" (symmetric NF4: no mean, per_channel_kv.py:354-357)
+# is the descriptor's "sparse" mode with no DC channel, so every mean is 0
+ZERO_POINTS = {"calibrated": 0, "sparse": 1, "bias": 2, "symmetric": 1}
 # key forms: per-channel asym-NF4, per-channel uniform, PolarQuant (the value
 # encode on the keys: per-token norms, rotated codes on the value codebook)
 KEY_GRIDS = {"nf4_asym": 0, "uniform": 1, "polar": 2}
@@ -68,7 +70,7 @@ class TQKVPool:
         if zero_point != "calibrated":
             if key_grid != "nf4_asym":
                 raise ValueError(f"zero_point={zero_point!r} requires asym-NF4 keys")
-            if rope_theta is None:
+            if rope_theta is None and zero_point != "symmetric":
                 raise ValueError(f"zero_point={zero_point!r} requires rope_theta")
         if zero_point == "bias" and k_bias is None:
             raise ValueError('zero_point="bias" requires k_bias')
@@ -104,7 +106,8 @@ class TQKVPool:
         self.key_grid = key_grid
         self.zero_point, self.rope_theta = zero_point, rope_theta
         # "sparse": the channels whose rotary wavelength exceeds a group
-        self.dc_mask = dc_channel_mask(rope_theta, head_dim, G) if zero_point == "sparse" else None
+        self.dc_mask = (dc_channel_mask(rope_theta, head_dim, G) if zero_point == "sparse"
+                        else np.zeros(head_dim, bool) if zero_point == "symmetric" else None)
         if self.dc_mask is not None:
             self.desc.dc_mask[:] = dc_mask_words(self.dc_mask)
         self.k_bias = None if k_bias is None else np.asarray(k_bias, np.float32).reshape(n_kv_heads, head_dim)
@@ -462,14 +465,16 @@ class TQKVPool:
                               else nf4_codes(v32, scale[h, j], mean[h, j]))
         kp = pack_key_codes(codes, kb)
         # the reference's stored zero point: every channel's ("calibrated"),
-        # the DC channels' ("sparse") or none ("bias": recomputed from the bias)
+        # the DC channels' ("sparse") or none ("bias": recomputed from the
+        # bias; "symmetric": there is none, and the container says
+        # "calibrated" with no mean, per_channel_kv.py:354-357)
         stored_mean = (mean[:, self.dc_mask] if self.zero_point == "sparse"
-                       else None if self.zero_point == "bias" else mean)
+                       else None if self.zero_point in ("bias", "symmetric") else mean)
         return {
             "kpacked": kp.reshape(-1),
             "nf4_scale": scale,
             "nf4_mean": stored_mean,
-            "zp_mode": self.zero_point,
+            "zp_mode": "calibrated" if self.zero_point == "symmetric" else self.zero_point,
             "position_start": g * G,
             "outlier_idx": oidx.astype(np.int32),
             "outlier_val": oval,
@@ -531,6 +536,8 @@ class TQKVPool:
             self.gscale[slot] = torch.from_numpy(np.asarray(keys["nf4_scale"], np.float32).reshape(H, D)).to(self.device)
             if self.zero_point == "bias":
                 self.gmean[slot] = self.zp_mean[g]
+            elif self.zero_point == "symmetric":
+                self.gmean[slot] = 0.0
             elif self.zero_point == "sparse":
                 full = np.zeros((H, D), np.float32)
                 full[:, self.dc_mask] = np.asarray(keys["nf4_mean"], np.float32).reshape(H, -1)
