@@ -14,7 +14,8 @@
  *     never throws or aborts across the ABI.
  *   - Work is enqueued on the given HIP stream (hipStream_t passed as void*;
  *     NULL = the default stream) and is stream-ordered.
- *   - fp16 data is passed as uint16_t bit patterns (IEEE binary16).
+ *   - fp16 data is passed as uint16_t bit patterns (IEEE binary16); K/V/q
+ *     buffers typed void* are fp16, or fp32 when the descriptor's input_f32 is 1.
  *
  * Storage layout in HBM (one cache pool = one attention layer):
  *   kcodes [n_kv_heads][n_pages][page_tokens][head_dim/2]     u8   (storage of record)
@@ -26,27 +27,31 @@
  *   gmean  [num_gslots][n_kv_heads][head_dim]                 f32  (nf4_mean)
  *   ocount [num_gslots][n_kv_heads][8]  i32 cumulative outlier counts at tokens 32,64,..,256 (last = total)
  *   oent   [num_gslots][n_kv_heads][outlier_cap]              u32  ((s*D + j) | fp16 << 16)
- *   hot_k, hot_v [batch][n_kv_heads][hot_ring][head_dim]      fp16 ring, token t at t % hot_ring
+ *   hot_k, hot_v [batch][n_kv_heads][hot_ring][head_dim]      fp16 (fp32 when input_f32) ring,
+ *                                                             token t at t % hot_ring
  *   block_table [batch][max_pages_per_seq]   i32 physical page of logical page t / page_tokens
  *   group_table [batch][max_groups_per_seq]  i32 group slot of group t / group_tokens
  * The K and V rows are the reference's packed layouts
  * (turboquant_pro/per_channel_kv.py:87-93 and turboquant_pro/core.py:350-398):
  * the key bytes of one (group, head) in page order are the reference
- * container's `indices` slice for that head, except that every position held
- * in oent stores the code whose level is 0 -- NF4's code 7 (nibble 0xE) for
+ * container's `indices` slice for that head, except that (fp16 caches) every
+ * position held in oent stores the code whose level is 0 -- NF4's code 7 (nibble 0xE) for
  * key_grid 0, code 0 for key_grid 1 -- so that the dense part of a decode
  * contributes exactly gmean there and the side-list adds val - gmean (exact
- * only because the stored level's reconstruction equals gmean).  The
+ * only because the stored level's reconstruction equals gmean; fp32 caches
+ * keep the reference's codes there and the VALU decode subtracts the dense
+ * level it reads).  The
  * reference's code at such a position is the nearest level to the stored
  * fp16 value (recomputed on export).  Value bytes are the reference's
- * per-token pack when page_tokens % 16 != 0 or group_tokens % 32 != 0; otherwise
+ * per-token pack when head_dim != 128, input_f32, page_tokens % 16 != 0 or
+ * group_tokens % 32 != 0; otherwise
  * each 16-token tile of a page holds 64 units of head_dim*vb/32 bytes, unit
  * (lg, c) = tokens [4lg, 4lg+4) x channels [8c, 8c+8) with the code of token u,
  * channel nt at bit (2*nt + u/2)*2*vb + (u%2)*vb -- a lossless permutation of
  * the same bits that lets one MFMA lane load its operand with one access.
  * kcodes rows are head_dim*key_bits/8 bytes.  4-bit keys use the reference's
  * pack as above; 3- and 2-bit keys (uniform) a permutation of it: each row is
- * four 32-channel chunks of head_dim*key_bits/32 bytes, and in chunk c the
+ * head_dim/32 chunks of 32 channels (4*key_bits bytes each), and in chunk c the
  * little-endian field i (2*key_bits bits at bit 2*key_bits*i) holds
  * code(32c + 2i) | code(32c + 2i + 1) << key_bits, so one MFMA lane loads its
  * 32 channels with one access and reads a channel pair with one field.
@@ -70,7 +75,8 @@ extern "C" {
 typedef struct tqk_cache_desc {
   int32_t n_kv_heads;           /* Hkv */
   int32_t n_q_heads;            /* Hq, a multiple of Hkv (q-head i reads kv-head i / (Hq/Hkv)) */
-  int32_t head_dim;             /* D; 128 */
+  int32_t head_dim;             /* D: 64, 128 or 256 (the MFMA decode serves 128; 64 and 256 run
+                                   the VALU decode) */
   int32_t hot_window;           /* W; groups flush when the hot window exceeds W */
   int32_t group_tokens;         /* G = (W + 1) / 2, 1..256 */
   int32_t page_tokens;          /* P, divides G */
@@ -93,7 +99,11 @@ typedef struct tqk_cache_desc {
                                    0 "calibrated", the channel mean over the group;
                                    1 "sparse", the channel mean on the dc_mask channels, 0 elsewhere;
                                    2 "bias", zp_mean[g] of the group's index g (host-computed) */
-  uint32_t dc_mask[4];          /* sparse: channel j is a DC channel when bit j % 32 of word j / 32 is set */
+  int32_t input_f32;            /* 0: keys, values and queries arrive as fp16 (the hot ring is fp16);
+                                   1: as fp32 (an fp32 hot ring; codes from the fp32 values, bit-exact
+                                   to the reference on fp32 input, true codes kept at side-list
+                                   positions; decoded by the VALU kernel) */
+  uint32_t dc_mask[8];          /* sparse: channel j is a DC channel when bit j % 32 of word j / 32 is set */
 } tqk_cache_desc;
 
 typedef struct tqk_cache_ptrs {
@@ -104,8 +114,8 @@ typedef struct tqk_cache_ptrs {
   float* gmean;
   int32_t* ocount;
   uint32_t* oent;
-  uint16_t* hot_k;
-  uint16_t* hot_v;
+  void* hot_k;          /* fp16, or fp32 when input_f32 */
+  void* hot_v;
   const int32_t* block_table;
   const int32_t* group_table;
   const float* pi;      /* (D, D) row-major: unrotate y -> y @ pi */
@@ -117,7 +127,7 @@ typedef struct tqk_cache_ptrs {
   float* knorm;         /* key_grid 2: [n_kv_heads][n_pages][page_tokens] f32 key norms; unused otherwise */
 } tqk_cache_ptrs;
 
-/* Library ABI version (bumped on any signature or layout change); this header is version 8. */
+/* Library ABI version (bumped on any signature or layout change); this header is version 9. */
 int tqk_version(void);
 
 /* Validate a descriptor; TQK_OK when the GPU path supports it. */
@@ -139,14 +149,14 @@ size_t tqk_decode_workspace_bytes(const tqk_cache_desc* d, int32_t batch, int32_
  * sequence: out[b][i] = softmax(q[b][i] . K_b^T * sm_scale) V_b over all
  * seq_lens[b] cached tokens of kv-head i / (Hq/Hkv), with the coded groups
  * attended in code space (no reconstruction) and the hot window in fp16.
- *   q        [batch][n_q_heads][head_dim] fp16
+ *   q        [batch][n_q_heads][head_dim] fp16 (fp32 when input_f32)
  *   seq_lens [batch] i32 (device), every entry in [1, max_len]
  *   out      [batch][n_q_heads][head_dim] fp32
  * Replaces TurboQuantKVCache.fused_decode (turboquant_pro/core.py:1168-1265)
  * and the per-page kernel launches behind it (turboquant_pro/kv_kernel.py:319-381).
  */
 int tqk_decode(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t batch,
-               const uint16_t* q, const int32_t* seq_lens, int32_t max_len, float* out,
+               const void* q, const int32_t* seq_lens, int32_t max_len, float* out,
                void* workspace, size_t workspace_bytes, void* stream);
 
 /*
@@ -164,7 +174,7 @@ int tqk_decode(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t batch,
  * counters on `stream`.
  */
 int tqk_decode_noalloc(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t batch,
-                       const uint16_t* q, const int32_t* seq_lens, int32_t max_len, float* out,
+                       const void* q, const int32_t* seq_lens, int32_t max_len, float* out,
                        void* stream);
 
 /*
@@ -175,7 +185,7 @@ int tqk_decode_noalloc(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t
  * partial contract of turboquant_pro/kv_kernel.py:212-213).
  */
 int tqk_decode_partials(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t batch,
-                        const uint16_t* q, const int32_t* seq_lens, int32_t max_len,
+                        const void* q, const int32_t* seq_lens, int32_t max_len,
                         float* m, float* l, float* acc, void* workspace,
                         size_t workspace_bytes, void* stream);
 
@@ -187,7 +197,7 @@ int tqk_decode_partials(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_
  * normalises.  Same arguments and workspace as tqk_decode.
  */
 int tqk_decode_splits(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t batch,
-                      const uint16_t* q, const int32_t* seq_lens, int32_t max_len,
+                      const void* q, const int32_t* seq_lens, int32_t max_len,
                       void* workspace, size_t workspace_bytes, void* stream);
 int tqk_decode_merge(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t batch,
                      int32_t max_len, float* out, void* workspace, size_t workspace_bytes,
@@ -210,7 +220,7 @@ int tqk_decode_merge(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t b
  */
 int tqk_encode_groups(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t batch,
                       int32_t n_items, const int32_t* items, const int32_t* prev_len,
-                      const uint16_t* chunk_k, const uint16_t* chunk_v, int32_t chunk_tokens,
+                      const void* chunk_k, const void* chunk_v, int32_t chunk_tokens,
                       int32_t* overflow, void* stream);
 
 /*
@@ -221,7 +231,7 @@ int tqk_encode_groups(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t 
  */
 int tqk_append_hot(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t batch,
                    const int32_t* prev_len, const int32_t* n_new, const int32_t* hot_start,
-                   const uint16_t* chunk_k, const uint16_t* chunk_v, int32_t chunk_tokens,
+                   const void* chunk_k, const void* chunk_v, int32_t chunk_tokens,
                    void* stream);
 
 /*
@@ -245,14 +255,14 @@ typedef struct tqk_block_desc {
   int32_t batch;                /* B */
   int32_t n_heads;              /* H */
   int32_t tokens;               /* S >= 1 */
-  int32_t head_dim;             /* D = 128 */
+  int32_t head_dim;             /* D: 64, 128 or 256 */
   int32_t bits;                 /* keys: 4, 3 or 2 (3 and 2 uniform only); values: 2, 3 or 4 */
   int32_t key_grid;             /* keys: 0 asym-NF4, 1 uniform */
   int32_t zero_point;           /* asym-NF4 keys: 0 calibrated, 1 sparse, 2 given (zp), as in tqk_cache_desc */
   int32_t outliers_per_channel; /* keys: k = max(1, round(S * outlier_frac)), 0 = no side-list */
   int32_t outlier_cap;          /* keys: side-list capacity per (b, h) */
   int32_t input_f32;            /* 1: x is fp32, 0: x is fp16 */
-  uint32_t dc_mask[4];          /* sparse: DC channels, as in tqk_cache_desc */
+  uint32_t dc_mask[8];          /* sparse: DC channels, as in tqk_cache_desc */
 } tqk_block_desc;
 
 /*

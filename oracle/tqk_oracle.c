@@ -15,7 +15,8 @@
  *   flat C-order index over (1, H, S, D).
  * Values, one vector (D) fp32, turboquant_pro/core.py:569-606:
  *   norm  = sqrt of NumPy's pairwise sum of squares (8 strided accumulators
- *           for D <= 128, combined ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)))
+ *           per run of <= 128, combined ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7));
+ *           a longer row is its halves' sums added)
  *   u     = v / max(norm, 1e-30)
  *   y_e   = sequential-over-d fl(y + fl(u_d * PiT[d][e]))   (np.einsum, no FMA)
  *   code  = #{ b < y }                                      (searchsorted left)
@@ -37,13 +38,21 @@ static int cmp_float(const void* a, const void* b) {
   return (x > y) - (x < y);
 }
 
-/* NumPy's pairwise summation for a contiguous float32 run of n <= 128 values
- * (numpy/_core/src/umath/loops_utils.h.src, pairwise_sum). */
+/* NumPy's pairwise summation of a contiguous float32 run
+ * (numpy/_core/src/umath/loops_utils.h.src, pairwise_sum): n < 8 sequential;
+ * n <= 128 eight strided accumulators combined as a tree, then the remainder;
+ * longer runs split at n / 2 rounded down to a multiple of 8, halves summed
+ * apart and added. */
 static float pairwise_sum_f32(const float* a, int n) {
   if (n < 8) {
     float r = 0.0f;  /* numpy starts from -0.0 for n<8 then adds; equal for our use */
     for (int i = 0; i < n; ++i) r += a[i];
     return r;
+  }
+  if (n > 128) {
+    int n2 = n / 2;
+    n2 -= n2 % 8;
+    return pairwise_sum_f32(a, n2) + pairwise_sum_f32(a + n2, n - n2);
   }
   float r[8];
   for (int k = 0; k < 8; ++k) r[k] = a[k];

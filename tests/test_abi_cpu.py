@@ -46,7 +46,9 @@ def test_check_desc_status_codes():
     N, lib = _lib()
     ok = _desc(N)
     assert lib.tqk_check_desc(ctypes.byref(ok)) == N.TQK_OK
-    assert lib.tqk_check_desc(ctypes.byref(_desc(N, head_dim=64))) == N.TQK_EUNSUPPORTED
+    # head dims the kernels are built for: 64, 128, 256
+    for D, rc in ((64, N.TQK_OK), (256, N.TQK_OK), (96, N.TQK_EUNSUPPORTED), (512, N.TQK_EUNSUPPORTED)):
+        assert lib.tqk_check_desc(ctypes.byref(_desc(N, head_dim=D))) == rc, D
     assert lib.tqk_check_desc(ctypes.byref(_desc(N, value_bits=2))) == N.TQK_OK
     assert lib.tqk_check_desc(ctypes.byref(_desc(N, value_bits=5))) == N.TQK_EUNSUPPORTED
     assert lib.tqk_check_desc(ctypes.byref(_desc(N, zero_point=2))) == N.TQK_OK

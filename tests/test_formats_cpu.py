@@ -130,3 +130,24 @@ def test_uniform_outlier_codes_round_trip(golden_dir):
         back = F.restore_outlier_codes(stored, idx, z[f"{tag}_oval"], z[f"{tag}_scale"], z[f"{tag}_zero"],
                                        grid="uniform")
         assert np.array_equal(back, kp)
+
+
+def test_key_rows_follow_the_chunk_layout_at_every_head_dim():
+    """3- and 2-bit key rows: D / 32 chunks of 4 * bits bytes, chunk c's
+    little-endian field i = code(32c + 2i) | code(32c + 2i + 1) << bits,
+    checked bit by bit from that definition, and the unpack inverts it."""
+    rng = np.random.default_rng(4)
+    for D in (64, 128, 256):
+        for bits in (2, 3, 4):
+            codes = rng.integers(0, 2 ** bits, size=(5, D), dtype=np.uint8)
+            rows = F.key_rows_from_codes(codes, bits)
+            assert rows.shape == (5, D * bits // 8)
+            assert np.array_equal(F.codes_from_key_rows(rows, bits, D), codes), (D, bits)
+            if bits == 4:
+                continue
+            for t in range(5):
+                for c in range(D // 32):
+                    chunk = int.from_bytes(rows[t, 4 * bits * c:4 * bits * (c + 1)].tobytes(), "little")
+                    for i in range(16):
+                        f = (chunk >> (2 * bits * i)) & ((1 << 2 * bits) - 1)
+                        assert f == int(codes[t, 32 * c + 2 * i]) | int(codes[t, 32 * c + 2 * i + 1]) << bits

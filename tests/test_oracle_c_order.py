@@ -63,20 +63,52 @@ def test_keys_c_equals_numpy_with_ties(clib):
     assert np.array_equal(codes, want.codes) and np.array_equal(oidx, want.outlier_idx)
 
 
-@pytest.mark.parametrize("bits", [3, 4])
-def test_values_c_equals_numpy(clib, bits):
-    _, v, _ = O.synthetic_kv(5, 1, 2, 2, 256)
+@pytest.mark.parametrize("bits,D", [(3, 128), (4, 128), (3, 64), (2, 64), (3, 256), (4, 256)])
+def test_values_c_equals_numpy(clib, bits, D):
+    _, v, _ = O.synthetic_kv(5, 1, 2, 2, 256, D=D)
     x = v[0].astype(np.float32)
-    pi, pi_t = O.rotation(0, 128)
-    cent, bnd = O.polar_codebook(bits, 128)
+    pi, pi_t = O.rotation(0, D)
+    cent, bnd = O.polar_codebook(bits, D)
     want = O.encode_values(x, pi_t, bnd, bits)
-    rows = np.ascontiguousarray(x.reshape(-1, 128))
+    rows = np.ascontiguousarray(x.reshape(-1, D))
     codes = np.zeros(rows.shape, np.uint8)
     norms = np.zeros(rows.shape[0], np.float32)
-    clib.tqo_encode_values(_p(rows), rows.shape[0], 128, _p(pi_t), _p(bnd), bnd.size,
+    clib.tqo_encode_values(_p(rows), rows.shape[0], D, _p(pi_t), _p(bnd), bnd.size,
                            _p(codes), _p(norms))
     assert np.array_equal(norms, want.norms.reshape(-1))
-    assert np.array_equal(codes, want.codes.reshape(-1, 128))
+    assert np.array_equal(codes, want.codes.reshape(-1, D))
+
+
+@pytest.mark.parametrize("D", [64, 256])
+def test_keys_c_equals_numpy_head_dims(clib, D):
+    k, _, _ = O.synthetic_kv(11, 1, 2, 2, 256, D=D)
+    x = k[0].astype(np.float32)
+    want = O.encode_keys(x, 0.02)
+    codes, scale, mean, oidx = _c_keys(clib, x, O.outlier_count_per_channel(256, 0.02))
+    assert np.array_equal(scale, want.nf4_scale) and np.array_equal(mean, want.nf4_mean)
+    assert np.array_equal(codes, want.codes) and np.array_equal(oidx, want.outlier_idx)
+
+
+def _blocked8(sq):
+    """Eight strided accumulators over the whole row, one tree: NumPy's order
+    for rows of at most 128 values only."""
+    r = sq[:, :8].copy()
+    for i in range(8, sq.shape[1], 8):
+        r = r + sq[:, i:i + 8]
+    return ((r[:, 0] + r[:, 1]) + (r[:, 2] + r[:, 3])) + ((r[:, 4] + r[:, 5]) + (r[:, 6] + r[:, 7]))
+
+
+def test_norm_split_at_256_is_pinned():
+    """At D = 256 NumPy sums the two 128-channel halves apart: one 8-way
+    block over all 256 values differs from np.linalg.norm's sum on some rows,
+    so the half split the C oracle (and the kernels) use is what the bit-exact
+    norm tests above pin."""
+    rows = np.random.default_rng(3).standard_normal((4096, 256)).astype(np.float32) * 3
+    sq = rows * rows
+    ref = np.add.reduce(sq, axis=-1)
+    halves = _blocked8(sq[:, :128]) + _blocked8(sq[:, 128:])
+    assert np.array_equal(halves, ref)
+    assert np.count_nonzero(_blocked8(sq) != ref) > 0
 
 
 def test_fma_order_would_be_caught(clib):

@@ -68,9 +68,11 @@ def test_per_channel_constructor_validation():
     # valid reference configurations without a gfx950 encode
     uni = PL.create("per_channel", bits=4, outlier_frac=0.02)      # the reference's default mode
     assert uni.uniform and uni.key_grid == "uniform"
-    for cfg in (dict(nuq=True), dict(nf4_asym=True, head_dim=64)):
+    for cfg in (dict(nuq=True), dict(nf4_asym=True, head_dim=96)):
         with pytest.raises(NotImplementedError):
             PL.create("per_channel", **cfg)
+    for D in (64, 256):                                               # head dims of the kernels
+        assert PL.create("per_channel", nf4_asym=True, head_dim=D).head_dim == D
     sym = PL.create("per_channel", nf4=True)                         # symmetric NF4
     assert sym.symmetric and sym.key_grid == "nf4_asym" and not sym.uniform
     for b in (2, 3):                                                  # uniform 3- and 2-bit keys
@@ -90,7 +92,7 @@ def test_polar_constructor_validation():
     with pytest.raises(ValueError):
         PL.create("polar", value_bits=1)
     with pytest.raises(NotImplementedError):
-        PL.create("polar", head_dim=64)
+        PL.create("polar", head_dim=96)
     # widths per kind, as TurboQuantKV._resolve_bits (turboquant_pro/core.py:528-540)
     kv = PL.create("polar", bits=3, key_bits=4, value_bits=2, seed=0)
     assert (kv._width(None), kv._width("key"), kv._width("value")) == (3, 4, 2)

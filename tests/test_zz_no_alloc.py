@@ -8,7 +8,6 @@ import ctypes
 import numpy as np
 import pytest
 
-from gpu_util import assert_attn_close
 from oracle import tq_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -55,11 +54,6 @@ def test_noalloc_matches_workspace_decode_on_shrinking_calls():
         pool, q = _pool_with(torch, B, Hkv, Hq, lens, hot_window=W, seed=10 + i)
         ref, got = _both(torch, pool, q)
         assert np.isfinite(got).all()
-        if W == 512:
-            # the MFMA kernel is deterministic: the same kernels over the same
-            # data give identical outputs
-            assert np.array_equal(ref, got), f"call {i}: max diff {np.abs(ref - got).max():.3e}"
-        else:
-            # the VALU kernel adds outlier corrections with LDS float atomics,
-            # whose order varies from run to run (last-bit differences)
-            assert_attn_close(got, ref, atol=1e-5, rtol=1e-5, what=f"call {i}")
+        # both decode kernels are deterministic: the same kernels over the
+        # same data give identical outputs
+        assert np.array_equal(ref, got), f"call {i}: max diff {np.abs(ref - got).max():.3e}"

@@ -16,15 +16,15 @@
 //               code = clip(rint((x - min) / scale), 0, 2^bits - 1)
 //   key packing (per_channel_kv.py:87-100): each code's bits LSB first, in
 //   MSB-first bytes, codes in (b, h, s, j) order (4-bit: byte n =
-//   rev4(code[2n]) << 4 | rev4(code[2n+1]); a token row is 16 * bits bytes)
+//   rev4(code[2n]) << 4 | rev4(code[2n+1]); a token row is D * bits / 8 bytes)
 //     outliers: threshold = k-th largest |x| over s; every |x| >= it, (s, j) order
-//   values (turboquant_pro/core.py:569-606): pairwise-8 norm, u = x / max(norm, 1e-30),
+//   values (turboquant_pro/core.py:569-606): pairwise norm, u = x / max(norm, 1e-30),
 //     y_e = sequential over d of u_d * Pi[e][d], code = #{ boundaries < y_e }
 #include "tqk_common.h"
 
 namespace {
 
-constexpr int kKbThreads = 256;  // key block: one workgroup per (b, h)
+constexpr int kKbThreads = 256;  // key dequant kernels
 constexpr int kVbThreads = 512;  // value block: 64 tokens per workgroup
 constexpr int kVbTokens = 64;
 
@@ -65,8 +65,10 @@ struct KeyBlockArgs {
   int32_t* out_count;
 };
 
-__global__ __launch_bounds__(kKbThreads) void tqk_key_block(KeyBlockArgs a) {
-  constexpr int D = TQK_D;
+// one workgroup of 2 * D threads per (b, h)
+template <int D>
+__global__ __launch_bounds__(2 * D) void tqk_key_block(KeyBlockArgs a) {
+  constexpr int T = 2 * D;  // threads
   const tqk_block_desc& d = a.d;
   const int bh = blockIdx.x, h = bh % d.n_heads, tid = threadIdx.x;
   const int S = d.tokens, f32 = d.input_f32, kout = d.outliers_per_channel;
@@ -75,9 +77,9 @@ __global__ __launch_bounds__(kKbThreads) void tqk_key_block(KeyBlockArgs a) {
 
   __shared__ float cent_s[D][17];  // per-channel grid (uniform: min, scale)
   __shared__ float thr_s[D];       // outlier threshold magnitude per channel
-  __shared__ int32_t wsum_s[kKbThreads / 64];
+  __shared__ int32_t wsum_s[T / 64];
 
-  // ---- per-channel statistics (threads 0..127) and thresholds (128..255)
+  // ---- per-channel statistics (threads 0..D-1) and thresholds (D..2D-1)
   if (tid < D) {
     const int j = tid;
     if (d.key_grid == 1) {
@@ -136,21 +138,21 @@ __global__ __launch_bounds__(kKbThreads) void tqk_key_block(KeyBlockArgs a) {
 
   // ---- codes of 3- and 2-bit (uniform) keys: one token row per thread
   if (d.bits != 4) {
-    const int bits = d.bits, rwords = 4 * bits;  // 16 * bits bytes per token
+    const int bits = d.bits, rwords = D * bits / 32;  // D * bits / 8 bytes per token
     const float qmax = (float)((1 << bits) - 1);
-    for (int s = tid; s < S; s += kKbThreads) {
-      uint32_t rw[16] = {0u};
+    for (int s = tid; s < S; s += T) {
+      uint32_t rw[D / 8] = {0u};
       for (int j = 0; j < D; ++j) {
         const float r = __builtin_rintf(__fdiv_rn(__fsub_rn(X(s, j), cent_s[j][0]), cent_s[j][1]));
         put_code_ref(rw, j, bits, (uint32_t)fminf(fmaxf(r, 0.0f), qmax));
       }
-      uint32_t* dst = reinterpret_cast<uint32_t*>(a.packed + ((size_t)bh * S + s) * (size_t)(16 * bits));
+      uint32_t* dst = reinterpret_cast<uint32_t*>(a.packed + ((size_t)bh * S + s) * (size_t)(D * bits / 8));
       for (int w = 0; w < rwords; ++w) dst[w] = rw[w];
     }
   }
   // ---- 4-bit codes: thread = (channel pair, token slice), one byte per (token, pair)
   else {
-    const int jp = tid & 63, sq = tid >> 6;
+    const int jp = tid % (D / 2), sq = tid / (D / 2);  // four token slices
     const int per = (S + 3) / 4, s0 = sq * per, s1 = min(S, s0 + per);
     uint8_t* out = a.packed + base / 2 + jp;
     if (d.key_grid == 1) {
@@ -190,7 +192,7 @@ __global__ __launch_bounds__(kKbThreads) void tqk_key_block(KeyBlockArgs a) {
   // range, counts its entries, takes its offset from a block scan, writes
   if (kout > 0) {
     const bool all = kout >= S;
-    const int chunk = (S + kKbThreads - 1) / kKbThreads;
+    const int chunk = (S + T - 1) / T;
     const int s0 = min(S, tid * chunk), s1 = min(S, s0 + chunk);
     int cnt = 0;
     for (int s = s0; s < s1; ++s)
@@ -204,7 +206,7 @@ __global__ __launch_bounds__(kKbThreads) void tqk_key_block(KeyBlockArgs a) {
     if ((tid & 63) == 63) wsum_s[tid >> 6] = incl;
     __syncthreads();
     int off = incl - cnt, total = 0;
-    for (int w = 0; w < kKbThreads / 64; ++w) {
+    for (int w = 0; w < T / 64; ++w) {
       if (w < (tid >> 6)) off += wsum_s[w];
       total += wsum_s[w];
     }
@@ -240,9 +242,8 @@ struct ValueBlockArgs {
 // norm in the reference's pairwise order and stage the normalised row in LDS;
 // then the rotation as in the group encode (DPP row broadcasts of register-
 // held row slices, a column of Pi_T per lane).
-template <int VB>
+template <int VB, int D>
 __global__ __launch_bounds__(kVbThreads) void tqk_value_block(ValueBlockArgs a) {
-  constexpr int D = TQK_D;
   constexpr int VROW = D * VB / 8;
   const tqk_block_desc& d = a.d;
   const int S = d.tokens, bh = blockIdx.y, t0 = blockIdx.x * kVbTokens, tid = threadIdx.x;
@@ -255,84 +256,35 @@ __global__ __launch_bounds__(kVbThreads) void tqk_value_block(ValueBlockArgs a) 
     const int tt = tid >> 2, q = tid & 3;
     if (tt < nb) {
       const size_t row = (tok0 + tt) * D;
-      float x0[16], x1[16];
+      float x0[D / 8], x1[D / 8];
 #pragma unroll
-      for (int m = 0; m < 16; ++m) {  // channels 8m + 2q, 8m + 2q + 1
+      for (int m = 0; m < D / 8; ++m) {  // channels 8m + 2q, 8m + 2q + 1
         x0[m] = load_x(a.x, d.input_f32, row + 8 * m + 2 * q);
         x1[m] = load_x(a.x, d.input_f32, row + 8 * m + 2 * q + 1);
       }
-      float r0 = __fmul_rn(x0[0], x0[0]), r1 = __fmul_rn(x1[0], x1[0]);
-#pragma unroll
-      for (int m = 1; m < 16; ++m) {
-        r0 = __fadd_rn(r0, __fmul_rn(x0[m], x0[m]));
-        r1 = __fadd_rn(r1, __fmul_rn(x1[m], x1[m]));
-      }
-      // pairwise tree ((r0 + r1) + (r2 + r3)) + ((r4 + r5) + (r6 + r7))
-      const float pa = __fadd_rn(r0, r1);
-      const float po = __shfl_xor(pa, 1, 4);
-      const float pb = (q & 1) ? __fadd_rn(po, pa) : __fadd_rn(pa, po);
-      const float pbo = __shfl_xor(pb, 2, 4);
-      const float ss = (q & 2) ? __fadd_rn(pbo, pb) : __fadd_rn(pb, pbo);
+      const float ss = pairwise_sumsq<D>(x0, x1, q);
       const float nrm = __builtin_sqrtf(ss);  // correctly rounded (-fhip-fp32-correctly-rounded-divide-sqrt)
       const float safe = fmaxf(nrm, 1e-30f);
 #pragma unroll
-      for (int m = 0; m < 16; ++m) {
+      for (int m = 0; m < D / 8; ++m) {
         u_s[tt][8 * m + 2 * q] = __fdiv_rn(x0[m], safe);
         u_s[tt][8 * m + 2 * q + 1] = __fdiv_rn(x1[m], safe);
       }
       if (q == 0) a.norms[tok0 + tt] = nrm;
     }
   }
-  // rotation: wave w owns the 16 rotated channels [16w, 16w + 16), lane l
-  // column e = 16w + (l & 15) of Pi_T (row e of Pi) in registers; each 16-lane
-  // row takes one token of a 4-token step, holds eight channels of its
-  // normalised row and broadcasts them to the row by DPP (no LDS broadcast
-  // reads); every y_e is the sequential, separately rounded sum over d
-  const int lane = tid & 63, wv = tid >> 6, rt = lane >> 4, li = lane & 15;
-  const int ecol = 16 * wv + li;
-  static_assert(kVbThreads / 64 * 16 == D, "eight waves of 16 rotated channels");
-  float pcol[D];
-#pragma unroll
-  for (int k = 0; k < D / 4; ++k) {
-    const float4 p4 = reinterpret_cast<const float4*>(a.pi + (size_t)ecol * D)[k];
-    pcol[4 * k] = p4.x;
-    pcol[4 * k + 1] = p4.y;
-    pcol[4 * k + 2] = p4.z;
-    pcol[4 * k + 3] = p4.w;
-  }
+  // rotation: wave w owns the rotated channels [16w + 128p, +16) of pass p,
+  // lane l column e = 16w + 128p + (l & 15) of Pi_T (row e of Pi) in
+  // registers; each 16-lane row takes one token of a 4-token step, holds
+  // eight channels of its normalised row and broadcasts them to the row by
+  // DPP (rotate_codes, no LDS broadcast reads)
+  const int lane = tid & 63, wv = tid >> 6;
   float bnd[15];
 #pragma unroll
   for (int k = 0; k < (1 << VB) - 1; ++k) bnd[k] = a.vbnd[k];
   __syncthreads();
-  for (int j0 = 0; j0 < nb; j0 += 8) {
-    const int ja = j0 + rt, jb = j0 + 4 + rt;
-    float ua[8], ub[8];
-    {
-      const float4* ra = reinterpret_cast<const float4*>(&u_s[min(ja, nb - 1)][8 * li]);
-      const float4* rb = reinterpret_cast<const float4*>(&u_s[min(jb, nb - 1)][8 * li]);
-      const float4 a0 = ra[0], a1 = ra[1], b0 = rb[0], b1 = rb[1];
-      ua[0] = a0.x; ua[1] = a0.y; ua[2] = a0.z; ua[3] = a0.w;
-      ua[4] = a1.x; ua[5] = a1.y; ua[6] = a1.z; ua[7] = a1.w;
-      ub[0] = b0.x; ub[1] = b0.y; ub[2] = b0.z; ub[3] = b0.w;
-      ub[4] = b1.x; ub[5] = b1.y; ub[6] = b1.z; ub[7] = b1.w;
-    }
-    float y0 = 0.f, y1 = 0.f;
-    rotate_row_dpp<0>(y0, y1, ua, ub, pcol);
-    // keeps the sums out of the conditional stores below: sunk into them, the
-    // multiplies would leave their broadcasts behind as separate moves
-    asm volatile("" : "+v"(y0), "+v"(y1));
-    uint32_t c0 = 0, c1 = 0;
-#pragma unroll
-    for (int k = 0; k < (1 << VB) - 1; ++k) {
-      c0 += (bnd[k] < y0) ? 1u : 0u;
-      c1 += (bnd[k] < y1) ? 1u : 0u;
-    }
-    // searchsorted places NaN after every boundary
-    if (y0 != y0) c0 = (1u << VB) - 1u;
-    if (y1 != y1) c1 = (1u << VB) - 1u;
-    if (ja < nb) vc_s[ja][ecol] = (uint8_t)c0;
-    if (jb < nb) vc_s[jb][ecol] = (uint8_t)c1;
-  }
+  for (int e0 = 16 * wv; e0 < D; e0 += 16 * (kVbThreads / 64))
+    rotate_codes<D, VB>(a.pi, u_s, nb, e0 + (lane & 15), lane, bnd, vc_s);
   __syncthreads();
   // the reference's little-endian bit stream, one token per thread
   if (tid < nb) {
@@ -363,8 +315,8 @@ struct KeyDequantArgs {
 // one thread per code byte (two channels): zero + scale * level[code]; 3- and
 // 2-bit keys one thread per code
 __global__ __launch_bounds__(kKbThreads) void tqk_key_block_dequant(KeyDequantArgs a) {
-  constexpr int D = TQK_D;
   const tqk_block_desc& d = a.d;
+  const int D = d.head_dim;
   if (d.bits != 4) {
     const size_t n = (size_t)d.batch * d.n_heads * d.tokens * D;
     const size_t i = (size_t)blockIdx.x * kKbThreads + threadIdx.x;
@@ -410,9 +362,8 @@ struct ValueDequantArgs {
 };
 
 // one thread per token: y = vcent[code]; x_e = sequential over j of y_j * Pi[j][e]; x * norm
-template <int VB>
+template <int VB, int D>
 __global__ __launch_bounds__(kKbThreads) void tqk_value_block_dequant(ValueDequantArgs a) {
-  constexpr int D = TQK_D;
   constexpr int VROW = D * VB / 8;
   const tqk_block_desc& d = a.d;
   const size_t n = (size_t)d.batch * d.n_heads * d.tokens;
@@ -438,9 +389,9 @@ __global__ __launch_bounds__(kKbThreads) void tqk_value_block_dequant(ValueDequa
 
 int check_block(const tqk_block_desc* d, bool key) {
   if (!d) return TQK_EINVAL;
-  if (d->head_dim != TQK_D) return TQK_EUNSUPPORTED;
+  if (!head_dim_ok(d->head_dim)) return TQK_EUNSUPPORTED;
   if (d->batch <= 0 || d->n_heads <= 0 || d->tokens <= 0) return TQK_EINVAL;
-  if ((long long)d->batch * d->n_heads * d->tokens * TQK_D >= (1LL << 40)) return TQK_EINVAL;
+  if ((long long)d->batch * d->n_heads * d->tokens * d->head_dim >= (1LL << 40)) return TQK_EINVAL;
   if (key) {
     if (d->bits < 2 || d->bits > 4) return TQK_EUNSUPPORTED;
     if (d->key_grid != 0 && d->key_grid != 1) return TQK_EINVAL;
@@ -449,11 +400,31 @@ int check_block(const tqk_block_desc* d, bool key) {
       return TQK_EINVAL;
     if (d->outliers_per_channel < 0 || d->outlier_cap < 0) return TQK_EINVAL;
     // side-list positions s * D + j are 32-bit
-    if ((long long)d->tokens * TQK_D >= (1LL << 32)) return TQK_EUNSUPPORTED;
+    if ((long long)d->tokens * d->head_dim >= (1LL << 32)) return TQK_EUNSUPPORTED;
   } else if (d->bits < 2 || d->bits > 4) {
     return TQK_EUNSUPPORTED;
   }
   return TQK_OK;
+}
+
+// one kernel instance per (bits, head_dim)
+template <int D>
+void launch_value(int vb, dim3 grid, hipStream_t st, const ValueBlockArgs& a) {
+  if (vb == 2)
+    hipLaunchKernelGGL((tqk_value_block<2, D>), grid, dim3(kVbThreads), 0, st, a);
+  else if (vb == 3)
+    hipLaunchKernelGGL((tqk_value_block<3, D>), grid, dim3(kVbThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL((tqk_value_block<4, D>), grid, dim3(kVbThreads), 0, st, a);
+}
+template <int D>
+void launch_value(int vb, dim3 grid, hipStream_t st, const ValueDequantArgs& a) {
+  if (vb == 2)
+    hipLaunchKernelGGL((tqk_value_block_dequant<2, D>), grid, dim3(kKbThreads), 0, st, a);
+  else if (vb == 3)
+    hipLaunchKernelGGL((tqk_value_block_dequant<3, D>), grid, dim3(kKbThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL((tqk_value_block_dequant<4, D>), grid, dim3(kKbThreads), 0, st, a);
 }
 
 }  // namespace
@@ -469,8 +440,14 @@ int tqk_encode_key_block(const tqk_block_desc* d, const void* x, const float* zp
   if (d->key_grid == 0 && d->zero_point == 2 && !zp) return TQK_EINVAL;
   if (d->outliers_per_channel > 0 && d->outlier_cap > 0 && (!out_pos || !out_val)) return TQK_EINVAL;
   KeyBlockArgs a{*d, x, zp, packed, scale, zero, out_pos, out_val, out_count};
-  hipLaunchKernelGGL(tqk_key_block, dim3(d->batch * d->n_heads), dim3(kKbThreads), 0,
-                     reinterpret_cast<hipStream_t>(stream), a);
+  const dim3 grid(d->batch * d->n_heads);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (d->head_dim == 64)
+    hipLaunchKernelGGL(tqk_key_block<64>, grid, dim3(128), 0, st, a);
+  else if (d->head_dim == 128)
+    hipLaunchKernelGGL(tqk_key_block<128>, grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL(tqk_key_block<256>, grid, dim3(512), 0, st, a);
   return hipGetLastError() == hipSuccess ? TQK_OK : TQK_EHIP;
 }
 
@@ -482,12 +459,12 @@ int tqk_encode_value_block(const tqk_block_desc* d, const void* x, const float* 
   ValueBlockArgs a{*d, x, pi, vbnd, packed, norms};
   const dim3 grid((d->tokens + kVbTokens - 1) / kVbTokens, d->batch * d->n_heads);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (d->bits == 2)
-    hipLaunchKernelGGL(tqk_value_block<2>, grid, dim3(kVbThreads), 0, st, a);
-  else if (d->bits == 3)
-    hipLaunchKernelGGL(tqk_value_block<3>, grid, dim3(kVbThreads), 0, st, a);
+  if (d->head_dim == 64)
+    launch_value<64>(d->bits, grid, st, a);
+  else if (d->head_dim == 128)
+    launch_value<128>(d->bits, grid, st, a);
   else
-    hipLaunchKernelGGL(tqk_value_block<4>, grid, dim3(kVbThreads), 0, st, a);
+    launch_value<256>(d->bits, grid, st, a);
   return hipGetLastError() == hipSuccess ? TQK_OK : TQK_EHIP;
 }
 
@@ -499,7 +476,7 @@ int tqk_dequant_key_block(const tqk_block_desc* d, const uint8_t* packed, const 
   if (!packed || !scale || !zero || !out || n_out < 0 || (n_out > 0 && (!out_idx || !out_val)))
     return TQK_EINVAL;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const size_t total = (size_t)d->batch * d->n_heads * d->tokens * TQK_D;
+  const size_t total = (size_t)d->batch * d->n_heads * d->tokens * d->head_dim;
   const size_t n = d->bits == 4 ? total / 2 : total;  // threads: code bytes, or codes
   KeyDequantArgs a{*d, packed, scale, zero, out};
   hipLaunchKernelGGL(tqk_key_block_dequant, dim3((unsigned)((n + kKbThreads - 1) / kKbThreads)),
@@ -519,12 +496,12 @@ int tqk_dequant_value_block(const tqk_block_desc* d, const uint8_t* packed, cons
   ValueDequantArgs a{*d, packed, norms, pi, vcent, out};
   const dim3 grid((unsigned)((n + kKbThreads - 1) / kKbThreads));
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (d->bits == 2)
-    hipLaunchKernelGGL(tqk_value_block_dequant<2>, grid, dim3(kKbThreads), 0, st, a);
-  else if (d->bits == 3)
-    hipLaunchKernelGGL(tqk_value_block_dequant<3>, grid, dim3(kKbThreads), 0, st, a);
+  if (d->head_dim == 64)
+    launch_value<64>(d->bits, grid, st, a);
+  else if (d->head_dim == 128)
+    launch_value<128>(d->bits, grid, st, a);
   else
-    hipLaunchKernelGGL(tqk_value_block_dequant<4>, grid, dim3(kKbThreads), 0, st, a);
+    launch_value<256>(d->bits, grid, st, a);
   return hipGetLastError() == hipSuccess ? TQK_OK : TQK_EHIP;
 }
 

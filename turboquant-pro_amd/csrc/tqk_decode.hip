@@ -22,7 +22,7 @@ namespace {
 struct DecodeArgs {
   tqk_cache_desc d;
   tqk_cache_ptrs p;
-  const uint16_t* q;
+  const void* q;  // fp16, or fp32 (input_f32: VALU kernel only)
   const int32_t* seq_lens;
   float* pm;    // [batch][Hq][n_splits]
   float* pl;    // [batch][Hq][n_splits]
@@ -112,10 +112,20 @@ __device__ __forceinline__ void softmax_update(float (*sc)[kThreads], int n, flo
   __syncthreads();
 }
 
-template <int GQ, int VB>
+// The VALU split kernel: pools the MFMA kernel does not take (head_dim 64 or
+// 256, per-token value rows, a hot ring that is not whole 32-token blocks).
+// Scores one token per thread; values one channel pair per thread over a
+// slice of the tokens (D / 2 pairs x 512 / D slices).  Deterministic: every
+// sum has a fixed order (a token's outlier corrections are added by the
+// thread that scores it, in side-list order).
+template <int GQ, int VB, int D>
 __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) {
-  constexpr int D = TQK_D;
   constexpr int VROW = D * VB / 8;
+  constexpr int NP = D / 2;             // channel pairs
+  constexpr int NQ = kThreads / NP;     // token slices of the value pass
+  constexpr int TS = kThreads / NQ;     // tokens per slice (a group or hot split has <= 256)
+  constexpr int NW = D / 64;            // waves that hold the per-channel bias terms (>= 1)
+  static_assert(NP * NQ == kThreads && NW >= 1, "head_dim 64, 128 or 256");
   const int split = blockIdx.x + a.split_base, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x;
   const tqk_cache_desc& d = a.d;
@@ -133,15 +143,18 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
   __shared__ float vl_s[1 << (2 * VB)][2];
   __shared__ float red_s[4][GQ];
   __shared__ float a_s[D], mu_s[D];
-  __shared__ float accr_s[4][GQ][D];
+  __shared__ float accr_s[NQ][GQ][D];
 
   // GQ is the kernel's power-of-two head count; the last GQ - gq heads are
   // zero-query padding whose states are never written
   const int gq = Hq / Hkv;
-  for (int i = tid; i < GQ * D; i += kThreads)
-    q_s[i / D][i % D] = (i / D < gq) ? h2f(a.q[((size_t)b * Hq + h * gq + i / D) * D + i % D]) : 0.f;
+  const bool f32 = d.input_f32 != 0;  // fp32 query and hot ring
+  for (int i = tid; i < GQ * D; i += kThreads) {
+    const size_t qi = ((size_t)b * Hq + h * gq + i / D) * D + i % D;
+    q_s[i / D][i % D] = (i / D >= gq) ? 0.f
+                        : f32 ? static_cast<const float*>(a.q)[qi] : h2f(static_cast<const uint16_t*>(a.q)[qi]);
+  }
   // key pair table: index of a channel pair (the code byte, or the 3-/2-bit
-  // pair field) -> its two levels
   // pair field) -> its two levels (PolarQuant keys: value centroids)
   const bool polar = a.d.key_grid == 2;
   {
@@ -176,7 +189,7 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
   }
   __syncthreads();
 
-  const int jp = tid & 63, tq = tid >> 6;
+  const int jp = tid % NP, tq = tid / NP;
   const int32_t* __restrict__ bt = a.p.block_table;
 
   if (split < a.n_cold_splits) {
@@ -204,17 +217,25 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
       __syncthreads();
       float bias[GQ];
 #pragma unroll
-      for (int i = 0; i < GQ; ++i) bias[i] = red_s[0][i] + red_s[1][i];
+      for (int i = 0; i < GQ; ++i) {
+        bias[i] = red_s[0][i];
+        if constexpr (NW == 2) bias[i] = red_s[0][i] + red_s[1][i];
+        if constexpr (NW == 4) bias[i] = (red_s[0][i] + red_s[1][i]) + (red_s[2][i] + red_s[3][i]);
+      }
       __syncthreads();
 
-      // dense key scores: one token per thread
+      // key scores, one token per thread: the dense part, then the token's
+      // outlier corrections q_j * (val - dense_j) in side-list order (the
+      // side-list is sorted by token; the cumulative counts at every 32nd
+      // token bound the token's run, a binary search finds its start)
+      const size_t obase = (size_t)slot * Hkv + h;
       float norm_t = 0.f;
       if (tid < G) {
         const size_t row = page_row(bt, d.max_pages_per_seq, b, g * G + tid, P, d.n_pages, h);
         const int kb = d.key_bits;
-        const uint32_t* kr = reinterpret_cast<const uint32_t*>(a.p.kcodes + row * k_row_bytes(kb));
+        const uint32_t* kr = reinterpret_cast<const uint32_t*>(a.p.kcodes + row * k_row_bytes(kb, D));
         uint32_t rw[D / 8];
-        for (int w2 = 0; w2 < k_row_bytes(kb) / 4; ++w2) rw[w2] = kr[w2];
+        for (int w2 = 0; w2 < k_row_bytes(kb, D) / 4; ++w2) rw[w2] = kr[w2];
         float s[GQ];
 #pragma unroll
         for (int i = 0; i < GQ; ++i) s[i] = 0.f;
@@ -225,39 +246,45 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
 #pragma unroll
           for (int i = 0; i < GQ; ++i) s[i] += w_s[i][j] * k0 + w_s[i][j + 1] * k1;
         }
+#pragma unroll
+        for (int i = 0; i < GQ; ++i) s[i] += bias[i];
+        if (d.outliers_per_channel > 0) {
+          const int* oc = a.p.ocount + obase * TQK_NOB;
+          const int cap = d.outlier_cap;
+          const int blk = tid / TQK_OBLK;
+          int lo = blk > 0 ? min(oc[blk - 1], cap) : 0;
+          int hi = min(oc[blk], cap);
+          const uint32_t* oe = a.p.oent + obase * cap;
+          const uint32_t first = (uint32_t)tid * D;
+          while (lo < hi) {  // first entry of the run at or after (tid, 0)
+            const int mid = (lo + hi) >> 1;
+            if ((oe[mid] & 0xFFFFu) < first) lo = mid + 1; else hi = mid;
+          }
+          const int end = min(oc[blk], cap);
+          for (int e = lo; e < end; ++e) {
+            const uint32_t ent = oe[e];
+            const uint32_t pos = ent & 0xFFFFu;
+            if (pos >= first + D) break;
+            const int j = (int)(pos - first);
+            const uint32_t f = k_pair_index(rw, kb, j >> 1);
+            const uint32_t c = (j & 1) ? k_code_odd(f, kb) : k_code_even(f, kb);
+            const float delta = h2f((uint16_t)(ent >> 16)) - (a_s[j] * key_level(a.d.key_grid, c) + mu_s[j]);
+#pragma unroll
+            for (int i = 0; i < GQ; ++i) s[i] += q_s[i][j] * delta;
+          }
+        }
         const float kn = polar ? a.p.knorm[row] * sm : sm;  // score = |k| * (q_rot . centroids)
 #pragma unroll
-        for (int i = 0; i < GQ; ++i) sc_s[i][tid] = (s[i] + bias[i]) * kn;
+        for (int i = 0; i < GQ; ++i) sc_s[i][tid] = s[i] * kn;
         norm_t = a.p.vnorm[row];
-      }
-      __syncthreads();
-
-      // sparse outlier corrections: q_j * (val - dense) added to token rows
-      const size_t obase = (size_t)slot * Hkv + h;
-      const int no = min(a.p.ocount[obase * TQK_NOB + TQK_NOB - 1], d.outlier_cap);
-      for (int e = tid; e < no; e += kThreads) {
-        const uint32_t ent = a.p.oent[obase * d.outlier_cap + e];
-        const int pos = ent & 0xFFFFu;
-        const float val = h2f((uint16_t)(ent >> 16));
-        const int tt = pos >> 7, j = pos & (D - 1);
-        const size_t row = page_row(bt, d.max_pages_per_seq, b, g * G + tt, P, d.n_pages, h);
-        const int kb = d.key_bits;
-        const uint32_t* kr = reinterpret_cast<const uint32_t*>(a.p.kcodes + row * k_row_bytes(kb));
-        uint32_t rw[D / 8];
-        for (int w2 = 0; w2 < k_row_bytes(kb) / 4; ++w2) rw[w2] = kr[w2];
-        const uint32_t f = k_pair_index(rw, kb, j >> 1);
-        const uint32_t c = (j & 1) ? k_code_odd(f, kb) : k_code_even(f, kb);
-        const float delta = val - (a_s[j] * key_level(a.d.key_grid, c) + mu_s[j]);
-#pragma unroll
-        for (int i = 0; i < GQ; ++i) atomicAdd(&sc_s[i][tt], q_s[i][j] * delta * sm);
       }
       __syncthreads();
 
       softmax_update<GQ>(sc_s, G, m_run, l_run, acc0, acc1, red_s, norm_t);
 
-      // value accumulation in rotated code space: thread = (channel pair, token quarter)
-      const int tend = min(G, tq * 64 + 64);
-      for (int tt = tq * 64; tt < tend; ++tt) {
+      // value accumulation in rotated code space: thread = (channel pair, token slice)
+      const int tend = min(G, tq * TS + TS);
+      for (int tt = tq * TS; tt < tend; ++tt) {
         const size_t row = page_row(bt, d.max_pages_per_seq, b, g * G + tt, P, d.n_pages, h);
         // the 2*VB-bit field of channels 2jp, 2jp + 1 in the token's bit stream
         const uint32_t* vr = reinterpret_cast<const uint32_t*>(a.p.vcodes + row * VROW);
@@ -276,7 +303,7 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
       __syncthreads();
     }
   } else {
-    // fp16 hot window slice
+    // hot window slice (fp16, or fp32 for input_f32)
     const int hs = split - a.n_cold_splits;
     const int t0 = n_cold + hs * a.hot_per_split;
     const int t1 = min(L, t0 + a.hot_per_split);
@@ -285,21 +312,32 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
       const int R = d.hot_ring;
       const size_t hbase = ((size_t)b * Hkv + h) * R;
       if (tid < n) {
-        const uint4* kr = reinterpret_cast<const uint4*>(a.p.hot_k + (hbase + (t0 + tid) % R) * D);
+        const size_t krow = (hbase + (t0 + tid) % R) * D;
         float s[GQ];
 #pragma unroll
         for (int i = 0; i < GQ; ++i) s[i] = 0.f;
+        if (f32) {
+          const float2* kr = reinterpret_cast<const float2*>(static_cast<const float*>(a.p.hot_k) + krow);
+#pragma unroll 4
+          for (int jp2 = 0; jp2 < D / 2; ++jp2) {
+            const float2 kk = kr[jp2];
 #pragma unroll
-        for (int c = 0; c < 16; ++c) {
-          const uint4 w4 = kr[c];
-          const uint32_t wv[4] = {w4.x, w4.y, w4.z, w4.w};
+            for (int i = 0; i < GQ; ++i) s[i] += q_s[i][2 * jp2] * kk.x + q_s[i][2 * jp2 + 1] * kk.y;
+          }
+        } else {
+          const uint4* kr = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.p.hot_k) + krow);
+#pragma unroll 4
+          for (int c = 0; c < D / 8; ++c) {
+            const uint4 w4 = kr[c];
+            const uint32_t wv[4] = {w4.x, w4.y, w4.z, w4.w};
 #pragma unroll
-          for (int wi = 0; wi < 4; ++wi) {
-            const float k0 = h2f((uint16_t)(wv[wi] & 0xFFFFu));
-            const float k1 = h2f((uint16_t)(wv[wi] >> 16));
-            const int j = c * 8 + wi * 2;
+            for (int wi = 0; wi < 4; ++wi) {
+              const float k0 = h2f((uint16_t)(wv[wi] & 0xFFFFu));
+              const float k1 = h2f((uint16_t)(wv[wi] >> 16));
+              const int j = c * 8 + wi * 2;
 #pragma unroll
-            for (int i = 0; i < GQ; ++i) s[i] += q_s[i][j] * k0 + q_s[i][j + 1] * k1;
+              for (int i = 0; i < GQ; ++i) s[i] += q_s[i][j] * k0 + q_s[i][j + 1] * k1;
+            }
           }
         }
 #pragma unroll
@@ -307,11 +345,19 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
       }
       __syncthreads();
       softmax_update<GQ>(sc_s, n, m_run, l_run, acc0, acc1, red_s, 1.0f);
-      const int tend = min(n, tq * 64 + 64);
-      for (int tt = tq * 64; tt < tend; ++tt) {
-        const uint32_t two =
-            reinterpret_cast<const uint32_t*>(a.p.hot_v + (hbase + (t0 + tt) % R) * D)[jp];
-        const float c0 = h2f((uint16_t)(two & 0xFFFFu)), c1 = h2f((uint16_t)(two >> 16));
+      const int tend = min(n, tq * TS + TS);
+      for (int tt = tq * TS; tt < tend; ++tt) {
+        const size_t vrow = (hbase + (t0 + tt) % R) * D;
+        float c0, c1;
+        if (f32) {
+          const float2 two = reinterpret_cast<const float2*>(static_cast<const float*>(a.p.hot_v) + vrow)[jp];
+          c0 = two.x;
+          c1 = two.y;
+        } else {
+          const uint32_t two = reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(a.p.hot_v) + vrow)[jp];
+          c0 = h2f((uint16_t)(two & 0xFFFFu));
+          c1 = h2f((uint16_t)(two >> 16));
+        }
 #pragma unroll
         for (int i = 0; i < GQ; ++i) {
           const float pp = sc_s[i][tt];
@@ -322,7 +368,7 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
     }
   }
 
-  // combine the four token quarters and write the split's state
+  // combine the token slices and write the split's state
 #pragma unroll
   for (int i = 0; i < GQ; ++i) {
     accr_s[tq][i][2 * jp] = acc0[i];
@@ -332,8 +378,16 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
   const int ns = a.n_cold_splits + a.n_hot_splits;
   for (int x = tid; x < gq * D; x += kThreads) {
     const int i = x / D, j = x % D;
-    const float s4 = (accr_s[0][i][j] + accr_s[1][i][j]) + (accr_s[2][i][j] + accr_s[3][i][j]);
-    a.pacc[(((size_t)b * Hq + h * gq + i) * ns + split) * D + j] = s4;
+    float sq;
+    if constexpr (NQ == 2) {
+      sq = accr_s[0][i][j] + accr_s[1][i][j];
+    } else if constexpr (NQ == 4) {
+      sq = (accr_s[0][i][j] + accr_s[1][i][j]) + (accr_s[2][i][j] + accr_s[3][i][j]);
+    } else {
+      sq = ((accr_s[0][i][j] + accr_s[1][i][j]) + (accr_s[2][i][j] + accr_s[3][i][j])) +
+           ((accr_s[4][i][j] + accr_s[5][i][j]) + (accr_s[6][i][j] + accr_s[7][i][j]));
+    }
+    a.pacc[(((size_t)b * Hq + h * gq + i) * ns + split) * D + j] = sq;
   }
 #pragma unroll
   for (int i = 0; i < GQ; ++i) {
@@ -595,7 +649,7 @@ __device__ __forceinline__ float ld_agent(const float* p) {
 // e^{M_old - M_new} when a round raises it) over rounds of 2 * kMergeFast
 // partials, every load of a round issued before its first use.  Both merges
 // (tqk_merge and the in-kernel one) use it, so they agree bit for bit.
-template <class Load>
+template <int D, class Load>
 __device__ __forceinline__ void merge_chunked(Load ld, const float* pl, const float* pm,
                                               const float* pacc, size_t base, int ns, int n_cold,
                                               int j, float& M, float& dn, float& cr, float& hh) {
@@ -609,7 +663,7 @@ __device__ __forceinline__ void merge_chunked(Load ld, const float* pl, const fl
       const bool ok = s0 + k < ns;
       vl[k] = ok ? ld(pl + base + s0 + k) : 0.f;
       vm[k] = ok ? ld(pm + base + s0 + k) : -INFINITY;
-      va[k] = ok ? ld(pacc + (base + s0 + k) * TQK_D + j) : 0.f;
+      va[k] = ok ? ld(pacc + (base + s0 + k) * D + j) : 0.f;
     }
     float Mc = M;
 #pragma unroll
@@ -818,7 +872,8 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   // zero-query padding (their columns score 0) whose states are never written
   const int gq = Hq / Hkv;
   for (int i = tid; i < GQ * D; i += kMThreads) {
-    const uint32_t qr = (i / D < gq) ? a.q[((size_t)b * Hq + h * gq + i / D) * D + i % D] : 0u;
+    const uint32_t qr =
+        (i / D < gq) ? static_cast<const uint16_t*>(a.q)[((size_t)b * Hq + h * gq + i / D) * D + i % D] : 0u;
     qc_s[i % D][i / D] = (uint16_t)qr;
     qf_s[i / D][i % D] = (uint16_t)qr;
     q_h_s[i / D][i % D] = h2f((uint16_t)qr) * qscale;
@@ -1483,8 +1538,8 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       // are consecutive and inside the ring, so every row is loaded (keys and
       // values together) and rows at or past L are masked afterwards
       const int t0 = n_cold + 32 * hb;
-      const uint16_t* kr = a.p.hot_k + (hbase + (t0 % R)) * D;
-      const uint16_t* vr = a.p.hot_v + (hbase + (t0 % R)) * D;
+      const uint16_t* kr = static_cast<const uint16_t*>(a.p.hot_k) + (hbase + (t0 % R)) * D;
+      const uint16_t* vr = static_cast<const uint16_t*>(a.p.hot_v) + (hbase + (t0 % R)) * D;
       H8 ka[4], kb[4];
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
@@ -1702,7 +1757,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         if (qi < gq) {
           const size_t base = ((size_t)b * Hq + h * gq + qi) * ns;
           float M, dn, cr, hh;
-          merge_chunked([](const float* p) { return ld_agent(p); }, a.pl, a.pm, a.pacc, base, ns,
+          merge_chunked<D>([](const float* p) { return ld_agent(p); }, a.pl, a.pm, a.pacc, base, ns,
                         a.n_cold_splits, j, M, dn, cr, hh);
           q_h_s[qi][j] = cr;
           hr[r] = hh;
@@ -1728,14 +1783,16 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
 // query heads half, half + 2, ... for channel j, rotates their coded part back
 // (sum_k acc[k] * Pi[k][j]) and adds the hot part (turboquant_pro/kv_fused.py:139-153).
 // Pi is staged in LDS once (every thread's wide loads issued before its
-// stores) and shared by the GQ query heads.
-constexpr int kMergeThreads = 2 * TQK_D;
-__global__ __launch_bounds__(kMergeThreads) void tqk_merge(MergeArgs a) {
-  constexpr int D = TQK_D;
+// stores) and shared by the GQ query heads; at head_dim 256 (256 KiB of Pi)
+// the rotation reads Pi from global memory instead.
+template <int D>
+__global__ __launch_bounds__(2 * D) void tqk_merge(MergeArgs a) {
+  constexpr int kMergeThreads = 2 * D;
+  constexpr bool kPiLds = D <= 128;
   const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
   const int j = tid & (D - 1), half = tid / D;
   const int GQ = a.n_q_heads / a.n_kv_heads;
-  __shared__ __align__(16) float pi_s[D * D];
+  __shared__ __align__(16) float pi_s[kPiLds ? D * D : 4];
   __shared__ float crot_s[8][D];
   // every partial load of the thread's heads in flight at once when the
   // split count allows (the partials were just written: each round trip is an
@@ -1756,7 +1813,7 @@ __global__ __launch_bounds__(kMergeThreads) void tqk_merge(MergeArgs a) {
       }
     }
   }
-  {
+  if constexpr (kPiLds) {
     constexpr int NV = D * D / 4 / kMergeThreads;
     float4 v[NV];
 #pragma unroll
@@ -1764,6 +1821,7 @@ __global__ __launch_bounds__(kMergeThreads) void tqk_merge(MergeArgs a) {
 #pragma unroll
     for (int r = 0; r < NV; ++r) reinterpret_cast<float4*>(pi_s)[tid + r * kMergeThreads] = v[r];
   }
+  const float* __restrict__ pim = kPiLds ? pi_s : a.pi;
   float hr[4], den[4], mx[4];
   // merge of query head qi's splits for channel j: M = max m over splits with
   // l > 0, weights e^{m - M}; cold accumulators summed apart from the hot one
@@ -1803,7 +1861,7 @@ __global__ __launch_bounds__(kMergeThreads) void tqk_merge(MergeArgs a) {
       if (qi < GQ) {
         const size_t base = ((size_t)b * a.n_q_heads + h * GQ + qi) * a.n_splits;
         float M, dn, cr, hh;
-        merge_chunked([](const float* p) { return *p; }, a.pl, a.pm, a.pacc, base, a.n_splits,
+        merge_chunked<D>([](const float* p) { return *p; }, a.pl, a.pm, a.pacc, base, a.n_splits,
                       a.n_cold_splits, j, M, dn, cr, hh);
         crot_s[qi][j] = cr;
         hr[u] = hh;
@@ -1819,7 +1877,7 @@ __global__ __launch_bounds__(kMergeThreads) void tqk_merge(MergeArgs a) {
     if (qi < GQ) {
       float o = hr[u];
 #pragma unroll 8
-      for (int k = 0; k < D; ++k) o += crot_s[qi][k] * pi_s[k * D + j];
+      for (int k = 0; k < D; ++k) o += crot_s[qi][k] * pim[k * D + j];
       const size_t qh = (size_t)b * a.n_q_heads + h * GQ + qi;
       if (a.out) {
         a.out[qh * D + j] = o / den[u];
@@ -1837,7 +1895,7 @@ __global__ __launch_bounds__(kMergeThreads) void tqk_merge(MergeArgs a) {
 // The MFMA kernel needs tiled value codes and a hot ring of whole 32-token blocks.
 // (its loads use 32-bit buffer offsets: one head's page region stays below 4 GiB)
 __host__ __device__ inline bool mfma_path(const tqk_cache_desc& d) {
-  return v_tiled(d.group_tokens, d.page_tokens) && (d.hot_ring % 32 == 0) &&
+  return v_tiled(d.group_tokens, d.page_tokens, d.head_dim, d.input_f32) && (d.hot_ring % 32 == 0) &&
          (long long)d.n_pages * d.page_tokens * (TQK_D / 2) < (1LL << 32);
 }
 
@@ -1942,7 +2000,7 @@ Plan make_plan(const tqk_cache_desc* d, int batch, int max_len) {
   // counters stay zero between calls whatever the batch and split counts.
   const size_t n_counters = (size_t)counter_seqs(*d) * d->n_kv_heads;
   pl.counter_bytes = (n_counters * sizeof(uint32_t) + 255) & ~(size_t)255;
-  pl.partial_bytes = per * sizeof(float) * (2 + TQK_D);
+  pl.partial_bytes = per * sizeof(float) * (2 + d->head_dim);
   pl.ws_bytes = pl.counter_bytes + pl.partial_bytes + 256;
   return pl;
 }
@@ -1959,15 +2017,25 @@ void launch_mfma_kb(const DecodeArgs& a, dim3 g1, hipStream_t st) {
     hipLaunchKernelGGL((tqk_decode_split_mfma<GQ, 4, KB, false>), g1, dim3(kMThreads), 0, st, a);
 }
 
+template <int GQ, int D>
+void launch_valu(const DecodeArgs& a, dim3 grid, hipStream_t st) {
+  if (a.d.value_bits == 2)
+    hipLaunchKernelGGL((tqk_decode_split_valu<GQ, 2, D>), grid, dim3(kThreads), 0, st, a);
+  else if (a.d.value_bits == 3)
+    hipLaunchKernelGGL((tqk_decode_split_valu<GQ, 3, D>), grid, dim3(kThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL((tqk_decode_split_valu<GQ, 4, D>), grid, dim3(kThreads), 0, st, a);
+}
+
 template <int GQ>
 hipError_t launch_split(const DecodeArgs& a, dim3 grid, hipStream_t st) {
   if (!mfma_path(a.d)) {
-    if (a.d.value_bits == 2)
-      hipLaunchKernelGGL((tqk_decode_split_valu<GQ, 2>), grid, dim3(kThreads), 0, st, a);
-    else if (a.d.value_bits == 3)
-      hipLaunchKernelGGL((tqk_decode_split_valu<GQ, 3>), grid, dim3(kThreads), 0, st, a);
+    if (a.d.head_dim == 64)
+      launch_valu<GQ, 64>(a, grid, st);
+    else if (a.d.head_dim == 128)
+      launch_valu<GQ, 128>(a, grid, st);
     else
-      hipLaunchKernelGGL((tqk_decode_split_valu<GQ, 4>), grid, dim3(kThreads), 0, st, a);
+      launch_valu<GQ, 256>(a, grid, st);
     return hipGetLastError();
   }
   // one-dimensional over (split, kv head, seq) items
@@ -1982,7 +2050,7 @@ hipError_t launch_split(const DecodeArgs& a, dim3 grid, hipStream_t st) {
 }
 
 DecodeArgs make_args(const tqk_cache_desc* d, const tqk_cache_ptrs* p, const Plan& pl, int batch,
-                     const uint16_t* q, const int32_t* seq_lens, const WsView& w) {
+                     const void* q, const int32_t* seq_lens, const WsView& w) {
   const int ns = pl.n_cold_splits + pl.n_hot_splits;
   const size_t per = (size_t)batch * d->n_q_heads * ns;
   DecodeArgs a;
@@ -2023,7 +2091,7 @@ int check_decode_args(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int batc
 // The split kernel (validated arguments); `out` non-null selects the MFMA
 // kernel's in-kernel merge.
 int launch_splits(const tqk_cache_desc* d, const tqk_cache_ptrs* p, const Plan& pl, int batch,
-                  const uint16_t* q, const int32_t* seq_lens, const WsView& w, void* stream,
+                  const void* q, const int32_t* seq_lens, const WsView& w, void* stream,
                   float* out) {
   DecodeArgs a = make_args(d, p, pl, batch, q, seq_lens, w);
   if (out && mfma_path(*d)) a.out = out;
@@ -2063,12 +2131,18 @@ int launch_merge(const tqk_cache_desc* d, const tqk_cache_ptrs* p, const Plan& p
   m.m_out = m_out;
   m.l_out = l_out;
   m.acc_out = acc_out;
-  hipLaunchKernelGGL(tqk_merge, dim3(d->n_kv_heads, batch), dim3(kMergeThreads), 0,
-                     reinterpret_cast<hipStream_t>(stream), m);
+  const dim3 grid(d->n_kv_heads, batch);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (d->head_dim == 64)
+    hipLaunchKernelGGL(tqk_merge<64>, grid, dim3(128), 0, st, m);
+  else if (d->head_dim == 128)
+    hipLaunchKernelGGL(tqk_merge<128>, grid, dim3(256), 0, st, m);
+  else
+    hipLaunchKernelGGL(tqk_merge<256>, grid, dim3(512), 0, st, m);
   return hipGetLastError() == hipSuccess ? TQK_OK : TQK_EHIP;
 }
 
-int run_splits(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int batch, const uint16_t* q,
+int run_splits(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int batch, const void* q,
                const int32_t* seq_lens, int max_len, void* ws, size_t ws_bytes, void* stream,
                float* out = nullptr) {
   int rc = check_decode_args(d, p, batch, max_len);
@@ -2134,11 +2208,12 @@ int noalloc_scratch(hipStream_t stream, void** out) {
 
 extern "C" {
 
-int tqk_version(void) { return 8; }
+int tqk_version(void) { return 9; }
 
 int tqk_check_desc(const tqk_cache_desc* d) {
   if (!d) return TQK_EINVAL;
-  if (d->head_dim != TQK_D) return TQK_EUNSUPPORTED;
+  if (!head_dim_ok(d->head_dim)) return TQK_EUNSUPPORTED;
+  if (d->input_f32 != 0 && d->input_f32 != 1) return TQK_EINVAL;
   if (d->key_bits < 2 || d->key_bits > 4) return TQK_EUNSUPPORTED;
   if (d->key_grid < 0 || d->key_grid > 2) return TQK_EINVAL;
   // NF4 is a 4-bit grid; 3- and 2-bit keys are uniform or PolarQuant
@@ -2167,7 +2242,7 @@ size_t tqk_decode_workspace_bytes(const tqk_cache_desc* d, int32_t batch, int32_
 }
 
 int tqk_decode(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t batch,
-               const uint16_t* q, const int32_t* seq_lens, int32_t max_len, float* out,
+               const void* q, const int32_t* seq_lens, int32_t max_len, float* out,
                void* workspace, size_t workspace_bytes, void* stream) {
   if (!out) return TQK_EINVAL;
   int rc = run_splits(d, p, batch, q, seq_lens, max_len, workspace, workspace_bytes, stream, out);
@@ -2179,7 +2254,7 @@ int tqk_decode(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t batch,
 }
 
 int tqk_decode_noalloc(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t batch,
-                       const uint16_t* q, const int32_t* seq_lens, int32_t max_len, float* out,
+                       const void* q, const int32_t* seq_lens, int32_t max_len, float* out,
                        void* stream) {
   int rc = check_decode_args(d, p, batch, max_len);
   if (rc != TQK_OK) return rc;
@@ -2200,7 +2275,7 @@ int tqk_decode_noalloc(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t
 }
 
 int tqk_decode_partials(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t batch,
-                        const uint16_t* q, const int32_t* seq_lens, int32_t max_len,
+                        const void* q, const int32_t* seq_lens, int32_t max_len,
                         float* m, float* l, float* acc, void* workspace,
                         size_t workspace_bytes, void* stream) {
   if (!m || !l || !acc) return TQK_EINVAL;
@@ -2210,7 +2285,7 @@ int tqk_decode_partials(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_
 }
 
 int tqk_decode_splits(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t batch,
-                      const uint16_t* q, const int32_t* seq_lens, int32_t max_len,
+                      const void* q, const int32_t* seq_lens, int32_t max_len,
                       void* workspace, size_t workspace_bytes, void* stream) {
   return run_splits(d, p, batch, q, seq_lens, max_len, workspace, workspace_bytes, stream);
 }

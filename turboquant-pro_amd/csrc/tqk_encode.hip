@@ -12,7 +12,7 @@
 //     code  = first argmin_l |x - cent_l|               (NaN counts as minimal)
 //     outlier threshold = k-th largest |x| (ties kept), flat (s, j) order
 //   values (turboquant_pro/core.py:569-606, CPU full-QR branch)
-//     norm  = sqrt(pairwise-8 sum of squares)            (numpy pairwise_sum, n = 128)
+//     norm  = sqrt(pairwise sum of squares)              (numpy pairwise_sum, n = D)
 //     u     = v / max(norm, 1e-30)
 //     y_e   = sequential over d of (u_d * PiT[d][e]), separately rounded
 //     code  = #{ boundaries < y_e }                      (searchsorted, side="left";
@@ -32,21 +32,24 @@ struct EncodeArgs {
   tqk_cache_ptrs p;
   const int32_t* items;
   const int32_t* prev_len;
-  const uint16_t* chunk_k;
-  const uint16_t* chunk_v;
+  const void* chunk_k;  // fp16, or fp32 (input_f32)
+  const void* chunk_v;
   int chunk_tokens;
   int32_t* overflow;
 };
 
-// Source row (fp16, D values) of token t of sequence b, kv head h: the hot
-// ring for tokens already in the cache, the appended chunk for new ones.
-__device__ __forceinline__ const uint16_t* token_src(const EncodeArgs& a, const uint16_t* ring,
-                                                     const uint16_t* chunk, int b, int h, int t) {
+// Source row (D values of type T: fp16 bits or fp32) of token t of sequence
+// b, kv head h: the hot ring for tokens already in the cache, the appended
+// chunk for new ones.
+template <int D, typename T = uint16_t>
+__device__ __forceinline__ const T* token_src(const EncodeArgs& a, const void* ring,
+                                              const void* chunk, int b, int h, int t) {
   const tqk_cache_desc& d = a.d;
   const int prev = a.prev_len[b];
   if (t < prev)
-    return ring + (((size_t)b * d.n_kv_heads + h) * d.hot_ring + (t % d.hot_ring)) * TQK_D;
-  return chunk + (((size_t)b * d.n_kv_heads + h) * a.chunk_tokens + (t - prev)) * TQK_D;
+    return static_cast<const T*>(ring) +
+           (((size_t)b * d.n_kv_heads + h) * d.hot_ring + (t % d.hot_ring)) * D;
+  return static_cast<const T*>(chunk) + (((size_t)b * d.n_kv_heads + h) * a.chunk_tokens + (t - prev)) * D;
 }
 
 __device__ __forceinline__ uint32_t abs_h(uint16_t x) { return x & 0x7FFFu; }
@@ -117,9 +120,8 @@ __device__ __forceinline__ int sum_quarters(int x) {
 }
 
 
-template <int VB>
+template <int VB, int D>
 __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
-  constexpr int D = TQK_D;
   const int item = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
   const int lane = tid & 63, wv = tid >> 6;
   const tqk_cache_desc& d = a.d;
@@ -148,15 +150,15 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
 
   if (d.key_grid != 2) {
     // ---- stage the key tile ----------------------------------------------
-    for (int idx = tid; idx < G * 16; idx += kEncThreads) {
-      const int t = idx >> 4, c = idx & 15;
+    for (int idx = tid; idx < G * (D / 8); idx += kEncThreads) {
+      const int t = idx / (D / 8), c = idx % (D / 8);
       const uint4* src =
-          reinterpret_cast<const uint4*>(token_src(a, a.p.hot_k, a.chunk_k, b, h, g * G + t));
+          reinterpret_cast<const uint4*>(token_src<D>(a, a.p.hot_k, a.chunk_k, b, h, g * G + t));
       reinterpret_cast<uint4*>(&kt_s[t][0])[c] = src[c];
     }
     __syncthreads();
 
-    // ---- per-channel statistics (threads 0..127) ---------------------------
+    // ---- per-channel statistics (thread j: channel j) ------------------------
     if (tid < D && d.key_grid == 1) {
       // uniform keys (turboquant_pro/per_channel_kv.py:303-306): channel min and
       // max over the tokens, scale = max(max - min, 1e-8) / (2^bits - 1) (NaN propagates)
@@ -263,7 +265,9 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
       // as packed 16-bit pairs, bit 15 of each half of m + bias is the test
       // m >= T; NaN magnitudes (m > 0x7C00, where m + 0x03FF reaches bit 15)
       // are never selected, as |x| >= t is false for them
-      uint32_t om[D / 32] = {0u, 0u, 0u, 0u};
+      uint32_t om[D / 32];
+#pragma unroll
+      for (int k = 0; k < D / 32; ++k) om[k] = 0u;
       if (tid < G) {
 #pragma unroll
         for (int c8 = 0; c8 < D / 8; ++c8) {
@@ -280,11 +284,16 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
             om[c8 >> 2] |= two << (8 * (c8 & 3) + 2 * i);
           }
         }
-        if (all) om[0] = om[1] = om[2] = om[3] = 0xFFFFFFFFu;
+        if (all) {
+#pragma unroll
+          for (int k = 0; k < D / 32; ++k) om[k] = 0xFFFFFFFFu;
+        }
       }
-      const int cnt = tid < G ? __builtin_popcount(om[0]) + __builtin_popcount(om[1]) +
-                                    __builtin_popcount(om[2]) + __builtin_popcount(om[3])
-                              : 0;
+      int cnt = 0;
+      if (tid < G) {
+#pragma unroll
+        for (int k = 0; k < D / 32; ++k) cnt += __builtin_popcount(om[k]);
+      }
       // block exclusive scan of cnt
       int incl = cnt;
 #pragma unroll
@@ -335,8 +344,8 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
     // of a uniform grid -- so the dense part of a decode contributes gmean
     // there and the side-list adds val - gmean; export restores the
     // reference's code.
-    {
-      const int jp = lane, kb = d.key_bits;
+    for (int jp = lane; jp < D / 2; jp += 64) {
+      const int kb = d.key_bits;
       const int per_q = (G + kEncWaves - 1) / kEncWaves;
       const int s0 = wv * per_q, s1 = min(G, s0 + per_q);
       const uint32_t zc = d.key_grid == 1 ? 0u : 7u;
@@ -430,59 +439,43 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
 
   // ---- values -------------------------------------------------------------
   constexpr int VROW = D * VB / 8;
-  const bool tiled = v_tiled(G, P);
+  const bool tiled = v_tiled(G, P, D, d.input_f32);
   // PolarQuant codes of the group's tokens (the value encode; PolarQuant keys
   // run it on the keys): norms to nout, codes staged in vc_s[token][channel]
   // (the first TQK_MAX_G * D bytes of the key tile area)
-  auto polar_phase = [&](const uint16_t* ring, const uint16_t* chunk, float* nout, bool vcheck) {
-    // Rotation operands: in pass p, wave w owns the 16 rotated channels
-    // [64p + 16w, +16); lane l holds column e = 64p + 16w + (l & 15) of Pi_T
-    // (pi[e][0..D)) in registers, and its 16-lane row (l >> 4) works on one
-    // token of a 4-token step.  The token's normalised row u sits in LDS
-    // (kVBatch tokens at a time, after the code staging area); each lane of
-    // the row loads channels [8(l & 15), 8(l & 15) + 8) of it, and u_d reaches
-    // the row's 16 lanes by a DPP row broadcast from lane d / 8 folded into
-    // the multiply -- no LDS broadcast reads, which would cost the LDS a full
-    // wave's bandwidth each.  Every y_e is still the sequential, separately
-    // rounded sum over d.
-    const int rt = lane >> 4, li = lane & 15;
+  auto polar_phase = [&](const void* ring, const void* chunk, float* nout, bool vcheck) {
+    // Rotation: in pass p, wave w owns the 16 rotated channels [64p + 16w,
+    // +16), lane l column e = 64p + 16w + (l & 15) of Pi_T (pi[e][0..D)) in
+    // registers; the tokens' normalised rows sit in LDS (kVBatch at a time,
+    // after the code staging area) and reach the lanes by DPP row broadcasts
+    // (rotate_codes) -- no LDS broadcast reads, which would cost the LDS a
+    // full wave's bandwidth each.
     float bnd[15];
 #pragma unroll
     for (int k = 0; k < (1 << VB) - 1; ++k) bnd[k] = a.p.vbnd[k];
-    constexpr int kVBatch = 64;
+    constexpr int kVBatch = 64;  // rows per batch (rotate_codes takes at most 64)
     float (*u_s)[D] = reinterpret_cast<float (*)[D]>(&kt_s[0][0] + TQK_MAX_G * D / 2);
     for (int t0 = 0; t0 < G; t0 += kVBatch) {
       const int nb = min(kVBatch, G - t0);
       // (1) norms and normalised rows, four threads per token: thread q holds
-      // the pairwise partial sums r[2q], r[2q + 1] (channels 8m + 2q, 8m + 2q + 1)
+      // channels 8m + 2q, 8m + 2q + 1 (pairwise_sumsq's partial sums)
       {
         const int tt = tid >> 2, q = tid & 3;
         if (tt < nb) {
           const int t = g * G + t0 + tt;
-          const uint32_t* src = reinterpret_cast<const uint32_t*>(token_src(a, ring, chunk, b, h, t));
-          float x0[16], x1[16];
+          const uint32_t* src = reinterpret_cast<const uint32_t*>(token_src<D>(a, ring, chunk, b, h, t));
+          float x0[D / 8], x1[D / 8];
 #pragma unroll
-          for (int m = 0; m < 16; ++m) {
+          for (int m = 0; m < D / 8; ++m) {
             const uint32_t w2 = src[4 * m + q];  // channels 8m + 2q, 8m + 2q + 1
             x0[m] = h2f((uint16_t)(w2 & 0xFFFFu));
             x1[m] = h2f((uint16_t)(w2 >> 16));
           }
-          float r0 = __fmul_rn(x0[0], x0[0]), r1 = __fmul_rn(x1[0], x1[0]);
-#pragma unroll
-          for (int m = 1; m < 16; ++m) {
-            r0 = __fadd_rn(r0, __fmul_rn(x0[m], x0[m]));
-            r1 = __fadd_rn(r1, __fmul_rn(x1[m], x1[m]));
-          }
-          // pairwise tree ((r0 + r1) + (r2 + r3)) + ((r4 + r5) + (r6 + r7))
-          const float pa = __fadd_rn(r0, r1);
-          const float po = __shfl_xor(pa, 1, 4);
-          const float pb = (q & 1) ? __fadd_rn(po, pa) : __fadd_rn(pa, po);
-          const float pbo = __shfl_xor(pb, 2, 4);
-          const float ss = (q & 2) ? __fadd_rn(pbo, pb) : __fadd_rn(pb, pbo);
+          const float ss = pairwise_sumsq<D>(x0, x1, q);
           const float nrm = __builtin_sqrtf(ss);  // correctly rounded (-fhip-fp32-correctly-rounded-divide-sqrt)
           const float safe = fmaxf(nrm, 1e-30f);
 #pragma unroll
-          for (int m = 0; m < 16; ++m) {
+          for (int m = 0; m < D / 8; ++m) {
             u_s[tt][8 * m + 2 * q] = __fdiv_rn(x0[m], safe);
             u_s[tt][8 * m + 2 * q + 1] = __fdiv_rn(x1[m], safe);
           }
@@ -493,49 +486,10 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
         }
       }
       __syncthreads();
-      // (2) rotation and codes, D / (16 * kEncWaves) passes over the channels:
-      // tokens ja = j0 + rt and jb = ja + 4 of the batch per step (two chains per lane)
-      for (int pass = 0; pass < D / (16 * kEncWaves); ++pass) {
-        const int ecol = 16 * kEncWaves * pass + 16 * wv + li;
-        float pcol[D];
-#pragma unroll
-        for (int k = 0; k < D / 4; ++k) {
-          const float4 p4 = reinterpret_cast<const float4*>(a.p.pi + (size_t)ecol * D)[k];
-          pcol[4 * k] = p4.x;
-          pcol[4 * k + 1] = p4.y;
-          pcol[4 * k + 2] = p4.z;
-          pcol[4 * k + 3] = p4.w;
-        }
-        for (int j0 = 0; j0 < nb; j0 += 8) {
-          const int ja = j0 + rt, jb = j0 + 4 + rt;
-          float ua[8], ub[8];
-          {
-            const float4* ra = reinterpret_cast<const float4*>(&u_s[min(ja, nb - 1)][8 * li]);
-            const float4* rb = reinterpret_cast<const float4*>(&u_s[min(jb, nb - 1)][8 * li]);
-            const float4 a0 = ra[0], a1 = ra[1], b0 = rb[0], b1 = rb[1];
-            ua[0] = a0.x; ua[1] = a0.y; ua[2] = a0.z; ua[3] = a0.w;
-            ua[4] = a1.x; ua[5] = a1.y; ua[6] = a1.z; ua[7] = a1.w;
-            ub[0] = b0.x; ub[1] = b0.y; ub[2] = b0.z; ub[3] = b0.w;
-            ub[4] = b1.x; ub[5] = b1.y; ub[6] = b1.z; ub[7] = b1.w;
-          }
-          float y0 = 0.f, y1 = 0.f;
-          rotate_row_dpp<0>(y0, y1, ua, ub, pcol);
-          // keeps the sums out of the conditional stores below: sunk into them,
-          // the multiplies would leave their broadcasts behind as separate moves
-          asm volatile("" : "+v"(y0), "+v"(y1));
-          uint32_t c0 = 0, c1 = 0;
-#pragma unroll
-          for (int k = 0; k < (1 << VB) - 1; ++k) {
-            c0 += (bnd[k] < y0) ? 1u : 0u;
-            c1 += (bnd[k] < y1) ? 1u : 0u;
-          }
-          // searchsorted places NaN after every boundary
-          if (y0 != y0) c0 = (1u << VB) - 1u;
-          if (y1 != y1) c1 = (1u << VB) - 1u;
-          if (ja < nb) vc_s[t0 + ja][ecol] = (uint8_t)c0;
-          if (jb < nb) vc_s[t0 + jb][ecol] = (uint8_t)c1;
-        }
-      }
+      // (2) rotation and codes, D / (16 * kEncWaves) passes over the channels
+      for (int pass = 0; pass < D / (16 * kEncWaves); ++pass)
+        rotate_codes<D, VB>(a.p.pi, u_s, nb, 16 * kEncWaves * pass + 16 * wv + (lane & 15), lane, bnd,
+                            vc_s + t0);
       __syncthreads();
     }
   };
@@ -550,9 +504,19 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
     // there is no side-list
     polar_phase(a.p.hot_k, a.chunk_k, a.p.knorm, false);
     for (int t = wv; t < G; t += kEncWaves) {
-      const uint32_t cc = *reinterpret_cast<const uint16_t*>(&vc_s[t][2 * lane]);
-      const uint32_t c0 = cc & 0xFFu, c1 = cc >> 8;
-      vc_s[t][lane] = (uint8_t)(d.key_bits == 4 ? ((rev4(c0) << 4) | rev4(c1)) : (c0 | (c1 << d.key_bits)));
+      // every pair of the row read before any index is written over it
+      constexpr int NPL = (D / 2 + 63) / 64;  // channel pairs per lane
+      uint32_t f[NPL];
+#pragma unroll
+      for (int k = 0; k < NPL; ++k) {
+        const int pr = lane + 64 * k;
+        const uint32_t cc = pr < D / 2 ? *reinterpret_cast<const uint16_t*>(&vc_s[t][2 * pr]) : 0u;
+        const uint32_t c0 = cc & 0xFFu, c1 = cc >> 8;
+        f[k] = d.key_bits == 4 ? ((rev4(c0) << 4) | rev4(c1)) : (c0 | (c1 << d.key_bits));
+      }
+#pragma unroll
+      for (int k = 0; k < NPL; ++k)
+        if (lane + 64 * k < D / 2) vc_s[t][lane + 64 * k] = (uint8_t)f[k];
     }
     kc_base = &vc_s[0][0];
     kc_stride = D;
@@ -564,7 +528,7 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
   }
   __syncthreads();
   // key code rows, one 32-channel chunk (16 pair indices) per thread
-  const int KROW = k_row_bytes(d.key_bits);
+  const int KROW = k_row_bytes(d.key_bits, D);
   for (int idx = tid; idx < G * (D / 32); idx += kEncThreads) {
     const int t = idx / (D / 32), ch = idx % (D / 32);
     const size_t row = page_row(a.p.block_table, d.max_pages_per_seq, b, g * G + t, P, d.n_pages, h);
@@ -582,7 +546,7 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
         o[w] |= f << sh;
         if (sh + 2 * kb > 32) o[w + 1] |= f >> (32 - sh);
       }
-      uint32_t* dst = reinterpret_cast<uint32_t*>(a.p.kcodes + row * KROW + (KROW / 4) * ch);
+      uint32_t* dst = reinterpret_cast<uint32_t*>(a.p.kcodes + row * KROW + 4 * kb * ch);
       for (int w = 0; w < kb; ++w) dst[w] = o[w];
     }
   }
@@ -590,7 +554,7 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
   polar_phase(a.p.hot_v, a.chunk_v, a.p.vnorm, true);
   // (3) the code rows: 4-token x 8-channel units of 16-token tiles, or the
   // reference's little-endian bit stream per token
-  if (tiled) {
+  if (D == TQK_D && tiled) {
     // one unit = tokens [16T + 4lg, +4) x channels [8c, +8) of 16-token tile T
     for (int un = tid; un < (G / 16) * 64; un += kEncThreads) {
       const int T = un >> 6, lg = (un >> 4) & 3, c = un & 15;
@@ -623,23 +587,321 @@ __global__ __launch_bounds__(kEncThreads) void tqk_encode_group(EncodeArgs a) {
       if ((bitpos & 31) + VB > 32) outw[(bitpos >> 5) + 1] |= code >> (32 - (bitpos & 31));
     }
     const size_t row = page_row(a.p.block_table, d.max_pages_per_seq, b, g * G + tid, P, d.n_pages, h);
-    uint4* dst = reinterpret_cast<uint4*>(a.p.vcodes + row * VROW);
+    // 16-byte stores where the row is whole 16-byte pieces (3-bit rows at
+    // head_dim 64 are 24 bytes: dword stores)
+    if constexpr (VROW % 16 == 0) {
+      uint4* dst = reinterpret_cast<uint4*>(a.p.vcodes + row * VROW);
 #pragma unroll
-    for (int k = 0; k < VROW / 16; ++k)
-      dst[k] = make_uint4(outw[4 * k], outw[4 * k + 1], outw[4 * k + 2], outw[4 * k + 3]);
+      for (int k = 0; k < VROW / 16; ++k)
+        dst[k] = make_uint4(outw[4 * k], outw[4 * k + 1], outw[4 * k + 2], outw[4 * k + 3]);
+    } else {
+      uint32_t* dst = reinterpret_cast<uint32_t*>(a.p.vcodes + row * VROW);
+#pragma unroll
+      for (int k = 0; k < VROW / 4; ++k) dst[k] = outw[k];
+    }
+  }
+}
+
+
+// ---------------------------------------------------------------------------
+// Quantize-on-flush of an fp32 cache (input_f32): the same codes, stats and
+// side-list as the fp16 encode, in the same NumPy operation order, from fp32
+// rows read through L1/L2 (an fp32 group does not fit the LDS key tile).  The
+// side-list positions keep the reference's codes (argmin on the fp32 value);
+// value codes are per-token rows.  Value norms are not bounded: the VALU
+// decode, the one that serves fp32 caches, keeps its weights in fp32.
+template <int VB, int D>
+__global__ __launch_bounds__(kEncThreads) void tqk_encode_group_f32(EncodeArgs a) {
+  const int item = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+  const int lane = tid & 63, wv = tid >> 6;
+  const tqk_cache_desc& d = a.d;
+  const int b = a.items[2 * item], g = a.items[2 * item + 1];
+  const int G = d.group_tokens, P = d.page_tokens, Hkv = d.n_kv_heads;
+  const int slot = a.p.group_table[(size_t)b * d.max_groups_per_seq + g];
+  const int kout = d.outliers_per_channel;
+  const size_t mbase = ((size_t)slot * Hkv + h) * D;
+  const size_t obase = (size_t)slot * Hkv + h;
+  constexpr int kVBatch = 64;  // rows per value batch (rotate_codes takes at most 64)
+  constexpr int VROW = D * VB / 8;
+
+  __shared__ const float* krow_s[TQK_MAX_G];                // source row of each key token
+  __shared__ float stat_s[D][2];                             // (mean, amax) or (min, scale)
+  __shared__ float thr_s[D];                                 // outlier magnitude threshold
+  __shared__ __align__(16) uint8_t kc_s[TQK_MAX_G][D / 2];   // table index per (token, channel pair)
+  __shared__ __align__(16) float u_s[kVBatch][D];
+  __shared__ __align__(16) uint8_t vc_s[kVBatch][D];
+  __shared__ int32_t wsum_s[kEncWaves];
+
+  for (int t = tid; t < G; t += kEncThreads)
+    krow_s[t] = token_src<D, float>(a, a.p.hot_k, a.chunk_k, b, h, g * G + t);
+  __syncthreads();
+
+  // norms and normalised rows of tokens [t0, t0 + nb) (four threads per
+  // token, pairwise_sumsq), then their rotated codes into vc_s
+  float bnd[15];
+#pragma unroll
+  for (int k = 0; k < (1 << VB) - 1; ++k) bnd[k] = a.p.vbnd[k];
+  auto polar_batch = [&](const void* ring, const void* chunk, int t0, int nb, float* nout) {
+    const int tt = tid >> 2, q = tid & 3;
+    if (tt < nb) {
+      const int t = g * G + t0 + tt;
+      const float2* src = reinterpret_cast<const float2*>(token_src<D, float>(a, ring, chunk, b, h, t));
+      float x0[D / 8], x1[D / 8];
+#pragma unroll
+      for (int m = 0; m < D / 8; ++m) {
+        const float2 w2 = src[4 * m + q];  // channels 8m + 2q, 8m + 2q + 1
+        x0[m] = w2.x;
+        x1[m] = w2.y;
+      }
+      const float nrm = __builtin_sqrtf(pairwise_sumsq<D>(x0, x1, q));
+      const float safe = fmaxf(nrm, 1e-30f);
+#pragma unroll
+      for (int m = 0; m < D / 8; ++m) {
+        u_s[tt][8 * m + 2 * q] = __fdiv_rn(x0[m], safe);
+        u_s[tt][8 * m + 2 * q + 1] = __fdiv_rn(x1[m], safe);
+      }
+      if (q == 0) nout[page_row(a.p.block_table, d.max_pages_per_seq, b, t, P, d.n_pages, h)] = nrm;
+    }
+    __syncthreads();
+    for (int pass = 0; pass < D / (16 * kEncWaves); ++pass)
+      rotate_codes<D, VB>(a.p.pi, u_s, nb, 16 * kEncWaves * pass + 16 * wv + (lane & 15), lane, bnd, vc_s);
+    __syncthreads();
+  };
+
+  if (d.key_grid != 2) {
+    auto X = [&](int s, int j) { return krow_s[s][j]; };
+    // ---- per-channel statistics, thread j: channel j
+    if (tid < D) {
+      const int j = tid;
+      float st0, st1;
+      if (d.key_grid == 1) {
+        float mn = X(0, j), mx = mn;
+        bool nan = (mn != mn);
+        for (int s = 1; s < G; ++s) {
+          const float xv = X(s, j);
+          nan |= (xv != xv);
+          mn = fminf(mn, xv);
+          mx = fmaxf(mx, xv);
+        }
+        st1 = nan ? __builtin_nanf("") : __fdiv_rn(fmaxf(__fsub_rn(mx, mn), 1e-8f), (float)((1 << d.key_bits) - 1));
+        st0 = nan ? __builtin_nanf("") : mn;
+      } else {
+        float mu;
+        if (d.zero_point == 2) {
+          mu = a.p.zp_mean[((size_t)g * Hkv + h) * D + j];
+        } else {
+          float acc = 0.0f;
+          for (int s = 0; s < G; ++s) acc = __fadd_rn(acc, X(s, j));
+          mu = (float)((double)acc / (double)G);
+          if (d.zero_point == 1) mu = __fmul_rn(mu, ((d.dc_mask[j >> 5] >> (j & 31)) & 1u) ? 1.0f : 0.0f);
+        }
+        float amax = 0.0f;
+        bool nan = (mu != mu);
+        for (int s = 0; s < G; ++s) {
+          const float dv = fabsf(__fsub_rn(X(s, j), mu));
+          nan |= (dv != dv);
+          amax = fmaxf(amax, dv);
+        }
+        st0 = mu;
+        st1 = nan ? __builtin_nanf("") : fmaxf(amax, 1e-8f);
+      }
+      stat_s[j][0] = st0;
+      stat_s[j][1] = st1;
+      a.p.gscale[mbase + j] = st1;
+      a.p.gmean[mbase + j] = st0;
+      // outlier threshold: the k-th largest |x| of the channel as the largest
+      // fp32 magnitude pattern T with #{ |x_s| >= T } >= k (NaN patterns order
+      // above inf, as np.partition places NaN last); the k <= 8 largest are
+      // kept directly, otherwise a bitwise search
+      if (kout > 0 && kout < G) {
+        uint32_t T = 0;
+        if (kout <= 8) {
+          uint32_t top[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) top[i] = 0u;
+          for (int s = 0; s < G; ++s) {
+            uint32_t v = __float_as_uint(fabsf(X(s, j)));
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              const uint32_t hi = max(top[i], v);
+              v = min(top[i], v);
+              top[i] = hi;
+            }
+          }
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            if (i == kout - 1) T = top[i];
+        } else {
+          for (int bit = 30; bit >= 0; --bit) {
+            const uint32_t cand = T | (1u << bit);
+            int cnt = 0;
+            for (int s = 0; s < G; ++s) cnt += __float_as_uint(fabsf(X(s, j))) >= cand ? 1 : 0;
+            if (cnt >= kout) T = cand;
+          }
+        }
+        thr_s[j] = __uint_as_float(T);  // a NaN threshold selects nothing, as |x| >= NaN
+      }
+    }
+    __syncthreads();
+
+    // ---- outlier side-list in flat (token, channel) order, one token per
+    // thread (the cumulative counts at every TQK_OBLK-token boundary as the
+    // fp16 encode writes them)
+    if (kout > 0) {
+      const bool all = kout >= G;
+      int cnt = 0;
+      if (tid < G) {
+        const float* row = krow_s[tid];
+        for (int j = 0; j < D; ++j) cnt += (all || fabsf(row[j]) >= thr_s[j]) ? 1 : 0;
+      }
+      int incl = cnt;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int v = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += v;
+      }
+      if (lane == 63) wsum_s[wv] = incl;
+      __syncthreads();
+      int wofs = 0, total = 0;
+      for (int w = 0; w < kEncWaves; ++w) {
+        if (w < wv) wofs += wsum_s[w];
+        total += wsum_s[w];
+      }
+      int off = wofs + incl - cnt;
+      if (tid < G && ((tid + 1) % TQK_OBLK) == 0 && (tid + 1) / TQK_OBLK <= TQK_NOB)
+        a.p.ocount[obase * TQK_NOB + (tid + 1) / TQK_OBLK - 1] = off + cnt;
+      if (tid < TQK_NOB && TQK_OBLK * (tid + 1) > G) a.p.ocount[obase * TQK_NOB + tid] = total;
+      if (tid < G && cnt > 0) {
+        const float* row = krow_s[tid];
+        for (int j = 0; j < D && off < d.outlier_cap; ++j) {
+          const float xv = row[j];
+          if (all || fabsf(xv) >= thr_s[j]) {
+            a.p.oent[obase * d.outlier_cap + off] = (uint32_t)(tid * D + j) | ((uint32_t)f2h(xv) << 16);
+            ++off;
+          }
+        }
+      }
+      if (tid == 0 && total > d.outlier_cap && a.overflow) atomicOr(a.overflow, TQK_OVF_OUTLIERS);
+    } else if (tid < TQK_NOB) {
+      a.p.ocount[obase * TQK_NOB + tid] = 0;
+    }
+
+    // ---- codes: thread = (channel pair, token slice = wave), the reference's
+    // code everywhere (side-list positions included)
+    const int kb = d.key_bits;
+    const int per_q = (G + kEncWaves - 1) / kEncWaves;
+    const int s0 = wv * per_q, s1 = min(G, s0 + per_q);
+    for (int jp = lane; jp < D / 2; jp += 64) {
+      const float st00 = stat_s[2 * jp][0], st01 = stat_s[2 * jp][1];
+      const float st10 = stat_s[2 * jp + 1][0], st11 = stat_s[2 * jp + 1][1];
+      if (d.key_grid == 1) {
+        const float qmax = (float)((1 << kb) - 1);
+        for (int s = s0; s < s1; ++s) {
+          const float2 xx = *reinterpret_cast<const float2*>(krow_s[s] + 2 * jp);
+          const float r0 = __builtin_rintf(__fdiv_rn(__fsub_rn(xx.x, st00), st01));
+          const float r1 = __builtin_rintf(__fdiv_rn(__fsub_rn(xx.y, st10), st11));
+          const uint32_t b0 = (uint32_t)fminf(fmaxf(r0, 0.0f), qmax);
+          const uint32_t b1 = (uint32_t)fminf(fmaxf(r1, 0.0f), qmax);
+          kc_s[s][jp] = (uint8_t)(kb == 4 ? ((rev4(b0) << 4) | rev4(b1)) : (b0 | (b1 << kb)));
+        }
+      } else {
+        float c0[16], c1[16];
+#pragma unroll
+        for (int l = 0; l < 16; ++l) {
+          c0[l] = __fadd_rn(st00, __fmul_rn(st01, kNF4[l]));
+          c1[l] = __fadd_rn(st10, __fmul_rn(st11, kNF4[l]));
+        }
+        for (int s = s0; s < s1; ++s) {
+          const float2 xx = *reinterpret_cast<const float2*>(krow_s[s] + 2 * jp);
+          uint32_t b0 = 0, b1 = 0;
+          float d0 = fabsf(__fsub_rn(xx.x, c0[0])), d1 = fabsf(__fsub_rn(xx.y, c1[0]));
+#pragma unroll
+          for (int l = 1; l < 16; ++l) {
+            const float e0 = fabsf(__fsub_rn(xx.x, c0[l])), e1 = fabsf(__fsub_rn(xx.y, c1[l]));
+            // np.argmin: strictly smaller wins; the first NaN wins over any number
+            if (e0 < d0 || (e0 != e0 && d0 == d0)) { d0 = e0; b0 = l; }
+            if (e1 < d1 || (e1 != e1 && d1 == d1)) { d1 = e1; b1 = l; }
+          }
+          kc_s[s][jp] = (uint8_t)((rev4(b0) << 4) | rev4(b1));
+        }
+      }
+    }
+  } else {
+    // PolarQuant keys: the value encode on the key tokens, norms to knorm;
+    // each token's codes become one table index per channel pair
+    for (int t0 = 0; t0 < G; t0 += kVBatch) {
+      const int nb = min(kVBatch, G - t0);
+      polar_batch(a.p.hot_k, a.chunk_k, t0, nb, a.p.knorm);
+      for (int i = tid; i < nb * (D / 2); i += kEncThreads) {
+        const int t = i / (D / 2), pr = i % (D / 2);
+        const uint32_t c0 = vc_s[t][2 * pr], c1 = vc_s[t][2 * pr + 1];
+        kc_s[t0 + t][pr] = (uint8_t)(d.key_bits == 4 ? ((rev4(c0) << 4) | rev4(c1)) : (c0 | (c1 << d.key_bits)));
+      }
+    }
+    if (tid < D) {
+      a.p.gscale[mbase + tid] = 1.0f;
+      a.p.gmean[mbase + tid] = 0.0f;
+    }
+    if (tid < TQK_NOB) a.p.ocount[obase * TQK_NOB + tid] = 0;
+  }
+  __syncthreads();
+  // key code rows, one 32-channel chunk (16 table indices) per thread
+  const int KROW = k_row_bytes(d.key_bits, D);
+  for (int idx = tid; idx < G * (D / 32); idx += kEncThreads) {
+    const int t = idx / (D / 32), ch = idx % (D / 32);
+    const size_t row = page_row(a.p.block_table, d.max_pages_per_seq, b, g * G + t, P, d.n_pages, h);
+    const uint4 f16 = *reinterpret_cast<const uint4*>(&kc_s[t][16 * ch]);
+    if (d.key_bits == 4) {
+      *reinterpret_cast<uint4*>(a.p.kcodes + row * KROW + 16 * ch) = f16;
+    } else {
+      const int kb = d.key_bits;
+      const uint32_t fw[4] = {f16.x, f16.y, f16.z, f16.w};
+      uint32_t o[3] = {0u, 0u, 0u};
+      for (int i = 0; i < 16; ++i) {
+        const uint32_t f = (fw[i >> 2] >> (8 * (i & 3))) & 0xFFu;
+        const int bo = 2 * kb * i, w = bo >> 5, sh = bo & 31;
+        o[w] |= f << sh;
+        if (sh + 2 * kb > 32) o[w + 1] |= f >> (32 - sh);
+      }
+      uint32_t* dst = reinterpret_cast<uint32_t*>(a.p.kcodes + row * KROW + 4 * kb * ch);
+      for (int w = 0; w < kb; ++w) dst[w] = o[w];
+    }
+  }
+  // ---- values, kVBatch tokens at a time: codes, then the reference's
+  // little-endian bit stream per token
+  for (int t0 = 0; t0 < G; t0 += kVBatch) {
+    const int nb = min(kVBatch, G - t0);
+    polar_batch(a.p.hot_v, a.chunk_v, t0, nb, a.p.vnorm);
+    if (tid < nb) {
+      uint32_t outw[VROW / 4];
+#pragma unroll
+      for (int k = 0; k < VROW / 4; ++k) outw[k] = 0u;
+#pragma unroll
+      for (int e = 0; e < D; ++e) {
+        const uint32_t code = vc_s[tid][e];
+        const int bitpos = e * VB;
+        outw[bitpos >> 5] |= code << (bitpos & 31);
+        if ((bitpos & 31) + VB > 32) outw[(bitpos >> 5) + 1] |= code >> (32 - (bitpos & 31));
+      }
+      const size_t row = page_row(a.p.block_table, d.max_pages_per_seq, b, g * G + t0 + tid, P, d.n_pages, h);
+      uint32_t* dst = reinterpret_cast<uint32_t*>(a.p.vcodes + row * VROW);
+#pragma unroll
+      for (int k = 0; k < VROW / 4; ++k) dst[k] = outw[k];
+    }
+    __syncthreads();  // vc_s is the next batch's
   }
 }
 
 
 struct HotArgs {
   tqk_cache_desc d;
-  uint16_t* hot_k;
-  uint16_t* hot_v;
+  uint8_t* hot_k;
+  uint8_t* hot_v;
   const int32_t* prev_len;
   const int32_t* n_new;
   const int32_t* hot_start;
-  const uint16_t* chunk_k;
-  const uint16_t* chunk_v;
+  const uint8_t* chunk_k;
+  const uint8_t* chunk_v;
   int chunk_tokens;
 };
 
@@ -657,12 +919,13 @@ __global__ __launch_bounds__(kThreads) void tqk_append_hot_kernel(HotArgs a) {
   const int R = d.hot_ring;
   const size_t rb = ((size_t)b * d.n_kv_heads + h) * R;
   const size_t cb = ((size_t)b * d.n_kv_heads + h) * a.chunk_tokens;
+  const int rowb = d.head_dim * (d.input_f32 ? 4 : 2), nc = rowb / 16;  // 16-byte pieces per row
   for (int s0 = t0 + (int)blockIdx.z * kHotSlice; s0 < t1; s0 += (int)gridDim.z * kHotSlice) {
     const int n = min(kHotSlice, t1 - s0);
-    for (int idx = tid; idx < n * 16; idx += kThreads) {
-      const int t = s0 + (idx >> 4), c = idx & 15;
-      const size_t src = (cb + (t - prev)) * TQK_D;
-      const size_t dst = (rb + (t % R)) * TQK_D;
+    for (int idx = tid; idx < n * nc; idx += kThreads) {
+      const int t = s0 + idx / nc, c = idx % nc;
+      const size_t src = (cb + (t - prev)) * rowb;
+      const size_t dst = (rb + (t % R)) * rowb;
       reinterpret_cast<uint4*>(a.hot_k + dst)[c] = reinterpret_cast<const uint4*>(a.chunk_k + src)[c];
       reinterpret_cast<uint4*>(a.hot_v + dst)[c] = reinterpret_cast<const uint4*>(a.chunk_v + src)[c];
     }
@@ -679,9 +942,8 @@ struct DequantArgs {
 
 // grid (n_items, Hkv), one token per thread: reconstruct keys (grid value then
 // the fp16 outlier overwrite) and values ((cent[code] @ Pi) * norm, NumPy order).
-template <int VB>
+template <int VB, int D>
 __global__ __launch_bounds__(kThreads) void tqk_dequant_group(DequantArgs a) {
-  constexpr int D = TQK_D;
   constexpr int VROW = D * VB / 8;
   const int item = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
   const tqk_cache_desc& d = a.d;
@@ -693,8 +955,8 @@ __global__ __launch_bounds__(kThreads) void tqk_dequant_group(DequantArgs a) {
   float* vo = a.vout + ((size_t)item * Hkv + h) * G * D;
   if (tid < G) {
     const size_t row = page_row(a.p.block_table, d.max_pages_per_seq, b, g * G + tid, P, d.n_pages, h);
-    const int kb = d.key_bits, KROW = k_row_bytes(kb);
-    uint32_t rw[TQK_D / 8];
+    const int kb = d.key_bits, KROW = k_row_bytes(kb, D);
+    uint32_t rw[D / 8];
     const uint32_t* kr = reinterpret_cast<const uint32_t*>(a.p.kcodes + row * KROW);
     for (int w = 0; w < KROW / 4; ++w) rw[w] = kr[w];
     if (d.key_grid == 2) {
@@ -723,7 +985,7 @@ __global__ __launch_bounds__(kThreads) void tqk_dequant_group(DequantArgs a) {
       }
     }
     float y[D];
-    if (v_tiled(G, P)) {
+    if (D == TQK_D && v_tiled(G, P, D, d.input_f32)) {
       // unit (lg, c) of the token's 16-token tile; tile rows start at row - (t % 16)
       const int tt = (g * G + tid) % 16;
       const uint8_t* tile = a.p.vcodes + (row - tt) * VROW;
@@ -761,13 +1023,41 @@ __global__ __launch_bounds__(kThreads) void tqk_dequant_group(DequantArgs a) {
   }
 }
 
+// one kernel instance per (value bits, head_dim)
+template <int D>
+void launch_by_vb(int vb, dim3 grid, hipStream_t st, const EncodeArgs& a) {
+  if (a.d.input_f32) {
+    if (vb == 2)
+      hipLaunchKernelGGL((tqk_encode_group_f32<2, D>), grid, dim3(kEncThreads), 0, st, a);
+    else if (vb == 3)
+      hipLaunchKernelGGL((tqk_encode_group_f32<3, D>), grid, dim3(kEncThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL((tqk_encode_group_f32<4, D>), grid, dim3(kEncThreads), 0, st, a);
+  } else if (vb == 2) {
+    hipLaunchKernelGGL((tqk_encode_group<2, D>), grid, dim3(kEncThreads), 0, st, a);
+  } else if (vb == 3) {
+    hipLaunchKernelGGL((tqk_encode_group<3, D>), grid, dim3(kEncThreads), 0, st, a);
+  } else {
+    hipLaunchKernelGGL((tqk_encode_group<4, D>), grid, dim3(kEncThreads), 0, st, a);
+  }
+}
+template <int D>
+void launch_by_vb(int vb, dim3 grid, hipStream_t st, const DequantArgs& a) {
+  if (vb == 2)
+    hipLaunchKernelGGL((tqk_dequant_group<2, D>), grid, dim3(kThreads), 0, st, a);
+  else if (vb == 3)
+    hipLaunchKernelGGL((tqk_dequant_group<3, D>), grid, dim3(kThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL((tqk_dequant_group<4, D>), grid, dim3(kThreads), 0, st, a);
+}
+
 }  // namespace
 
 extern "C" {
 
 int tqk_encode_groups(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t batch,
                       int32_t n_items, const int32_t* items, const int32_t* prev_len,
-                      const uint16_t* chunk_k, const uint16_t* chunk_v, int32_t chunk_tokens,
+                      const void* chunk_k, const void* chunk_v, int32_t chunk_tokens,
                       int32_t* overflow, void* stream) {
   int rc = tqk_check_desc(d);
   if (rc != TQK_OK) return rc;
@@ -787,18 +1077,18 @@ int tqk_encode_groups(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t 
   if (d->key_grid == 0 && d->zero_point == 2 && !p->zp_mean) return TQK_EINVAL;
   if (d->key_grid == 2 && !p->knorm) return TQK_EINVAL;
   const dim3 grid(n_items, d->n_kv_heads);
-  if (d->value_bits == 2)
-    hipLaunchKernelGGL(tqk_encode_group<2>, grid, dim3(kEncThreads), 0, st, a);
-  else if (d->value_bits == 3)
-    hipLaunchKernelGGL(tqk_encode_group<3>, grid, dim3(kEncThreads), 0, st, a);
+  if (d->head_dim == 64)
+    launch_by_vb<64>(d->value_bits, grid, st, a);
+  else if (d->head_dim == 128)
+    launch_by_vb<128>(d->value_bits, grid, st, a);
   else
-    hipLaunchKernelGGL(tqk_encode_group<4>, grid, dim3(kEncThreads), 0, st, a);
+    launch_by_vb<256>(d->value_bits, grid, st, a);
   return hipGetLastError() == hipSuccess ? TQK_OK : TQK_EHIP;
 }
 
 int tqk_append_hot(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t batch,
                    const int32_t* prev_len, const int32_t* n_new, const int32_t* hot_start,
-                   const uint16_t* chunk_k, const uint16_t* chunk_v, int32_t chunk_tokens,
+                   const void* chunk_k, const void* chunk_v, int32_t chunk_tokens,
                    void* stream) {
   int rc = tqk_check_desc(d);
   if (rc != TQK_OK) return rc;
@@ -807,13 +1097,13 @@ int tqk_append_hot(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t bat
     return TQK_EINVAL;
   HotArgs a;
   a.d = *d;
-  a.hot_k = p->hot_k;
-  a.hot_v = p->hot_v;
+  a.hot_k = static_cast<uint8_t*>(p->hot_k);
+  a.hot_v = static_cast<uint8_t*>(p->hot_v);
   a.prev_len = prev_len;
   a.n_new = n_new;
   a.hot_start = hot_start;
-  a.chunk_k = chunk_k;
-  a.chunk_v = chunk_v;
+  a.chunk_k = static_cast<const uint8_t*>(chunk_k);
+  a.chunk_v = static_cast<const uint8_t*>(chunk_v);
   a.chunk_tokens = chunk_tokens;
   // the surviving tokens of a sequence number at most min(chunk, ring)
   const int span = min(chunk_tokens, d->hot_ring);
@@ -838,12 +1128,12 @@ int tqk_dequant_groups(const tqk_cache_desc* d, const tqk_cache_ptrs* p, int32_t
   a.vout = vout;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid(n_items, d->n_kv_heads);
-  if (d->value_bits == 2)
-    hipLaunchKernelGGL(tqk_dequant_group<2>, grid, dim3(kThreads), 0, st, a);
-  else if (d->value_bits == 3)
-    hipLaunchKernelGGL(tqk_dequant_group<3>, grid, dim3(kThreads), 0, st, a);
+  if (d->head_dim == 64)
+    launch_by_vb<64>(d->value_bits, grid, st, a);
+  else if (d->head_dim == 128)
+    launch_by_vb<128>(d->value_bits, grid, st, a);
   else
-    hipLaunchKernelGGL(tqk_dequant_group<4>, grid, dim3(kThreads), 0, st, a);
+    launch_by_vb<256>(d->value_bits, grid, st, a);
   return hipGetLastError() == hipSuccess ? TQK_OK : TQK_EHIP;
 }
 

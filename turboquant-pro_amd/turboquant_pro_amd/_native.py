@@ -19,7 +19,7 @@ TQK_EUNSUPPORTED = 2
 TQK_EHIP = 3
 TQK_EWORKSPACE = 4
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 # Every symbol include/tqk.h declares (checked by the CPU test suite).
 EXPORTS = (
@@ -36,7 +36,7 @@ class CacheDesc(ctypes.Structure):
         "key_bits", "value_bits", "outliers_per_channel", "outlier_cap",
         "max_pages_per_seq", "max_groups_per_seq", "hot_ring", "n_pages")] + [
         ("sm_scale", ctypes.c_float), ("key_grid", ctypes.c_int32), ("zero_point", ctypes.c_int32),
-        ("dc_mask", ctypes.c_uint32 * 4)]
+        ("input_f32", ctypes.c_int32), ("dc_mask", ctypes.c_uint32 * 8)]
 
 
 class CachePtrs(ctypes.Structure):
@@ -49,7 +49,7 @@ class BlockDesc(ctypes.Structure):
     """``tqk_block_desc``: one (B, H, S, D) block for the stateless quantizers."""
     _fields_ = [(n, ctypes.c_int32) for n in (
         "batch", "n_heads", "tokens", "head_dim", "bits", "key_grid", "zero_point",
-        "outliers_per_channel", "outlier_cap", "input_f32")] + [("dc_mask", ctypes.c_uint32 * 4)]
+        "outliers_per_channel", "outlier_cap", "input_f32")] + [("dc_mask", ctypes.c_uint32 * 8)]
 
 
 _lib = None

@@ -24,6 +24,9 @@ LLOYD_MAX_LEVELS = {
 }
 
 SUPPORTED_BITS = tuple(sorted(LLOYD_MAX_LEVELS))
+# head dims the gfx950 kernels are built for (the MFMA decode serves 128, the
+# VALU decode 64 and 256)
+HEAD_DIMS = (64, 128, 256)
 
 
 def value_codebook(bits: int, head_dim: int) -> tuple[np.ndarray, np.ndarray]:
@@ -81,10 +84,14 @@ def dc_channel_mask(rope_theta: float, head_dim: int, window: int) -> np.ndarray
 
 
 def dc_mask_words(mask: np.ndarray) -> list[int]:
-    """A ``(128,)`` bool channel mask as the descriptor's four uint32 words:
-    channel j is bit j % 32 of word j // 32."""
+    """A ``(head_dim,)`` bool channel mask (head_dim <= 256) as the
+    descriptor's eight uint32 words: channel j is bit j % 32 of word j // 32,
+    words past the mask are 0."""
     m = np.asarray(mask, bool).reshape(-1)
-    return [int(sum(1 << b for b in range(32) if m[32 * w + b])) for w in range(len(m) // 32)]
+    if m.size > 256 or m.size % 32:
+        raise ValueError(f"channel mask of {m.size} channels")
+    words = [int(sum(1 << b for b in range(32) if m[32 * w + b])) for w in range(m.size // 32)]
+    return words + [0] * (8 - len(words))
 
 
 def rope_averaged_bias(k_bias: np.ndarray, rope_theta: float, head_dim: int, start: int,

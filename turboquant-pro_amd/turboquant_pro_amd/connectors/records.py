@@ -52,9 +52,10 @@ class BlockRecord:
 
 @dataclasses.dataclass
 class RawTokens:
-    """Tokens kept as they are, fp16 ``(1, H, n, D)``: the payload of the hot
-    window's records in a pool's live-path save (``<layer>#hot<i>``), so a
-    restore gives back exactly what the pool held.  Its blob member is
+    """Tokens kept as they are, fp16 or fp32 ``(1, H, n, D)`` (the pool's
+    precision): the payload of the hot window's records in a pool's live-path
+    save (``<layer>#hot<i>``), so a restore gives back exactly what the pool
+    held.  A format of this library only.  Its blob member is
     ``k.data`` / ``v.data``; a reader without this payload type sees a record
     its quantizer cannot decode, which the store treats as a miss."""
 

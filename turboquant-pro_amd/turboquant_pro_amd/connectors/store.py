@@ -160,10 +160,14 @@ class TurboQuantBlockStore:
         """Store one sequence's layer K/V ``(H, L, D)`` the way a paged pool
         holds it: one record per coded group of the flush cadence
         (``<layer>#g<i>``, ``group_tokens`` tokens each, so each is exactly the
-        pool's group) and the hot window as it is, fp16 (``<layer>#hot0``, a
-        :class:`RawTokens` payload), so that a restore is the pool it came
-        from.  Every record is a ``tqp-kv-npz/1`` record.  Returns the groups."""
+        pool's group) and the hot window as it is (``<layer>#hot0``, a
+        :class:`RawTokens` payload: fp16 for fp16 K/V, fp32 otherwise, the
+        precision of the pool they came from), so that a restore is the pool
+        it came from.  The group records are ``tqp-kv-npz/1`` records the
+        reference reads; the hot record is this library's own.  Returns the
+        groups."""
         from ..codebooks import n_groups_for
+        hot_dtype = np.float16 if str(getattr(keys, "dtype", "")).endswith("float16") else np.float32
         k, v = self._host_f32(keys), self._host_f32(values)
         k4, v4 = self._as_bhsd(k), self._as_bhsd(v)
         if k4.shape[0] != 1 or k4.shape != v4.shape:
@@ -175,11 +179,11 @@ class TurboQuantBlockStore:
                     position_start=g * G)
                 for g in range(ng)}
         if L > ng * G:
-            hk = np.ascontiguousarray(k4[:, :, ng * G:], dtype=np.float16)
-            hv = np.ascontiguousarray(v4[:, :, ng * G:], dtype=np.float16)
+            hk = np.ascontiguousarray(k4[:, :, ng * G:], dtype=hot_dtype)
+            hv = np.ascontiguousarray(v4[:, :, ng * G:], dtype=hot_dtype)
             recs[f"{layer_name}#hot0"] = BlockRecord(
                 key_payload=RawTokens(hk), value_payload=RawTokens(hv), shape=tuple(hk.shape[1:]),
-                dtype="float16", num_tokens=int(hk.shape[2]), head_dim=int(hk.shape[3]),
+                dtype=np.dtype(hot_dtype).name, num_tokens=int(hk.shape[2]), head_dim=int(hk.shape[3]),
                 n_heads=int(hk.shape[1]))
         with self._lock:
             for name, rec in recs.items():
@@ -192,7 +196,7 @@ class TurboQuantBlockStore:
     def load_into_pool(self, request_id: str, layer_name: str, pool, b: int) -> int:
         """Restore a sequence saved by :meth:`save_sequence` into sequence ``b``
         of ``pool`` (empty): the coded groups go in as codes, unchanged (no
-        dequantize / re-encode), the hot window as the fp16 tokens it held.
+        dequantize / re-encode), the hot window as the tokens it held.
         Returns the tokens restored, 0 when nothing is stored (a miss).
         Raises ``ValueError`` when the records are not in the pool's format
         (key grid, zero point and, for sparse/bias zero points, rope_theta and
@@ -264,10 +268,12 @@ class TurboQuantBlockStore:
                            "outlier_idx": kp.outlier_idx, "outlier_val": kp.outlier_val},
                           {"vpacked": vp.indices, "vnorms": vp.norms[0]}))
         if hot is not None:
-            hk = torch.from_numpy(np.asarray(hot.key_payload.data, np.float16)[0])
-            hv = torch.from_numpy(np.asarray(hot.value_payload.data, np.float16)[0])
+            hk = torch.from_numpy(np.ascontiguousarray(hot.key_payload.data)[0])
+            hv = torch.from_numpy(np.ascontiguousarray(hot.value_payload.data)[0])
+            if pool.dtype == torch.float16 and hk.dtype != torch.float16:
+                raise ValueError("the stored hot window is fp32; this pool holds fp16 tokens")
         else:
-            hk = hv = torch.zeros((H, 0, D), dtype=torch.float16)
+            hk = hv = torch.zeros((H, 0, D), dtype=pool.dtype)
         pool.load_sequence(b, items, hk, hv)
         return len(items) * G + int(hk.shape[1])
 

@@ -19,8 +19,8 @@ Differences from the reference, all deliberate:
     kernels consume); codes are bit-exact with the reference for fp16 inputs;
   * ``per_channel_keys=False`` (PolarQuant keys, turboquant_pro/core.py:1028-1029)
     requires ``key_bits == value_bits``, as the reference's fused decode does;
-  * configurations without a gfx950 form (symmetric-NF4 and quantile keys;
-    head_dim != 128) raise
+  * configurations without a gfx950 form (quantile keys; head_dim other than
+    64, 128 or 256) raise
     NotImplementedError at construction instead of silently running on the CPU;
   * an optional ``n_q_heads`` (a multiple of ``n_heads``) serves GQA queries.
 """
@@ -31,7 +31,7 @@ import logging
 
 import numpy as np
 
-from .codebooks import SUPPORTED_BITS, group_tokens_for, n_groups_for
+from .codebooks import HEAD_DIMS, SUPPORTED_BITS, group_tokens_for, n_groups_for
 from .pool import TQKVPool
 
 logger = logging.getLogger(__name__)
@@ -40,6 +40,26 @@ logger = logging.getLogger(__name__)
 def _torch():
     import torch
     return torch
+
+
+def merge_partials(parts):
+    """Final attention output ``(H, D)`` of unnormalised online-softmax states
+    ``[(m (H,), l (H,), acc (H, D)), ...]`` over disjoint key sets -- e.g.
+    :meth:`TurboQuantKVCache.fused_decode_partials` and a state over extra
+    keys (the contract of turboquant_pro/kv_fused.py:139-153).  NumPy arrays or
+    torch tensors; each state is rescaled to the largest running max."""
+    if not parts:
+        raise ValueError("no partial states to merge")
+    torch = _torch() if any(isinstance(p[0], _torch().Tensor) for p in parts) else None
+    if torch is not None:
+        m = torch.stack([torch.as_tensor(p[0]) for p in parts])
+        l_ = torch.stack([torch.as_tensor(p[1]) for p in parts])
+        acc = torch.stack([torch.as_tensor(p[2]) for p in parts])
+        w = torch.exp(m - m.max(dim=0).values)
+    else:
+        m, l_, acc = (np.stack([np.asarray(p[i]) for p in parts]) for i in range(3))
+        w = np.exp(m - m.max(axis=0))
+    return (acc * w[..., None]).sum(0) / (l_ * w).sum(0)[..., None]
 
 
 class TurboQuantKVCache:
@@ -61,7 +81,8 @@ class TurboQuantKVCache:
                  key_nf4: bool = False, key_nf4_asym: bool = False,
                  key_outlier_frac: float = 0.0, key_zero_point: str = "calibrated",
                  key_rope_theta: float | None = None, key_k_bias=None, *,
-                 n_q_heads: int | None = None, capacity: int = 4096) -> None:
+                 n_q_heads: int | None = None, capacity: int = 4096,
+                 input_dtype: str | None = None) -> None:
         self.head_dim = head_dim
         self.n_heads = n_heads
         self.n_q_heads = n_heads if n_q_heads is None else n_q_heads
@@ -119,12 +140,21 @@ class TurboQuantKVCache:
         # the asym-NF4 encode with no mean
         self._pool_zero_point = ("symmetric" if per_channel_keys and key_nf4 and not key_nf4_asym
                                  else key_zero_point)
-        if head_dim != 128:
-            raise NotImplementedError("the gfx950 kernels are built for head_dim=128")
+        if head_dim not in HEAD_DIMS:
+            raise NotImplementedError(f"head_dim {head_dim}: the gfx950 kernels serve {HEAD_DIMS}")
         if group_tokens_for(hot_window) > 256 or hot_window < 1:
             raise NotImplementedError("hot_window must be in [1, 512] for the gfx950 kernels")
         self._device = _torch().device(f"cuda:{device_id}")
         self._capacity = max(capacity, hot_window + 1)
+        # the precision the cache takes its tokens in: fixed ("float16",
+        # "float32") or, with None, that of the first tokens appended to the
+        # empty cache -- fp16 tokens make an fp16 cache, any other float dtype
+        # (fp32, bf16: both exact in fp32) an fp32 one, whose codes are the
+        # reference's on the same fp32 values
+        if input_dtype not in (None, "float16", "float32"):
+            raise ValueError(f"input_dtype must be None, 'float16' or 'float32', not {input_dtype!r}")
+        self.input_dtype = input_dtype
+        self._pool_dtype = input_dtype or "float16"
         self._pool = self._new_pool(self._capacity, rotation=None)
         self._rotation = (self._pool.pi.cpu().numpy(), self._pool.pi_t.cpu().numpy())
 
@@ -136,7 +166,7 @@ class TurboQuantKVCache:
                         seed=self.seed, rotation=rotation,
                         device=self._device, key_grid=self.key_grid,
                         zero_point=self._pool_zero_point, rope_theta=self.key_rope_theta,
-                        k_bias=self.key_k_bias)
+                        k_bias=self.key_k_bias, input_dtype=self._pool_dtype)
 
     def _grow(self, need: int) -> None:
         """Reallocate to hold ``need`` tokens (at least doubling), moving the
@@ -159,7 +189,8 @@ class TurboQuantKVCache:
 
     # --------------------------------------------------------------- append --
     def _as_tokens(self, x):
-        """(H, D) / (1, H, 1, D) / (H, n, D) -> fp16 device tensor (1, H, n, D)."""
+        """(H, D) / (1, H, 1, D) / (H, n, D) -> device tensor (1, H, n, D) in the
+        pool's input dtype."""
         torch = _torch()
         t = x if isinstance(x, torch.Tensor) else torch.from_numpy(np.asarray(x))
         if t.dim() == 2:
@@ -169,7 +200,19 @@ class TurboQuantKVCache:
         if t.dim() != 4 or t.shape[0] != 1 or t.shape[1] != self.n_heads or t.shape[3] != self.head_dim:
             raise ValueError(f"expected (H, D), (1, H, 1, D) or (H, n, D) with H={self.n_heads}, "
                              f"D={self.head_dim}; got {tuple(x.shape)}")
-        return t.to(device=self._device, dtype=torch.float16).contiguous()
+        return t.to(device=self._device, dtype=self._pool.dtype).contiguous()
+
+    def _adopt_dtype(self, x) -> None:
+        """With no fixed input_dtype, an empty cache takes the precision of the
+        tokens appended to it (a fresh pool of the same rotation)."""
+        if self.input_dtype is not None or self.length:
+            return
+        torch = _torch()
+        dt = x.dtype if isinstance(x, torch.Tensor) else np.asarray(x).dtype
+        want = "float16" if dt in (torch.float16, np.float16) else "float32"
+        if want != self._pool_dtype:
+            self._pool_dtype = want
+            self._pool = self._new_pool(self._capacity, rotation=self._rotation)
 
     def append(self, key, value) -> None:
         """Add one token's key/value ``(H, D)`` or ``(1, H, 1, D)``
@@ -179,6 +222,7 @@ class TurboQuantKVCache:
     def extend(self, keys, values) -> None:
         """Append several tokens at once, ``(H, n, D)`` or ``(1, H, n, D)``;
         identical to n ``append`` calls."""
+        self._adopt_dtype(keys)
         k, v = self._as_tokens(keys), self._as_tokens(values)
         if k.shape != v.shape:
             raise ValueError("keys and values must have the same shape")
@@ -227,23 +271,25 @@ class TurboQuantKVCache:
             raise RuntimeError("cache is empty")
         is_np = not isinstance(query, torch.Tensor)
         q = query if not is_np else torch.from_numpy(np.asarray(query))
-        q = q.reshape(self.n_q_heads, self.head_dim).to(device=self._device, dtype=torch.float16)
+        # an fp32 cache takes the query in fp32; an fp16 cache rounds it to fp16
+        q = q.reshape(self.n_q_heads, self.head_dim).to(device=self._device, dtype=self._pool.dtype)
         out = self._pool.decode(q[None].contiguous())[0]
         return out.cpu().numpy() if is_np else out
 
     def fused_decode_partials(self, query):
         """Unnormalised ``(m (Hq,), l (Hq,), acc (Hq, D))`` of one step, mergeable
-        with :func:`turboquant_pro_amd.kv_fused.merge_partials`."""
+        with :func:`merge_partials`."""
         torch = _torch()
         q = torch.as_tensor(np.asarray(query) if not isinstance(query, torch.Tensor) else query)
-        q = q.reshape(self.n_q_heads, self.head_dim).to(device=self._device, dtype=torch.float16)
+        q = q.reshape(self.n_q_heads, self.head_dim).to(device=self._device, dtype=self._pool.dtype)
         m, l_, acc = self._pool.decode_partials(q[None].contiguous())
         return m[0], l_[0], acc[0]
 
     # ---------------------------------------------------------------- stats --
     def memory_stats(self) -> dict[str, float]:
         """Byte accounting in the reference's container terms
-        (turboquant_pro/core.py:1267-1295); hot tokens are held in fp16."""
+        (turboquant_pro/core.py:1267-1295); hot tokens are held in the
+        cache's input dtype (fp16 or fp32)."""
         H, D, G = self.n_heads, self.head_dim, self._pool.group_tokens
         ng = self._pool.n_groups(0)
         n_out = int(self._pool.ocount[:ng, :, -1].sum().item()) if ng else 0
@@ -258,7 +304,7 @@ class TurboQuantKVCache:
             key_bytes = ng * (H * G * D * self.key_bits // 8 + H * D * 4 + H * zp_ch * 4) + n_out * 6
         val_bytes = ng * (H * G * D * self.value_bits // 8 + H * G * 4)
         cold = float(key_bytes + val_bytes)
-        hot = float(self.hot_length * H * D * 2 * 2)
+        hot = float(self.hot_length * H * D * 2 * self._pool.hot_k.element_size())
         unc = float(self.length * H * D * 4 * 2)
         return {"cold_bytes": cold, "hot_bytes": hot, "total_bytes": cold + hot,
                 "uncompressed_equivalent_bytes": unc,

@@ -98,7 +98,7 @@ def codes_from_key_rows(rows: np.ndarray, bits: int, D: int = 128) -> np.ndarray
     n = rows.shape[0]
     if bits == 4:
         return unpack_keys(rows.reshape(-1), n * D).reshape(n, D)
-    bitv = np.unpackbits(rows.reshape(n, D // 32, D * bits // 32), axis=-1, bitorder="little")
+    bitv = np.unpackbits(rows.reshape(n, D // 32, 4 * bits), axis=-1, bitorder="little")
     bitv = bitv.reshape(n, D, bits).astype(np.uint8)
     return (bitv << np.arange(bits, dtype=np.uint8)).sum(axis=-1, dtype=np.uint32).astype(np.uint8)
 

@@ -20,7 +20,8 @@ GPU (quantize-on-append in the encode kernel) and:
 Differences from the reference layer, by design of the pool: tokens leave
 the hot window in groups of ``(hot_window + 1) // 2`` (the cadence of
 ``TurboQuantKVCache``, turboquant_pro/core.py:1015-1038) instead of
-overflow-sized spills; the hot window is kept in fp16; head_dim is 128; a
+overflow-sized spills; the hot window is kept in fp16 (or fp32 with
+``input_dtype="float32"``); head_dim is 64, 128 or 256; a
 layer starts with room for 4096 tokens per sequence (or twice its first
 chunk) and doubles on demand, moving its codes, up to ``max_cache_len`` (else
 the model config's ``max_position_embeddings``) as a bound only.
@@ -62,7 +63,8 @@ class TurboQuantLayer(CacheLayerMixin):
 
     def __init__(self, hot_window: int = 512, key_bits: int = 4, value_bits: int = 4,
                  outlier_frac: float = 0.02, seed: int = 0, n_q_heads: int | None = None,
-                 max_cache_len: int | None = None, fused_decode: bool = False) -> None:
+                 max_cache_len: int | None = None, fused_decode: bool = False,
+                 input_dtype: str = "float16") -> None:
         super().__init__()
         if hot_window < 1:
             raise ValueError("hot_window must be >= 1")
@@ -71,6 +73,9 @@ class TurboQuantLayer(CacheLayerMixin):
         self.n_q_heads = n_q_heads
         self.max_cache_len = max_cache_len
         self.fused_decode = bool(fused_decode)
+        # "float16": states rounded to fp16 (the MFMA decode); "float32": kept
+        # exactly (bf16 and fp32 models; codes the reference's, VALU decode)
+        self.input_dtype = input_dtype
         self.pool = None
         self.head_dim = self.n_kv_heads = self.batch = None
 
@@ -89,7 +94,8 @@ class TurboQuantLayer(CacheLayerMixin):
             n_kv_heads=self.n_kv_heads, n_q_heads=self.n_q_heads or self.n_kv_heads,
             head_dim=self.head_dim, max_batch=self.batch, max_seq_len=max(cap, first),
             hot_window=self.hot_window, key_bits=self.key_bits, value_bits=self.value_bits,
-            outlier_frac=self.outlier_frac, seed=self.seed, device=self.device)
+            outlier_frac=self.outlier_frac, seed=self.seed, device=self.device,
+            input_dtype=self.input_dtype)
         self.is_initialized = True
 
     def _ingest(self, key_states, value_states) -> None:
@@ -107,8 +113,8 @@ class TurboQuantLayer(CacheLayerMixin):
             if self.max_cache_len:
                 cap = min(cap, int(self.max_cache_len))
             self.pool = self.pool.grown(cap)
-        self.pool.append(key_states.to(torch.float16).contiguous(),
-                         value_states.to(torch.float16).contiguous())
+        self.pool.append(key_states.to(self.pool.dtype).contiguous(),
+                         value_states.to(self.pool.dtype).contiguous())
 
     def update(self, key_states, value_states, *args, **kwargs):
         """Append the new tokens; return dense K/V, or for a fused decode step
@@ -127,7 +133,7 @@ class TurboQuantLayer(CacheLayerMixin):
     def dense(self, dtype=None):
         """The whole cache as dense ``(B, H, L, D)`` K/V in ``dtype`` (the model
         dtype by default): coded groups through the GPU dequant (fp32), then
-        the fp16 hot window."""
+        the hot window."""
         pool = self.pool
         B, H, D, G = self.batch, self.n_kv_heads, self.head_dim, pool.group_tokens
         ng = pool.n_groups(0)
@@ -150,7 +156,7 @@ class TurboQuantLayer(CacheLayerMixin):
             raise ValueError(f"the layer's pool serves {pool.n_q_heads} query heads, "
                              f"got {query.shape[1]} (pass the model config)")
         pool.desc.sm_scale = float(scaling)
-        return pool.decode(query[:, :, 0].to(torch.float16).contiguous())
+        return pool.decode(query[:, :, 0].to(pool.dtype).contiguous())
 
     # ------------------------------------------------------------ contract
     def get_seq_length(self) -> int:
@@ -257,11 +263,14 @@ class TurboQuantCache(Cache):
     :class:`TurboQuantLayer` per model layer.  ``config`` (the model config)
     gives the query-head count the fused decode needs and the default
     capacity; ``fused_decode`` routes decode steps to the kernel and needs the
-    model's attention implementation to be ``"tqk_gfx950"``."""
+    model's attention implementation to be ``"tqk_gfx950"``; ``input_dtype``
+    "float32" keeps bf16/fp32 states exact (the reference's codes) instead
+    of rounding them to fp16."""
 
     def __init__(self, hot_window: int = 512, key_bits: int = 4, value_bits: int = 4,
                  outlier_frac: float = 0.02, seed: int = 0, *, config=None,
-                 max_cache_len: int | None = None, fused_decode: bool = False) -> None:
+                 max_cache_len: int | None = None, fused_decode: bool = False,
+                 input_dtype: str = "float16") -> None:
         if not _HAS_TRANSFORMERS:  # pragma: no cover - dependency guard
             raise ImportError("TurboQuantCache requires transformers (v5+) and torch")
         self.hot_window, self.key_bits, self.value_bits = int(hot_window), int(key_bits), int(value_bits)
@@ -274,7 +283,8 @@ class TurboQuantCache(Cache):
         super().__init__(layer_class_to_replicate=partial(
             TurboQuantLayer, hot_window=self.hot_window, key_bits=self.key_bits,
             value_bits=self.value_bits, outlier_frac=self.outlier_frac, seed=self.seed,
-            n_q_heads=n_q, max_cache_len=max_cache_len, fused_decode=fused_decode))
+            n_q_heads=n_q, max_cache_len=max_cache_len, fused_decode=fused_decode,
+            input_dtype=input_dtype))
 
 
 def enable_turboquant_cache(model, **kwargs):

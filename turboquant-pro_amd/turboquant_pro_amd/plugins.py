@@ -37,7 +37,7 @@ from typing import Any, Protocol, runtime_checkable
 
 import numpy as np
 
-from .codebooks import outliers_per_channel, random_rotation
+from .codebooks import HEAD_DIMS, outliers_per_channel, random_rotation
 from .formats import NF4, pack_values, unpack_key_codes, unpack_values
 
 logger = logging.getLogger(__name__)
@@ -296,7 +296,7 @@ class PerChannelKVQuantizer:
     The constructor validates like ``PerChannelKV.__init__``
     (turboquant_pro/per_channel_kv.py:182-213) and raises
     ``NotImplementedError`` for the modes the library does not encode
-    (data-fit quantiles, head_dim != 128)."""
+    (data-fit quantiles, head_dim other than 64, 128 or 256)."""
 
     _ZP_MODES = ("calibrated", "sparse", "bias")
 
@@ -322,10 +322,10 @@ class PerChannelKVQuantizer:
         if zero_point == "bias" and k_bias is None:
             raise ValueError('zero_point="bias" requires k_bias')
         uniform = not nf4 and not nuq
-        if nuq or head_dim != 128:
+        if nuq or head_dim not in HEAD_DIMS:
             raise NotImplementedError("the gfx950 key encode is per-channel asym-NF4 (any zero point), "
                                       "symmetric NF4 "
-                                      "or uniform 2/3/4-bit, at head_dim 128")
+                                      f"or uniform 2/3/4-bit, at head_dim {HEAD_DIMS}")
         self.head_dim, self.n_heads, self.bits = head_dim, n_heads, bits
         self.uniform = uniform
         # symmetric NF4 (nf4 without nf4_asym): the asym-NF4 encode with no mean
@@ -417,9 +417,9 @@ class PerChannelKVQuantizer:
         uniform = c.nf4_scale is None and c.levels is None and c.scale is not None and c.zero is not None
         if c.levels is not None or (not uniform and c.nf4_scale is None):
             raise NotImplementedError("data-fit (quantile) key grids have no gfx950 dequant")
-        if c.bits not in (2, 3, 4) or (c.bits != 4 and not uniform) or D != 128:
+        if c.bits not in (2, 3, 4) or (c.bits != 4 and not uniform) or D not in HEAD_DIMS:
             raise NotImplementedError("the gfx950 dequant reads asym-NF4 4-bit or uniform 2/3/4-bit "
-                                      "keys at head_dim 128")
+                                      f"keys at head_dim {HEAD_DIMS}")
         if uniform:
             scale = np.asarray(c.scale, np.float32)[:, :, 0, :]
             zero = np.asarray(c.zero, np.float32)[:, :, 0, :]
@@ -522,7 +522,7 @@ class PolarQuantizer:
     Constructor as ``TurboQuantKV.__init__`` (turboquant_pro/core.py:178-228):
     ``bits`` is the default width, ``key_bits`` / ``value_bits`` override it
     per kind (``compress(kind=...)``); the rotation is the reference's
-    ``seed`` recipe.  ``head_dim`` other than 128 has no gfx950 form."""
+    ``seed`` recipe.  ``head_dim`` is 64, 128 or 256 (the gfx950 kernels')."""
 
     def __init__(self, head_dim: int = 128, n_heads: int = 32, bits: int = 3,
                  key_bits: int | None = None, value_bits: int | None = None, use_gpu: bool = True,
@@ -532,8 +532,8 @@ class PolarQuantizer:
         for name, v in (("bits", bits), ("key_bits", self.key_bits), ("value_bits", self.value_bits)):
             if v not in (2, 3, 4):
                 raise ValueError(f"Unsupported {name}={v}; choose from [2, 3, 4]")
-        if head_dim != 128:
-            raise NotImplementedError("the gfx950 PolarQuant encode serves head_dim 128")
+        if head_dim not in HEAD_DIMS:
+            raise NotImplementedError(f"the gfx950 PolarQuant encode serves head_dim {HEAD_DIMS}")
         self.head_dim, self.n_heads, self.bits, self.seed = head_dim, n_heads, bits, seed
         self.device = device
         # drawn once, as TurboQuantKV does (core.py:178-228): with seed=None the

@@ -6,7 +6,8 @@ sequences in HBM, in the layout documented in ``include/tqk.h``:
 * coded groups live in pages (``page_tokens`` tokens x all kv heads) found
   through a per-sequence block table, with per-(group, head) metadata (NF4
   scale/mean, outlier side-list) in group slots found through a group table;
-* the fp16 hot window is a per-(sequence, head) ring of ``hot_window`` tokens.
+* the hot window is a per-(sequence, head) ring of ``hot_window`` tokens,
+  fp16 (or fp32: ``input_dtype="float32"``, codes then from the fp32 values).
 
 Appending runs the quantize-on-flush kernel for every group that the append
 completes (the reference flush cadence: first flush at ``hot_window + 1``
@@ -26,7 +27,7 @@ from . import _native as N
 from .formats import (NF4_ZERO_CODE, codes_from_key_rows, key_rows_from_codes, nf4_codes,
                       pack_key_codes, pack_values, tile_value_rows, uniform_codes, unpack_key_codes,
                       unpack_values, untile_value_rows)
-from .codebooks import (dc_channel_mask, dc_mask_words, group_tokens_for, n_groups_for,
+from .codebooks import (HEAD_DIMS, dc_channel_mask, dc_mask_words, group_tokens_for, n_groups_for,
                         outliers_per_channel, random_rotation, rope_averaged_bias, value_codebook)
 
 # key zero points; "symmetric" (symmetric NF4: no mean, per_channel_kv.py:354-357)
@@ -49,14 +50,14 @@ class TQKVPool:
                  page_tokens: int | None = None, outlier_cap: int | None = None,
                  seed=None, rotation: tuple | None = None, block_table=None, device=None,
                  key_grid: str = "nf4_asym", zero_point: str = "calibrated",
-                 rope_theta: float | None = None, k_bias=None):
+                 rope_theta: float | None = None, k_bias=None, input_dtype: str = "float16"):
         torch = _torch()
         self._init_args = dict(n_kv_heads=n_kv_heads, n_q_heads=n_q_heads, head_dim=head_dim,
                                max_batch=max_batch, hot_window=hot_window, key_bits=key_bits,
                                value_bits=value_bits, outlier_frac=outlier_frac,
                                page_tokens=page_tokens, outlier_cap=outlier_cap, device=device,
                                key_grid=key_grid, zero_point=zero_point, rope_theta=rope_theta,
-                               k_bias=k_bias)
+                               k_bias=k_bias, input_dtype=input_dtype)
         self._custom_table = block_table is not None
         if zero_point not in ZERO_POINTS:
             raise ValueError(f"zero_point must be one of {tuple(ZERO_POINTS)}")
@@ -94,15 +95,24 @@ class TQKVPool:
         self.key_bits, self.value_bits, self.outlier_frac = key_bits, value_bits, outlier_frac
         self.group_tokens, self.page_tokens = G, P
         self.max_groups, self.max_pages = max_groups, max_pages
-        # value codes in the MFMA-tiled byte order (see formats.py)
-        self.tiled = (P % 16 == 0) and (G % 32 == 0)
+        if head_dim not in HEAD_DIMS:
+            raise NotImplementedError(f"head_dim {head_dim}: the gfx950 kernels serve {HEAD_DIMS}")
+        if input_dtype not in ("float16", "float32"):
+            raise ValueError(f"input_dtype must be 'float16' or 'float32', not {input_dtype!r}")
+        # fp32 caches: fp32 hot ring, query and appended tokens; codes from the
+        # fp32 values (the VALU decode serves them)
+        self.input_dtype = input_dtype
+        self.f32 = input_dtype == "float32"
+        # value codes in the MFMA-tiled byte order (see formats.py); head_dim
+        # 128 and fp16 inputs only, the MFMA decode's
+        self.tiled = head_dim == 128 and not self.f32 and (P % 16 == 0) and (G % 32 == 0)
         self.desc = N.CacheDesc(
             n_kv_heads=n_kv_heads, n_q_heads=Hq, head_dim=head_dim, hot_window=hot_window,
             group_tokens=G, page_tokens=P, key_bits=key_bits, value_bits=value_bits,
             outliers_per_channel=k_out, outlier_cap=outlier_cap,
             max_pages_per_seq=max_pages, max_groups_per_seq=max_groups,
             hot_ring=hot_window, n_pages=max_batch * max_pages, sm_scale=1.0 / math.sqrt(head_dim),
-            key_grid=KEY_GRIDS[key_grid], zero_point=ZERO_POINTS[zero_point])
+            key_grid=KEY_GRIDS[key_grid], zero_point=ZERO_POINTS[zero_point], input_f32=int(self.f32))
         self.key_grid = key_grid
         self.zero_point, self.rope_theta = zero_point, rope_theta
         # "sparse": the channels whose rotary wavelength exceeds a group
@@ -129,8 +139,9 @@ class TQKVPool:
         # cumulative outlier counts at every 32-token boundary of a group (last = total)
         self.ocount = torch.zeros((n_slots, n_kv_heads, 8), dtype=i32, device=dev)
         self.oent = torch.zeros((n_slots, n_kv_heads, max(outlier_cap, 1)), dtype=i32, device=dev)
-        self.hot_k = torch.zeros((max_batch, n_kv_heads, hot_window, head_dim), dtype=f16, device=dev)
-        self.hot_v = torch.zeros((max_batch, n_kv_heads, hot_window, head_dim), dtype=f16, device=dev)
+        self.dtype = f32 if self.f32 else f16  # hot ring, appended tokens and queries
+        self.hot_k = torch.zeros((max_batch, n_kv_heads, hot_window, head_dim), dtype=self.dtype, device=dev)
+        self.hot_v = torch.zeros((max_batch, n_kv_heads, hot_window, head_dim), dtype=self.dtype, device=dev)
         if block_table is None:
             bt = self._clustered_table(max_batch, max_pages, P, G)
         else:
@@ -283,17 +294,17 @@ class TQKVPool:
 
     # ------------------------------------------------------------------ #
     def append(self, k, v, n_new=None, check_overflow: bool = True) -> None:
-        """Append tokens: ``k``, ``v`` fp16 ``(max_batch, Hkv, T, D)`` on the
-        device; sequence ``b`` takes its first ``n_new[b]`` tokens (all T by
-        default).  Equivalent to T one-token ``TurboQuantKVCache.append`` calls
+        """Append tokens: ``k``, ``v`` ``(max_batch, Hkv, T, D)`` on the device,
+        fp16 (fp32 for an fp32 pool); sequence ``b`` takes its first
+        ``n_new[b]`` tokens (all T by default).  Equivalent to T one-token ``TurboQuantKVCache.append`` calls
         per sequence (turboquant_pro/core.py:986-1038)."""
         torch = _torch()
         self.check(wait=False)
         B, T = self.max_batch, int(k.shape[2])
         if tuple(k.shape) != (B, self.n_kv_heads, T, self.head_dim) or k.shape != v.shape:
             raise ValueError(f"append expects ({B}, {self.n_kv_heads}, T, {self.head_dim}) K and V")
-        if k.dtype != torch.float16 or v.dtype != torch.float16:
-            raise ValueError("append expects fp16 keys and values")
+        if k.dtype != self.dtype or v.dtype != self.dtype:
+            raise ValueError(f"append expects {self.input_dtype} keys and values")
         k = k.contiguous()
         v = v.contiguous()
         n_new = [T] * B if n_new is None else [int(x) for x in n_new]
@@ -348,14 +359,16 @@ class TQKVPool:
     def _check_q(self, q):
         torch = _torch()
         B = self.max_batch
-        if tuple(q.shape) != (B, self.n_q_heads, self.head_dim) or q.dtype != torch.float16:
-            raise ValueError(f"decode expects fp16 q of shape ({B}, {self.n_q_heads}, {self.head_dim})")
+        if tuple(q.shape) != (B, self.n_q_heads, self.head_dim) or q.dtype != self.dtype:
+            raise ValueError(f"decode expects {self.input_dtype} q of shape "
+                             f"({B}, {self.n_q_heads}, {self.head_dim})")
         if min(self.lengths) <= 0:
             raise RuntimeError("cache is empty")
         return q.contiguous()
 
     def decode(self, q, out=None):
-        """One decode step for every sequence: ``q`` fp16 ``(B, Hq, D)`` ->
+        """One decode step for every sequence: ``q`` ``(B, Hq, D)`` (fp16, or
+        fp32 for an fp32 pool) ->
         fp32 ``(B, Hq, D)`` attention output over each sequence's whole cache."""
         torch = _torch()
         q = self._check_q(q)
@@ -405,7 +418,8 @@ class TQKVPool:
         return kout, vout
 
     def hot_window_tokens(self, b: int):
-        """fp16 ``(Hkv, n_hot, D)`` keys and values of sequence b's hot window."""
+        """``(Hkv, n_hot, D)`` keys and values of sequence b's hot window, in the
+        pool's input dtype."""
         torch = _torch()
         L, n_cold = self.lengths[b], self.n_groups(b) * self.group_tokens
         idx = torch.arange(n_cold, L, device=self.device) % self.hot_window
@@ -455,10 +469,11 @@ class TQKVPool:
         oval = np.concatenate(val).view(np.float16) if val else np.zeros(0, np.float16)
         scale, mean = self.gscale[slot].cpu().numpy(), self.gmean[slot].cpu().numpy()
         # the reference's codes: the stored rows, with the code of the stored
-        # fp16 value put back at every outlier position, in the reference's pack
+        # fp16 value put back at every outlier position (an fp32 pool stores
+        # the reference's codes there already), in the reference's pack
         kb = self.key_bits
         codes = codes_from_key_rows(kp.reshape(H * G, -1), kb, D).reshape(H, G, D)
-        if oidx.size:
+        if oidx.size and not self.f32:
             h, t, j = oidx // (G * D), (oidx // D) % G, oidx % D
             v32 = oval.astype(np.float32)
             codes[h, t, j] = (uniform_codes(v32, scale[h, j], mean[h, j], kb) if self.key_grid == "uniform"
@@ -525,10 +540,10 @@ class TQKVPool:
                 raise ValueError("outlier_idx and outlier_val differ in length")
             if oidx.size and (oidx.min() < 0 or oidx.max() >= H * G * D):
                 raise ValueError("outlier_idx outside the (H, G, D) block")
-            # stored form: the zero-level code at every outlier position, in the
-            # pool's row layout
+            # stored form: the zero-level code at every outlier position (fp32
+            # pools keep the reference's codes), in the pool's row layout
             codes = unpack_key_codes(kp, H * G * D, kb).reshape(H, G, D)
-            if oidx.size:
+            if oidx.size and not self.f32:
                 zc = 0 if self.key_grid == "uniform" else NF4_ZERO_CODE
                 codes[oidx // (G * D), (oidx // D) % G, oidx % D] = zc
             kp = key_rows_from_codes(codes.reshape(H * G, D), kb).reshape(H, G, -1)
@@ -579,7 +594,7 @@ class TQKVPool:
         """Restore sequence ``b`` (empty) from coded groups and hot tokens:
         ``groups`` = ``[(keys, values), ...]`` in :meth:`import_group`'s
         layout, written as they are (no re-encode), then ``hot_k``/``hot_v``
-        fp16 ``(Hkv, n_hot, D)`` into the hot ring.  The split must be the
+        ``(Hkv, n_hot, D)`` into the hot ring (in the pool's input dtype).  The split must be the
         flush cadence's: ``n_groups_for(len(groups) * G + n_hot)`` is
         ``len(groups)``."""
         torch = _torch()
@@ -597,7 +612,7 @@ class TQKVPool:
             self.import_group(b, g, keys=keys, values=values)
         if n_hot:
             idx = torch.arange(L - n_hot, L, device=self.device) % W
-            self.hot_k[b][:, idx] = hot_k.to(device=self.device, dtype=torch.float16)
-            self.hot_v[b][:, idx] = hot_v.to(device=self.device, dtype=torch.float16)
+            self.hot_k[b][:, idx] = hot_k.to(device=self.device, dtype=self.dtype)
+            self.hot_v[b][:, idx] = hot_v.to(device=self.device, dtype=self.dtype)
         self.lengths[b] = L
         self.seq_lens[b] = L
