@@ -1455,6 +1455,12 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     // issues the loads of block i + kColdBuf - 1 and computes block i.
     int jp = 0, kbp = kb0;  // computed block: wave group jp, block kbp
     int si = 0;             // stream index of the computed block
+    // Waves w and w + 4 share a SIMD, and its arbiter favours the older wave
+    // when both can issue: with whole-group shares, waves 4-7 finished ~15 us
+    // after waves 0-3 at the headline and the SIMDs ended with one wave each.
+    // Waves 4-7 raise their issue priority for every other 4-block stretch,
+    // which evens the pairs out (issue order only: the results are the same).
+    const bool pair_prio = wu >= 4 && a.wave_blocks == 0;
     auto step = [&](const ColdBlock<VB>& cur, ColdBlock<VB>& nxt, const ColdBlock<VB>& nx1) {
       store_group_stats();  // block i + 1's group
       const bool starts = kbp + 1 == nblk;  // block i + 1 starts wave group jp + 1
@@ -1479,6 +1485,13 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         ++jp;
       }
       ++si;
+      // waves 4-7: issue priority up for alternate 4-block stretches
+      if (pair_prio && (si & 3) == 0) {
+        if (si & 4)
+          __builtin_amdgcn_s_setprio(0);
+        else
+          __builtin_amdgcn_s_setprio(1);
+      }
     };
     if (T > 0) {
       // the first group: stats and the side-list of the first block's segment
@@ -1508,6 +1521,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         key_tile(ring[0].kB, x);
         qk_tile(x, CBn);
       }
+      if (pair_prio) __builtin_amdgcn_s_setprio(1);
       for (int i = 0; i < T; i += kColdBuf) {
 #pragma unroll
         for (int s = 0; s < kColdBuf; ++s) {
@@ -1522,6 +1536,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   // (its partial is not rotated back, unlike the coded one).  The coded state
   // waits in registers meanwhile: the code table, where the waves' states are
   // folded, is still read by waves that have not finished their groups.
+  __builtin_amdgcn_s_setprio(0);
   const WaveState cst = st;
   reset_state(st);
   {
