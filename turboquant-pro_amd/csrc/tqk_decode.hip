@@ -1649,9 +1649,23 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   float* const co = cl + kMWaves * GQ;              // [8][GQ][D]
   put_state(cst, cm + w * GQ, cl + w * GQ, co + w * GQ * D);
   __syncthreads();
-  // fold the eight waves of each: partial n_cold_splits * hot + split
+  // fold the eight waves of each: partial n_cold_splits * hot + split.
+  // With one coded split per (seq, kv head) and 4 or 8 heads, the thread
+  // that folds (coded/hot, head i, channel j) is the one that merges head i
+  // for channel j below (u = tid / D): the two partials stay in its
+  // registers (dvm/dvl/dva, the values the stores would write) and the
+  // merge reads them there -- no stores, arrival or reloads.
   const int ns = a.n_cold_splits + a.n_hot_splits;
-  for (int x = tid; x < 2 * GQ * D; x += kMThreads) {
+  constexpr int kFoldIt = (2 * GQ * D + kMThreads - 1) / kMThreads;
+  const bool direct = (GQ == 4 || GQ == 8) && a.out != nullptr && a.n_cold_splits == 1;
+  float dvm[kFoldIt], dvl[kFoldIt], dva[kFoldIt];
+#pragma unroll
+  for (int it = 0; it < kFoldIt; ++it) {
+    dvm[it] = -INFINITY;
+    dvl[it] = 0.f;
+    dva[it] = 0.f;
+    const int x = tid + it * kMThreads;
+    if (x >= 2 * GQ * D) continue;
     const int hot = x >= GQ * D;
     const int i = (x % (GQ * D)) / D, j = x % D;
     if (i >= gq) continue;
@@ -1675,11 +1689,16 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         }
       }
     }
-    const size_t o = ((size_t)b * Hq + h * gq + i) * ns + (hot ? a.n_cold_splits : 0) + split;
-    st_agent(a.pacc + o * D + j, acc);
-    if (j == 0) {
-      st_agent(a.pm + o, M * 0.6931471805599453f);  // back to the natural-log domain of the partials
-      st_agent(a.pl + o, den);
+    dvm[it] = M * 0.6931471805599453f;  // back to the natural-log domain of the partials
+    dvl[it] = den;
+    dva[it] = acc;
+    if (!direct) {
+      const size_t o = ((size_t)b * Hq + h * gq + i) * ns + (hot ? a.n_cold_splits : 0) + split;
+      st_agent(a.pacc + o * D + j, acc);
+      if (j == 0) {
+        st_agent(a.pm + o, dvm[it]);
+        st_agent(a.pl + o, den);
+      }
     }
   }
 
@@ -1695,17 +1714,21 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   // last arrival's loads are issued after it has read the count.  The counter
   // wraps back to zero on the last arrival, so it is zero for the next call.
   __shared__ int last_s;
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's partial stores are done
-  __syncthreads();
-  // acquire-release at agent scope: the workgroup's partial stores (ordered
-  // before this RMW by the barrier above) are released to the last arrival,
-  // whose loads below are ordered after its acquire
-  if (tid == 0)
-    last_s = __builtin_amdgcn_atomic_inc32(a.arrive + (size_t)b * Hkv + h,
-                                           (uint32_t)(a.n_cold_splits - 1), __ATOMIC_ACQ_REL,
-                                           "agent") == (uint32_t)(a.n_cold_splits - 1);
-  __syncthreads();
-  if (!last_s) return;
+  if (!direct) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's partial stores are done
+    __syncthreads();
+    // acquire-release at agent scope: the workgroup's partial stores (ordered
+    // before this RMW by the barrier above) are released to the last arrival,
+    // whose loads below are ordered after its acquire
+    if (tid == 0)
+      last_s = __builtin_amdgcn_atomic_inc32(a.arrive + (size_t)b * Hkv + h,
+                                             (uint32_t)(a.n_cold_splits - 1), __ATOMIC_ACQ_REL,
+                                             "agent") == (uint32_t)(a.n_cold_splits - 1);
+    __syncthreads();
+    if (!last_s) return;
+  } else {
+    __syncthreads();  // every wave past the fold's reads of the code table's area (Pi goes there)
+  }
   {
     // thread (u, j): query heads u, u + 4 for channel j; the coded sums go to
     // q_h_s.  Up to kMergeFast splits, every partial load is issued before
@@ -1737,7 +1760,20 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     for (int r = 0; r < NH; ++r) hr[r] = den[r] = 0.f;
     const bool fast = ns <= kMergeFast;
     float vl[NH][kMergeFast], vm[NH][kMergeFast], va[NH][kMergeFast];
-    if (fast) {
+    if (direct) {
+      // split 0 = the coded partial (fold iteration r), split 1 = the hot one
+      // (iteration kFoldIt / 2 + r), as the stores would have laid them out
+#pragma unroll
+      for (int r = 0; r < NH; ++r) {
+#pragma unroll
+        for (int s2 = 0; s2 < kMergeFast; ++s2) {
+          const int itc = s2 == 0 ? r : kFoldIt / 2 + r;
+          vl[r][s2] = s2 < 2 ? dvl[itc < kFoldIt ? itc : 0] : 0.f;
+          vm[r][s2] = s2 < 2 ? dvm[itc < kFoldIt ? itc : 0] : -INFINITY;
+          va[r][s2] = s2 < 2 ? dva[itc < kFoldIt ? itc : 0] : 0.f;
+        }
+      }
+    } else if (fast) {
 #pragma unroll
       for (int r = 0; r < NH; ++r) {
         const int qi = u + 4 * r;
