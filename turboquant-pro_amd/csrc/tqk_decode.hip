@@ -808,7 +808,6 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   const tqk_cache_desc& d = a.d;
   const int Hkv = d.n_kv_heads, Hq = d.n_q_heads, G = d.group_tokens, P = d.page_tokens;
   const int L = a.seq_lens[b];
-  const int ng = n_groups_of(L, d.hot_window, G);
   // scores in the log2 domain: q * sm_scale * log2(e), softmax with exp2
   const float qscale = d.sm_scale * 1.4426950408889634f;
 
@@ -834,83 +833,82 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   // per wave and head: the lo columns' initial value, the group's mean bias
   // q . mean (four copies: one tile's accumulator)
   __shared__ __align__(16) float bias_s[kMWaves][GQ][4];
-  // NF4 levels [0, 16) and value centroids [16, 16 + 2^vb), for the table fill
-  __shared__ float lvl_s[32];
-  if (tid < 16) lvl_s[tid] = PK ? (tid < (1 << KB) ? a.p.vcent[tid] : 0.f) : key_level(a.d.key_grid, tid);
-  else if (tid < 16 + (1 << VB)) lvl_s[tid] = a.p.vcent[tid - 16];
+  // NF4 levels [0, 16) and value centroids [16, 16 + 2^vb) in lanes of every
+  // wave, for the table fill (loaded first: the fill waits for them only)
+  // (both loads unconditional and the pick by bit masks: a select the
+  // compiler turns into branches would sink each load into its own)
+  const uint32_t cen = fbits(a.p.vcent[(lane & 15) & ((1 << VB) - 1)]);
+  const uint32_t nf4 = fbits(kNF4[lane & 15]);
+  const uint32_t unif = fbits((float)(lane & 15));
+  const bool is_cen = lane < 16 ? PK && lane < (1 << KB) : lane < 16 + (1 << VB);
+  const bool is_key = lane < 16 && !PK;
+  const uint32_t mk_c = is_cen ? ~0u : 0u, mk_k = is_key ? ~0u : 0u, mk_u = a.d.key_grid ? ~0u : 0u;
+  const float lvl = bitsf((cen & mk_c) | (((nf4 & ~mk_u) | (unif & mk_u)) & mk_k));
   // Metadata of the split's groups, read once here so the block stream issues
-  // nothing but block loads: [0, 16) first row of each 16-token tile,
-  // [16, 24) cumulative outlier bounds, [24] slot * Hkv + h.
+  // nothing but block loads: [0, 16) first row of each 16-token tile
+  // (relative to this head's page region), [16, 24) cumulative outlier
+  // bounds, [24] slot * Hkv + h; rows past the split's groups are zero (slot
+  // 0 of head 0: a valid address, although nothing reads them).  Thread tid
+  // fills field mf of rows tid / kMetaInts + kMetaRows * r.  The set-up is
+  // two memory round trips: the group slots and tile rows of every row are
+  // loaded before the sequence length is known (indices clamped to the
+  // tables' rows; rows past the split's groups are dropped once it is),
+  // together with the length, the levels and q; the code tables are filled
+  // while they are in flight; then the outlier bounds of the split's groups
+  // are loaded by slot.
   __shared__ int meta_s[kMaxGPS][kMetaInts];
-  {
-    const int gbeg = split * a.groups_per_split;
-    const int gcnt = max(0, min(ng, gbeg + a.groups_per_split) - gbeg);
-    // rows past the split's groups are zero (slot 0 of head 0: a valid
-    // address, although nothing reads them)
-    for (int x = gcnt * kMetaInts + tid; x < kMaxGPS * kMetaInts; x += kMThreads)
-      meta_s[x / kMetaInts][x % kMetaInts] = 0;
-    for (int x = tid; x < gcnt * kMetaInts; x += kMThreads) {
-      const int jg = x / kMetaInts, f = x % kMetaInts, g = gbeg + jg;
-      const int slot = a.p.group_table[(size_t)b * d.max_groups_per_seq + g];
-      const uint32_t obase = (uint32_t)slot * (uint32_t)Hkv + (uint32_t)h;
-      int v = 0;
-      if (f < 16) {
-        // first row of tile f, relative to this head's page region
-        if (f < G / 16)
-          v = (int)(page_row(a.p.block_table, d.max_pages_per_seq, b, g * G + 16 * f, P, d.n_pages, h) -
-                    (size_t)h * d.n_pages * P);
-      } else if (f < 16 + TQK_NOB) {
-        v = min(a.p.ocount[(size_t)obase * TQK_NOB + (f - 16)], d.outlier_cap);
-      } else if (f == 16 + TQK_NOB) {
-        v = (int)obase;
-      }
-      meta_s[jg][f] = v;
-    }
+  constexpr int kMetaRows = kMThreads / kMetaInts;
+  constexpr int kMetaIt = kMaxGPS / kMetaRows;
+  static_assert(kMThreads % kMetaInts == 0 && kMaxGPS % kMetaRows == 0, "metadata rows");
+  const int mf = tid % kMetaInts;
+  const int gbeg_m = split * a.groups_per_split;
+  // (every load below is issued by every thread, at an index inside its
+  // table, and its value selected afterwards: a load inside a branch would
+  // be waited for where the branches join)
+  // (tables without rows: entry 0 of seq_lens stands in, never used)
+  const bool tables = d.max_groups_per_seq > 0 && d.max_pages_per_seq > 0;
+  const int mg = max(d.max_groups_per_seq, 1), mp = max(d.max_pages_per_seq, 1);
+  const int32_t* const gtab = tables ? a.p.group_table : a.seq_lens;
+  const int32_t* const btab = tables ? a.p.block_table : a.seq_lens;
+  int slot_r[kMetaIt], phys_r[kMetaIt];
+#pragma unroll
+  for (int r = 0; r < kMetaIt; ++r) {
+    const int g = min(gbeg_m + tid / kMetaInts + kMetaRows * r, mg - 1);
+    const int t = g * G + 16 * (mf & 15);
+    slot_r[r] = gtab[tables ? (size_t)b * mg + g : 0];
+    phys_r[r] = btab[tables ? (size_t)b * mp + min(t / P, mp - 1) : 0];
   }
-
   // GQ is the kernel's power-of-two head count; the last GQ - gq heads are
   // zero-query padding (their columns score 0) whose states are never written
   const int gq = Hq / Hkv;
-  for (int i = tid; i < GQ * D; i += kMThreads) {
-    const uint32_t qr =
-        (i / D < gq) ? static_cast<const uint16_t*>(a.q)[((size_t)b * Hq + h * gq + i / D) * D + i % D] : 0u;
-    qc_s[i % D][i / D] = (uint16_t)qr;
-    qf_s[i / D][i % D] = (uint16_t)qr;
-    q_h_s[i / D][i % D] = h2f((uint16_t)qr) * qscale;
-  }
-  __syncthreads();
-  if constexpr (PK) {
-    // the coded keys' weights: the rotated query q @ pi_t (scaled), from the raw q
-    float qrot[(GQ * D + kMThreads - 1) / kMThreads];
+  constexpr int kQIt = (GQ * D + kMThreads - 1) / kMThreads;
+  uint32_t qraw[kQIt];
 #pragma unroll
-    for (int r = 0; r < (GQ * D + kMThreads - 1) / kMThreads; ++r) {
-      const int i = tid + r * kMThreads;
-      float x = 0.f;
-      if (i < GQ * D)
-        for (int dd = 0; dd < D; ++dd) x += h2f(qf_s[i / D][dd]) * a.p.pi_t[dd * D + i % D];
-      qrot[r] = x * qscale;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int r = 0; r < (GQ * D + kMThreads - 1) / kMThreads; ++r) {
-      const int i = tid + r * kMThreads;
-      if (i < GQ * D) q_h_s[i / D][i % D] = qrot[r];
-    }
-    __syncthreads();
+  for (int r = 0; r < kQIt; ++r) {
+    const int i = min(tid + r * kMThreads, GQ * D - 1);
+    const int hi = min(i / D, gq - 1);
+    const uint32_t x = static_cast<const uint16_t*>(a.q)[((size_t)b * Hq + h * gq + hi) * D + i % D];
+    qraw[r] = i / D < gq ? x : 0u;
   }
+  const int ng = n_groups_of(L, d.hot_window, G);
+  // the levels go through the wave's own stats slot (free until the stream
+  // starts): a wave-local exchange, no workgroup barrier in front of the fill
+  if (lane < 32) gsm_s[w][lane] = lvl;
+  wave_sync();
   {
     // key unit u (8 bytes): entry u / copies, copy u % copies; consecutive
     // lanes write consecutive units; levels come from LDS, so the fill issues
     // no memory loads
+    const float* lv = &gsm_s[w][0];
     using LG = LutGeom<KB, VB, GQ>;
     constexpr int NC = LG::kKeyCopies;
     constexpr int NK = LG::kKeyEntries;
     for (int u = tid; u < NK * NC; u += kMThreads) {
       const uint32_t e = (uint32_t)(u / NC);
       *reinterpret_cast<uint2*>(lut + LG::kKeyBase + e * kLutEntry + (uint32_t)(u % NC) * 8u) =
-          split_pair(lvl_s[k_code_even(e, KB)], lvl_s[k_code_odd(e, KB)]);
+          split_pair(lv[k_code_even(e, KB)], lv[k_code_odd(e, KB)]);
     }
-    const float* cv = &lvl_s[16];  // value centroids
+    const float* cv = lv + 16;  // value centroids
     if constexpr (LG::kQuad12) {
       // entry e: centroids of codes e & 7, e >> 3 & 7, e >> 6 & 7, e >> 9
       for (uint32_t e = tid; e < 4096u; e += kMThreads)
@@ -932,7 +930,63 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       }
     }
   }
+  {
+    // the outlier bounds of the split's groups by slot, then the rows
+    const int gcnt = max(0, min(ng, gbeg_m + a.groups_per_split) - gbeg_m);
+    int oc_r[kMetaIt];
+#pragma unroll
+    for (int r = 0; r < kMetaIt; ++r) {
+      const bool in = tid / kMetaInts + kMetaRows * r < gcnt;
+      const uint32_t obase = (uint32_t)slot_r[r] * (uint32_t)Hkv + (uint32_t)h;
+      // (entry 0 for the rows and fields that take no bound)
+      const size_t oi = in && mf >= 16 && mf < 16 + TQK_NOB ? (size_t)obase * TQK_NOB + (mf - 16) : 0;
+      oc_r[r] = a.p.ocount[oi];
+    }
+#pragma unroll
+    for (int r = 0; r < kMetaIt; ++r) {
+      const int jg = tid / kMetaInts + kMetaRows * r;
+      const int g = min(gbeg_m + jg, mg - 1);
+      const int t = g * G + 16 * (mf & 15);
+      const uint32_t obase = (uint32_t)slot_r[r] * (uint32_t)Hkv + (uint32_t)h;
+      int v = 0;
+      if (mf < G / 16)  // first row of tile mf, phys P + t % P inside head h's region
+        v = (int)((uint32_t)phys_r[r] * (uint32_t)P + (uint32_t)(t % P));
+      else if (mf >= 16 && mf < 16 + TQK_NOB)
+        v = min(oc_r[r], d.outlier_cap);
+      else if (mf == 16 + TQK_NOB)
+        v = (int)obase;
+      meta_s[jg][mf] = jg < gcnt ? v : 0;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kQIt; ++r) {
+    const int i = tid + r * kMThreads;
+    if (i < GQ * D) {
+      qc_s[i % D][i / D] = (uint16_t)qraw[r];
+      qf_s[i / D][i % D] = (uint16_t)qraw[r];
+      q_h_s[i / D][i % D] = h2f((uint16_t)qraw[r]) * qscale;
+    }
+  }
   __syncthreads();
+  if constexpr (PK) {
+    // the coded keys' weights: the rotated query q @ pi_t (scaled), from the raw q
+    float qrot[(GQ * D + kMThreads - 1) / kMThreads];
+#pragma unroll
+    for (int r = 0; r < (GQ * D + kMThreads - 1) / kMThreads; ++r) {
+      const int i = tid + r * kMThreads;
+      float x = 0.f;
+      if (i < GQ * D)
+        for (int dd = 0; dd < D; ++dd) x += h2f(qf_s[i / D][dd]) * a.p.pi_t[dd * D + i % D];
+      qrot[r] = x * qscale;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < (GQ * D + kMThreads - 1) / kMThreads; ++r) {
+      const int i = tid + r * kMThreads;
+      if (i < GQ * D) q_h_s[i / D][i % D] = qrot[r];
+    }
+    __syncthreads();
+  }
 
   // Columns of the score tiles and rows of the PV tiles: c < 8 carry fp16 hi
   // parts, c >= 8 the fp16 lo parts, of head c & (GQ - 1) (heads repeat when
