@@ -1243,7 +1243,32 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       // One entry, without branches: a run closing inside the lane that is
       // not its first is stored at its token, every other step stores into
       // the lane's own slot past the row's tokens.
-      auto entry = [&](int k, uint32_t x) {
+      // An entry's LDS operands, the channel's group mean and q of every head
+      // (fp16, exact), gathered for four entries before their arithmetic so
+      // that the four gathers share one wait.  (Read for every lane: an
+      // invalid entry's channel is still in range.)
+      constexpr int kQW = (GQ + 1) / 2;
+      struct EntryOps {
+        float mean;
+        uint32_t q[kQW];
+      };
+      auto gather = [&](uint32_t x, EntryOps& o) {
+        const int jc = (int)(x & (uint32_t)(D - 1));
+        o.mean = gsm_s[w][D + jc];
+        if constexpr (GQ >= 4) {
+#pragma unroll
+          for (int i = 0; i < GQ; i += 4) {
+            const uint2 q4 = *reinterpret_cast<const uint2*>(&qc_s[jc][i]);
+            o.q[i / 2] = q4.x;
+            o.q[i / 2 + 1] = q4.y;
+          }
+        } else if constexpr (GQ == 2) {
+          o.q[0] = *reinterpret_cast<const uint32_t*>(&qc_s[jc][0]);
+        } else {
+          o.q[0] = qc_s[jc][0];
+        }
+      };
+      auto entry = [&](int k, uint32_t x, const EntryOps& o) {
         // (an entry outside the segment's tokens is dropped, whatever the
         // list holds: every LDS index below stays in corr_s)
         const int tx = (int)((x >> 7) & 0xFFu) - t0;
@@ -1259,33 +1284,33 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         tfirst = first ? tcur : tfirst;
         const bool same = t == tcur;
         tcur = t;
-        const int jc = (int)(x & (uint32_t)(D - 1));
-        // (read for every lane: an invalid entry's channel is still in range)
-        const float dv0 = (h2f((uint16_t)(x >> 16)) - gsm_s[w][D + jc]) * qscale;
+        const float dv0 = (h2f((uint16_t)(x >> 16)) - o.mean) * qscale;
         const float dv = valid ? dv0 : 0.f;
-        // q of every head at channel jc, fp16 (exact), into fp32 FMAs
-        _Float16 qv[GQ];
-        if constexpr (GQ >= 4) {
+        // q of every head at the entry's channel into fp32 FMAs
 #pragma unroll
-          for (int i = 0; i < GQ; i += 4) {
-            const uint2 q4 = *reinterpret_cast<const uint2*>(&qc_s[jc][i]);
-            qv[i] = __builtin_bit_cast(_Float16, (uint16_t)(q4.x & 0xFFFFu));
-            qv[i + 1] = __builtin_bit_cast(_Float16, (uint16_t)(q4.x >> 16));
-            qv[i + 2] = __builtin_bit_cast(_Float16, (uint16_t)(q4.y & 0xFFFFu));
-            qv[i + 3] = __builtin_bit_cast(_Float16, (uint16_t)(q4.y >> 16));
-          }
-        } else {
-#pragma unroll
-          for (int i = 0; i < GQ; ++i) qv[i] = __builtin_bit_cast(_Float16, qc_s[jc][i]);
+        for (int i = 0; i < GQ; ++i) {
+          const _Float16 qv = __builtin_bit_cast(_Float16, (uint16_t)(o.q[i / 2] >> (16 * (i & 1))));
+          acc[i] = fmaf((float)qv, dv, same ? acc[i] : 0.f);
         }
-#pragma unroll
-        for (int i = 0; i < GQ; ++i) acc[i] = fmaf((float)qv[i], dv, same ? acc[i] : 0.f);
       };
+      static_assert(kPre % 4 == 0, "entries in fours");
 #pragma unroll
-      for (int k = 0; k < kPre; ++k)
-        if (k < E) entry(k, gent[k]);
-      for (int k = kPre; k < E; ++k)  // long lists only; reads past the list return 0
-        entry(k, __builtin_amdgcn_raw_buffer_load_b32(ro, 4 * (lo + lane * E + k), 0, 0));
+      for (int k0 = 0; k0 < kPre; k0 += 4) {
+        if (k0 < E) {
+          EntryOps o[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) gather(gent[k0 + u], o[u]);
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            if (k0 + u < E) entry(k0 + u, gent[k0 + u], o[u]);
+        }
+      }
+      for (int k = kPre; k < E; ++k) {  // long lists only; reads past the list return 0
+        const uint32_t x = __builtin_amdgcn_raw_buffer_load_b32(ro, 4 * (lo + lane * E + k), 0, 0);
+        EntryOps o;
+        gather(x, o);
+        entry(k, x, o);
+      }
       // The lane's first and last runs may continue in its neighbours (the
       // list is sorted, so the lanes that share a token are consecutive, all
       // but the two ends holding that token only).  An inclusive scan of the
@@ -1550,19 +1575,22 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     if (T > 0) {
       // the first group: stats and the side-list of the first block's segment
       // synchronously; the group of the second block's stats into the pending
-      // registers
+      // registers; the first block's codes are requested with them, so that
+      // they arrive while its group's weights and corrections are built (the
+      // side-list entries of its segment are the ones just loaded)
       const int j1 = (kb0 + min(1, T - 1)) / nblk;
       const int sg0 = kb0 / SB;
       load_group_stats(meta(0, 16 + TQK_NOB));
       load_seg_entries(0, sg0);
+      ColdBlock<VB> ring[kColdBuf];
+      load_next(ring[0]);
       store_group_stats();
       wave_sync();
       begin_group();
       seg_pass(0, sg0);
       load_group_stats(meta(j1, 16 + TQK_NOB));
-      ColdBlock<VB> ring[kColdBuf];
 #pragma unroll
-      for (int s = 0; s < kColdBuf - 1; ++s) {
+      for (int s = 1; s < kColdBuf - 1; ++s) {
         load_block_entries();
         load_next(ring[s]);
       }
