@@ -269,6 +269,46 @@ def test_decode_heavy_outliers(frac):
     assert_attn_close(got[0], seqs[0].attend(q[0]), what=f"frac={frac}")
 
 
+@pytest.mark.parametrize("hq", [8, 16])
+def test_decode_token_outliers_span_lanes(hq):
+    """A few tokens per group large in every channel: each is an outlier in
+    all 128 channels, so its run of side-list entries is longer than two of
+    the correction pass's per-lane shares (E = ceil(n / 64) entries each) and
+    covers three or more lanes: the pass's cross-lane scan, which the usual
+    spread of outliers never needs, joins the run.  GQA 4 (256-token
+    segments) and 8 (128-token segments); codes bit-exact, decode within the
+    bar."""
+    B, Hkv, L = 1, 2, 1100
+    print(f"[decode token outliers span lanes] hq={hq}", flush=True)
+    k, v, q = O.synthetic_kv(91, B, Hkv, hq, L)
+    rng = np.random.default_rng(5)
+    spikes = np.sort(rng.choice(768, size=12, replace=False))
+    k = k.astype(np.float32)
+    k[:, :, spikes, :] *= 6.0
+    k = k.astype(np.float16)
+    seqs, rot = oracle_state(k, v, 512, 3, seed=4, outlier_frac=0.02)
+    # the property the test is about: some segment holds a token with more
+    # than 2 E entries
+    seg = 256 if hq // Hkv <= 4 else 128
+    longest = 0
+    for kg in seqs[0].keys:
+        idx = np.asarray(kg.outlier_idx, np.int64)
+        h_s = idx // 128                      # (head, token) of each entry
+        for h in range(Hkv):
+            tok = h_s[(h_s // 256) == h] % 256
+            for s0 in range(0, 256, seg):
+                run = tok[(tok >= s0) & (tok < s0 + seg)]
+                if run.size:
+                    e = -(-run.size // 64)
+                    longest = max(longest, int(np.bincount(run - s0).max()) / e)
+    assert longest > 2, f"no token covers three lanes (longest run {longest:.1f} E)"
+    pool = _pool(n_kv_heads=Hkv, n_q_heads=hq, max_batch=B, max_seq_len=L, rotation=rot)
+    _fill(pool, k, v)
+    _check_codes(pool, seqs, B)
+    got = pool.decode(_dev(q)).cpu().numpy()
+    assert_attn_close(got[0], seqs[0].attend(q[0]), what=f"hq={hq}")
+
+
 @pytest.mark.parametrize("vbits", [3, 4])
 def test_uniform_keys_encode_dequant_decode(vbits):
     """Uniform per-channel keys (turboquant_pro/per_channel_kv.py:303-317,

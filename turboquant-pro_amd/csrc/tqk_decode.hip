@@ -1323,20 +1323,25 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       for (int i = 0; i < GQ; ++i) sv[i] = acc[i];
       const int tl = tcur;                         // last run's token (-1: none)
       const int tf = tfirst >= 0 ? tfirst : tcur;  // first run's token
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const int kd = __shfl_up(tl, d);
-        const bool add = lane >= d && kd == tl && tl >= 0;
-#pragma unroll
-        for (int i = 0; i < GQ; ++i) {
-          const float v = __shfl_up(sv[i], d);
-          sv[i] += add ? v : 0.f;
-        }
-      }
       // (every lane takes part in each shuffle: a lane outside the exec mask
       // has nothing to hand over; the edges are resolved after the shuffle)
       const int tl_up = __shfl_up(tl, 1), tf_dn = __shfl_down(tf, 1);
       const int tl_prev = lane > 0 ? tl_up : -1;
+      // A lane's last run continues its left neighbour's only when every
+      // entry of the lane is that one token: only such chains (a token over
+      // three or more lanes) need the scan; otherwise each lane's sum is its own.
+      if (__builtin_amdgcn_ballot_w64(tl >= 0 && tl == tl_prev) != 0) {
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+          const int kd = __shfl_up(tl, d);
+          const bool add = lane >= d && kd == tl && tl >= 0;
+#pragma unroll
+          for (int i = 0; i < GQ; ++i) {
+            const float v = __shfl_up(sv[i], d);
+            sv[i] += add ? v : 0.f;
+          }
+        }
+      }
       const int tf_next = lane < 63 ? tf_dn : -1;
       float sprev[GQ];
 #pragma unroll
@@ -1537,8 +1542,10 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     // Waves w and w + 4 share a SIMD, and its arbiter favours the older wave
     // when both can issue: with whole-group shares, waves 4-7 finished ~15 us
     // after waves 0-3 at the headline and the SIMDs ended with one wave each.
-    // Waves 4-7 raise their issue priority for every other 4-block stretch,
-    // which evens the pairs out (issue order only: the results are the same).
+    // Waves 4-7 raise their issue priority for three blocks of every four
+    // (half of them left the older waves ~7 us ahead; all of them turned the
+    // order round), which evens the pairs out (issue order only: the results
+    // are the same).
     const bool pair_prio = wu >= 4 && a.wave_blocks == 0;
     auto step = [&](const ColdBlock<VB>& cur, ColdBlock<VB>& nxt, const ColdBlock<VB>& nx1) {
       store_group_stats();  // block i + 1's group
@@ -1564,11 +1571,11 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         ++jp;
       }
       ++si;
-      // waves 4-7: issue priority up for alternate 4-block stretches
-      if (pair_prio && (si & 3) == 0) {
-        if (si & 4)
+      // waves 4-7: issue priority up for three blocks of every four
+      if (pair_prio) {
+        if ((si & 3) == 3)
           __builtin_amdgcn_s_setprio(0);
-        else
+        else if ((si & 3) == 0)
           __builtin_amdgcn_s_setprio(1);
       }
     };
