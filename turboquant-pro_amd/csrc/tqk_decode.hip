@@ -450,7 +450,7 @@ constexpr int kMergeFast = 8;  // split counts merged with all partial loads iss
 #define TQK_COLD_BUFFERS 3
 #endif
 constexpr int kColdBuf = TQK_COLD_BUFFERS;  // cold-stream register buffers (one more than blocks in flight)
-constexpr int kMaxGPS = 64;      // groups per cold split of the MFMA kernel (metadata in LDS)
+constexpr int kMaxGPS = 128;     // groups per cold split of the MFMA kernel (metadata in LDS)
 constexpr int kMetaInts = 32;    // per group: 16 tile rows, 8 outlier bounds, slot*Hkv+h
 constexpr int kLutEntry = 256;   // bytes per table entry
 
@@ -825,10 +825,9 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   __shared__ __align__(16) float gsm_s[kMWaves][2 * D];
   // per wave: the QK^T initial value of every token of its current group
   // segment (kSegTokens tokens) and head, mean bias plus outlier corrections
-  // ([head][token]); each row ends in 64 per-lane slots that take the
-  // corrections' unused stores (the pass stores every step, no branch)
+  // ([head][token])
   constexpr int kCT = kSegTokens<GQ>;
-  constexpr int kRow = kCT + 64;
+  constexpr int kRow = kCT;
   __shared__ __align__(16) float corr_s[kMWaves][GQ][kRow];
   // per wave and head: the lo columns' initial value, the group's mean bias
   // q . mean (four copies: one tile's accumulator)
@@ -847,9 +846,10 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   // Metadata of the split's groups, read once here so the block stream issues
   // nothing but block loads: [0, 16) first row of each 16-token tile
   // (relative to this head's page region), [16, 24) cumulative outlier
-  // bounds, [24] slot * Hkv + h; rows past the split's groups are zero (slot
-  // 0 of head 0: a valid address, although nothing reads them).  Thread tid
-  // fills field mf of rows tid / kMetaInts + kMetaRows * r.  The set-up is
+  // bounds, [24] slot * Hkv + h.  Only rows below the split's group count
+  // are read (the waves' groups); the rows of the last row block past it are
+  // zero, later ones are not written.  Thread tid fills field mf of rows
+  // tid / kMetaInts + kMetaRows * r.  The set-up is
   // two memory round trips: the group slots and tile rows of every row are
   // loaded before the sequence length is known (indices clamped to the
   // tables' rows; rows past the split's groups are dropped once it is),
@@ -870,13 +870,23 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   const int mg = max(d.max_groups_per_seq, 1), mp = max(d.max_pages_per_seq, 1);
   const int32_t* const gtab = tables ? a.p.group_table : a.seq_lens;
   const int32_t* const btab = tables ? a.p.block_table : a.seq_lens;
+  // Only the row blocks a split of groups_per_split groups can use are
+  // loaded; the others load from an empty buffer (zeros, no memory access),
+  // so that every thread issues the same loads and the fill below waits for
+  // the levels alone.
+  const int n_it = (a.groups_per_split + kMetaRows - 1) / kMetaRows;
+  const __amdgpu_buffer_rsrc_t rg = buf_rsrc(gtab, tables ? 4u * (uint32_t)a.batch * (uint32_t)mg : 4u);
+  const __amdgpu_buffer_rsrc_t rb = buf_rsrc(btab, tables ? 4u * (uint32_t)a.batch * (uint32_t)mp : 4u);
+  const __amdgpu_buffer_rsrc_t rnone = buf_rsrc(gtab, 0u);
   int slot_r[kMetaIt], phys_r[kMetaIt];
 #pragma unroll
   for (int r = 0; r < kMetaIt; ++r) {
     const int g = min(gbeg_m + tid / kMetaInts + kMetaRows * r, mg - 1);
     const int t = g * G + 16 * (mf & 15);
-    slot_r[r] = gtab[tables ? (size_t)b * mg + g : 0];
-    phys_r[r] = btab[tables ? (size_t)b * mp + min(t / P, mp - 1) : 0];
+    const uint32_t gi = tables ? (uint32_t)b * (uint32_t)mg + (uint32_t)g : 0u;
+    const uint32_t bi = tables ? (uint32_t)b * (uint32_t)mp + (uint32_t)min(t / P, mp - 1) : 0u;
+    slot_r[r] = (int)__builtin_amdgcn_raw_buffer_load_b32(r < n_it ? rg : rnone, (int)(4u * gi), 0, 0);
+    phys_r[r] = (int)__builtin_amdgcn_raw_buffer_load_b32(r < n_it ? rb : rnone, (int)(4u * bi), 0, 0);
   }
   // GQ is the kernel's power-of-two head count; the last GQ - gq heads are
   // zero-query padding (their columns score 0) whose states are never written
@@ -936,6 +946,8 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     int oc_r[kMetaIt];
 #pragma unroll
     for (int r = 0; r < kMetaIt; ++r) {
+      oc_r[r] = 0;
+      if (r >= n_it) continue;
       const bool in = tid / kMetaInts + kMetaRows * r < gcnt;
       const uint32_t obase = (uint32_t)slot_r[r] * (uint32_t)Hkv + (uint32_t)h;
       // (entry 0 for the rows and fields that take no bound)
@@ -944,6 +956,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     }
 #pragma unroll
     for (int r = 0; r < kMetaIt; ++r) {
+      if (r >= n_it) continue;
       const int jg = tid / kMetaInts + kMetaRows * r;
       const int g = min(gbeg_m + jg, mg - 1);
       const int t = g * G + 16 * (mf & 15);
@@ -1240,9 +1253,8 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
 #pragma unroll
       for (int i = 0; i < GQ; ++i) acc[i] = facc[i] = 0.f;
       int tcur = -1, tfirst = -1;  // open run's token, first closed run's token (segment-relative)
-      // One entry, without branches: a run closing inside the lane that is
-      // not its first is stored at its token, every other step stores into
-      // the lane's own slot past the row's tokens.
+      // One entry: a run closing inside the lane that is not its first is
+      // stored at its token (an exec-masked store); the first is kept in facc.
       // An entry's LDS operands, the channel's group mean and q of every head
       // (fp16, exact), gathered for four entries before their arithmetic so
       // that the four gathers share one wait.  (Read for every lane: an
@@ -1276,9 +1288,10 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
         const int t = valid ? tx : -1;
         const bool close = t != tcur && tcur >= 0;
         const bool first = close && tfirst < 0;
-        const int st_tok = close && tfirst >= 0 ? tcur : kCT + lane;
+        if (close && tfirst >= 0) {  // a run that closes inside the lane, not its first
 #pragma unroll
-        for (int i = 0; i < GQ; ++i) corr[i * kRow + st_tok] = acc[i];
+          for (int i = 0; i < GQ; ++i) corr[i * kRow + tcur] = acc[i];
+        }
 #pragma unroll
         for (int i = 0; i < GQ; ++i) facc[i] = first ? acc[i] : facc[i];
         tfirst = first ? tcur : tfirst;
