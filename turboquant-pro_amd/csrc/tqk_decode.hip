@@ -647,24 +647,35 @@ __device__ __forceinline__ float ld_agent(const float* p) {
 // Merge of one query head's ns split partials for channel j when there are
 // more than kMergeFast: one online pass (running max M, the sums rescaled by
 // e^{M_old - M_new} when a round raises it) over rounds of 2 * kMergeFast
-// partials, every load of a round issued before its first use.  Both merges
-// (tqk_merge and the in-kernel one) use it, so they agree bit for bit.
+// partials.  The loads of the next round are issued before the current one is
+// combined (each round is a round trip to memory).  Partials at or past
+// n_live are known to be empty (l = 0, which the pass skips anyway): they are
+// not loaded.  Both merges (tqk_merge and the in-kernel one) use it, so they
+// agree bit for bit whatever n_live they pass.
 template <int D, class Load>
 __device__ __forceinline__ void merge_chunked(Load ld, const float* pl, const float* pm,
-                                              const float* pacc, size_t base, int ns, int n_cold,
-                                              int j, float& M, float& dn, float& cr, float& hh) {
+                                              const float* pacc, size_t base, int ns, int n_live,
+                                              int n_cold, int j, float& M, float& dn, float& cr,
+                                              float& hh) {
   constexpr int C = 2 * kMergeFast;
   M = -INFINITY;
   dn = cr = hh = 0.f;
-  for (int s0 = 0; s0 < ns; s0 += C) {
-    float vl[C], vm[C], va[C];
+  const int nl = min(ns, n_live);
+  if (nl <= 0) return;
+  // (every load of a round is issued, at a clamped index, and its value
+  // dropped past nl: the waits then stay exact)
+  auto load_round = [&](int s0, float (&vl)[C], float (&vm)[C], float (&va)[C]) {
 #pragma unroll
     for (int k = 0; k < C; ++k) {
-      const bool ok = s0 + k < ns;
-      vl[k] = ok ? ld(pl + base + s0 + k) : 0.f;
-      vm[k] = ok ? ld(pm + base + s0 + k) : -INFINITY;
-      va[k] = ok ? ld(pacc + (base + s0 + k) * D + j) : 0.f;
+      const bool ok = s0 + k < nl;
+      const size_t si = base + (size_t)min(s0 + k, nl - 1);
+      const float l = ld(pl + si), m = ld(pm + si), x = ld(pacc + si * D + j);
+      vl[k] = ok ? l : 0.f;
+      vm[k] = ok ? m : -INFINITY;
+      va[k] = ok ? x : 0.f;
     }
+  };
+  auto combine_round = [&](int s0, const float (&vl)[C], const float (&vm)[C], const float (&va)[C]) {
     float Mc = M;
 #pragma unroll
     for (int k = 0; k < C; ++k)
@@ -685,6 +696,16 @@ __device__ __forceinline__ void merge_chunked(Load ld, const float* pl, const fl
         if (s0 + k < n_cold) cr += x; else hh += x;
       }
     }
+  };
+  // two register sets, rounds in pairs: A holds rounds s0, B rounds s0 + C
+  float al[C], am[C], aa[C], bl[C], bm[C], ba[C];
+  load_round(0, al, am, aa);
+  for (int s0 = 0; s0 < nl; s0 += 2 * C) {
+    if (s0 + C < nl) load_round(s0 + C, bl, bm, ba);
+    combine_round(s0, al, am, aa);
+    if (s0 + C >= nl) break;
+    if (s0 + 2 * C < nl) load_round(s0 + 2 * C, al, am, aa);
+    combine_round(s0 + C, bl, bm, ba);
   }
 }
 
@@ -1861,6 +1882,9 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
 #pragma unroll
     for (int r = 0; r < NH; ++r) hr[r] = den[r] = 0.f;
     const bool fast = ns <= kMergeFast;
+    // hot partials past the hot window's blocks (split s takes blocks 8s + w
+    // onwards) are empty
+    const int hot_live = min(a.n_cold_splits, ((L - ng * G + 31) / 32 + kMWaves - 1) / kMWaves);
     float vl[NH][kMergeFast], vm[NH][kMergeFast], va[NH][kMergeFast];
     if (direct) {
       // split 0 = the coded partial (fold iteration r), split 1 = the hot one
@@ -1905,13 +1929,14 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       for (int r = 0; r < NH; ++r)
         if (u + 4 * r < gq) combine(r, u + 4 * r, vl[r], vm[r], va[r]);
     } else {
+#pragma unroll
       for (int r = 0; r < NH; ++r) {
         const int qi = u + 4 * r;
         if (qi < gq) {
           const size_t base = ((size_t)b * Hq + h * gq + qi) * ns;
           float M, dn, cr, hh;
           merge_chunked<D>([](const float* p) { return ld_agent(p); }, a.pl, a.pm, a.pacc, base, ns,
-                        a.n_cold_splits, j, M, dn, cr, hh);
+                           a.n_cold_splits + hot_live, a.n_cold_splits, j, M, dn, cr, hh);
           q_h_s[qi][j] = cr;
           hr[r] = hh;
           den[r] = dn;
@@ -2015,7 +2040,7 @@ __global__ __launch_bounds__(2 * D) void tqk_merge(MergeArgs a) {
         const size_t base = ((size_t)b * a.n_q_heads + h * GQ + qi) * a.n_splits;
         float M, dn, cr, hh;
         merge_chunked<D>([](const float* p) { return *p; }, a.pl, a.pm, a.pacc, base, a.n_splits,
-                      a.n_cold_splits, j, M, dn, cr, hh);
+                         a.n_splits, a.n_cold_splits, j, M, dn, cr, hh);
         crot_s[qi][j] = cr;
         hr[u] = hh;
         den[u] = dn;
