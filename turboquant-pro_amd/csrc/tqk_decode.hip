@@ -500,6 +500,16 @@ __device__ __forceinline__ uint2 split_pair(float x0, float x1) {
                         ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16));
 }
 
+// Workgroup barrier for LDS data only: this wave's LDS operations complete
+// (lgkmcnt 0), then s_barrier.  Unlike __syncthreads it leaves the wave's
+// global loads in flight.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // vmcnt 63, expcnt 7, lgkmcnt 0
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // Orders LDS accesses of one wave across lanes.  A wave's LDS instructions
 // execute in issue order, so program order is enough; this only stops the
 // compiler from moving memory operations across the point (and, unlike a
@@ -870,7 +880,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   // bounds, [24] slot * Hkv + h.  Only rows below the split's group count
   // are read (the waves' groups); the rows of the last row block past it are
   // zero, later ones are not written.  Thread tid fills field mf of rows
-  // tid / kMetaInts + kMetaRows * r.  The set-up is
+  // mrow(r).  The set-up is
   // two memory round trips: the group slots and tile rows of every row are
   // loaded before the sequence length is known (indices clamped to the
   // tables' rows; rows past the split's groups are dropped once it is),
@@ -881,7 +891,11 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   constexpr int kMetaRows = kMThreads / kMetaInts;
   constexpr int kMetaIt = kMaxGPS / kMetaRows;
   static_assert(kMThreads % kMetaInts == 0 && kMaxGPS % kMetaRows == 0, "metadata rows");
+  static_assert(kMetaRows == 2 * kMWaves && kMetaInts == 32, "two metadata rows per wave and block");
   const int mf = tid % kMetaInts;
+  // row of block r filled by this thread: wave w fills rows w + 8k, the rows
+  // of the groups it streams when splits are shared out in whole groups
+  auto mrow = [&](int r) { return w + kMWaves * (2 * r + (lane >> 5)); };
   const int gbeg_m = split * a.groups_per_split;
   // (every load below is issued by every thread, at an index inside its
   // table, and its value selected afterwards: a load inside a branch would
@@ -902,7 +916,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
   int slot_r[kMetaIt], phys_r[kMetaIt];
 #pragma unroll
   for (int r = 0; r < kMetaIt; ++r) {
-    const int g = min(gbeg_m + tid / kMetaInts + kMetaRows * r, mg - 1);
+    const int g = min(gbeg_m + mrow(r), mg - 1);
     const int t = g * G + 16 * (mf & 15);
     const uint32_t gi = tables ? (uint32_t)b * (uint32_t)mg + (uint32_t)g : 0u;
     const uint32_t bi = tables ? (uint32_t)b * (uint32_t)mp + (uint32_t)min(t / P, mp - 1) : 0u;
@@ -969,7 +983,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     for (int r = 0; r < kMetaIt; ++r) {
       oc_r[r] = 0;
       if (r >= n_it) continue;
-      const bool in = tid / kMetaInts + kMetaRows * r < gcnt;
+      const bool in = mrow(r) < gcnt;
       const uint32_t obase = (uint32_t)slot_r[r] * (uint32_t)Hkv + (uint32_t)h;
       // (entry 0 for the rows and fields that take no bound)
       const size_t oi = in && mf >= 16 && mf < 16 + TQK_NOB ? (size_t)obase * TQK_NOB + (mf - 16) : 0;
@@ -978,7 +992,7 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
 #pragma unroll
     for (int r = 0; r < kMetaIt; ++r) {
       if (r >= n_it) continue;
-      const int jg = tid / kMetaInts + kMetaRows * r;
+      const int jg = mrow(r);
       const int g = min(gbeg_m + jg, mg - 1);
       const int t = g * G + 16 * (mf & 15);
       const uint32_t obase = (uint32_t)slot_r[r] * (uint32_t)Hkv + (uint32_t)h;
@@ -1001,8 +1015,10 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
       q_h_s[i / D][i % D] = h2f((uint16_t)qraw[r]) * qscale;
     }
   }
-  __syncthreads();
+  // (the set-up's workgroup barrier is the stream's lds_barrier below: until
+  // it a wave reads only its own metadata rows)
   if constexpr (PK) {
+    __syncthreads();
     // the coded keys' weights: the rotated query q @ pi_t (scaled), from the raw q
     float qrot[(GQ * D + kMThreads - 1) / kMThreads];
 #pragma unroll
@@ -1090,7 +1106,9 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
     // Every step issues the same block loads (past the end: the last block
     // again, already in L2), so the waits on the oldest buffer stay exact.
     int jl = 0, kbl = kb0, nl = 0;  // next block to load: wave group jl, block kbl, stream index nl
-    load_meta(0);
+    // whole-group shares: the wave's rows are its own (filled by it above)
+    const bool own_rows = a.wave_blocks == 0;
+    if (own_rows) load_meta(0);
     auto load_next = [&](ColdBlock<VB>& cb) {
       // rows of the two tiles in this head's region (wave-uniform: SGPR offsets)
       const uint32_t rowA = (uint32_t)meta_l(2 * kbl);
@@ -1613,18 +1631,30 @@ __global__ __launch_bounds__(kMThreads, 1) void tqk_decode_split_mfma(DecodeArgs
           __builtin_amdgcn_s_setprio(1);
       }
     };
+    // The first group: stats and the side-list of the first block's segment
+    // synchronously; the group of the second block's stats into the pending
+    // registers; the first block's codes are requested with them, so that
+    // they arrive while its group's weights and corrections are built (the
+    // side-list entries of its segment are the ones just loaded).  A wave
+    // that reads its own metadata rows issues these loads before the
+    // set-up's workgroup barrier, which then waits for LDS only.
+    ColdBlock<VB> ring[kColdBuf];
+    auto first_loads = [&]() {
+      load_group_stats(meta(0, 16 + TQK_NOB));
+      load_seg_entries(0, kb0 / SB);
+      load_next(ring[0]);
+    };
+    // (one load site, so that the waits on these loads stay exact; own_rows
+    // is the same for every wave, so each wave takes one barrier)
+    if (!own_rows) {
+      lds_barrier();
+      load_meta(0);
+    }
+    if (T > 0) first_loads();
+    if (own_rows) lds_barrier();
     if (T > 0) {
-      // the first group: stats and the side-list of the first block's segment
-      // synchronously; the group of the second block's stats into the pending
-      // registers; the first block's codes are requested with them, so that
-      // they arrive while its group's weights and corrections are built (the
-      // side-list entries of its segment are the ones just loaded)
       const int j1 = (kb0 + min(1, T - 1)) / nblk;
       const int sg0 = kb0 / SB;
-      load_group_stats(meta(0, 16 + TQK_NOB));
-      load_seg_entries(0, sg0);
-      ColdBlock<VB> ring[kColdBuf];
-      load_next(ring[0]);
       store_group_stats();
       wave_sync();
       begin_group();
