@@ -86,9 +86,12 @@ def test_in_kernel_merge_equals_merge_kernel(gq, vbits):
 
 
 def test_in_kernel_merge_many_splits():
-    """A long single sequence: 10 coded splits per kv head, 20 partials, so both
-    merges take their chunked form (more than 8 splits); still bit for bit
-    equal, and within the bar of dequantize-then-attend."""
+    """A long single sequence over two kv heads: the planner gives each kv head
+    dozens of short coded splits (77 groups, few (seq, kv head) pairs for 256
+    CUs), so both merges take their chunked form over several rounds of 16
+    partials (the in-kernel one skipping the hot partials past the hot
+    window's blocks); still bit for bit equal, and within the bar of
+    dequantize-then-attend."""
     from turboquant_pro_amd import TQKVPool
     B, Hkv, Hq, L = 1, 2, 8, 20000
     print(f"[merge] long context L={L}", flush=True)
