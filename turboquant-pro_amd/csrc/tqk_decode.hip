@@ -62,6 +62,7 @@ struct MergeArgs {
 };
 
 constexpr int kThreads = 256;
+constexpr int kVOEnt = 2048;  // VALU decode: side-list entries staged in LDS per group
 
 template <int GQ, bool IS_MAX>
 __device__ __forceinline__ void block_reduce(float (&v)[GQ], float (*red)[GQ]) {
@@ -112,6 +113,33 @@ __device__ __forceinline__ void softmax_update(float (*sc)[kThreads], int n, flo
   __syncthreads();
 }
 
+// A token's outlier corrections in the VALU decode: q_j * (val - dense_j) for
+// its run of the token-sorted side-list oe (entries [lo, end) of its 32-token
+// block hold it), found by binary search, added in list order.  Inlined at
+// each call, so that a list staged in LDS is read with LDS loads.
+template <int GQ, int D>
+__device__ __forceinline__ void outlier_walk(const uint32_t* oe, int lo, int end, uint32_t first,
+                                             const uint32_t (&rw)[D / 8], int kb, int key_grid,
+                                             const float* a_s, const float* mu_s,
+                                             const float (*q_s)[D], float (&s)[GQ]) {
+  int hi = end;
+  while (lo < hi) {  // first entry of the run at or after (token, 0)
+    const int mid = (lo + hi) >> 1;
+    if ((oe[mid] & 0xFFFFu) < first) lo = mid + 1; else hi = mid;
+  }
+  for (int e = lo; e < end; ++e) {
+    const uint32_t ent = oe[e];
+    const uint32_t pos = ent & 0xFFFFu;
+    if (pos >= first + D) break;
+    const int j = (int)(pos - first);
+    const uint32_t f = k_pair_index(rw, kb, j >> 1);
+    const uint32_t c = (j & 1) ? k_code_odd(f, kb) : k_code_even(f, kb);
+    const float delta = h2f((uint16_t)(ent >> 16)) - (a_s[j] * key_level(key_grid, c) + mu_s[j]);
+#pragma unroll
+    for (int i = 0; i < GQ; ++i) s[i] += q_s[i][j] * delta;
+  }
+}
+
 // The VALU split kernel: pools the MFMA kernel does not take (head_dim 64 or
 // 256, per-token value rows, a hot ring that is not whole 32-token blocks).
 // Scores one token per thread; values one channel pair per thread over a
@@ -137,7 +165,12 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
 
   __shared__ float q_s[GQ][D];
   __shared__ float qr_s[GQ][D];  // q @ pi_t (PolarQuant keys' weights)
-  __shared__ float w_s[GQ][D];
+  // the group's key weights by channel pair and head: one 8-byte read gives a
+  // head's two weights of a pair
+  __shared__ float2 w2_s[NP][GQ];
+  // the group's side-list, when it holds at most kVOEnt entries (the token
+  // threads' searches and walks then read LDS, not memory)
+  __shared__ uint32_t oe_s[kVOEnt];
   __shared__ float sc_s[GQ][kThreads];
   __shared__ float kl_s[256][2];
   __shared__ float vl_s[1 << (2 * VB)][2];
@@ -198,6 +231,15 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
     for (int g = g0; g < g1; ++g) {
       const int slot = a.p.group_table[(size_t)b * d.max_groups_per_seq + g];
       const size_t mbase = ((size_t)slot * Hkv + h) * D;
+      const size_t obase = (size_t)slot * Hkv + h;
+      const int n_oe = d.outliers_per_channel > 0
+                           ? min(a.p.ocount[obase * TQK_NOB + (G - 1) / TQK_OBLK], d.outlier_cap)
+                           : 0;
+      // (not at 8 heads and head_dim 256: a second inlined walk, or one over a
+      // generic pointer, takes all 256 VGPRs there)
+      const bool oe_lds = !(GQ >= 8 && D >= 256) && n_oe <= kVOEnt;
+      if (oe_lds)
+        for (int e = tid; e < n_oe; e += kThreads) oe_s[e] = a.p.oent[obase * d.outlier_cap + e];
       if (tid < D) {
         const float av = a.p.gscale[mbase + tid];
         const float mv = a.p.gmean[mbase + tid];
@@ -206,7 +248,7 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
         float bias_part[GQ];
 #pragma unroll
         for (int i = 0; i < GQ; ++i) {
-          w_s[i][tid] = (polar ? qr_s[i][tid] : q_s[i][tid]) * av;
+          reinterpret_cast<float*>(&w2_s[tid >> 1][i])[tid & 1] = (polar ? qr_s[i][tid] : q_s[i][tid]) * av;
           bias_part[i] = wave_sum(q_s[i][tid] * mv);
         }
         if ((tid & 63) == 0) {
@@ -228,7 +270,6 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
       // outlier corrections q_j * (val - dense_j) in side-list order (the
       // side-list is sorted by token; the cumulative counts at every 32nd
       // token bound the token's run, a binary search finds its start)
-      const size_t obase = (size_t)slot * Hkv + h;
       float norm_t = 0.f;
       if (tid < G) {
         const size_t row = page_row(bt, d.max_pages_per_seq, b, g * G + tid, P, d.n_pages, h);
@@ -239,12 +280,19 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
         float s[GQ];
 #pragma unroll
         for (int i = 0; i < GQ; ++i) s[i] = 0.f;
+        // (unrolled by 4, at 8 heads by 2 or not at all, only: a full unroll at head_dim 64
+        // hoists every weight read and takes all 256 VGPRs, one wave per SIMD)
+        constexpr int kQKUnroll = GQ >= 8 ? (D >= 256 ? 1 : 2) : 4;
+#pragma unroll kQKUnroll
         for (int jp2 = 0; jp2 < D / 2; ++jp2) {
           const uint32_t f = k_pair_index(rw, kb, jp2);
-          const int j = 2 * jp2;
-          const float k0 = kl_s[f][0], k1 = kl_s[f][1];
+          const float2 kk = *reinterpret_cast<const float2*>(&kl_s[f][0]);
+          const float k0 = kk.x, k1 = kk.y;
 #pragma unroll
-          for (int i = 0; i < GQ; ++i) s[i] += w_s[i][j] * k0 + w_s[i][j + 1] * k1;
+          for (int i = 0; i < GQ; ++i) {
+            const float2 ww = w2_s[jp2][i];
+            s[i] += ww.x * k0 + ww.y * k1;
+          }
         }
 #pragma unroll
         for (int i = 0; i < GQ; ++i) s[i] += bias[i];
@@ -252,25 +300,14 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
           const int* oc = a.p.ocount + obase * TQK_NOB;
           const int cap = d.outlier_cap;
           const int blk = tid / TQK_OBLK;
-          int lo = blk > 0 ? min(oc[blk - 1], cap) : 0;
-          int hi = min(oc[blk], cap);
-          const uint32_t* oe = a.p.oent + obase * cap;
-          const uint32_t first = (uint32_t)tid * D;
-          while (lo < hi) {  // first entry of the run at or after (tid, 0)
-            const int mid = (lo + hi) >> 1;
-            if ((oe[mid] & 0xFFFFu) < first) lo = mid + 1; else hi = mid;
-          }
+          const int lo0 = blk > 0 ? min(oc[blk - 1], cap) : 0;
           const int end = min(oc[blk], cap);
-          for (int e = lo; e < end; ++e) {
-            const uint32_t ent = oe[e];
-            const uint32_t pos = ent & 0xFFFFu;
-            if (pos >= first + D) break;
-            const int j = (int)(pos - first);
-            const uint32_t f = k_pair_index(rw, kb, j >> 1);
-            const uint32_t c = (j & 1) ? k_code_odd(f, kb) : k_code_even(f, kb);
-            const float delta = h2f((uint16_t)(ent >> 16)) - (a_s[j] * key_level(a.d.key_grid, c) + mu_s[j]);
-#pragma unroll
-            for (int i = 0; i < GQ; ++i) s[i] += q_s[i][j] * delta;
+          const uint32_t first = (uint32_t)tid * D;
+          if (oe_lds) {
+            outlier_walk<GQ, D>(oe_s, lo0, end, first, rw, kb, a.d.key_grid, a_s, mu_s, q_s, s);
+          } else {
+            outlier_walk<GQ, D>(a.p.oent + obase * cap, lo0, end, first, rw, kb, a.d.key_grid, a_s, mu_s,
+                                q_s, s);
           }
         }
         const float kn = polar ? a.p.knorm[row] * sm : sm;  // score = |k| * (q_rot . centroids)
