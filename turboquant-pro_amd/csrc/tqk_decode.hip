@@ -321,6 +321,10 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
 
       // value accumulation in rotated code space: thread = (channel pair, token slice)
       const int tend = min(G, tq * TS + TS);
+      // (unrolled so that several tokens' row and code loads are in flight;
+      // not at 8 heads and head_dim 256, where it takes all 256 VGPRs)
+      constexpr int kVU = GQ >= 8 && D >= 256 ? 1 : 4;
+#pragma unroll kVU
       for (int tt = tq * TS; tt < tend; ++tt) {
         const size_t row = page_row(bt, d.max_pages_per_seq, b, g * G + tt, P, d.n_pages, h);
         // the 2*VB-bit field of channels 2jp, 2jp + 1 in the token's bit stream
@@ -383,6 +387,8 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
       __syncthreads();
       softmax_update<GQ>(sc_s, n, m_run, l_run, acc0, acc1, red_s, 1.0f);
       const int tend = min(n, tq * TS + TS);
+      constexpr int kVUh = GQ >= 8 && D >= 256 ? 1 : 4;
+#pragma unroll kVUh
       for (int tt = tq * TS; tt < tend; ++tt) {
         const size_t vrow = (hbase + (t0 + tt) % R) * D;
         float c0, c1;
