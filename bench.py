@@ -56,7 +56,18 @@ CONFIGS = {
     # its outliers) and uniform (PerChannelKV's default grid)
     "k4v3_nf4_noout": dict(B=16, Hkv=8, Hq=32, L=32768, vbits=3, kbits=4, key_grid="nf4_asym", ofrac=0.0),
     "k4v3_uniform": dict(B=16, Hkv=8, Hq=32, L=32768, vbits=3, kbits=4, key_grid="uniform", ofrac=0.0),
+    # pools the MFMA decode does not take, served by the VALU decode (split
+    # kernel + merge kernel): head_dim 64, head_dim 256 (gemma-2-9b's 16 q /
+    # 8 kv heads) and an fp32 cache (fp32 hot window and queries)
+    "d64_8k": dict(B=16, Hkv=8, Hq=32, L=8192, vbits=3, D=64),
+    "d256_8k": dict(B=16, Hkv=8, Hq=16, L=8192, vbits=3, D=256),
+    "f32_8k": dict(B=16, Hkv=8, Hq=32, L=8192, vbits=3, dtype="float32"),
 }
+
+
+def mfma_config(cfg):
+    """Whether the config's pool runs the MFMA decode (head_dim 128, fp16)."""
+    return cfg.get("D", 128) == 128 and cfg.get("dtype", "float16") == "float16"
 
 
 def config_lengths(cfg):
@@ -72,11 +83,13 @@ def n_groups(L, W=512):
     return 0 if L <= W else (L - (W + 1)) // G + 1
 
 
-def step_bytes(lens, Hkv, Hq, D=128, kbits=4, vbits=3, W=512, n_out=640, out_bytes=2, polar_keys=False):
+def step_bytes(lens, Hkv, Hq, D=128, kbits=4, vbits=3, W=512, n_out=640, out_bytes=2, polar_keys=False,
+               tok_bytes=2):
     """Canonical compressed bytes of one decode step (storage-of-record sizes):
     per (sequence, kv head) n_cold*(D*kb/8 + D*vb/8 + 4) + n_grp*(2*D*4 + n_out*6)
-    + n_hot*2*D*2, plus q in and output per query head.  PolarQuant keys carry
-    a 4-byte norm per token instead of the per-group scale and mean."""
+    + n_hot*2*D*tok_bytes, plus q in and output per query head.  PolarQuant
+    keys carry a 4-byte norm per token instead of the per-group scale and mean;
+    fp32 caches (tok_bytes 4) keep fp32 hot tokens and take fp32 queries."""
     G = (W + 1) // 2
     tot = 0
     for L in lens:
@@ -84,7 +97,8 @@ def step_bytes(lens, Hkv, Hq, D=128, kbits=4, vbits=3, W=512, n_out=640, out_byt
         n_cold, n_hot = ng * G, L - ng * G
         per_tok = D * kbits // 8 + D * vbits // 8 + 4 + (4 if polar_keys else 0)
         per_grp = (0 if polar_keys else 2 * D * 4) + n_out * 6
-        tot += Hkv * (n_cold * per_tok + ng * per_grp + n_hot * 2 * D * 2 + (Hq // Hkv) * D * (2 + out_bytes))
+        tot += Hkv * (n_cold * per_tok + ng * per_grp + n_hot * 2 * D * tok_bytes
+                      + (Hq // Hkv) * D * (tok_bytes + out_bytes))
     return tot
 
 
@@ -99,16 +113,18 @@ def key_form(cfg):
 
 
 def config_step_bytes(cfg):
-    """step_bytes of a config: its key form, widths and outlier count (2 % of
-    a 256-token group per channel: 5 x 128)."""
-    n_out = 640 if cfg.get("ofrac", 0.02) > 0 else 0
-    return step_bytes(config_lengths(cfg), cfg["Hkv"], cfg["Hq"], kbits=cfg.get("kbits", 4),
-                      vbits=cfg["vbits"], n_out=n_out, polar_keys=cfg.get("key_grid") == "polar")
+    """step_bytes of a config: its key form, widths, head_dim, token width and
+    outlier count (2 % of a 256-token group per channel: 5 x head_dim)."""
+    D = cfg.get("D", 128)
+    n_out = 5 * D if cfg.get("ofrac", 0.02) > 0 else 0
+    return step_bytes(config_lengths(cfg), cfg["Hkv"], cfg["Hq"], D=D, kbits=cfg.get("kbits", 4),
+                      vbits=cfg["vbits"], n_out=n_out, polar_keys=cfg.get("key_grid") == "polar",
+                      tok_bytes=4 if cfg.get("dtype") == "float32" else 2)
 
 
-def synth_chunk(torch, gen, scale, t0, n, B, Hkv, D=128, theta=10000.0):
-    """fp16 keys/values for positions [t0, t0+n): N(0,1) * per-channel scale,
-    RoPE (rotate_half); values N(0,1)."""
+def synth_chunk(torch, gen, scale, t0, n, B, Hkv, D=128, theta=10000.0, dtype=None):
+    """fp16 (or ``dtype``) keys/values for positions [t0, t0+n): N(0,1) *
+    per-channel scale, RoPE (rotate_half); values N(0,1)."""
     dev = scale.device
     k = torch.randn((B, Hkv, n, D), generator=gen, device=dev, dtype=torch.float32) * scale
     half = D // 2
@@ -117,8 +133,9 @@ def synth_chunk(torch, gen, scale, t0, n, B, Hkv, D=128, theta=10000.0):
     cos = torch.cat([ang.cos(), ang.cos()], 1).float()
     sin = torch.cat([ang.sin(), ang.sin()], 1).float()
     rh = torch.cat([-k[..., half:], k[..., :half]], -1)
-    k = (k * cos + rh * sin).half()
-    v = torch.randn((B, Hkv, n, D), generator=gen, device=dev, dtype=torch.float32).half()
+    dt = torch.float16 if dtype is None else dtype
+    k = (k * cos + rh * sin).to(dt)
+    v = torch.randn((B, Hkv, n, D), generator=gen, device=dev, dtype=torch.float32).to(dt)
     return k, v
 
 
@@ -126,6 +143,7 @@ def build_pool(torch, cfg, seed, chunk=4096):
     from turboquant_pro_amd import TQKVPool
     import numpy as np
     B, Hkv, Hq, L = cfg["B"], cfg["Hkv"], cfg["Hq"], cfg["L"]
+    D, dtype = cfg.get("D", 128), cfg.get("dtype", "float16")
     lens = config_lengths(cfg)
     extra = {}
     if cfg.get("page"):
@@ -134,20 +152,21 @@ def build_pool(torch, cfg, seed, chunk=4096):
         extra = dict(page_tokens=P, block_table=np.random.default_rng(4).permutation(B * max_pages).astype(np.int32))
     if "key_grid" in cfg:
         extra.update(key_grid=cfg["key_grid"], key_bits=cfg["kbits"], outlier_frac=cfg["ofrac"])
-    pool = TQKVPool(n_kv_heads=Hkv, n_q_heads=Hq, max_batch=B, max_seq_len=L,
-                    value_bits=cfg["vbits"], seed=seed, **extra)
+    pool = TQKVPool(n_kv_heads=Hkv, n_q_heads=Hq, head_dim=D, max_batch=B, max_seq_len=L,
+                    value_bits=cfg["vbits"], seed=seed, input_dtype=dtype, **extra)
     gen = torch.Generator(device="cuda")
     gen.manual_seed(seed)
-    scale = torch.exp(torch.randn((B, Hkv, 1, 128), generator=gen, device="cuda"))
-    n_hot_ch = round(0.02 * 128)
+    scale = torch.exp(torch.randn((B, Hkv, 1, D), generator=gen, device="cuda"))
+    n_hot_ch = round(0.02 * D)
     for b in range(B):
         for h in range(Hkv):
-            ch = torch.randperm(128, generator=gen, device="cuda")[:n_hot_ch]
+            ch = torch.randperm(D, generator=gen, device="cuda")[:n_hot_ch]
             scale[b, h, 0, ch] *= 10.0
     t = 0
     while t < L:
         n = min(chunk, L - t)
-        k, v = synth_chunk(torch, gen, scale, t, n, B, Hkv)
+        k, v = synth_chunk(torch, gen, scale, t, n, B, Hkv, D=D,
+                           dtype=torch.float32 if dtype == "float32" else None)
         pool.append(k, v, n_new=[min(n, max(0, x - t)) for x in lens])
         t += n
     torch.cuda.synchronize()
@@ -349,8 +368,11 @@ def main():
         sys.exit(2)
 
     cfg = CONFIGS[args.config]
+    if args.encode and not mfma_config(cfg):
+        print(json.dumps({"error": "the encode bench covers head_dim 128 fp16 configs only"}))
+        sys.exit(2)
     cpu = None
-    if not args.encode and not args.no_cpu_baseline and "key_grid" not in cfg:
+    if not args.encode and not args.no_cpu_baseline and "key_grid" not in cfg and mfma_config(cfg):
         # single-threaded BLAS in each worker process; set before NumPy loads
         for var in ("OPENBLAS_NUM_THREADS", "MKL_NUM_THREADS"):
             os.environ[var] = "1"
@@ -370,8 +392,11 @@ def main():
     print(f"[bench] prefill done in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
     gen = torch.Generator(device="cuda")
     gen.manual_seed(7)
-    q = torch.randn((B, Hq, 128), generator=gen, device="cuda").half()
-    outs = [torch.empty((B, Hq, 128), dtype=torch.float32, device="cuda") for _ in pools]
+    D = cfg.get("D", 128)
+    f32 = cfg.get("dtype") == "float32"
+    q = torch.randn((B, Hq, D), generator=gen, device="cuda")
+    q = q if f32 else q.half()
+    outs = [torch.empty((B, Hq, D), dtype=torch.float32, device="cuda") for _ in pools]
 
     def step(i):
         pools[i % len(pools)].decode(q, out=outs[i % len(pools)])
@@ -391,11 +416,12 @@ def main():
     torch.cuda.synchronize()
     ms_per_step = e0.elapsed_time(e1) / args.steps
 
-    # the kernel's average launch duration: each step is exactly one
-    # tqk_decode launch (the in-kernel merge writes the output), so the event
-    # pair around the `steps` back-to-back launches of the timed region,
-    # divided by `steps`, is the average launch duration; the kernel trace
-    # of the same command (rocprofv3 --kernel-trace) cross-checks it
+    # the kernel's average launch duration: each step of an MFMA config is
+    # exactly one tqk_decode launch (the in-kernel merge writes the output),
+    # so the event pair around the `steps` back-to-back launches of the timed
+    # region, divided by `steps`, is the average launch duration; the kernel
+    # trace of the same command (rocprofv3 --kernel-trace) cross-checks it.
+    # A VALU config's step is two launches (split kernel, merge kernel).
     kernel_ms = ms_per_step
     nbytes = config_step_bytes(cfg)
     achieved = nbytes / (kernel_ms * 1e-3) / 1e9
@@ -413,7 +439,7 @@ def main():
     traffic, traffic_src = measured_traffic(args.config)
 
     enc = None
-    if not args.no_encode:
+    if not args.no_encode and mfma_config(cfg):
         del pools
         torch.cuda.empty_cache()
         enc = encode_bench(torch, dict(cfg, name=args.config), 5)
@@ -432,15 +458,15 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp32",
-        "data": "synthetic (seeded lognormal-scaled RoPE fp16 keys with 2% x10 channels, N(0,1) "
-                "values and queries), cache filled through the GPU encode path",
+        "data": f"synthetic (seeded lognormal-scaled RoPE {'fp32' if f32 else 'fp16'} keys with 2% x10 "
+                "channels, N(0,1) values and queries), cache filled through the GPU encode path",
         "config": {"workload": f"decode step, batch {B} x context "
                                + (f"U[1024, {L}] (seeded, mean {sum(config_lengths(cfg)) // B}), "
                                   f"{cfg['page']}-token pages, permuted block table"
                                   if cfg.get("ragged") else f"{L}")
                                + f", {Hq} q-heads / {Hkv} kv-heads, "
-                               f"head_dim 128, {key_form(cfg)}, V{cfg['vbits']} "
-                               f"PolarQuant, fp16 hot window 512",
+                               f"head_dim {D}, {key_form(cfg)}, V{cfg['vbits']} "
+                               f"PolarQuant, {'fp32' if f32 else 'fp16'} hot window 512",
                    "name": args.config, "batch": B, "context": L, "n_q_heads": Hq,
                    "n_kv_heads": Hkv, "replicas": args.replicas},
         "step_bytes": nbytes,
@@ -449,11 +475,14 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic,
                      "traffic_source": traffic_src,
-                     "kernel": "tqk_decode_split_mfma", "kernel_us": round(kernel_ms * 1e3, 2),
+                     "kernel": "tqk_decode_split_mfma" if mfma_config(cfg)
+                               else "tqk_decode_split_valu + tqk_merge",
+                     "kernel_us": round(kernel_ms * 1e3, 2),
                      "kernel_us_method": f"the timed region: one HIP event pair on the launch "
                                          f"stream around {args.steps} back-to-back decode steps "
-                                         "of one tqk_decode launch each, divided by "
-                                         f"{args.steps}"},
+                                         + ("of one tqk_decode launch each" if mfma_config(cfg)
+                                            else "of two launches each (split, merge)")
+                                         + f", divided by {args.steps}"},
         "encode": enc,
         "cpu_baseline": cpu,
     }
