@@ -275,8 +275,25 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
         const size_t row = page_row(bt, d.max_pages_per_seq, b, g * G + tid, P, d.n_pages, h);
         const int kb = d.key_bits;
         const uint32_t* kr = reinterpret_cast<const uint32_t*>(a.p.kcodes + row * k_row_bytes(kb, D));
+        // the token's key row: 16-byte loads where the row is whole 16-byte
+        // pieces (a dword load per word touches each row's cache lines once
+        // per word: one token per lane, rows a row apart)
         uint32_t rw[D / 8];
-        for (int w2 = 0; w2 < k_row_bytes(kb, D) / 4; ++w2) rw[w2] = kr[w2];
+        const int kwords = k_row_bytes(kb, D) / 4;
+        if ((kwords & 3) == 0) {
+#pragma unroll
+          for (int c4 = 0; c4 < D / 32; ++c4) {
+            if (4 * c4 < kwords) {
+              const uint4 x = reinterpret_cast<const uint4*>(kr)[c4];
+              rw[4 * c4] = x.x;
+              rw[4 * c4 + 1] = x.y;
+              rw[4 * c4 + 2] = x.z;
+              rw[4 * c4 + 3] = x.w;
+            }
+          }
+        } else {
+          for (int w2 = 0; w2 < kwords; ++w2) rw[w2] = kr[w2];
+        }
         float s[GQ];
 #pragma unroll
         for (int i = 0; i < GQ; ++i) s[i] = 0.f;
