@@ -171,6 +171,13 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
   // the group's side-list, when it holds at most kVOEnt entries (the token
   // threads' searches and walks then read LDS, not memory)
   __shared__ uint32_t oe_s[kVOEnt];
+  // the group's value code rows, staged by the token threads (one row each,
+  // wide loads) for the value pass, whose threads walk the tokens of a slice
+  // (not at 8 heads: the staging loads, live across the key loop, take all
+  // 256 VGPRs of a wave there, and the value pass reads the rows itself)
+  constexpr bool kStageV = GQ < 8;
+  __shared__ __align__(16) uint32_t vrow_s[kStageV ? kThreads : 1][VROW / 4];
+  static_assert(VROW % 4 == 0, "value rows of whole dwords");
   __shared__ float sc_s[GQ][kThreads];
   __shared__ float kl_s[256][2];
   __shared__ float vl_s[1 << (2 * VB)][2];
@@ -294,6 +301,20 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
         } else {
           for (int w2 = 0; w2 < kwords; ++w2) rw[w2] = kr[w2];
         }
+        // the token's value code row into LDS for the value pass (stored here,
+        // before the score loop, so the row is not held in registers across it)
+        if constexpr (kStageV) {
+          const uint8_t* vsrc = a.p.vcodes + row * VROW;
+          if constexpr (VROW % 16 == 0) {
+#pragma unroll
+            for (int c4 = 0; c4 < VROW / 16; ++c4)
+              reinterpret_cast<uint4*>(&vrow_s[tid][0])[c4] = reinterpret_cast<const uint4*>(vsrc)[c4];
+          } else {
+#pragma unroll
+            for (int w4 = 0; w4 < VROW / 4; ++w4) vrow_s[tid][w4] = reinterpret_cast<const uint32_t*>(vsrc)[w4];
+          }
+          asm volatile("" ::: "memory");
+        }
         float s[GQ];
 #pragma unroll
         for (int i = 0; i < GQ; ++i) s[i] = 0.f;
@@ -336,19 +357,27 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
 
       softmax_update<GQ>(sc_s, G, m_run, l_run, acc0, acc1, red_s, norm_t);
 
-      // value accumulation in rotated code space: thread = (channel pair, token slice)
+      // value accumulation in rotated code space: thread = (channel pair, token
+      // slice), the code rows from LDS where staged above (softmax_update's
+      // barriers order the stores before these reads), else from memory
       const int tend = min(G, tq * TS + TS);
-      // (unrolled so that several tokens' row and code loads are in flight;
-      // not at 8 heads and head_dim 256, where it takes all 256 VGPRs)
-      constexpr int kVU = GQ >= 8 && D >= 256 ? 1 : 4;
+      // (unrolled so that several tokens' loads are in flight; not at 8 heads
+      // and head_dim 256, where it takes all 256 VGPRs)
+      constexpr int kVU = kStageV ? 2 : (D >= 256 ? 1 : 4);
 #pragma unroll kVU
       for (int tt = tq * TS; tt < tend; ++tt) {
-        const size_t row = page_row(bt, d.max_pages_per_seq, b, g * G + tt, P, d.n_pages, h);
         // the 2*VB-bit field of channels 2jp, 2jp + 1 in the token's bit stream
-        const uint32_t* vr = reinterpret_cast<const uint32_t*>(a.p.vcodes + row * VROW);
         const int bit = 2 * VB * jp, wd = bit >> 5, sh = bit & 31;
-        const uint32_t lo = vr[wd];
-        const uint32_t hi = (sh + 2 * VB > 32) ? vr[wd + 1] : 0u;
+        uint32_t lo, hi;
+        if constexpr (kStageV) {
+          lo = vrow_s[tt][wd];
+          hi = (sh + 2 * VB > 32) ? vrow_s[tt][wd + 1] : 0u;
+        } else {
+          const size_t row = page_row(bt, d.max_pages_per_seq, b, g * G + tt, P, d.n_pages, h);
+          const uint32_t* vr = reinterpret_cast<const uint32_t*>(a.p.vcodes + row * VROW);
+          lo = vr[wd];
+          hi = (sh + 2 * VB > 32) ? vr[wd + 1] : 0u;
+        }
         const uint32_t f = (uint32_t)(((((uint64_t)hi) << 32) | lo) >> sh) & ((1u << (2 * VB)) - 1u);
         const float c0 = vl_s[f][0], c1 = vl_s[f][1];
 #pragma unroll
