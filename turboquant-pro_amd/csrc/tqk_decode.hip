@@ -2278,8 +2278,27 @@ Plan make_plan(const tqk_cache_desc* d, int batch, int max_len) {
       }
     }
   } else {
-    gps = (int)((units + 4095) / 4096);
-    if (gps < 1) gps = 1;
+    // VALU kernel: a workgroup pays its set-up (query, code tables, the
+    // split's partial, the merge's share) once for its gps groups, about a
+    // group's time, and about three of its workgroups fit a CU.  Pick gps from
+    // the bound of at most 4096 coded workgroups (which bounds the partials)
+    // up to 8x that, minimising rounds of the CUs times (gps + 1), the hot
+    // splits' workgroups counted in the rounds.
+    const long slots = 3L * device_cus();
+    const long pairs = (long)batch * d->n_kv_heads;
+    const int g_lo = units > 4096 ? (int)((units + 4095) / 4096) : 1;
+    const int g_hi = ngmax > g_lo ? (8 * g_lo < ngmax ? 8 * g_lo : ngmax) : g_lo;
+    double best = 1e30;
+    gps = g_lo;
+    for (int g = g_lo; g <= g_hi; ++g) {
+      const long blocks = pairs * ((ngmax + g - 1) / g + pl.n_hot_splits);
+      const long rounds = (blocks + slots - 1) / slots;
+      const double cost = (double)rounds * (g + 1);
+      if (cost < best - 1e-9) {
+        best = cost;
+        gps = g;
+      }
+    }
   }
   pl.groups_per_split = gps;
   pl.n_cold_splits = ngmax > 0 ? (ngmax + gps - 1) / gps : 0;
