@@ -235,8 +235,28 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
   if (split < a.n_cold_splits) {
     const int g0 = split * a.groups_per_split;
     const int g1 = min(ng, g0 + a.groups_per_split);
+    // the group's slot and the token thread's page are read a group ahead
+    // (their loads overlap the current group's instead of starting its chain;
+    // not at 8 heads and head_dim 256, where the carried registers take all
+    // 256 VGPRs)
+    constexpr bool kAhead = !(GQ >= 8 && D >= 256);
+    const int32_t* gt = a.p.group_table + (size_t)b * d.max_groups_per_seq;
+    const int32_t* btb = bt + (size_t)b * d.max_pages_per_seq;
+    int slot_nx = kAhead && g0 < g1 ? gt[g0] : 0;
+    int phys_nx = kAhead && g0 < g1 && tid < G ? btb[(g0 * G + tid) / P] : 0;
     for (int g = g0; g < g1; ++g) {
-      const int slot = a.p.group_table[(size_t)b * d.max_groups_per_seq + g];
+      int slot, phys;
+      if constexpr (kAhead) {
+        slot = slot_nx;
+        phys = phys_nx;
+        if (g + 1 < g1) {
+          slot_nx = gt[g + 1];
+          if (tid < G) phys_nx = btb[((g + 1) * G + tid) / P];
+        }
+      } else {
+        slot = gt[g];
+        phys = 0;
+      }
       const size_t mbase = ((size_t)slot * Hkv + h) * D;
       const size_t obase = (size_t)slot * Hkv + h;
       const int n_oe = d.outliers_per_channel > 0
@@ -279,7 +299,8 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
       // token bound the token's run, a binary search finds its start)
       float norm_t = 0.f;
       if (tid < G) {
-        const size_t row = page_row(bt, d.max_pages_per_seq, b, g * G + tid, P, d.n_pages, h);
+        const size_t row = kAhead ? ((size_t)h * d.n_pages + phys) * P + (g * G + tid) % P
+                                  : page_row(bt, d.max_pages_per_seq, b, g * G + tid, P, d.n_pages, h);
         const int kb = d.key_bits;
         const uint32_t* kr = reinterpret_cast<const uint32_t*>(a.p.kcodes + row * k_row_bytes(kb, D));
         // the token's key row: 16-byte loads where the row is whole 16-byte
@@ -301,6 +322,17 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
         } else {
           for (int w2 = 0; w2 < kwords; ++w2) rw[w2] = kr[w2];
         }
+        // the token's side-list run bounds (the cumulative counts of its
+        // 32-token block and the one before) and norms, read beside the row
+        // (where used, kAhead: again not at 8 heads and head_dim 256)
+        const bool has_oe = d.outliers_per_channel > 0;
+        const int* oc = a.p.ocount + obase * TQK_NOB;
+        const int blk = tid / TQK_OBLK;
+        const int oc_lo = kAhead && has_oe && blk > 0 ? oc[blk - 1] : 0;
+        const int oc_hi = kAhead && has_oe ? oc[blk] : 0;
+        const float vn = kAhead ? a.p.vnorm[row] : 0.f;
+        // score = |k| * (q_rot . centroids)
+        const float kn = kAhead ? (polar ? a.p.knorm[row] * sm : sm) : 0.f;
         // the token's value code row into LDS for the value pass (stored here,
         // before the score loop, so the row is not held in registers across it)
         if constexpr (kStageV) {
@@ -334,12 +366,10 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
         }
 #pragma unroll
         for (int i = 0; i < GQ; ++i) s[i] += bias[i];
-        if (d.outliers_per_channel > 0) {
-          const int* oc = a.p.ocount + obase * TQK_NOB;
+        if (has_oe) {
           const int cap = d.outlier_cap;
-          const int blk = tid / TQK_OBLK;
-          const int lo0 = blk > 0 ? min(oc[blk - 1], cap) : 0;
-          const int end = min(oc[blk], cap);
+          const int lo0 = min(kAhead ? oc_lo : (blk > 0 ? oc[blk - 1] : 0), cap);
+          const int end = min(kAhead ? oc_hi : oc[blk], cap);
           const uint32_t first = (uint32_t)tid * D;
           if (oe_lds) {
             outlier_walk<GQ, D>(oe_s, lo0, end, first, rw, kb, a.d.key_grid, a_s, mu_s, q_s, s);
@@ -348,10 +378,10 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
                                 q_s, s);
           }
         }
-        const float kn = polar ? a.p.knorm[row] * sm : sm;  // score = |k| * (q_rot . centroids)
+        const float kn2 = kAhead ? kn : (polar ? a.p.knorm[row] * sm : sm);
 #pragma unroll
-        for (int i = 0; i < GQ; ++i) sc_s[i][tid] = s[i] * kn;
-        norm_t = a.p.vnorm[row];
+        for (int i = 0; i < GQ; ++i) sc_s[i][tid] = s[i] * kn2;
+        norm_t = kAhead ? vn : a.p.vnorm[row];
       }
       __syncthreads();
 
