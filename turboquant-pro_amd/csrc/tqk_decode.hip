@@ -119,7 +119,7 @@ __device__ __forceinline__ void softmax_update(float (*sc)[kThreads], int n, flo
 // each call, so that a list staged in LDS is read with LDS loads.
 template <int GQ, int D>
 __device__ __forceinline__ void outlier_walk(const uint32_t* oe, int lo, int end, uint32_t first,
-                                             const uint32_t (&rw)[D / 8], int kb, int key_grid,
+                                             const uint32_t* __restrict__ krow, int kb, int key_grid,
                                              const float* a_s, const float* mu_s,
                                              const float (*q_s)[D], float (&s)[GQ]) {
   int hi = end;
@@ -132,11 +132,46 @@ __device__ __forceinline__ void outlier_walk(const uint32_t* oe, int lo, int end
     const uint32_t pos = ent & 0xFFFFu;
     if (pos >= first + D) break;
     const int j = (int)(pos - first);
-    const uint32_t f = k_pair_index(rw, kb, j >> 1);
+    const uint32_t f = k_pair_index(krow, kb, j >> 1);
     const uint32_t c = (j & 1) ? k_code_odd(f, kb) : k_code_even(f, kb);
     const float delta = h2f((uint16_t)(ent >> 16)) - (a_s[j] * key_level(key_grid, c) + mu_s[j]);
 #pragma unroll
     for (int i = 0; i < GQ; ++i) s[i] += q_s[i][j] * delta;
+  }
+}
+
+// A token's dense key scores s[i] += w_i(pair) . levels(pair), pair by pair
+// in channel order, by 32-channel chunks (KB words of the row each, read once
+// per chunk): the 16 pairs of a chunk take their fields at fixed bit offsets
+// (no per-pair switch on the key width or register-indexed row read).
+template <int KB, int GQ, int D>
+__device__ __forceinline__ void key_chunk_scores(const uint32_t (&rw)[D / 8], const float (*kl)[2],
+                                                 const float2 (*w2)[GQ], float (&s)[GQ]) {
+#pragma unroll 1
+  for (int c = 0; c < D / 32; ++c) {
+    uint32_t cw[KB];
+#pragma unroll
+    for (int i = 0; i < KB; ++i) cw[i] = rw[c * KB + i];
+#pragma unroll
+    for (int p = 0; p < 16; ++p) {
+      uint32_t f;
+      if constexpr (KB == 4) {
+        f = (cw[p >> 2] >> (8 * (p & 3))) & 0xFFu;
+      } else {
+        constexpr int kF = 2 * KB;
+        const int o = kF * p, w = o >> 5, sh = o & 31;
+        uint32_t v = cw[w] >> sh;
+        if (sh + kF > 32) v |= cw[w + 1] << (32 - sh);
+        f = v & ((1u << kF) - 1u);
+      }
+      const float2 kk = *reinterpret_cast<const float2*>(&kl[f][0]);
+      const float k0 = kk.x, k1 = kk.y;
+#pragma unroll
+      for (int i = 0; i < GQ; ++i) {
+        const float2 ww = w2[c * 16 + p][i];
+        s[i] += ww.x * k0 + ww.y * k1;
+      }
+    }
   }
 }
 
@@ -350,19 +385,25 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
         float s[GQ];
 #pragma unroll
         for (int i = 0; i < GQ; ++i) s[i] = 0.f;
-        // (unrolled by 4, at 8 heads by 2 or not at all, only: a full unroll at head_dim 64
-        // hoists every weight read and takes all 256 VGPRs, one wave per SIMD)
-        constexpr int kQKUnroll = GQ >= 8 ? (D >= 256 ? 1 : 2) : 4;
-#pragma unroll kQKUnroll
-        for (int jp2 = 0; jp2 < D / 2; ++jp2) {
-          const uint32_t f = k_pair_index(rw, kb, jp2);
-          const float2 kk = *reinterpret_cast<const float2*>(&kl_s[f][0]);
-          const float k0 = kk.x, k1 = kk.y;
+        if constexpr (GQ >= 8 && D >= 256) {
+          // (pair by pair, not unrolled: a chunk's 16 pairs at 8 heads hoist
+          // 128 weight pairs and take all 256 VGPRs)
+#pragma unroll 1
+          for (int jp2 = 0; jp2 < D / 2; ++jp2) {
+            const uint32_t f = k_pair_index(rw, kb, jp2);
+            const float2 kk = *reinterpret_cast<const float2*>(&kl_s[f][0]);
 #pragma unroll
-          for (int i = 0; i < GQ; ++i) {
-            const float2 ww = w2_s[jp2][i];
-            s[i] += ww.x * k0 + ww.y * k1;
+            for (int i = 0; i < GQ; ++i) {
+              const float2 ww = w2_s[jp2][i];
+              s[i] += ww.x * kk.x + ww.y * kk.y;
+            }
           }
+        } else if (kb == 4) {
+          key_chunk_scores<4, GQ, D>(rw, kl_s, w2_s, s);
+        } else if (kb == 3) {
+          key_chunk_scores<3, GQ, D>(rw, kl_s, w2_s, s);
+        } else {
+          key_chunk_scores<2, GQ, D>(rw, kl_s, w2_s, s);
         }
 #pragma unroll
         for (int i = 0; i < GQ; ++i) s[i] += bias[i];
@@ -372,10 +413,16 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
           const int end = min(kAhead ? oc_hi : oc[blk], cap);
           const uint32_t first = (uint32_t)tid * D;
           if (oe_lds) {
-            outlier_walk<GQ, D>(oe_s, lo0, end, first, rw, kb, a.d.key_grid, a_s, mu_s, q_s, s);
+            outlier_walk<GQ, D>(oe_s, lo0, end, first, kr, kb, a.d.key_grid, a_s, mu_s, q_s, s);
           } else {
-            outlier_walk<GQ, D>(a.p.oent + obase * cap, lo0, end, first, rw, kb, a.d.key_grid, a_s, mu_s,
-                                q_s, s);
+            // (at 8 heads and head_dim 256 from the row's registers: the
+            // row pointer held across the walk there takes all 256 VGPRs)
+            if constexpr (GQ >= 8 && D >= 256)
+              outlier_walk<GQ, D>(a.p.oent + obase * cap, lo0, end, first, rw, kb, a.d.key_grid, a_s,
+                                  mu_s, q_s, s);
+            else
+              outlier_walk<GQ, D>(a.p.oent + obase * cap, lo0, end, first, kr, kb, a.d.key_grid, a_s,
+                                  mu_s, q_s, s);
           }
         }
         const float kn2 = kAhead ? kn : (polar ? a.p.knorm[row] * sm : sm);
