@@ -447,8 +447,12 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
         const int bit = 2 * VB * jp, wd = bit >> 5, sh = bit & 31;
         uint32_t lo, hi;
         if constexpr (kStageV) {
+          // (3-bit codes: the next word read for every lane, its bits shifted
+          // out where the field does not cross; the last word's fields end
+          // inside it, so its index is clamped to the row)
           lo = vrow_s[tt][wd];
-          hi = (sh + 2 * VB > 32) ? vrow_s[tt][wd + 1] : 0u;
+          if constexpr (VB == 3) hi = vrow_s[tt][min(wd + 1, VROW / 4 - 1)];
+          else hi = (sh + 2 * VB > 32) ? vrow_s[tt][wd + 1] : 0u;
         } else {
           const size_t row = page_row(bt, d.max_pages_per_seq, b, g * G + tt, P, d.n_pages, h);
           const uint32_t* vr = reinterpret_cast<const uint32_t*>(a.p.vcodes + row * VROW);
