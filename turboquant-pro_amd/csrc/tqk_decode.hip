@@ -165,11 +165,10 @@ __device__ __forceinline__ void key_chunk_scores(const uint32_t (&rw)[D / 8], co
         f = v & ((1u << kF) - 1u);
       }
       const float2 kk = *reinterpret_cast<const float2*>(&kl[f][0]);
-      const float k0 = kk.x, k1 = kk.y;
 #pragma unroll
       for (int i = 0; i < GQ; ++i) {
         const float2 ww = w2[c * 16 + p][i];
-        s[i] += ww.x * k0 + ww.y * k1;
+        s[i] = __builtin_fmaf(ww.y, kk.y, __builtin_fmaf(ww.x, kk.x, s[i]));
       }
     }
   }
@@ -459,7 +458,8 @@ __global__ __launch_bounds__(kThreads) void tqk_decode_split_valu(DecodeArgs a) 
           lo = vr[wd];
           hi = (sh + 2 * VB > 32) ? vr[wd + 1] : 0u;
         }
-        const uint32_t f = (uint32_t)(((((uint64_t)hi) << 32) | lo) >> sh) & ((1u << (2 * VB)) - 1u);
+        // (hi:lo) >> sh in one funnel shift
+        const uint32_t f = __builtin_amdgcn_alignbit(hi, lo, (uint32_t)sh) & ((1u << (2 * VB)) - 1u);
         const float c0 = vl_s[f][0], c1 = vl_s[f][1];
 #pragma unroll
         for (int i = 0; i < GQ; ++i) {
