@@ -2254,7 +2254,10 @@ __global__ __launch_bounds__(2 * D) void tqk_merge(MergeArgs a) {
     const int qi = half + 2 * u;
     if (qi < GQ) {
       float o = hr[u];
-#pragma unroll 8
+      // (Pi from global memory at head_dim 256: 32 rows' loads in flight per
+      // batch; same sum, in row order)
+      constexpr int kRotU = kPiLds ? 8 : 32;
+#pragma unroll kRotU
       for (int k = 0; k < D; ++k) o += crot_s[qi][k] * pim[k * D + j];
       const size_t qh = (size_t)b * a.n_q_heads + h * GQ + qi;
       if (a.out) {
