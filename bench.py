@@ -341,6 +341,61 @@ def preroll(fn, min_ms):
             return n, ms
 
 
+def block_bench(torch, steps, S=32768, H=8, D=128):
+    """The block store's whole-request key save: ``tqk_encode_key_block`` (the
+    ``per_channel`` plugin's compress, turboquant_pro/per_channel_kv.py:285-401)
+    on one (1, H, S, D) fp16 block, asym-NF4 + 2 % outliers, each (b, h) one
+    group.  Bytes: fp16 keys in + 4-bit codes, per-channel scale and mean and
+    the side-list (6 B an entry) out.  Median of ``steps`` timed calls after
+    one untimed call."""
+    import ctypes
+    import statistics
+    from turboquant_pro_amd import _native as N
+    from turboquant_pro_amd.codebooks import outliers_per_channel
+    from turboquant_pro_amd.plugins import _block_desc
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(11)
+    x = (torch.randn((1, H, S, D), generator=gen, device="cuda") *
+         torch.exp(0.5 * torch.randn((1, H, 1, D), generator=gen, device="cuda"))).half()
+    k = outliers_per_channel(S, 0.02)
+    cap = min(S * D, 4 * k * D)
+    kp = torch.empty(H * S * D // 2, dtype=torch.uint8, device="cuda")
+    scale = torch.empty((1, H, D), dtype=torch.float32, device="cuda")
+    zero = torch.empty_like(scale)
+    count = torch.zeros(H, dtype=torch.int32, device="cuda")
+    pos = torch.empty((H, cap), dtype=torch.int32, device="cuda")
+    val = torch.empty((H, cap), dtype=torch.float16, device="cuda")
+    d = _block_desc(x.shape, 4, 0, 0, k, cap, 0, None)
+    st = torch.cuda.current_stream()
+
+    def call():
+        N.check(N.lib().tqk_encode_key_block(
+            ctypes.byref(d), x.data_ptr(), None, kp.data_ptr(), scale.data_ptr(), zero.data_ptr(),
+            pos.data_ptr(), val.data_ptr(), count.data_ptr(), ctypes.c_void_p(st.cuda_stream)),
+            "tqk_encode_key_block")
+
+    call()
+    torch.cuda.synchronize()
+    n_out = int(count.sum().item())
+    times = []
+    for _ in range(max(steps, 1)):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        call()
+        e1.record(st)
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1))
+    ms = statistics.median(times)
+    nbytes = H * S * D * 2 + H * S * D // 2 + H * D * 8 + n_out * 6
+    return {"metric": "block key encode ms + GB/s (fp16 keys in, codes and side-list out)",
+            "value": round(ms, 3), "unit": "ms", "higher_is_better": False,
+            "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1), "bytes": nbytes, "calls": len(times),
+            "workgroups": H, "outliers": n_out,
+            "config": {"workload": f"tqk_encode_key_block, one (1, {H}, {S}, {D}) fp16 block, "
+                                   "asym-NF4 + 2% outliers"},
+            "data": "synthetic (seeded N(0,1) x lognormal per-channel scale, fp16)"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -357,6 +412,9 @@ def main():
     ap.add_argument("--encode", action="store_true",
                     help="measure the prefill encode instead (quantize-on-append of 4096-token chunks "
                          "of the chosen config; prints its own JSON line, not the decode metric)")
+    ap.add_argument("--block", action="store_true",
+                    help="measure the plugins' stateless key-block encode on one (1, 8, 32768, 128) "
+                         "block instead (prints its own JSON line)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="after timing, copy a 256 MiB buffer 3 times (calibration kernel for "
                          "the FETCH_SIZE / WRITE_SIZE counters)")
@@ -367,6 +425,10 @@ def main():
                           "out of scope here", "n_gpus": args.gpus}))
         sys.exit(2)
 
+    if args.block:
+        import torch
+        print(json.dumps(block_bench(torch, min(args.steps, 10))), flush=True)
+        return
     cfg = CONFIGS[args.config]
     if args.encode and not mfma_config(cfg):
         print(json.dumps({"error": "the encode bench covers head_dim 128 fp16 configs only"}))

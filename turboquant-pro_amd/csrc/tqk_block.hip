@@ -63,7 +63,42 @@ struct KeyBlockArgs {
   uint32_t* out_pos;
   uint16_t* out_val;
   int32_t* out_count;
+  int thr_pre;  // the thresholds were left in out_pos by tqk_key_block_thresholds
 };
+
+// The outlier thresholds of tqk_key_block ahead of it, spread over the chip:
+// one workgroup per (b, h) and 64 channels, a lane per channel and 16 waves
+// over interleaved token rows (each load one 128-byte row piece).  The same
+// search as tqk_key_block's threshold threads: T is the largest fp32
+// magnitude pattern with #{ |x_s| >= T } >= k, one bit per pass, each pass's
+// count an exact integer sum of the 16 waves' counts.  T is left in the
+// first D entries of the (b, h)'s side-list row (out_pos), which
+// tqk_key_block reads before it writes that row.
+template <int D>
+__global__ __launch_bounds__(1024) void tqk_key_block_thresholds(KeyBlockArgs a) {
+  constexpr int W = 16;
+  const tqk_block_desc& d = a.d;
+  const int bh = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int j = blockIdx.y * 64 + lane;
+  const int S = d.tokens, f32 = d.input_f32, kout = d.outliers_per_channel;
+  const size_t base = (size_t)bh * S * D + j;
+  __shared__ int cnt_s[2][W][64];
+  uint32_t T = 0;
+  for (int bit = 30; bit >= 0; --bit) {
+    const uint32_t cand = T | (1u << bit);
+    int cnt = 0;
+    for (int s = w; s < S; s += W) cnt += (__float_as_uint(fabsf(load_x(a.x, f32, base + (size_t)s * D))) >= cand);
+    // (two count buffers: a wave that runs ahead writes the other one; the
+    // next write to this one follows the next pass's barrier)
+    cnt_s[bit & 1][w][lane] = cnt;
+    __syncthreads();
+    int tot = 0;
+#pragma unroll
+    for (int v = 0; v < W; ++v) tot += cnt_s[bit & 1][v][lane];
+    if (tot >= kout) T = cand;
+  }
+  if (w == 0) a.out_pos[(size_t)bh * d.outlier_cap + j] = T;
+}
 
 // one workgroup of 2 * D threads per (b, h)
 template <int D>
@@ -126,11 +161,15 @@ __global__ __launch_bounds__(2 * D) void tqk_key_block(KeyBlockArgs a) {
     // #{ |x_s| >= T } >= k (NaN patterns order above inf, as np.partition does)
     const int j = tid - D;
     uint32_t T = 0;
-    for (int bit = 30; bit >= 0; --bit) {
-      const uint32_t cand = T | (1u << bit);
-      int cnt = 0;
-      for (int s = 0; s < S; ++s) cnt += (__float_as_uint(fabsf(X(s, j))) >= cand);
-      if (cnt >= kout) T = cand;
+    if (a.thr_pre) {
+      T = a.out_pos[(size_t)bh * d.outlier_cap + j];
+    } else {
+      for (int bit = 30; bit >= 0; --bit) {
+        const uint32_t cand = T | (1u << bit);
+        int cnt = 0;
+        for (int s = 0; s < S; ++s) cnt += (__float_as_uint(fabsf(X(s, j))) >= cand);
+        if (cnt >= kout) T = cand;
+      }
     }
     thr_s[j] = __uint_as_float(T);
   }
@@ -439,9 +478,21 @@ int tqk_encode_key_block(const tqk_block_desc* d, const void* x, const float* zp
   if (!x || !packed || !scale || !zero || !out_count) return TQK_EINVAL;
   if (d->key_grid == 0 && d->zero_point == 2 && !zp) return TQK_EINVAL;
   if (d->outliers_per_channel > 0 && d->outlier_cap > 0 && (!out_pos || !out_val)) return TQK_EINVAL;
-  KeyBlockArgs a{*d, x, zp, packed, scale, zero, out_pos, out_val, out_count};
+  KeyBlockArgs a{*d, x, zp, packed, scale, zero, out_pos, out_val, out_count, 0};
   const dim3 grid(d->batch * d->n_heads);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  // thresholds ahead, over the chip, where the side-list row can hold them
+  if (d->outliers_per_channel > 0 && d->outliers_per_channel < d->tokens &&
+      d->outlier_cap >= d->head_dim) {
+    a.thr_pre = 1;
+    const dim3 tgrid(d->batch * d->n_heads, d->head_dim / 64);
+    if (d->head_dim == 64)
+      hipLaunchKernelGGL(tqk_key_block_thresholds<64>, tgrid, dim3(1024), 0, st, a);
+    else if (d->head_dim == 128)
+      hipLaunchKernelGGL(tqk_key_block_thresholds<128>, tgrid, dim3(1024), 0, st, a);
+    else
+      hipLaunchKernelGGL(tqk_key_block_thresholds<256>, tgrid, dim3(1024), 0, st, a);
+  }
   if (d->head_dim == 64)
     hipLaunchKernelGGL(tqk_key_block<64>, grid, dim3(128), 0, st, a);
   else if (d->head_dim == 128)
