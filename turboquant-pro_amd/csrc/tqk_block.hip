@@ -31,6 +31,36 @@ constexpr int kVbTokens = 64;
 __device__ __forceinline__ float load_x(const void* x, int f32, size_t i) {
   return f32 ? reinterpret_cast<const float*>(x)[i] : h2f(reinterpret_cast<const uint16_t*>(x)[i]);
 }
+// N values of x at i0, i0 + stride, ..., every load issued before any is used
+template <int N>
+__device__ __forceinline__ void load_xn(const void* x, int f32, size_t i0, size_t stride, float (&v)[N]) {
+  if (f32) {
+    const float* p = reinterpret_cast<const float*>(x) + i0;
+#pragma unroll
+    for (int u = 0; u < N; ++u) v[u] = p[u * stride];
+  } else {
+    const uint16_t* p = reinterpret_cast<const uint16_t*>(x) + i0;
+    uint16_t r[N];
+#pragma unroll
+    for (int u = 0; u < N; ++u) r[u] = p[u * stride];
+#pragma unroll
+    for (int u = 0; u < N; ++u) v[u] = h2f(r[u]);
+  }
+}
+// f(s, x[s, col]) for s = s0, s0 + st, ... < s1, in that order, the loads of
+// eight tokens at a time in flight (rows of D elements)
+template <int D, typename F>
+__device__ __forceinline__ void for_tokens(const void* x, int f32, size_t col, int s0, int s1, int st, F f) {
+  constexpr int N = 8;
+  int s = s0;
+  for (; s + (N - 1) * st < s1; s += N * st) {
+    float v[N];
+    load_xn<N>(x, f32, col + (size_t)s * D, (size_t)st * D, v);
+#pragma unroll
+    for (int u = 0; u < N; ++u) f(s + u * st, v[u]);
+  }
+  for (; s < s1; s += st) f(s, load_x(x, f32, col + (size_t)s * D));
+}
 __device__ __forceinline__ bool dc_channel(const tqk_block_desc& d, int j) {
   return (d.dc_mask[j >> 5] >> (j & 31)) & 1u;
 }
@@ -87,7 +117,8 @@ __global__ __launch_bounds__(1024) void tqk_key_block_thresholds(KeyBlockArgs a)
   for (int bit = 30; bit >= 0; --bit) {
     const uint32_t cand = T | (1u << bit);
     int cnt = 0;
-    for (int s = w; s < S; s += W) cnt += (__float_as_uint(fabsf(load_x(a.x, f32, base + (size_t)s * D))) >= cand);
+    for_tokens<D>(a.x, f32, base, w, S, W,
+                  [&](int, float xv) { cnt += (__float_as_uint(fabsf(xv)) >= cand); });
     // (two count buffers: a wave that runs ahead writes the other one; the
     // next write to this one follows the next pass's barrier)
     cnt_s[bit & 1][w][lane] = cnt;
@@ -120,12 +151,11 @@ __global__ __launch_bounds__(2 * D) void tqk_key_block(KeyBlockArgs a) {
     if (d.key_grid == 1) {
       float mn = X(0, j), mx = mn;
       bool nan = (mn != mn);
-      for (int s = 1; s < S; ++s) {
-        const float xv = X(s, j);
+      for_tokens<D>(a.x, f32, base + j, 1, S, 1, [&](int, float xv) {
         nan |= (xv != xv);
         mn = fminf(mn, xv);
         mx = fmaxf(mx, xv);
-      }
+      });
       const float sc = nan ? __builtin_nanf("") : __fdiv_rn(fmaxf(__fsub_rn(mx, mn), 1e-8f),
                                                             (float)((1 << d.bits) - 1));
       if (nan) mn = __builtin_nanf("");
@@ -138,18 +168,18 @@ __global__ __launch_bounds__(2 * D) void tqk_key_block(KeyBlockArgs a) {
       if (d.zero_point == 2) {
         mu = a.zp[(size_t)h * D + j];
       } else {
-        float acc = 0.0f;
-        for (int s = 0; s < S; ++s) acc = __fadd_rn(acc, X(s, j));
+        float acc = 0.0f;  // in token order
+        for_tokens<D>(a.x, f32, base + j, 0, S, 1, [&](int, float xv) { acc = __fadd_rn(acc, xv); });
         mu = (float)((double)acc / (double)S);
         if (d.zero_point == 1) mu = __fmul_rn(mu, dc_channel(d, j) ? 1.0f : 0.0f);
       }
       float amax = 0.0f;
       bool nan = (mu != mu);
-      for (int s = 0; s < S; ++s) {
-        const float dv = fabsf(__fsub_rn(X(s, j), mu));
+      for_tokens<D>(a.x, f32, base + j, 0, S, 1, [&](int, float xv) {
+        const float dv = fabsf(__fsub_rn(xv, mu));
         nan |= (dv != dv);
         amax = fmaxf(amax, dv);
-      }
+      });
       amax = nan ? __builtin_nanf("") : fmaxf(amax, 1e-8f);
 #pragma unroll
       for (int l = 0; l < 16; ++l) cent_s[j][l] = __fadd_rn(mu, __fmul_rn(amax, kNF4[l]));
@@ -227,39 +257,59 @@ __global__ __launch_bounds__(2 * D) void tqk_key_block(KeyBlockArgs a) {
     }
   }
 
-  // ---- outlier side-list in (s, j) order: thread t owns a contiguous token
-  // range, counts its entries, takes its offset from a block scan, writes
+  // ---- outlier side-list in (s, j) order: wave w owns a contiguous token
+  // range and a lane one channel of each 64-channel piece of a token row (one
+  // coalesced row piece per load); the pieces' ballots count the wave's
+  // entries, its offset comes from the waves before it, and the entries are
+  // written at offset + the lanes before them in the ballot
   if (kout > 0) {
     const bool all = kout >= S;
-    const int chunk = (S + T - 1) / T;
-    const int s0 = min(S, tid * chunk), s1 = min(S, s0 + chunk);
-    int cnt = 0;
-    for (int s = s0; s < s1; ++s)
-      for (int j = 0; j < D; ++j) cnt += all || (fabsf(X(s, j)) >= thr_s[j]);
-    int incl = cnt;
+    constexpr int NWV = T / 64, NC = D / 64;
+    const int wv = tid >> 6, ln = tid & 63;
+    const int chunk = (S + NWV - 1) / NWV;
+    const int s0 = min(S, wv * chunk), s1 = min(S, s0 + chunk);
+    float th[NC];
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int v = __shfl_up(incl, o, 64);
-      if ((tid & 63) >= o) incl += v;
-    }
-    if ((tid & 63) == 63) wsum_s[tid >> 6] = incl;
+    for (int c = 0; c < NC; ++c) th[c] = thr_s[c * 64 + ln];
+    int cnt = 0;  // the same in every lane of the wave
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+      for_tokens<D>(a.x, f32, base + c * 64 + ln, s0, s1, 1, [&](int, float xv) {
+        cnt += __popcll(__ballot(all || fabsf(xv) >= th[c]));
+      });
+    if (ln == 0) wsum_s[wv] = cnt;
     __syncthreads();
-    int off = incl - cnt, total = 0;
-    for (int w = 0; w < T / 64; ++w) {
-      if (w < (tid >> 6)) off += wsum_s[w];
+    int off = 0, total = 0;
+    for (int w = 0; w < NWV; ++w) {
+      if (w < wv) off += wsum_s[w];
       total += wsum_s[w];
     }
     if (tid == 0) a.out_count[bh] = total;
     const size_t lb = (size_t)bh * d.outlier_cap;
-    for (int s = s0; s < s1 && off < d.outlier_cap; ++s) {
-      for (int j = 0; j < D; ++j) {
-        const float xv = X(s, j);
-        if (all || fabsf(xv) >= thr_s[j]) {
-          if (off < d.outlier_cap) {
-            a.out_pos[lb + off] = (uint32_t)s * D + (uint32_t)j;
-            a.out_val[lb + off] = f2h(xv);  // fp16, round to nearest even
+    const uint64_t before = (1ull << ln) - 1ull;  // the lanes ahead of this one
+    for (int s4 = s0; s4 < s1 && off < d.outlier_cap; s4 += 4) {
+      float xr[4][NC];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) xr[u][c] = X(min(s4 + u, s1 - 1), c * 64 + ln);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int s = s4 + u;
+        if (s >= s1) break;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const int j = c * 64 + ln;
+          const float xv = xr[u][c];
+          const bool hit = all || fabsf(xv) >= th[c];
+          const uint64_t m = __ballot(hit);
+          const int at = off + __popcll(m & before);
+          if (hit && at < d.outlier_cap) {
+            a.out_pos[lb + at] = (uint32_t)s * D + (uint32_t)j;
+            a.out_val[lb + at] = f2h(xv);  // fp16, round to nearest even
           }
-          ++off;
+          off += __popcll(m);
         }
       }
     }
