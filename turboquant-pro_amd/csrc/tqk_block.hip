@@ -48,10 +48,11 @@ __device__ __forceinline__ void load_xn(const void* x, int f32, size_t i0, size_
   }
 }
 // f(s, x[s, col]) for s = s0, s0 + st, ... < s1, in that order, the loads of
-// eight tokens at a time in flight (rows of D elements)
+// 32 tokens at a time in flight (rows of D elements; one or two waves per SIMD
+// run these loops, so each batch waits one memory latency)
 template <int D, typename F>
 __device__ __forceinline__ void for_tokens(const void* x, int f32, size_t col, int s0, int s1, int st, F f) {
-  constexpr int N = 8;
+  constexpr int N = 32;
   int s = s0;
   for (; s + (N - 1) * st < s1; s += N * st) {
     float v[N];
@@ -60,6 +61,20 @@ __device__ __forceinline__ void for_tokens(const void* x, int f32, size_t col, i
     for (int u = 0; u < N; ++u) f(s + u * st, v[u]);
   }
   for (; s < s1; s += st) f(s, load_x(x, f32, col + (size_t)s * D));
+}
+// f(s, x[s, col], x[s, col + 1]) in token order, 16 tokens' loads in flight
+template <int D, typename F>
+__device__ __forceinline__ void for_token_pairs(const void* x, int f32, size_t col, int s0, int s1, F f) {
+  constexpr int N = 16;
+  int s = s0;
+  for (; s + N - 1 < s1; s += N) {
+    float v0[N], v1[N];
+    load_xn<N>(x, f32, col + (size_t)s * D, D, v0);
+    load_xn<N>(x, f32, col + 1 + (size_t)s * D, D, v1);
+#pragma unroll
+    for (int u = 0; u < N; ++u) f(s + u, v0[u], v1[u]);
+  }
+  for (; s < s1; ++s) f(s, load_x(x, f32, col + (size_t)s * D), load_x(x, f32, col + 1 + (size_t)s * D));
 }
 __device__ __forceinline__ bool dc_channel(const tqk_block_desc& d, int j) {
   return (d.dc_mask[j >> 5] >> (j & 31)) & 1u;
@@ -227,13 +242,13 @@ __global__ __launch_bounds__(2 * D) void tqk_key_block(KeyBlockArgs a) {
     if (d.key_grid == 1) {
       const float mn0 = cent_s[2 * jp][0], sc0 = cent_s[2 * jp][1];
       const float mn1 = cent_s[2 * jp + 1][0], sc1 = cent_s[2 * jp + 1][1];
-      for (int s = s0; s < s1; ++s) {
-        const float r0 = __builtin_rintf(__fdiv_rn(__fsub_rn(X(s, 2 * jp), mn0), sc0));
-        const float r1 = __builtin_rintf(__fdiv_rn(__fsub_rn(X(s, 2 * jp + 1), mn1), sc1));
+      for_token_pairs<D>(a.x, f32, base + 2 * jp, s0, s1, [&](int s, float x0, float x1) {
+        const float r0 = __builtin_rintf(__fdiv_rn(__fsub_rn(x0, mn0), sc0));
+        const float r1 = __builtin_rintf(__fdiv_rn(__fsub_rn(x1, mn1), sc1));
         const uint32_t b0 = (uint32_t)fminf(fmaxf(r0, 0.0f), 15.0f);
         const uint32_t b1 = (uint32_t)fminf(fmaxf(r1, 0.0f), 15.0f);
         out[(size_t)s * (D / 2)] = (uint8_t)((rev4(b0) << 4) | rev4(b1));
-      }
+      });
     } else {
       float c0[16], c1[16];
 #pragma unroll
@@ -241,8 +256,7 @@ __global__ __launch_bounds__(2 * D) void tqk_key_block(KeyBlockArgs a) {
         c0[l] = cent_s[2 * jp][l];
         c1[l] = cent_s[2 * jp + 1][l];
       }
-      for (int s = s0; s < s1; ++s) {
-        const float x0 = X(s, 2 * jp), x1 = X(s, 2 * jp + 1);
+      for_token_pairs<D>(a.x, f32, base + 2 * jp, s0, s1, [&](int s, float x0, float x1) {
         int b0 = 0, b1 = 0;
         float d0 = fabsf(__fsub_rn(x0, c0[0])), d1 = fabsf(__fsub_rn(x1, c1[0]));
 #pragma unroll
@@ -253,7 +267,7 @@ __global__ __launch_bounds__(2 * D) void tqk_key_block(KeyBlockArgs a) {
           if (e1 < d1 || (e1 != e1 && d1 == d1)) { d1 = e1; b1 = l; }
         }
         out[(size_t)s * (D / 2)] = (uint8_t)((rev4(b0) << 4) | rev4(b1));
-      }
+      });
     }
   }
 
