@@ -108,7 +108,8 @@ struct KeyBlockArgs {
   uint32_t* out_pos;
   uint16_t* out_val;
   int32_t* out_count;
-  int thr_pre;  // the thresholds were left in out_pos by tqk_key_block_thresholds
+  int thr_pre;     // the thresholds were left in out_pos by tqk_key_block_thresholds
+  int codes_post;  // the 4-bit codes are written by tqk_key_block_codes4 afterwards
 };
 
 // The outlier thresholds of tqk_key_block ahead of it, spread over the chip:
@@ -235,7 +236,7 @@ __global__ __launch_bounds__(2 * D) void tqk_key_block(KeyBlockArgs a) {
     }
   }
   // ---- 4-bit codes: thread = (channel pair, token slice), one byte per (token, pair)
-  else {
+  else if (!a.codes_post) {
     const int jp = tid % (D / 2), sq = tid / (D / 2);  // four token slices
     const int per = (S + 3) / 4, s0 = sq * per, s1 = min(S, s0 + per);
     uint8_t* out = a.packed + base / 2 + jp;
@@ -329,6 +330,52 @@ __global__ __launch_bounds__(2 * D) void tqk_key_block(KeyBlockArgs a) {
     }
   } else if (tid == 0) {
     a.out_count[bh] = 0;
+  }
+}
+
+// The 4-bit codes of tqk_key_block over the chip: a workgroup per (b, h) and
+// 256 tokens, thread = (channel pair, token slice).  The levels are rebuilt
+// from the scale and zero point tqk_key_block stored, with its arithmetic
+// (NF4: mean + amax * level; uniform: min and step), so the codes are its.
+template <int D>
+__global__ __launch_bounds__(256) void tqk_key_block_codes4(KeyBlockArgs a) {
+  constexpr int NPR = D / 2, NS = 256 / NPR, TOK = 256, PER = TOK / NS;
+  const tqk_block_desc& d = a.d;
+  const int bh = blockIdx.x, tid = threadIdx.x, jp = tid % NPR, sq = tid / NPR;
+  const int S = d.tokens, f32 = d.input_f32;
+  const size_t base = (size_t)bh * S * D;
+  const int t0 = blockIdx.y * TOK, t1 = min(S, t0 + TOK);
+  const int s0 = min(t1, t0 + sq * PER), s1 = min(t1, s0 + PER);
+  uint8_t* out = a.packed + base / 2 + jp;
+  const size_t cj = (size_t)bh * D + 2 * jp;
+  const float sc0 = a.scale[cj], z0 = a.zero[cj], sc1 = a.scale[cj + 1], z1 = a.zero[cj + 1];
+  if (d.key_grid == 1) {
+    for_token_pairs<D>(a.x, f32, base + 2 * jp, s0, s1, [&](int s, float x0, float x1) {
+      const float r0 = __builtin_rintf(__fdiv_rn(__fsub_rn(x0, z0), sc0));
+      const float r1 = __builtin_rintf(__fdiv_rn(__fsub_rn(x1, z1), sc1));
+      const uint32_t b0 = (uint32_t)fminf(fmaxf(r0, 0.0f), 15.0f);
+      const uint32_t b1 = (uint32_t)fminf(fmaxf(r1, 0.0f), 15.0f);
+      out[(size_t)s * (D / 2)] = (uint8_t)((rev4(b0) << 4) | rev4(b1));
+    });
+  } else {
+    float c0[16], c1[16];
+#pragma unroll
+    for (int l = 0; l < 16; ++l) {
+      c0[l] = __fadd_rn(z0, __fmul_rn(sc0, kNF4[l]));
+      c1[l] = __fadd_rn(z1, __fmul_rn(sc1, kNF4[l]));
+    }
+    for_token_pairs<D>(a.x, f32, base + 2 * jp, s0, s1, [&](int s, float x0, float x1) {
+      int b0 = 0, b1 = 0;
+      float d0 = fabsf(__fsub_rn(x0, c0[0])), d1 = fabsf(__fsub_rn(x1, c1[0]));
+#pragma unroll
+      for (int l = 1; l < 16; ++l) {
+        const float e0 = fabsf(__fsub_rn(x0, c0[l])), e1 = fabsf(__fsub_rn(x1, c1[l]));
+        // np.argmin: strictly smaller wins; the first NaN wins over any number
+        if (e0 < d0 || (e0 != e0 && d0 == d0)) { d0 = e0; b0 = l; }
+        if (e1 < d1 || (e1 != e1 && d1 == d1)) { d1 = e1; b1 = l; }
+      }
+      out[(size_t)s * (D / 2)] = (uint8_t)((rev4(b0) << 4) | rev4(b1));
+    });
   }
 }
 
@@ -557,12 +604,24 @@ int tqk_encode_key_block(const tqk_block_desc* d, const void* x, const float* zp
     else
       hipLaunchKernelGGL(tqk_key_block_thresholds<256>, tgrid, dim3(1024), 0, st, a);
   }
+  // 4-bit codes afterwards, over the chip (a workgroup per 256 tokens)
+  const int n_tok_blocks = (d->tokens + 255) / 256;
+  a.codes_post = d->bits == 4 && n_tok_blocks <= 65535;
   if (d->head_dim == 64)
     hipLaunchKernelGGL(tqk_key_block<64>, grid, dim3(128), 0, st, a);
   else if (d->head_dim == 128)
     hipLaunchKernelGGL(tqk_key_block<128>, grid, dim3(256), 0, st, a);
   else
     hipLaunchKernelGGL(tqk_key_block<256>, grid, dim3(512), 0, st, a);
+  if (a.codes_post) {
+    const dim3 cgrid(d->batch * d->n_heads, n_tok_blocks);
+    if (d->head_dim == 64)
+      hipLaunchKernelGGL(tqk_key_block_codes4<64>, cgrid, dim3(256), 0, st, a);
+    else if (d->head_dim == 128)
+      hipLaunchKernelGGL(tqk_key_block_codes4<128>, cgrid, dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL(tqk_key_block_codes4<256>, cgrid, dim3(256), 0, st, a);
+  }
   return hipGetLastError() == hipSuccess ? TQK_OK : TQK_EHIP;
 }
 
