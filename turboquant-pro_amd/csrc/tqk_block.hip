@@ -116,8 +116,8 @@ struct KeyBlockArgs {
 // one workgroup per (b, h) and 64 channels, a lane per channel and 16 waves
 // over interleaved token rows (each load one 128-byte row piece).  The same
 // search as tqk_key_block's threshold threads: T is the largest fp32
-// magnitude pattern with #{ |x_s| >= T } >= k, one bit per pass, each pass's
-// count an exact integer sum of the 16 waves' counts.  T is left in the
+// magnitude pattern with #{ |x_s| >= T } >= k, found two bits a pass, each
+// pass's counts exact integer sums of the 16 waves' counts.  T is left in the
 // first D entries of the (b, h)'s side-list row (out_pos), which
 // tqk_key_block reads before it writes that row.
 template <int D>
@@ -128,21 +128,39 @@ __global__ __launch_bounds__(1024) void tqk_key_block_thresholds(KeyBlockArgs a)
   const int j = blockIdx.y * 64 + lane;
   const int S = d.tokens, f32 = d.input_f32, kout = d.outliers_per_channel;
   const size_t base = (size_t)bh * S * D + j;
-  __shared__ int cnt_s[2][W][64];
+  // Two bits a pass (bits 30..1 in pairs, then bit 0): the counts of the
+  // three candidates T | d << sh (d = 1, 2, 3) fall with d, so the largest d
+  // whose count reaches k is what two one-bit passes would pick.
+  __shared__ int cnt_s[2][3][W][64];
   uint32_t T = 0;
-  for (int bit = 30; bit >= 0; --bit) {
-    const uint32_t cand = T | (1u << bit);
-    int cnt = 0;
-    for_tokens<D>(a.x, f32, base, w, S, W,
-                  [&](int, float xv) { cnt += (__float_as_uint(fabsf(xv)) >= cand); });
+  int par = 0;
+  for (int sh = 29; sh >= -1; sh -= 2, par ^= 1) {
+    const bool two = sh >= 1;
+    const int shift = two ? sh : 0;
+    const uint32_t c1 = T | (1u << shift), c2 = T | (2u << shift), c3 = T | (3u << shift);
+    int n1 = 0, n2 = 0, n3 = 0;
+    for_tokens<D>(a.x, f32, base, w, S, W, [&](int, float xv) {
+      const uint32_t u = __float_as_uint(fabsf(xv));
+      n1 += u >= c1;
+      n2 += u >= c2;
+      n3 += u >= c3;
+    });
     // (two count buffers: a wave that runs ahead writes the other one; the
     // next write to this one follows the next pass's barrier)
-    cnt_s[bit & 1][w][lane] = cnt;
+    cnt_s[par][0][w][lane] = n1;
+    cnt_s[par][1][w][lane] = n2;
+    cnt_s[par][2][w][lane] = n3;
     __syncthreads();
-    int tot = 0;
+    int t1 = 0, t2 = 0, t3 = 0;
 #pragma unroll
-    for (int v = 0; v < W; ++v) tot += cnt_s[bit & 1][v][lane];
-    if (tot >= kout) T = cand;
+    for (int v = 0; v < W; ++v) {
+      t1 += cnt_s[par][0][v][lane];
+      t2 += cnt_s[par][1][v][lane];
+      t3 += cnt_s[par][2][v][lane];
+    }
+    const uint32_t dsel = two ? (t3 >= kout ? 3u : t2 >= kout ? 2u : t1 >= kout ? 1u : 0u)
+                              : (t1 >= kout ? 1u : 0u);
+    T |= dsel << shift;
   }
   if (w == 0) a.out_pos[(size_t)bh * d.outlier_cap + j] = T;
 }
